@@ -1,0 +1,271 @@
+"""Routed-decode benchmark on one MI355X.
+
+Workload (the 8B-geometry kernel check, one decode step of a Qwen3-8B-shaped
+model): 36 layers x 8 KV groups x 4 query heads, d=128, F=3000 buckets,
+Top-16, history H=65536 plus a 256-token generated tail, bf16 K/V ~ N(0,1),
+fp32 moment tables, bitmaps [8,3000,2048] u32 per layer; every key joins the
+buckets of its top-8 ReLU activations of a random SAE (W_enc ~ N(0,1/128)).
+Inputs are generated on the device (synthetic, seeded) and stay resident in
+HBM; 36 distinct layers (~17.7 GB) rotate so nothing is served from the
+256 MB Infinity Cache.
+
+A "step" is one decode step through all layers: for every layer route
+(moment scoring + Top-16), union (bitmap OR + compaction) and sparse AV,
+captured once in a HIP graph and replayed.  The headline value is the replay
+time per layer in microseconds (lower is better).  Per-stage times come from
+isolated-stage graphs (one launch per layer), and the roofline object reports
+the dominant kernel's algorithmic bytes per launch over its average launch
+time.  The CPU baseline times the C oracle (single thread) on a bounded
+sample of the same layer workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "routed decode µs/layer at 64K history (8 groups); per-stage HBM GB/s vs peak"
+PPU_US_PER_LAYER_64K = 108.3  # whole sparse chain, PPU-ZW810 (tail 8)
+G, HQ, D, F, TOPK = 8, 4, 128, 3000, 16
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--layers", type=int, default=36)
+    p.add_argument("--history", type=int, default=65536)
+    p.add_argument("--tail", type=int, default=256)
+    p.add_argument("--splits", type=int, default=64)
+    p.add_argument("--seed", type=int, default=2)
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU-baseline sample")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--stages", default="chain,route,union,attend,copy",
+                   help="comma list of timed regions (for profiling runs)")
+    return p.parse_args()
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+@torch.no_grad()
+def make_layer(lib_path, layer, H, T, seed, device):
+    """One layer: K/V/Q and its 8 group indices built on the device."""
+    from prismkv_amd import Native8B
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed * 1000 + layer)
+    k = torch.randn(G, H + T, D, generator=gen, device=device, dtype=torch.float32).to(torch.bfloat16)
+    v = torch.randn(G, H + T, D, generator=gen, device=device, dtype=torch.float32).to(torch.bfloat16)
+    q = torch.randn(G, HQ, D, generator=gen, device=device, dtype=torch.float32).to(torch.bfloat16)
+    counts = torch.zeros(G, F, dtype=torch.int64, device=device)
+    mean = torch.zeros(G, F, D, device=device)
+    var = torch.zeros(G, F, D, device=device)
+    csr, offs = [], []
+    for g in range(G):
+        W = torch.randn(F, D, generator=gen, device=device) / D ** 0.5
+        keys = k[g, :H].float()
+        toks, feats = [], []
+        for lo in range(0, H, 16384):
+            a = keys[lo:lo + 16384] @ W.T
+            val, idx = a.topk(8, dim=1)
+            keep = val > 0
+            rows = torch.arange(lo, lo + len(a), device=device)[:, None].expand_as(idx)
+            toks.append(rows[keep])
+            feats.append(idx[keep])
+        tok, feat = torch.cat(toks), torch.cat(feats)
+        order = torch.argsort(feat * H + tok)
+        tok, feat = tok[order], feat[order]
+        n = torch.bincount(feat, minlength=F)
+        counts[g] = n
+        mu = torch.zeros(F, D, device=device).index_add_(0, feat, keys[tok]) / n.clamp_min(1)[:, None]
+        dev = keys[tok] - mu[feat]
+        mean[g] = mu
+        var[g] = torch.zeros(F, D, device=device).index_add_(0, feat, dev * dev) / n.clamp_min(1)[:, None]
+        csr.append(tok.int())
+        offs.append(torch.cat((torch.zeros(1, dtype=torch.int64, device=device), n.cumsum(0))).int())
+    width = max(len(x) for x in csr)
+    csr = torch.stack([torch.nn.functional.pad(x, (0, width - len(x))) for x in csr])
+    op = Native8B.from_tables(H, counts, mean, var, csr, torch.stack(offs), lib_path)
+    return op, q, k, v
+
+
+def graph_time(fn, steps, warmup):
+    """Capture fn once, replay; returns (ms per replay by events, ms per replay wall)."""
+    cur = torch.cuda.current_stream()
+    side = torch.cuda.Stream()
+    side.wait_stream(cur)
+    with torch.cuda.stream(side):
+        fn()
+    cur.wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(steps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    return e0.elapsed_time(e1) / steps, wall, graph
+
+
+def stage_bytes(ops, H, T):
+    """Algorithmic HBM bytes per launch (8 groups of one layer), averaged over layers."""
+    nw = (H + 31) // 32
+    route = G * F * (2 * D * 4 + 4) + G * HQ * D * 2 + G * TOPK * 12 + G * 4
+    unions, avs, uniq = [], [], []
+    for op in ops:
+        u = op.count.cpu().numpy().astype(np.int64)
+        nsel = (op.valid.cpu().numpy() > 0).sum(1)
+        unions.append(int((nsel * nw * 4 + u * 4 + 4).sum() + G * TOPK * 12))
+        avs.append(int(((u + T) * 2 * D * 2 + u * 4 + 4).sum() + 2 * G * HQ * D * 2))
+        uniq.append(u.mean())
+    return route, float(np.mean(unions)), float(np.mean(avs)), float(np.mean(uniq))
+
+
+def cpu_baseline(op, q, k, v, H, budget_s):
+    """C oracle (single thread) on layer 0: route + union + AV for 8 groups."""
+    import oracle
+    oracle.build()
+    counts = op.n[:, :F].cpu().numpy().astype(np.int64)
+    from prismkv_amd import untile_moments
+    mean, var = (x.cpu().numpy() for x in untile_moments(op.moments))
+    qf = q.float().cpu().numpy()
+    kf = k.float().cpu().numpy()
+    vf = v.float().cpu().numpy()
+    bits = op.bits.cpu().numpy().view(np.uint32)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or not times:
+        t0 = time.perf_counter()
+        for g in range(G):
+            _, order, _, _ = oracle.bucket_scores(qf[g], counts[g], mean[g], var[g])
+            feats = np.zeros(TOPK, np.int64)
+            feats[:len(order)] = order
+            ids = oracle.union_bits(bits[g], H, feats, (np.arange(TOPK) < len(order)).astype(np.float32))
+            oracle.attend(qf[g], kf[g], vf[g], ids, H)
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)) * 1e6, len(times)
+
+
+def main():
+    a = parse()
+    if a.gpus != 1:
+        print(f"bench.py measures one MI355X only; --gpus {a.gpus} is not supported (this path shards by KV "
+              f"group or layer with no exchange; see the design notes).", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(2)
+    from prismkv_amd import _lib
+    lib_path = _lib.DEFAULT_LIBRARY
+    _lib.load(lib_path)
+    device = torch.device("cuda", 0)
+    torch.cuda.set_device(device)
+    stages = set(a.stages.split(","))
+    H, T = a.history, a.tail
+    log(f"building {a.layers} layers H={H} T={T} ...")
+    t0 = time.perf_counter()
+    layers = [make_layer(lib_path, i, H, T, a.seed, device) for i in range(a.layers)]
+    torch.cuda.synchronize()
+    log(f"built in {time.perf_counter() - t0:.1f}s; mem {torch.cuda.memory_allocated() / 2**30:.1f} GiB")
+
+    def chain():
+        for op, q, k, v in layers:
+            op.route(q)
+            op.attention(q, k, v, splits=a.splits)
+
+    def route_only():
+        for op, q, k, v in layers:
+            op.lib.call("prismkv_route", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(),
+                        op.route_work.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(), op.raw.data_ptr(),
+                        G, stream=torch.cuda.current_stream().cuda_stream)
+
+    def union_only():
+        for op, q, k, v in layers:
+            op.lib.call("prismkv_union", op.bits.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(),
+                        op.union_work.data_ptr(), op.ids.data_ptr(), op.count.data_ptr(), G, op.history,
+                        op.row_words, op.capacity, stream=torch.cuda.current_stream().cuda_stream)
+
+    def attend_only():
+        for op, q, k, v in layers:
+            op.attention(q, k, v, splits=a.splits)
+
+    result = {}
+    chain()  # populate ids/count for the byte model and the stage graphs
+    torch.cuda.synchronize()
+    ms, wall, _ = graph_time(chain, a.steps, a.warmup) if "chain" in stages else (float("nan"),) * 3
+    log(f"chain: {ms:.4f} ms/step events, {wall:.4f} ms/step wall")
+    per_stage = {}
+    for name, fn in (("route", route_only), ("union", union_only), ("attend", attend_only)):
+        if name in stages:
+            sm, _, _ = graph_time(fn, a.steps, a.warmup)
+            per_stage[name] = sm * 1e3 / a.layers
+            log(f"{name}: {per_stage[name]:.2f} us/launch")
+    b_route, b_union, b_av, uniq = stage_bytes([l[0] for l in layers], H, T)
+    nbytes = {"route": b_route, "union": b_union, "attend": b_av}
+    stage_report = {}
+    for name, us in per_stage.items():
+        gbs = nbytes[name] / (us * 1e-6) / 1e9
+        stage_report[name] = dict(us_per_launch=round(us, 3), algorithmic_bytes=int(nbytes[name]),
+                                  achieved_GBps=round(gbs, 1), frac_of_peak=round(gbs / HBM_PEAK_GBS, 4))
+    copy_gbs = None
+    if "copy" in stages:
+        src = torch.empty(2 ** 30, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(10):
+            dst.copy_(src)
+        e1.record()
+        torch.cuda.synchronize()
+        copy_gbs = 2 * 2 ** 30 * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9
+        log(f"copy probe: {copy_gbs:.0f} GB/s (read+write)")
+        del src, dst
+    dominant = max(stage_report, key=lambda n: stage_report[n]["us_per_launch"]) if stage_report else None
+    roofline = None
+    if dominant:
+        d = stage_report[dominant]
+        roofline = dict(bound="hbm", achieved=d["achieved_GBps"], peak=HBM_PEAK_GBS, unit="GB/s",
+                        frac=d["frac_of_peak"], traffic=None, kernel=dominant)
+    cpu = None
+    if not a.no_cpu_baseline:
+        op, q, k, v = layers[0]
+        us, reps = cpu_baseline(op, q, k, v, H, a.cpu_seconds)
+        cpu = dict(value=round(us, 1), unit="us/layer", cores=1, kind="port",
+                   sample=f"layer 0 of the workload (8 groups, H={H}, T={T}): C oracle route + union + AV, "
+                          f"median of {reps} repetitions, 1 thread")
+    value = ms * 1e3 / a.layers
+    result = {
+        "metric": METRIC, "value": round(value, 3), "unit": "us/layer", "n_gpus": 1, "steps": a.steps,
+        "warmup": a.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": round(value / PPU_US_PER_LAYER_64K, 4), "dtype": "fp32", "data": "synthetic",
+        "config": {"workload": f"8B-geometry routed decode, {a.layers} layers x 8 KV groups x 4 Q heads, d=128, "
+                               f"F=3000, Top-16, H={H} + {T} tail, bf16 KV, per-key top-8 SAE membership",
+                   "layers": a.layers, "groups": G, "history": H, "tail": T, "splits": a.splits,
+                   "kv_dtype": "bf16", "mean_unique_ids_per_group": round(uniq, 1), "parallelism": "single GPU"},
+        "wall_ms_per_step": round(wall, 4), "stages": stage_report, "copy_probe_GBps": copy_gbs and round(copy_gbs, 1),
+        "roofline": roofline, "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

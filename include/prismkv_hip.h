@@ -1,0 +1,98 @@
+/*
+ * prismkv_hip.h -- C ABI of libprismkv_hip.so, the MI355X (gfx950) kernels of
+ * PrismKV's routed decode path.
+ *
+ * Conventions (kept from the reference binding, src/prismkv/native8b.py:46-51):
+ *   - every device pointer is passed as uint64_t (torch `tensor.data_ptr()`),
+ *     then int / int64 sizes, then a trailing uint64_t hipStream_t;
+ *   - return 0 on success, -1 for an invalid size/range, -2 for an invalid
+ *     mode (kernels/ppu_8b/union.cu:40,47, av_tuned.cu:63,65), otherwise the
+ *     hipError_t of the launch;
+ *   - arguments are validated on the host before anything is enqueued; the
+ *     library allocates nothing, never synchronises and only enqueues work on
+ *     the given stream.  `work` buffers are caller-owned scratch, sized by the
+ *     matching *_work_bytes() call, zero-filled once before first use; the
+ *     kernels leave their counters at zero again, so launches can be replayed
+ *     from a captured graph.  Calls sharing a work buffer must not overlap.
+ *
+ * Geometry is the native 8B specialisation: F = 3000 buckets, d = 128,
+ * 4 query heads per KV group, Top-16 buckets (src/prismkv/native8b.py:1-6).
+ *
+ * Device layouts (per layer; G = groups):
+ *   q        bf16 [G][4][128]
+ *   moments  f32  [G][47][256][64]  bucket tiles: k < 128 mean, k >= 128 var;
+ *                                   bucket b -> tile b/64, lane b%64 (3008 padded)
+ *   counts   i32  [G][3008]         bucket sizes, padding buckets 0
+ *   bits     u32  [G][3000][row_words]  token t of bucket f: word t>>5, bit t&31
+ *   features i64  [G][16], valid f32 [G][16], raw i32 [G]
+ *   ids      i32  [G][ids_stride] (first count[g] valid, ascending), count i32 [G]
+ *   K, V     bf16 rows of 128, group stride ks / vs elements; rows [H, H+T) are the tail
+ *   out      bf16 [G][4][128]
+ */
+#ifndef PRISMKV_HIP_H
+#define PRISMKV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- reference-compatible entry points (same names and signatures) ---- */
+
+/* kernels/ppu_8b/pack.cu:4 -- bf16 q[32][128] -> f32 a[32][256] = [q, q*q]. */
+int pack(uint64_t q, uint64_t a, uint64_t stream);
+
+/* kernels/ppu_8b/pack.cu:6 -- CSR lists (ids i32 [8][C], offsets i32 [8][3001])
+ * -> bits u32 [8][3000][ceil(H/32)] (bits must be zeroed by the caller). */
+int build_bits(uint64_t ids, uint64_t offsets, uint64_t bits, int H, int C, uint64_t stream);
+
+/* kernels/ppu_8b/route_parallel.cu:33 -- prod f32 [8][4][3000], ln f32 [8][3000],
+ * ct i32 [8][3000] -> ids i64 [8][16], vals f32 [8][16], raw i32 [8]. */
+int fused_norm_top(uint64_t prod, uint64_t ln, uint64_t ct, uint64_t ids, uint64_t vals, uint64_t raw,
+                   uint64_t stream);
+
+/* kernels/ppu_8b/union.cu:39 -- bits u32 [U][3000][NW], mask u32 [U][NW] and
+ * tiles i32 [U][ceil(NW/128)] scratch -> selected i32 [U][H], counts i32 [U].
+ * U in [1,8], H in [1,131072], mode in {0,1,2} (all give identical output). */
+int launch_union_warp(uint64_t bits, uint64_t ids, uint64_t vals, uint64_t mask, uint64_t tiles,
+                      uint64_t selected, uint64_t counts, int U, int H, int mode, uint64_t stream);
+
+/* kernels/ppu_8b/av_tuned.cu:62 -- 8 groups; state f32 [32][S][130] scratch;
+ * S in [1,128]; KS, VS >= (H+T)*128; mode in {0,1,2} (identical output). */
+int attention_tuned(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t cnt, uint64_t state,
+                    uint64_t out, int H, int T, int KS, int VS, int S, int mode, uint64_t stream);
+
+/* ---- MI355X-native entry points ---- */
+
+/* Stage 1 (replaces pack + torch.bmm + fused_norm_top, src/prismkv/native8b.py:85-87;
+ * semantics src/prismkv/core.py:106-130): one launch for G groups. */
+size_t prismkv_route_work_bytes(int groups);
+int prismkv_route(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
+                  uint64_t valid, uint64_t raw, int groups, uint64_t stream);
+
+/* Stage 2 (replaces launch_union_warp, src/prismkv/native8b.py:88-89;
+ * semantics kernels/ppu_8b/union.cu:14-27): one launch, any H up to 2^29. */
+size_t prismkv_union_work_bytes(int groups, int H);
+int prismkv_union(uint64_t bits, uint64_t features, uint64_t valid, uint64_t work, uint64_t ids,
+                  uint64_t count, int groups, int H, int64_t row_words, int64_t ids_stride, uint64_t stream);
+
+/* Bitmap build from CSR (replaces build_bits, src/prismkv/native8b.py:66-70):
+ * ids i32 [G][cap], offsets i32 [G][3001]; bits must be zeroed by the caller. */
+int prismkv_build_bits(uint64_t ids, uint64_t offsets, uint64_t bits, int groups, int64_t cap,
+                       int64_t row_words, uint64_t stream);
+
+/* Stage 3 (replaces attention_tuned, src/prismkv/native8b.py:91-102;
+ * semantics src/prismkv/core.py:170-183): split-K with the merge fused into
+ * the last workgroup of each group; splits in [1,1024]. */
+size_t prismkv_attend_work_bytes(int groups, int splits);
+int prismkv_attend(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t count, uint64_t work,
+                   uint64_t out, int groups, int H, int T, int64_t ks, int64_t vs, int64_t ids_stride,
+                   int splits, uint64_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PRISMKV_HIP_H */

@@ -1,0 +1,100 @@
+"""Compile the HIP sources of this package into libprismkv_hip.so (gfx950).
+
+`compile_hip` mirrors the reference's `compile_ppu` contract
+(src/prismkv/native8b.py:16-31): the output directory must not exist yet; the
+call writes build.log and build.json (command, seconds, return code, source
+sha256) there and returns the library path.  `build_inplace` produces the
+in-tree library the package loads by default.
+"""
+from __future__ import annotations
+
+import hashlib
+import json
+import os
+import shutil
+import subprocess
+import tempfile
+import time
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PACKAGE = Path(__file__).resolve().parent
+CSRC = PACKAGE / "csrc"
+INCLUDE = PACKAGE.parent / "include"
+SOURCES = ["route.hip", "union.hip", "attend.hip", "update.hip"]
+LIBRARY_NAME = "libprismkv_hip.so"
+ARCH = "gfx950"
+
+# Packed-fp32 VALU forms are disabled for every HIP translation unit.
+HIP_FLAGS = ["-O3", "-std=c++17", f"--offload-arch={ARCH}", "-fPIC", "-Xclang", "-target-feature", "-Xclang",
+             "-packed-fp32-ops", "-Wno-unused-command-line-argument"]
+
+
+def _hipcc(rocm_root) -> str:
+    cand = Path(rocm_root) / "bin" / "hipcc"
+    return str(cand) if cand.exists() else (shutil.which("hipcc") or "hipcc")
+
+
+def _sources(source_root: Path):
+    return [source_root / s for s in SOURCES if (source_root / s).exists()]
+
+
+def _compile(hipcc, sources, output: Path, include_dirs, log):
+    """Compile each source to an object in parallel, then link the shared library."""
+    with tempfile.TemporaryDirectory(prefix="prismkv_build_") as tmp:
+        objects, commands = [], []
+        for src in sources:
+            obj = Path(tmp) / (src.stem + ".o")
+            cmd = [hipcc, *HIP_FLAGS, *[f"-I{d}" for d in include_dirs], "-c", str(src), "-o", str(obj)]
+            objects.append(obj)
+            commands.append(cmd)
+        with ThreadPoolExecutor(max_workers=min(len(commands), os.cpu_count() or 4)) as pool:
+            results = list(pool.map(lambda c: subprocess.run(c, capture_output=True, text=True), commands))
+        for cmd, res in zip(commands, results):
+            log.append(" ".join(cmd) + "\n" + res.stdout + res.stderr)
+        rc = next((r.returncode for r in results if r.returncode), 0)
+        if rc == 0:
+            tmp_out = output.with_name(output.name + ".tmp")
+            link = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objects), "-o", str(tmp_out)]
+            commands.append(link)
+            res = subprocess.run(link, capture_output=True, text=True)
+            log.append(" ".join(link) + "\n" + res.stdout + res.stderr)
+            rc = res.returncode
+            if rc == 0:
+                os.replace(tmp_out, output)
+        return rc, commands
+
+
+def compile_hip(source_root=CSRC, output_dir=None, rocm_root="/opt/rocm"):
+    """Build libprismkv_hip.so into a NEW directory; returns the library path."""
+    source_root = Path(source_root)
+    if output_dir is None:
+        raise ValueError("output_dir is required")
+    output_dir = Path(output_dir)
+    output_dir.mkdir(parents=True, exist_ok=False)
+    sources = _sources(source_root)
+    log: list[str] = []
+    start = time.perf_counter()
+    rc, commands = _compile(_hipcc(rocm_root), sources, output_dir / LIBRARY_NAME,
+                            [source_root, INCLUDE], log)
+    (output_dir / "build.log").write_text("\n".join(log), encoding="utf8")
+    (output_dir / "build.json").write_text(json.dumps(dict(
+        command=commands, seconds=time.perf_counter() - start, returncode=rc,
+        sources={p.name: hashlib.sha256(p.read_bytes()).hexdigest() for p in sources}), indent=2), encoding="utf8")
+    if rc:
+        raise subprocess.CalledProcessError(rc, commands[-1])
+    return output_dir / LIBRARY_NAME
+
+
+def build_inplace(rocm_root="/opt/rocm") -> Path:
+    """(Re)build the in-tree library next to this file; always compiles."""
+    out = PACKAGE / LIBRARY_NAME
+    log: list[str] = []
+    rc, commands = _compile(_hipcc(rocm_root), _sources(CSRC), out, [CSRC, INCLUDE], log)
+    if rc:
+        raise RuntimeError("HIP build failed:\n" + "\n".join(log))
+    return out
+
+
+if __name__ == "__main__":
+    print(build_inplace())

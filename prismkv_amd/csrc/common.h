@@ -1,0 +1,100 @@
+// Shared constants and device helpers for the PrismKV routed-decode kernels
+// (gfx950 / CDNA4, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace prismkv {
+
+// Qwen3-8B native geometry (src/prismkv/native8b.py:1-6).
+constexpr int kF = 3000;         // SAE feature buckets per KV group
+constexpr int kD = 128;          // head dimension
+constexpr int kHq = 4;           // query heads per KV group
+constexpr int kTop = 16;         // selected buckets per group
+constexpr int kChunk = 64;       // buckets per moment tile (one wave64 lane each)
+constexpr int kChunks = (kF + kChunk - 1) / kChunk;  // 47
+constexpr int kFP = kChunks * kChunk;                // 3008, padded bucket count
+constexpr int kRow = 2 * kD;     // per-bucket moment row: mean[128] then var[128]
+
+// Error convention of the C ABI (kernels/ppu_8b/union.cu:40,47, av_tuned.cu:63,65).
+constexpr int kBadSize = -1;
+constexpr int kBadMode = -2;
+
+__device__ __forceinline__ float bf16_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// fp32 -> bf16, round to nearest even, NaN kept quiet.
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// 16-byte streaming load (non-temporal hint: data read once per decode step).
+__device__ __forceinline__ uint4 load_nt16(const void* p) {
+  const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ __forceinline__ int wave_sum_i(int v) {
+#pragma unroll
+  for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+// Inclusive prefix sum over the lanes of a wave64.
+__device__ __forceinline__ unsigned wave_incl_scan(unsigned v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    unsigned y = __shfl_up(v, o);
+    if (lane >= o) v += y;
+  }
+  return v;
+}
+
+// Inclusive prefix sum over a workgroup of NT threads (NT a multiple of 64).
+// `wsum` is NT/64 words of LDS.  Contains two barriers.
+template <int NT>
+__device__ __forceinline__ unsigned block_incl_scan(unsigned v, unsigned* wsum) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  v = wave_incl_scan(v);
+  if (lane == 63) wsum[w] = v;
+  __syncthreads();
+  unsigned add = 0;
+#pragma unroll
+  for (int j = 0; j < NT / 64; ++j) add += (j < w) ? wsum[j] : 0u;
+  __syncthreads();
+  return v + add;
+}
+
+// Device-scope atomics / fences used by the last-workgroup and look-back
+// patterns.  Agent scope makes them coherent across the 8 XCD L2 caches.
+__device__ __forceinline__ unsigned atomic_add_agent(unsigned* p, unsigned v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned atomic_load_agent(const unsigned* p) {
+  return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void atomic_store_agent(unsigned* p, unsigned v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace prismkv

@@ -1,0 +1,197 @@
+"""MI355X binding of PrismKV's native 8B decode path -- drop-in for
+`prismkv.native8b` (src/prismkv/native8b.py).
+
+Same class and method names, keyword arguments, attribute names, dtypes and
+shapes as the reference binding:
+
+* ``Native8B(indices, library)`` builds the device tables once per prefill /
+  index rebuild (src/prismkv/native8b.py:35-74);
+* ``.route(q)`` runs stage 1 (bucket routing) and stage 2 (bitmap union and
+  compaction) and leaves ``features``, ``valid``, ``raw``, ``ids``, ``count``
+  on the device (src/prismkv/native8b.py:82-89);
+* ``.attention(q, k, v, *, splits=64, schedule=0)`` runs stage 3 and returns
+  the preallocated ``out`` buffer, overwritten by the next call
+  (src/prismkv/native8b.py:91-102);
+* ``__call__`` = route + attention; ``buffer_bytes()`` lists live buffers.
+
+All validation happens on the host before anything is enqueued (ValueError
+for shapes/dtypes/devices/strides, RuntimeError for a nonzero launch code).
+route/attention allocate nothing and never synchronise, so they can be
+captured into a HIP graph.  Instance buffers are shared state: use one
+instance per stream.  There is no CPU fallback: without the HIP library the
+constructor raises.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from .build import compile_hip  # noqa: F401  (re-exported: reference name compile_ppu)
+
+GROUPS, HEADS, DIM, FEATURES, TOPK = 8, 4, 128, 3000, 16
+CHUNK = 64
+CHUNKS = (FEATURES + CHUNK - 1) // CHUNK
+PADDED = CHUNKS * CHUNK
+
+
+@dataclass
+class FeatureIndex:
+    """Index state of one (layer, KV group), field-for-field the reference
+    container (src/prismkv/core.py:62-73): original-token lists per bucket and
+    count / mean / population diagonal variance of the original keys."""
+
+    history: int
+    center: torch.Tensor
+    counts: torch.Tensor
+    mean: torch.Tensor
+    variance: torch.Tensor
+    lists: list
+
+    @property
+    def memberships(self):
+        return sum(len(x) for x in self.lists)
+
+
+def tile_moments(mean: torch.Tensor, variance: torch.Tensor) -> torch.Tensor:
+    """[G,3000,128] mean and variance -> f32 [G,47,256,64] bucket tiles (k < 128 mean)."""
+    g = mean.shape[0]
+    rows = torch.cat((mean.float(), variance.float()), dim=-1)  # [G, F, 256]
+    rows = torch.nn.functional.pad(rows, (0, 0, 0, PADDED - FEATURES))
+    return rows.view(g, CHUNKS, CHUNK, 2 * DIM).permute(0, 1, 3, 2).contiguous()
+
+
+def untile_moments(tiles: torch.Tensor):
+    """Inverse of tile_moments -> (mean [G,3000,128], variance [G,3000,128])."""
+    g = tiles.shape[0]
+    rows = tiles.permute(0, 1, 3, 2).reshape(g, PADDED, 2 * DIM)[:, :FEATURES]
+    return rows[..., :DIM], rows[..., DIM:]
+
+
+def bitmap_row_words(capacity: int) -> int:
+    """uint32 words per bucket row, rounded to 16 bytes for vector loads."""
+    return ((capacity + 31) // 32 + 3) // 4 * 4
+
+
+class Native8B:
+    def __init__(self, indices, library=None, *, capacity=None):
+        if len(indices) != GROUPS:
+            raise ValueError("native specialization requires 8 KV groups")
+        h = int(indices[0].history)
+        device = indices[0].mean.device
+        if device.type != "cuda":
+            raise ValueError("native backend requires a device tensor")
+        if any(x.history != h or tuple(x.mean.shape) != (FEATURES, DIM) for x in indices):
+            raise ValueError("same history, F=3000, d=128 required")
+        with torch.cuda.device(device):
+            counts = torch.stack([torch.as_tensor(x.counts).to(device) for x in indices])
+            width = max(max(x.memberships for x in indices), 1)
+            # concatenate each group's lists where they live (host or device), then move once
+            lists = [torch.cat([torch.as_tensor(l).reshape(-1) for l in x.lists]).to(device=device, dtype=torch.int32)
+                     if x.memberships else torch.zeros(0, dtype=torch.int32, device=device) for x in indices]
+            csr = torch.stack([torch.nn.functional.pad(x, (0, width - len(x))) for x in lists])
+            offsets = torch.cat((torch.zeros(GROUPS, 1, dtype=torch.int64, device=device),
+                                 counts.long().cumsum(1)), dim=1).int()
+            self._setup(h, capacity, library, counts,
+                        torch.stack([torch.as_tensor(x.mean).to(device) for x in indices]),
+                        torch.stack([torch.as_tensor(x.variance).to(device) for x in indices]), csr, offsets)
+
+    @classmethod
+    def from_tables(cls, history, counts, mean, variance, csr_ids, offsets, library=None, *, capacity=None):
+        """Build from device tables directly: counts [8,3000], mean/variance
+        [8,3000,128] f32, csr_ids i32 [8,C] (bucket f owns columns
+        offsets[g,f] .. offsets[g,f+1]) and offsets i32 [8,3001]."""
+        if counts.device.type != "cuda":
+            raise ValueError("native backend requires a device tensor")
+        if tuple(mean.shape) != (GROUPS, FEATURES, DIM) or mean.shape != variance.shape:
+            raise ValueError("same history, F=3000, d=128 required")
+        obj = cls.__new__(cls)
+        with torch.cuda.device(counts.device):
+            obj._setup(int(history), capacity, library, counts, mean, variance, csr_ids.int().contiguous(),
+                       offsets.int().contiguous())
+        return obj
+
+    def _setup(self, h, capacity, library, counts, mean, variance, csr, offsets):
+        capacity = h if capacity is None else int(capacity)
+        if capacity < h or h < 1:
+            raise ValueError("history must be >= 1 and capacity >= history")
+        self.history = h
+        self.capacity = capacity
+        self.lib = _lib.load(library)
+        if self.lib.missing:
+            raise RuntimeError(f"{self.lib.path.name} lacks entry points {self.lib.missing}; rebuild it")
+        device = counts.device
+        if csr.numel() and (int(csr.max()) >= h or int(csr.min()) < 0):
+            raise ValueError("bucket lists must address tokens in [0, history)")
+        if offsets.shape != (GROUPS, FEATURES + 1) or int(offsets[:, -1].max()) > csr.shape[1]:
+            raise ValueError("offsets must be [8,3001] within the list width")
+        stream = torch.cuda.current_stream().cuda_stream
+        self.n = torch.zeros(GROUPS, PADDED, dtype=torch.int32, device=device)
+        self.n[:, :FEATURES] = counts.int()
+        self.moments = tile_moments(mean, variance)
+        self.features = torch.zeros(GROUPS, TOPK, dtype=torch.int64, device=device)
+        self.valid = torch.zeros(GROUPS, TOPK, device=device)
+        self.raw = torch.zeros(GROUPS, dtype=torch.int32, device=device)
+        self.ids = torch.zeros(GROUPS, self.capacity, dtype=torch.int32, device=device)
+        self.count = torch.zeros(GROUPS, dtype=torch.int32, device=device)
+        self.row_words = bitmap_row_words(self.capacity)
+        self.bits = torch.zeros(GROUPS, FEATURES, self.row_words, dtype=torch.int32, device=device)
+        self.lib.call("prismkv_build_bits", csr.data_ptr(), offsets.data_ptr(), self.bits.data_ptr(), GROUPS,
+                      csr.shape[1], self.row_words, stream=stream)
+        # Temporary CSR storage may be freed after this build barrier.
+        torch.cuda.synchronize(device)
+        self.route_work = torch.zeros(self.lib.query("prismkv_route_work_bytes", GROUPS), dtype=torch.uint8,
+                                      device=device)
+        self.union_work = torch.zeros(self.lib.query("prismkv_union_work_bytes", GROUPS, self.capacity),
+                                      dtype=torch.uint8, device=device)
+        self.state = torch.zeros(self.lib.query("prismkv_attend_work_bytes", GROUPS, 128), dtype=torch.uint8,
+                                 device=device)
+        self.out = torch.zeros(GROUPS, HEADS, DIM, dtype=torch.bfloat16, device=device)
+
+    def _stream(self):
+        return torch.cuda.current_stream().cuda_stream
+
+    def route(self, q):
+        if tuple(q.shape) != (GROUPS, HEADS, DIM) or q.dtype != torch.bfloat16 or not q.is_contiguous():
+            raise ValueError("contiguous BF16 Q[8,4,128] required")
+        if q.device != self.out.device:
+            raise ValueError("Q must live on the index device")
+        s = self._stream()
+        self.lib.call("prismkv_route", q.data_ptr(), self.moments.data_ptr(), self.n.data_ptr(),
+                      self.route_work.data_ptr(), self.features.data_ptr(), self.valid.data_ptr(),
+                      self.raw.data_ptr(), GROUPS, stream=s)
+        self.lib.call("prismkv_union", self.bits.data_ptr(), self.features.data_ptr(), self.valid.data_ptr(),
+                      self.union_work.data_ptr(), self.ids.data_ptr(), self.count.data_ptr(), GROUPS, self.history,
+                      self.row_words, self.capacity, stream=s)
+
+    def attention(self, q, k, v, *, splits=64, schedule=0):
+        """Stage 3.  `schedule` (0, 1, 2) is accepted for compatibility; every
+        schedule uses contiguous per-split row ranges and gives the same result."""
+        if not 1 <= splits <= 128 or schedule not in (0, 1, 2):
+            raise ValueError("unsupported attention partition/schedule")
+        if k.shape != v.shape or k.shape[0] != GROUPS or k.shape[-1] != DIM or k.shape[1] < self.history:
+            raise ValueError("K/V[8,total_length,128] required")
+        if k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16 or k.stride(-1) != 1 or v.stride(-1) != 1:
+            raise ValueError("BF16 KV with contiguous head dimension required")
+        if k.stride(1) != DIM or v.stride(1) != DIM:
+            raise ValueError("contiguous per-group KV rows required")
+        if tuple(q.shape) != (GROUPS, HEADS, DIM) or q.dtype != torch.bfloat16 or not q.is_contiguous():
+            raise ValueError("contiguous BF16 Q[8,4,128] required")
+        if not (q.device == k.device == v.device == self.out.device):
+            raise ValueError("Q/K/V must live on the index device")
+        if (q.data_ptr() | k.data_ptr() | v.data_ptr() | (k.stride(0) * 2) | (v.stride(0) * 2)) % 16:
+            raise ValueError("Q/K/V rows must be 16-byte aligned")
+        self.lib.call("prismkv_attend", q.data_ptr(), k.data_ptr(), v.data_ptr(), self.ids.data_ptr(),
+                      self.count.data_ptr(), self.state.data_ptr(), self.out.data_ptr(), GROUPS, self.history,
+                      k.shape[1] - self.history, k.stride(0), v.stride(0), self.capacity, splits,
+                      stream=self._stream())
+        return self.out
+
+    def __call__(self, q, k, v, **kwargs):
+        self.route(q)
+        return self.attention(q, k, v, **kwargs)
+
+    def buffer_bytes(self):
+        """Live tensors owned here; excludes model/KV, caller indices and build temporaries."""
+        return {name: x.numel() * x.element_size() for name, x in vars(self).items() if isinstance(x, torch.Tensor)}

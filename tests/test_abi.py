@@ -1,0 +1,94 @@
+"""CPU checks of the C ABI: the library loads, exports every entry point the
+header declares, and rejects invalid arguments on the host with the reference
+error codes (-1 size/range, -2 mode) before enqueuing anything."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "prismkv_hip.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from prismkv_amd import _lib
+    if not _lib.DEFAULT_LIBRARY.exists():
+        from prismkv_amd.build import build_inplace
+        build_inplace()
+    return _lib.load()
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    return re.findall(r"^\s*(?:int|size_t)\s+(\w+)\s*\(", text, flags=re.M)
+
+
+def test_header_declares_reference_symbols():
+    names = declared_symbols()
+    # src/prismkv/native8b.py:46-48: the five symbols a reference-shaped binding binds
+    for ref in ["pack", "build_bits", "fused_norm_top", "launch_union_warp", "attention_tuned"]:
+        assert ref in names
+    assert len(names) == len(set(names))
+
+
+def test_library_exports_every_declared_symbol(lib):
+    names = declared_symbols()
+    missing = [n for n in names if not lib.has(n)]
+    assert not missing, missing
+    from prismkv_amd import _lib
+    assert set(names) <= set(_lib.SIGNATURES), set(names) - set(_lib.SIGNATURES)
+
+
+def test_library_is_gfx950():
+    from prismkv_amd import _lib
+    data = _lib.DEFAULT_LIBRARY.read_bytes() if _lib.DEFAULT_LIBRARY.exists() else b""
+    assert b"gfx950" in data
+
+
+def test_work_size_queries(lib):
+    assert lib.query("prismkv_route_work_bytes", 8) >= 8 * 4 * 3008 * 4
+    assert lib.query("prismkv_route_work_bytes", 0) == 0
+    assert lib.query("prismkv_union_work_bytes", 8, 65536) > 8
+    assert lib.query("prismkv_attend_work_bytes", 8, 64) >= 8 * 4 * 64 * 130 * 4
+
+
+def call_raw(lib, name, *args):
+    return getattr(lib.cdll, name)(*args, 0)
+
+
+def test_compat_error_codes(lib):
+    # kernels/ppu_8b/union.cu:40,47: U in [1,8], H in [1,131072], mode in {0,1,2}
+    for U, H, mode, code in [(0, 100, 2, -1), (9, 100, 2, -1), (8, 0, 2, -1), (8, 131073, 2, -1),
+                             (8, 100, 3, -2), (8, 100, -1, -2)]:
+        assert call_raw(lib, "launch_union_warp", *[0] * 7, U, H, mode) == code
+    # kernels/ppu_8b/av_tuned.cu:63,65
+    H, T = 100, 5
+    good = (H + T) * 128
+    for S, h, t, ks, vs, mode, code in [(0, H, T, good, good, 0, -1), (129, H, T, good, good, 0, -1),
+                                         (64, 0, T, good, good, 0, -1), (64, H, -1, good, good, 0, -1),
+                                         (64, H, T, good - 1, good, 0, -1), (64, H, T, good, good - 1, 0, -1),
+                                         (64, H, T, good, good, 3, -2)]:
+        assert call_raw(lib, "attention_tuned", *[0] * 7, h, t, ks, vs, S, mode) == code
+
+
+def test_native_error_codes(lib):
+    assert call_raw(lib, "prismkv_route", *[0] * 7, 8) == -1          # null pointers
+    assert call_raw(lib, "prismkv_route", *[1] * 7, 0) == -1          # no groups
+    assert call_raw(lib, "prismkv_union", *[1] * 6, 8, 0, 1, 1) == -1  # H < 1
+    assert call_raw(lib, "prismkv_union", *[1] * 6, 8, 100, 3, 100) == -1  # row_words too small
+    assert call_raw(lib, "prismkv_union", *[1] * 6, 8, 100, 4, 99) == -1   # ids stride too small
+    assert call_raw(lib, "prismkv_attend", *[1] * 7, 8, 10, 2, 12 * 128, 12 * 128, 10, 0) == -1  # splits
+    assert call_raw(lib, "prismkv_attend", *[1] * 7, 8, 10, 2, 11 * 128, 12 * 128, 10, 4) == -1  # ks
+
+
+def test_native8b_host_validation_without_gpu():
+    import torch
+    from prismkv_amd import FeatureIndex, Native8B
+    idx = FeatureIndex(4, torch.zeros(128), torch.zeros(3000, dtype=torch.long), torch.zeros(3000, 128),
+                       torch.zeros(3000, 128), [torch.zeros(0, dtype=torch.long)] * 3000)
+    with pytest.raises(ValueError, match="8 KV groups"):
+        Native8B([idx] * 7)
+    with pytest.raises(ValueError, match="device tensor"):
+        Native8B([idx] * 8)
