@@ -20,8 +20,8 @@
  *
  * Device layouts (per layer; G = groups):
  *   q        bf16 [G][4][128]
- *   moments  f32  [G][47][256][64]  bucket tiles: k < 128 mean, k >= 128 var;
- *                                   bucket b -> tile b/64, lane b%64 (3008 padded)
+ *   moments  f32  [G][94][256][32]  bucket tiles: k < 128 mean, k >= 128 var;
+ *                                   bucket b -> tile b/32, column b%32 (3008 padded)
  *   counts   i32  [G][3008]         bucket sizes, padding buckets 0
  *   bits     u32  [G][3000][row_words]  token t of bucket f: word t>>5, bit t&31
  *   features i64  [G][16], valid f32 [G][16], raw i32 [G]

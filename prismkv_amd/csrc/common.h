@@ -12,8 +12,8 @@ constexpr int kF = 3000;         // SAE feature buckets per KV group
 constexpr int kD = 128;          // head dimension
 constexpr int kHq = 4;           // query heads per KV group
 constexpr int kTop = 16;         // selected buckets per group
-constexpr int kChunk = 64;       // buckets per moment tile (one wave64 lane each)
-constexpr int kChunks = (kF + kChunk - 1) / kChunk;  // 47
+constexpr int kChunk = 32;       // buckets per moment tile (128-byte tile rows)
+constexpr int kChunks = (kF + kChunk - 1) / kChunk;  // 94
 constexpr int kFP = kChunks * kChunk;                // 3008, padded bucket count
 constexpr int kRow = 2 * kD;     // per-bucket moment row: mean[128] then var[128]
 
@@ -85,16 +85,39 @@ __device__ __forceinline__ unsigned block_incl_scan(unsigned v, unsigned* wsum) 
   return v + add;
 }
 
-// Device-scope atomics / fences used by the last-workgroup and look-back
-// patterns.  Agent scope makes them coherent across the 8 XCD L2 caches.
-__device__ __forceinline__ unsigned atomic_add_agent(unsigned* p, unsigned v) {
-  return __hip_atomic_fetch_add(p, v, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+// Bounded spin used by every inter-workgroup wait: about 2^20 sleeps of 64
+// clocks (tens of milliseconds) before the waiter gives up and reports.
+constexpr int kSpinLimit = 1 << 20;
+
+// Cross-workgroup communication.  Data one workgroup hands to another is
+// written through to the device coherence point and read back from it with
+// relaxed agent-scope atomics (global_store/load ... sc1); a writer drains its
+// stores (s_waitcnt 0) before the workgroup barrier that precedes the
+// arrival-counter increment, and a reader only loads after it has observed
+// the counter.  No agent-scope fences: on gfx950 each one writes back or
+// invalidates the whole L2 of the XCD, which costs tens of microseconds when
+// hundreds of workgroups do it.
+template <typename T>
+__device__ __forceinline__ void st_dev(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ unsigned atomic_load_agent(const unsigned* p) {
-  return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+template <typename T>
+__device__ __forceinline__ T ld_dev(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ void atomic_store_agent(unsigned* p, unsigned v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+__device__ __forceinline__ unsigned inc_dev(unsigned* p) {
+  return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Waits until every memory operation this thread issued has completed.
+__device__ __forceinline__ void drain() { __builtin_amdgcn_s_waitcnt(0); }
+
+__device__ __forceinline__ void st_dev2(float* p, float a, float b) {
+  st_dev(reinterpret_cast<unsigned long long*>(p),
+         ((unsigned long long)__float_as_uint(b) << 32) | (unsigned long long)__float_as_uint(a));
+}
+__device__ __forceinline__ float2 ld_dev2(const float* p) {
+  const unsigned long long v = ld_dev(reinterpret_cast<const unsigned long long*>(p));
+  return make_float2(__uint_as_float((unsigned)v), __uint_as_float((unsigned)(v >> 32)));
 }
 
 }  // namespace prismkv

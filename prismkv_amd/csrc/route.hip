@@ -6,84 +6,112 @@
 //            kernels/ppu_8b/route_parallel.cu:12-32 (tie rule, padding, raw).
 //
 // Design (one launch per layer, no vendor GEMM):
-//   * Moment tables live in HBM as 64-bucket tiles [g][chunk][k][64] (k < 128:
-//     mean, k >= 128: variance), so one wave64 reads 256 contiguous bytes per
-//     k-row and each lane owns one bucket -- the 4-head dot products need no
-//     cross-lane reduction.  A workgroup of 4 waves splits k into quarters and
-//     combines the partial sums in LDS in a fixed order (ties stay exact).
-//   * Each workgroup writes its 64x4 logits plus per-head (max, sum-exp) chunk
-//     statistics; the last workgroup of the group (device-scope counter)
-//     merges the 47 chunk statistics, forms the head-averaged probabilities
-//     and selects the Top-16 with an LDS radix select on 64-bit keys
-//     (probability bits << 32 | ~bucket), i.e. value descending, bucket id
-//     ascending on ties -- the reference order.  The counter is restored to
-//     zero by that workgroup, so the launch can be replayed from a graph.
+//   * Moment tables live in HBM as 32-bucket tiles [g][chunk][k][32] (k < 128:
+//     mean, k >= 128: variance; 128-byte tile rows).  Workgroup (chunk, g)
+//     streams its 32 KB tile with eight independent 16-byte loads per thread
+//     (thread = 4 buckets x 8 k-rows), so a launch keeps ~750 workgroups and
+//     all of their loads in flight.  The per-thread products for 2 parts x 4
+//     heads x 4 buckets are reduced across the 8 k-row lanes of a wave with a
+//     transpose-reduce (28 shuffles) and across the 4 waves in LDS, in a fixed
+//     order, so results are run-to-run identical.
+//   * Logit = (log(count) + mean_term / sqrt(d)) + var_term / (2d): the
+//     accumulation order of core.py:122-127.  Each workgroup stores its 4x32
+//     logits and per-head (max, sum-exp) chunk statistics.
+//   * The last workgroup of the group (device-scope counter) merges the 94
+//     chunk statistics, forms the head-averaged probabilities and selects the
+//     Top-16 with an LDS radix select on 44-bit keys (probability bits << 12 |
+//     4095 - bucket): value descending, bucket id ascending on ties, the
+//     reference order.  It restores the counter to zero, so the launch is
+//     replayable from a graph without memset nodes.  Logits and statistics
+//     cross workgroups through write-through stores, not fences.
 #include "common.h"
 
 namespace prismkv {
 namespace {
 
-constexpr int kRT = 256;                    // route workgroup size
+constexpr int kRT = 256;                      // route workgroup size
 constexpr int kKeys = (kFP + kRT - 1) / kRT;  // 12 candidate keys per thread
+constexpr int kDigit = 11;                    // radix digit width of the Top-16 select
+constexpr int kBins = 1 << kDigit;
+constexpr int kKeyBits = 44;                  // 32 probability bits + 12 id bits
+constexpr float kSqrtD = 11.3137084989847604f;  // fp32(sqrt(128)), core.py:125
 
 struct SelectLds {
-  unsigned hist[256];
-  unsigned wsum[4];
+  unsigned hist[kBins];
+  unsigned wsum[kRT / 64];
   unsigned long long sel[kTop];
-  int nsel, digit, rem, stop, live;
+  int nsel, live, digit, rem, stop;
 };
 
-// Writes the min(kTop, live) largest nonzero keys of the workgroup into
-// lds.sel (unordered) and returns that count.  Keys are unique by
-// construction, so the selected set has exactly `need` members.
+__device__ __forceinline__ uint64_t make_key(float prob, int bucket) {
+  return ((uint64_t)__float_as_uint(prob) << 12) | (uint64_t)(4095 - bucket);
+}
+__device__ __forceinline__ int key_bucket(uint64_t k) { return 4095 - (int)(k & 4095u); }
+
+// Selects the min(kTop, live) largest nonzero keys (unique by construction)
+// into lds.sel, unordered; returns that count.  MSB-first radix select with
+// 11-bit digits and an early stop once the boundary digit holds exactly the
+// remaining number of keys.
 __device__ int select_top(const uint64_t (&key)[kKeys], SelectLds& lds) {
   const int tid = threadIdx.x;
   int nl = 0;
 #pragma unroll
   for (int i = 0; i < kKeys; ++i) nl += key[i] != 0;
-  if (tid == 0) { lds.live = 0; lds.nsel = 0; }
+  nl = wave_sum_i(nl);
+  if ((tid & 63) == 0) lds.wsum[tid >> 6] = (unsigned)nl;
+  if (tid == 0) lds.nsel = 0;
   __syncthreads();
-  if (nl) atomicAdd(&lds.live, nl);
-  __syncthreads();
-  const int live = lds.live;
+  int live = 0;
+#pragma unroll
+  for (int w = 0; w < kRT / 64; ++w) live += (int)lds.wsum[w];
   const int need = live < kTop ? live : kTop;
-  uint64_t prefix = 0;
-  int shift = 64;
+  uint64_t thr = 1;  // select every nonzero key >= thr
   if (live > need) {
-    // MSB-first radix select over 8-bit digits of the 64-bit key.
+    uint64_t prefix = 0;
     unsigned rem = (unsigned)need;
-    for (;;) {
-      shift -= 8;
-      lds.hist[tid] = 0;
+    for (int shift = kKeyBits - kDigit; shift >= 0; shift -= kDigit) {
+      __syncthreads();  // wsum / previous round's reads are complete
+#pragma unroll
+      for (int i = 0; i < kBins / kRT; ++i) lds.hist[tid + i * kRT] = 0;
       __syncthreads();
 #pragma unroll
       for (int i = 0; i < kKeys; ++i) {
         const uint64_t k = key[i];
-        if (k != 0 && (shift == 56 || (k >> (shift + 8)) == prefix))
-          atomicAdd(&lds.hist[(unsigned)(k >> shift) & 255u], 1u);
+        if (k != 0 && (k >> (shift + kDigit)) == prefix) atomicAdd(&lds.hist[(unsigned)(k >> shift) & (kBins - 1)], 1u);
       }
       __syncthreads();
-      // thread t looks at digit 255-t: inclusive scan = keys with digit >= 255-t
-      const unsigned c = lds.hist[255 - tid];
-      const unsigned incl = block_incl_scan<kRT>(c, lds.wsum);
-      const unsigned excl = incl - c;
-      if (excl < rem && incl >= rem) {
-        lds.digit = 255 - tid;
-        lds.rem = (int)(rem - excl);
-        lds.stop = (c == rem - excl);
+      // thread t owns digits 2047-8t .. 2040-8t (descending)
+      constexpr int kPer = kBins / kRT;
+      unsigned c[kPer], tot = 0;
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        c[u] = lds.hist[kBins - 1 - (tid * kPer + u)];
+        tot += c[u];
+      }
+      const unsigned incl = block_incl_scan<kRT>(tot, lds.wsum);
+      unsigned run = incl - tot;
+#pragma unroll
+      for (int u = 0; u < kPer; ++u) {
+        if (run < rem && run + c[u] >= rem) {
+          lds.digit = kBins - 1 - (tid * kPer + u);
+          lds.rem = (int)(rem - run);
+          lds.stop = (c[u] == rem - run);
+        }
+        run += c[u];
       }
       __syncthreads();
-      prefix = (prefix << 8) | (uint64_t)lds.digit;
+      prefix = (prefix << kDigit) | (uint64_t)lds.digit;
       rem = (unsigned)lds.rem;
-      const bool stop = lds.stop != 0;
-      __syncthreads();
-      if (stop || shift == 0) break;
+      if (lds.stop || shift == 0) {
+        thr = prefix << shift;
+        break;
+      }
     }
   }
 #pragma unroll
   for (int i = 0; i < kKeys; ++i) {
     const uint64_t k = key[i];
-    if (k != 0 && (live <= need || (k >> shift) >= prefix)) {
+    if (k != 0 && k >= thr) {
       const int s = atomicAdd(&lds.nsel, 1);
       if (s < kTop) lds.sel[s] = k;
     }
@@ -93,7 +121,8 @@ __device__ int select_top(const uint64_t (&key)[kKeys], SelectLds& lds) {
 }
 
 // Writes the selected keys in rank order: features[r] = bucket, valid[r] = 1
-// for r < need; remaining slots id 0 / valid 0; raw = sum of winner counts.
+// for r < need; remaining slots id 0 / valid 0 (route_parallel.cu:23,29);
+// raw = sum of winner counts.
 template <typename CountT>
 __device__ void write_selection(const SelectLds& lds, int need, const CountT* counts, int64_t* features,
                                 float* valid, int* raw) {
@@ -102,118 +131,161 @@ __device__ void write_selection(const SelectLds& lds, int need, const CountT* co
     const unsigned long long k = lds.sel[tid];
     int r = 0;
     for (int j = 0; j < need; ++j) r += lds.sel[j] > k;
-    features[r] = (int64_t)(0xffffffffu - (unsigned)(k & 0xffffffffu));
+    features[r] = (int64_t)key_bucket(k);
     valid[r] = 1.0f;
   } else if (tid < kTop) {
     features[tid] = 0;
     valid[tid] = 0.0f;
   }
-  if (tid == 0) {
-    int total = 0;
-    for (int j = 0; j < need; ++j) total += (int)counts[0xffffffffu - (unsigned)(lds.sel[j] & 0xffffffffu)];
-    *raw = total;
+  if (tid < 64) {
+    int n = tid < need ? (int)counts[key_bucket(lds.sel[tid])] : 0;
+    n = wave_sum_i(n);
+    if (tid == 0) *raw = n;
   }
 }
 
-__device__ __forceinline__ uint64_t make_key(float prob, int bucket) {
-  return ((uint64_t)__float_as_uint(prob) << 32) | (uint64_t)(0xffffffffu - (unsigned)bucket);
+// Transpose-reduce step: `x` holds 2n partial sums; lanes whose `mask` bit is
+// set keep the upper half, the others the lower half, and add the partner's
+// copy of the kept half.  After the step x[0..n) holds the new partial sums.
+template <int N>
+__device__ __forceinline__ void treduce(float* x, int mask) {
+  const bool hi = (threadIdx.x & mask) != 0;
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const float keep = hi ? x[j + N] : x[j];
+    const float send = hi ? x[j] : x[j + N];
+    x[j] = keep + __shfl_xor(send, mask);
+  }
 }
 
 // ---------------------------------------------------------------------------
 // Fused route: grid (kChunks, G) x 256.
 // ---------------------------------------------------------------------------
+struct RouteWork {
+  float* logits;    // [G][4][kFP]
+  float* stats;     // [G][kChunks][4][2] (max, sum of exp)
+  unsigned* sync;   // [G] arrival counters, zero between launches
+};
+
 __global__ __launch_bounds__(kRT) void route_kernel(const uint16_t* __restrict__ q,
                                                     const float* __restrict__ moments,
-                                                    const int* __restrict__ counts,
-                                                    float* __restrict__ logits, float* __restrict__ stats,
-                                                    unsigned* __restrict__ sync, int64_t* __restrict__ features,
-                                                    float* __restrict__ valid, int* __restrict__ raw) {
+                                                    const int* __restrict__ counts, RouteWork work,
+                                                    int64_t* __restrict__ features, float* __restrict__ valid,
+                                                    int* __restrict__ raw) {
   const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
   const int w = tid >> 6, lane = tid & 63;
-  __shared__ float4 qq[kRow];            // [k] -> 4 heads; k < 128: q, k >= 128: q*q
-  __shared__ float part[4][kHq][kChunk];  // [k quarter][head][bucket]
+  __shared__ float4 qq[kRow];                 // [k] -> 4 heads; k < 128: q, k >= 128: q*q
+  __shared__ float4 red[kRT / 64][64];        // cross-wave partials
+  __shared__ float dots[2][kHq][kChunk];      // [part][head][bucket]
   __shared__ int is_last;
-  __shared__ float gmax[kHq], gsum[kHq];
+  __shared__ float gmax[kHq], grz[kHq];
   __shared__ SelectLds lds;
 
+  // 16-byte tile loads first: thread = bucket quad (tid & 7) x k-row phase (tid >> 3)
+  const int quad = tid & 7, r = tid >> 3;
+  const float4* tile = reinterpret_cast<const float4*>(moments + (size_t)(g * kChunks + c) * kRow * kChunk);
+  float4 m4[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tile + (r + 32 * i) * (kChunk / 4) + quad));
+    m4[i] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+  }
   for (int i = tid; i < kHq * kD; i += kRT) {
     const int h = i >> 7, k = i & (kD - 1);
     const float x = bf16_to_f32(q[((size_t)g * kHq + h) * kD + k]);
     reinterpret_cast<float*>(&qq[k])[h] = x;
-    reinterpret_cast<float*>(&qq[kD + k])[h] = x * x;
+    reinterpret_cast<float*>(&qq[kD + k])[h] = x * x;  // core.py:127 q.square() in fp32
   }
   __syncthreads();
 
-  // wave w covers moment rows [64w, 64w+64) of this chunk's tile
-  const float* tile = moments + ((size_t)(g * kChunks + c) * kRow + w * 64) * kChunk + lane;
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-#pragma unroll 16
-  for (int kk = 0; kk < 64; ++kk) {
-    const float t = __builtin_nontemporal_load(tile + kk * kChunk);
-    const float4 qv = qq[w * 64 + kk];
-    a0 = fmaf(qv.x, t, a0);
-    a1 = fmaf(qv.y, t, a1);
-    a2 = fmaf(qv.z, t, a2);
-    a3 = fmaf(qv.w, t, a3);
+  // acc[part*16 + head*4 + j]: part 0 = mean rows, 1 = variance rows
+  float acc[32];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) acc[i] = 0.f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float4 qv = qq[r + 32 * i];
+    const float* hq = reinterpret_cast<const float*>(&qv);
+    const float* mv = reinterpret_cast<const float*>(&m4[i]);
+    const int part = i >> 2;
+#pragma unroll
+    for (int h = 0; h < kHq; ++h)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[part * 16 + h * 4 + j] = fmaf(hq[h], mv[j], acc[part * 16 + h * 4 + j]);
   }
-  part[w][0][lane] = a0;
-  part[w][1][lane] = a1;
-  part[w][2][lane] = a2;
-  part[w][3][lane] = a3;
+  // reduce over the 8 k-row lanes of the wave (lane bits 5,4,3)
+  treduce<16>(acc, 32);
+  treduce<8>(acc, 16);
+  treduce<4>(acc, 8);
+  // lane now holds part (lane>>5)&1, head (lane>>3)&3, buckets 4*quad .. +3
+  red[w][lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
   __syncthreads();
-
   {
-    // wave h finalises head h for the 64 buckets of the chunk
-    const int h = w, b = c * kChunk + lane;
-    const int n = counts[(size_t)g * kFP + b];
-    const float dm = part[0][h][lane] + part[1][h][lane];
-    const float dv = part[2][h][lane] + part[3][h][lane];
-    // core.py:122-127 order: log(count) + mean term + variance term
-    const float l = n > 0 ? (logf((float)n) + dm / 11.3137084989847604f) + dv * (1.0f / 256.0f) : -INFINITY;
-    logits[((size_t)g * kHq + h) * kFP + b] = l;
-    const float m = wave_max(l);
-    const float e = (l == -INFINITY) ? 0.f : expf(l - m);
-    const float z = wave_sum(e);
-    if (lane == 0) {
-      stats[(((size_t)g * kChunks + c) * kHq + h) * 2 + 0] = m;
-      stats[(((size_t)g * kChunks + c) * kHq + h) * 2 + 1] = z;
-    }
+    const int l = tid >> 2, j = tid & 3;
+    const float s = ((reinterpret_cast<const float*>(&red[0][l])[j] + reinterpret_cast<const float*>(&red[1][l])[j]) +
+                     reinterpret_cast<const float*>(&red[2][l])[j]) +
+                    reinterpret_cast<const float*>(&red[3][l])[j];
+    dots[(l >> 5) & 1][(l >> 3) & 3][4 * (l & 7) + j] = s;
   }
-  __threadfence();
   __syncthreads();
-  if (tid == 0) is_last = atomic_add_agent(&sync[g], 1u) == (unsigned)(kChunks - 1);
+
+  if (tid < kHq * kChunk) {
+    // thread = (head tid>>5, bucket tid&31); 32 lanes per head
+    const int h = tid >> 5, b = tid & 31, bucket = c * kChunk + b;
+    const int n = counts[(size_t)g * kFP + bucket];
+    float l = -INFINITY;
+    if (n > 0) {
+      // core.py:122-127: log(count) + (q @ mean^T) / sqrt(d) + (q^2 @ var^T) / (2d)
+      const float lc = logf((float)n);
+      l = (lc + dots[0][h][b] / kSqrtD) + dots[1][h][b] / (2.0f * kD);
+    }
+    st_dev(&work.logits[((size_t)g * kHq + h) * kFP + bucket], l);
+    float m = l;
+#pragma unroll
+    for (int o = 16; o; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+    float e = (l == -INFINITY) ? 0.f : expf(l - m);
+#pragma unroll
+    for (int o = 16; o; o >>= 1) e += __shfl_xor(e, o);
+    if (b == 0) st_dev2(&work.stats[(((size_t)g * kChunks + c) * kHq + h) * 2], m, e);
+  }
+  drain();
+  __syncthreads();
+  if (tid == 0) is_last = inc_dev(&work.sync[g]) == (unsigned)(kChunks - 1);
   __syncthreads();
   if (!is_last) return;
-  __threadfence();
-  if (tid == 0) atomic_store_agent(&sync[g], 0u);
+  if (tid == 0) st_dev(&work.sync[g], 0u);
 
   {
-    // merge chunk statistics: wave h handles head h, lane = chunk
+    // merge chunk statistics: wave h handles head h, lanes cover the 94 chunks
     const int h = w;
-    const float mc = lane < kChunks ? stats[(((size_t)g * kChunks + lane) * kHq + h) * 2 + 0] : -INFINITY;
-    const float zc = lane < kChunks ? stats[(((size_t)g * kChunks + lane) * kHq + h) * 2 + 1] : 0.f;
-    const float m = wave_max(mc);
-    const float z = wave_sum(mc == -INFINITY ? 0.f : zc * expf(mc - m));
+    const float* st = work.stats + ((size_t)g * kChunks * kHq + h) * 2;
+    const float2 s0 = lane < kChunks ? ld_dev2(st + lane * kHq * 2) : make_float2(-INFINITY, 0.f);
+    const float2 s1 = lane + 64 < kChunks ? ld_dev2(st + (lane + 64) * kHq * 2) : make_float2(-INFINITY, 0.f);
+    const float m = wave_max(fmaxf(s0.x, s1.x));
+    float z = (s0.x == -INFINITY ? 0.f : s0.y * expf(s0.x - m)) + (s1.x == -INFINITY ? 0.f : s1.y * expf(s1.x - m));
+    z = wave_sum(z);
     if (lane == 0) {
       gmax[h] = m;
-      gsum[h] = z;
+      grz[h] = z > 0.f ? 1.0f / z : 0.f;
     }
   }
   __syncthreads();
 
   uint64_t key[kKeys];
-  const float* lg = logits + (size_t)g * kHq * kFP;
+  const float* lg = work.logits + (size_t)g * kHq * kFP;
 #pragma unroll
   for (int i = 0; i < kKeys; ++i) {
     const int b = tid + i * kRT;
     key[i] = 0;
     if (b < kFP) {
-      const float l0 = lg[b];
+      const float l0 = ld_dev(lg + b), l1 = ld_dev(lg + kFP + b), l2 = ld_dev(lg + 2 * kFP + b),
+                  l3 = ld_dev(lg + 3 * kFP + b);
       if (l0 != -INFINITY) {
-        const float p0 = expf(l0 - gmax[0]) / gsum[0];
-        const float p1 = expf(lg[kFP + b] - gmax[1]) / gsum[1];
-        const float p2 = expf(lg[2 * kFP + b] - gmax[2]) / gsum[2];
-        const float p3 = expf(lg[3 * kFP + b] - gmax[3]) / gsum[3];
+        // per-head softmax, then the sum over heads in head order (core.py:128)
+        const float p0 = expf(l0 - gmax[0]) * grz[0];
+        const float p1 = expf(l1 - gmax[1]) * grz[1];
+        const float p2 = expf(l2 - gmax[2]) * grz[2];
+        const float p3 = expf(l3 - gmax[3]) * grz[3];
         key[i] = make_key(((p0 + p1) + p2) + p3, b);
       }
     }
@@ -300,26 +372,27 @@ __global__ void pack_kernel(const uint16_t* __restrict__ q, float* __restrict__ 
 
 using namespace prismkv;
 
+static size_t route_logits_bytes(int groups) { return (size_t)groups * kHq * kFP * sizeof(float); }
+static size_t route_stats_bytes(int groups) { return (size_t)groups * kChunks * kHq * sizeof(float2); }
+
 extern "C" {
 
 size_t prismkv_route_work_bytes(int groups) {
   if (groups < 1) return 0;
-  const size_t logits = (size_t)groups * kHq * kFP * sizeof(float);
-  const size_t stats = (size_t)groups * kChunks * kHq * 2 * sizeof(float);
   const size_t sync = (size_t)groups * sizeof(unsigned);
-  return logits + stats + ((sync + 255) & ~(size_t)255);
+  return route_logits_bytes(groups) + route_stats_bytes(groups) + ((sync + 255) & ~(size_t)255);
 }
 
 int prismkv_route(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features, uint64_t valid,
                   uint64_t raw, int groups, uint64_t stream) {
   if (groups < 1 || groups > 65535) return kBadSize;
   if (!q || !moments || !counts || !work || !features || !valid || !raw) return kBadSize;
-  float* logits = reinterpret_cast<float*>(work);
-  float* stats = logits + (size_t)groups * kHq * kFP;
-  unsigned* sync = reinterpret_cast<unsigned*>(stats + (size_t)groups * kChunks * kHq * 2);
+  char* base = reinterpret_cast<char*>(work);
+  RouteWork rw{reinterpret_cast<float*>(base), reinterpret_cast<float*>(base + route_logits_bytes(groups)),
+               reinterpret_cast<unsigned*>(base + route_logits_bytes(groups) + route_stats_bytes(groups))};
   hipLaunchKernelGGL(route_kernel, dim3(kChunks, groups), dim3(kRT), 0, (hipStream_t)stream,
                      reinterpret_cast<const uint16_t*>(q), reinterpret_cast<const float*>(moments),
-                     reinterpret_cast<const int*>(counts), logits, stats, sync, reinterpret_cast<int64_t*>(features),
+                     reinterpret_cast<const int*>(counts), rw, reinterpret_cast<int64_t*>(features),
                      reinterpret_cast<float*>(valid), reinterpret_cast<int*>(raw));
   return (int)hipGetLastError();
 }

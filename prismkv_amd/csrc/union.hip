@@ -6,14 +6,16 @@
 //            ascending emission of w*32+bit), kernels/ppu_8b/pack.cu:5 (bit
 //            order: token t <-> word t>>5, bit t&31), src/prismkv/core.py:142-167.
 //
-// Design: one launch.  Workgroup (tile, group) ORs up to 16 rows over its
-// 256 x WPT words (coalesced 4 or 16 bytes per lane), counts bits, and finds
-// its output offset with a decoupled look-back over the preceding tiles of the
-// same group (status words in caller-provided work memory, tiles only wait on
-// lower-numbered tiles, which the in-order dispatcher has already started;
-// the wait is bounded and reports through an error word instead of hanging).
-// The last tile to finish restores the status words to zero, so the launch
-// is replayable from a graph without memset nodes.
+// Design: one launch.  Workgroup (tile, group) ORs the selected rows over its
+// 256 x WPT words.  Rows are padded to 16 by repeating the last selected row
+// (OR is idempotent), so every thread issues 16 independent vector loads at
+// once.  The tile's output offset comes from a decoupled look-back in which
+// one wave inspects up to 64 predecessor status words per round in parallel;
+// tiles only wait on lower-numbered tiles of the same group, which the
+// in-order dispatcher has already started, and every wait is bounded (it
+// reports through an error word instead of hanging).  The last tile to finish
+// restores the status words to zero, so the launch is replayable from a graph
+// without memset nodes.
 #include "common.h"
 
 namespace prismkv {
@@ -23,7 +25,6 @@ constexpr int kUT = 256;                 // union workgroup size
 constexpr unsigned kFlagAgg = 1u << 30;  // status: tile aggregate available
 constexpr unsigned kFlagInc = 2u << 30;  // status: inclusive prefix available
 constexpr unsigned kValMask = (1u << 30) - 1;
-constexpr int kSpinLimit = 1 << 20;
 
 struct UnionWork {
   unsigned* status;  // [groups][tiles]
@@ -38,6 +39,66 @@ __host__ __device__ inline int union_tiles(int H, int wpt) {
 }
 
 template <int WPT>
+struct Words;
+template <>
+struct Words<1> {
+  static __device__ __forceinline__ void load(const uint32_t* p, uint32_t* m) { m[0] = __builtin_nontemporal_load(p); }
+};
+template <>
+struct Words<2> {
+  static __device__ __forceinline__ void load(const uint32_t* p, uint32_t* m) {
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 v = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+    m[0] = v.x;
+    m[1] = v.y;
+  }
+};
+template <>
+struct Words<4> {
+  static __device__ __forceinline__ void load(const uint32_t* p, uint32_t* m) {
+    const uint4 v = load_nt16(p);
+    m[0] = v.x; m[1] = v.y; m[2] = v.z; m[3] = v.w;
+  }
+};
+
+// Exclusive prefix of tile t of a group by decoupled look-back (run by wave 0).
+// Returns the prefix; publishes the inclusive status of tile t.
+__device__ unsigned look_back(unsigned* st, int t, unsigned total, unsigned* err) {
+  const int lane = threadIdx.x & 63;
+  if (t == 0) {
+    if (lane == 0) st_dev(&st[0], kFlagInc | total);
+    return 0;
+  }
+  if (lane == 0) st_dev(&st[t], kFlagAgg | total);
+  unsigned prefix = 0;
+  int end = t;  // window: tiles end-64 .. end-1, lane i looks at tile end-1-i
+  for (;;) {
+    const int p = end - 1 - lane;
+    unsigned s = p >= 0 ? ld_dev(&st[p]) : (kFlagInc | 0u);
+    for (int spins = 0;; ++spins) {
+      if (!__ballot((s >> 30) == 0)) break;
+      if (spins >= kSpinLimit) {  // a predecessor never published: report, do not hang
+        if (lane == 0) atomicOr(err, 1u);
+        s = kFlagInc | 0u;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      if ((s >> 30) == 0) s = ld_dev(&st[p]);
+    }
+    const unsigned long long inc = __ballot((s >> 30) == 2u);
+    if (inc) {
+      const int first = __ffsll((long long)inc) - 1;  // nearest predecessor with an inclusive prefix
+      prefix += (unsigned)wave_sum_i(lane <= first ? (int)(s & kValMask) : 0);
+      break;
+    }
+    prefix += (unsigned)wave_sum_i((int)(s & kValMask));
+    end -= 64;
+  }
+  if (lane == 0) st_dev(&st[t], kFlagInc | ((prefix + total) & kValMask));
+  return prefix;
+}
+
+template <int WPT>
 __global__ __launch_bounds__(kUT) void union_kernel(const uint32_t* __restrict__ bits, int64_t row_words,
                                                     const int64_t* __restrict__ features,
                                                     const float* __restrict__ valid, int32_t* __restrict__ ids,
@@ -48,40 +109,44 @@ __global__ __launch_bounds__(kUT) void union_kernel(const uint32_t* __restrict__
   __shared__ int nrows;
   __shared__ unsigned wsum[kUT / 64];
   __shared__ unsigned base;
-  if (tid == 0) {
-    int n = 0;
-    for (int j = 0; j < kTop; ++j)
-      if (valid[(size_t)g * kTop + j] > 0.f) {
-        const int64_t f = features[(size_t)g * kTop + j];
-        if (f >= 0 && f < kF) rows[n++] = (int)f;  // an out-of-range id selects nothing
-      }
-    nrows = n;
+  __shared__ int last;
+  if (tid < 64) {
+    // wave 0 compacts the valid, in-range selections (an out-of-range id selects nothing)
+    bool ok = false;
+    int f = 0;
+    if (tid < kTop && valid[(size_t)g * kTop + tid] > 0.f) {
+      const int64_t fe = features[(size_t)g * kTop + tid];
+      ok = fe >= 0 && fe < kF;
+      f = (int)fe;
+    }
+    const unsigned long long m = __ballot(ok);
+    if (ok) rows[__popcll(m & ((1ull << tid) - 1))] = f;
+    if (tid == 0) nrows = __popcll(m);
   }
   __syncthreads();
+  const int nr = nrows;
   const int nw = (H + 31) / 32;
   const int w0 = (t * kUT + tid) * WPT;
   uint32_t m[WPT];
 #pragma unroll
   for (int i = 0; i < WPT; ++i) m[i] = 0;
   const uint32_t* gb = bits + (size_t)g * kF * row_words;
-  const int nr = nrows;
-  if (w0 + WPT <= nw) {
-    for (int r = 0; r < nr; ++r) {
-      const uint32_t* src = gb + (size_t)rows[r] * row_words + w0;
-      if constexpr (WPT == 4) {
-        const uint4 v = load_nt16(src);
-        m[0] |= v.x; m[1] |= v.y; m[2] |= v.z; m[3] |= v.w;
-      } else {
+  if (nr > 0) {
+    if (w0 + WPT <= nw) {
+      uint32_t v[kTop][WPT];
 #pragma unroll
-        for (int i = 0; i < WPT; ++i) m[i] |= __builtin_nontemporal_load(src + i);
+      for (int r = 0; r < kTop; ++r) Words<WPT>::load(gb + (size_t)rows[r < nr ? r : nr - 1] * row_words + w0, v[r]);
+#pragma unroll
+      for (int r = 0; r < kTop; ++r)
+#pragma unroll
+        for (int i = 0; i < WPT; ++i) m[i] |= v[r][i];
+    } else {
+      for (int r = 0; r < nr; ++r) {
+        const uint32_t* src = gb + (size_t)rows[r] * row_words;
+#pragma unroll
+        for (int i = 0; i < WPT; ++i)
+          if (w0 + i < nw) m[i] |= src[w0 + i];
       }
-    }
-  } else {
-    for (int r = 0; r < nr; ++r) {
-      const uint32_t* src = gb + (size_t)rows[r] * row_words;
-#pragma unroll
-      for (int i = 0; i < WPT; ++i)
-        if (w0 + i < nw) m[i] |= src[w0 + i];
     }
   }
   // tokens at or beyond H are never members; clear them defensively
@@ -94,39 +159,16 @@ __global__ __launch_bounds__(kUT) void union_kernel(const uint32_t* __restrict__
   unsigned n = 0;
 #pragma unroll
   for (int i = 0; i < WPT; ++i) n += __popc(m[i]);
-  const unsigned incl = block_incl_scan<kUT>(n, wsum);
+  const unsigned incl = block_incl_scan<kUT>(n, wsum);  // wsum[3] = tile total afterwards
   const unsigned excl = incl - n;
-
-  if (tid == kUT - 1) {
-    // incl of the last thread is the tile total
-    unsigned* st = work.status + (size_t)g * tiles;
-    const unsigned total = incl;
-    unsigned prefix = 0;
-    if (t == 0) {
-      atomic_store_agent(&st[0], kFlagInc | total);
-    } else {
-      atomic_store_agent(&st[t], kFlagAgg | total);
-      int p = t - 1;
-      while (p >= 0) {
-        unsigned s = atomic_load_agent(&st[p]);
-        int spins = 0;
-        while ((s >> 30) == 0 && spins < kSpinLimit) {
-          __builtin_amdgcn_s_sleep(1);
-          s = atomic_load_agent(&st[p]);
-          ++spins;
-        }
-        if ((s >> 30) == 0) {  // predecessor never published: report, do not hang
-          atomicOr(work.err, 1u);
-          break;
-        }
-        prefix += s & kValMask;
-        if ((s >> 30) == 2u) break;
-        --p;
-      }
-      atomic_store_agent(&st[t], kFlagInc | ((prefix + total) & kValMask));
+  unsigned* st = work.status + (size_t)g * tiles;
+  if (tid < 64) {
+    const unsigned total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    const unsigned prefix = look_back(st, t, total, work.err);
+    if (tid == 0) {
+      base = prefix;
+      if (t == tiles - 1) count[g] = (int32_t)(prefix + total);
     }
-    base = prefix;
-    if (t == tiles - 1) count[g] = (int32_t)(prefix + total);
   }
   __syncthreads();
   int at = (int)(base + excl);
@@ -140,13 +182,12 @@ __global__ __launch_bounds__(kUT) void union_kernel(const uint32_t* __restrict__
       v &= v - 1u;
     }
   }
-  // last tile of the group to get here clears the status words for reuse
-  if (tid == kUT - 1) {
-    if (atomic_add_agent(&work.done[g], 1u) == (unsigned)(tiles - 1)) {
-      unsigned* st = work.status + (size_t)g * tiles;
-      for (int i = 0; i < tiles; ++i) atomic_store_agent(&st[i], 0u);
-      atomic_store_agent(&work.done[g], 0u);
-    }
+  // the last tile of the group to get here clears the status words for reuse
+  if (tid == 0) last = inc_dev(&work.done[g]) == (unsigned)(tiles - 1);
+  __syncthreads();
+  if (last) {
+    for (int i = tid; i < tiles; i += kUT) st_dev(&st[i], 0u);
+    if (tid == 0) st_dev(&work.done[g], 0u);
   }
 }
 
@@ -163,8 +204,10 @@ __global__ __launch_bounds__(kCT) void compat_count(const uint32_t* __restrict__
   __shared__ unsigned wsum[kCT / 64];
   uint32_t v = 0;
   if (w < nw) {
-    for (int j = 0; j < kTop; ++j)
-      if (vals[u * kTop + j] > 0.f) v |= bits[((size_t)u * kF + ids[u * kTop + j]) * nw + w];
+    for (int j = 0; j < kTop; ++j) {
+      const int64_t f = ids[u * kTop + j];
+      if (vals[u * kTop + j] > 0.f && f >= 0 && f < kF) v |= bits[((size_t)u * kF + f) * nw + w];
+    }
     mask[(size_t)u * nw + w] = v;
   }
   const unsigned incl = block_incl_scan<kCT>(__popc(v), wsum);
@@ -178,6 +221,7 @@ __global__ __launch_bounds__(kCT) void compat_extract(const uint32_t* __restrict
   __shared__ unsigned wsum[kCT / 64];
   __shared__ int base;
   uint32_t v = w < nw ? mask[(size_t)u * nw + w] : 0u;
+  if (w == nw - 1 && (H & 31)) v &= (1u << (H & 31)) - 1u;
   const unsigned n = __popc(v);
   const unsigned incl = block_incl_scan<kCT>(n, wsum);
   if (tid == 0) {
@@ -212,9 +256,13 @@ __global__ __launch_bounds__(256) void bits_kernel(const int* __restrict__ ids, 
 
 using namespace prismkv;
 
-// 16-byte row loads once a group has at least 8 such tiles and rows are 16-byte aligned.
+// Words per thread: the widest vector load that still leaves at least 8
+// tiles per group (and fits the row alignment).
 static int union_wpt(int H, int64_t row_words) {
-  return ((H + 31) / 32) >= 8 * kUT * 4 && (row_words & 3) == 0 ? 4 : 1;
+  const int nw = (H + 31) / 32;
+  if (nw >= 8 * kUT * 4 && (row_words & 3) == 0) return 4;
+  if (nw >= 8 * kUT * 2 && (row_words & 1) == 0) return 2;
+  return 1;
 }
 
 extern "C" {
@@ -232,19 +280,22 @@ int prismkv_union(uint64_t bits, uint64_t features, uint64_t valid, uint64_t wor
   if (!bits || !features || !valid || !work || !ids || !count) return kBadSize;
   const int wpt = union_wpt(H, row_words);
   const int tiles = union_tiles(H, wpt);
+  // fixed layout for any H: err word, done[groups], then status[groups][tiles]
   unsigned* w = reinterpret_cast<unsigned*>(work);
-  UnionWork uw{w, w + (size_t)groups * tiles, w + (size_t)groups * tiles + groups};
+  UnionWork uw{w + 1 + groups, w + 1, w};
   const dim3 grid(tiles, groups), block(kUT);
+  const uint32_t* b = reinterpret_cast<const uint32_t*>(bits);
+  const int64_t* f = reinterpret_cast<const int64_t*>(features);
+  const float* v = reinterpret_cast<const float*>(valid);
+  int32_t* o = reinterpret_cast<int32_t*>(ids);
+  int32_t* c = reinterpret_cast<int32_t*>(count);
+  hipStream_t s = (hipStream_t)stream;
   if (wpt == 4)
-    hipLaunchKernelGGL(union_kernel<4>, grid, block, 0, (hipStream_t)stream,
-                       reinterpret_cast<const uint32_t*>(bits), row_words, reinterpret_cast<const int64_t*>(features),
-                       reinterpret_cast<const float*>(valid), reinterpret_cast<int32_t*>(ids), ids_stride,
-                       reinterpret_cast<int32_t*>(count), uw, H, tiles);
+    hipLaunchKernelGGL(union_kernel<4>, grid, block, 0, s, b, row_words, f, v, o, ids_stride, c, uw, H, tiles);
+  else if (wpt == 2)
+    hipLaunchKernelGGL(union_kernel<2>, grid, block, 0, s, b, row_words, f, v, o, ids_stride, c, uw, H, tiles);
   else
-    hipLaunchKernelGGL(union_kernel<1>, grid, block, 0, (hipStream_t)stream,
-                       reinterpret_cast<const uint32_t*>(bits), row_words, reinterpret_cast<const int64_t*>(features),
-                       reinterpret_cast<const float*>(valid), reinterpret_cast<int32_t*>(ids), ids_stride,
-                       reinterpret_cast<int32_t*>(count), uw, H, tiles);
+    hipLaunchKernelGGL(union_kernel<1>, grid, block, 0, s, b, row_words, f, v, o, ids_stride, c, uw, H, tiles);
   return (int)hipGetLastError();
 }
 

@@ -31,7 +31,7 @@ from . import _lib
 from .build import compile_hip  # noqa: F401  (re-exported: reference name compile_ppu)
 
 GROUPS, HEADS, DIM, FEATURES, TOPK = 8, 4, 128, 3000, 16
-CHUNK = 64
+CHUNK = 32
 CHUNKS = (FEATURES + CHUNK - 1) // CHUNK
 PADDED = CHUNKS * CHUNK
 
@@ -55,7 +55,7 @@ class FeatureIndex:
 
 
 def tile_moments(mean: torch.Tensor, variance: torch.Tensor) -> torch.Tensor:
-    """[G,3000,128] mean and variance -> f32 [G,47,256,64] bucket tiles (k < 128 mean)."""
+    """[G,3000,128] mean and variance -> f32 [G,94,256,32] bucket tiles (k < 128 mean)."""
     g = mean.shape[0]
     rows = torch.cat((mean.float(), variance.float()), dim=-1)  # [G, F, 256]
     rows = torch.nn.functional.pad(rows, (0, 0, 0, PADDED - FEATURES))
