@@ -28,11 +28,10 @@
 namespace prismkv {
 namespace {
 
-constexpr int kAT = 256;
+constexpr int kAT = 512;                           // 8 waves
 constexpr int kStateW = kD + 2;                    // {max, den, acc[128]}
 constexpr float kLog2eScale = 0.12751743082459868f;  // log2(e) / sqrt(128): scores in the exp2 domain
 constexpr float kSlack = 8.0f;                     // lazy-rescale threshold (log2 units)
-constexpr int kPosChunk = 1024;                    // row positions staged in LDS per round
 constexpr int kStepRows = 16;                      // rows per wave step (4 slots x 4 rows)
 
 struct AttendArgs {
@@ -55,10 +54,22 @@ __device__ __forceinline__ void unpack8(const uint4 r, float (&f)[8]) {
 
 __device__ __forceinline__ float exp2_or_zero(float x) { return x == -INFINITY ? 0.f : exp2f(x); }
 
+constexpr int kSlotRows = 9;                 // rows per slot per round
+constexpr int kWaveRows = 4 * kSlotRows;     // rows per wave per round
+
+// LDS of one workgroup: the gather staging area of the 4 waves, reused for
+// the slot merge once every wave is done with it.
+constexpr int kSlots = kAT / 16;             // 32 slots of 16 lanes
+
 struct AttendLds {
-  int pos[kPosChunk];
-  float sm[16][kHq], sz[16][kHq];
-  float sacc[16][kHq][kD];
+  union {
+    uint4 kv[kAT / 64][2][kSlotRows][64];  // [wave][K, V][row of slot][lane] (147456 B)
+    struct {
+      float sm[kSlots][kHq], sz[kSlots][kHq];
+      float sacc[kSlots][kHq][kD];
+    } red;
+    float wts[kAT / 64][64];               // split weights of the final merge
+  };
 };
 
 // Per-lane running state of one slot: head-h scores live in lanes with
@@ -90,12 +101,12 @@ __device__ __forceinline__ void attend_step(const float (&qf)[kHq][8], const uin
 #pragma unroll
   for (int stage = 0; stage < 4; ++stage) {
     const int mask = 8 >> stage, n = 8 >> stage;
-    const bool hi = (q16 & mask) != 0;
+    const unsigned long long hi = __ballot((q16 & mask) != 0);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       if (j < n) {
-        const float keep = hi ? x[j + n] : x[j];
-        const float send = hi ? x[j] : x[j + n];
+        const float keep = lane_select(hi, x[j + n], x[j]);
+        const float send = lane_select(hi, x[j], x[j + n]);
         x[j] = keep + __shfl_xor(send, mask);
       }
     }
@@ -137,15 +148,23 @@ __device__ __forceinline__ void attend_step(const float (&qf)[kHq][8], const uin
 }
 
 // Computes this workgroup's split state and writes it to a.state.
+//
+// The group's row list (count[g] selected rows, then the T tail rows) is
+// dealt row by row to the 8*S waves of the group's S workgroups: wave
+// gw = 8p + w owns rows gw, gw + 8S, gw + 16S, ... -- every wave gets the
+// same number of rows to within one.  Row positions of the list do not depend on
+// count[g], so the id loads are issued together with the count load; then
+// every K and V row of the round (up to 36 per wave) is gathered straight
+// into the wave's LDS region with global_load_lds (16 bytes per lane, no
+// registers held by loads in flight) before any is consumed.
 __device__ void attend_split(const AttendArgs& a, int g, int p, AttendLds& lds) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int q16 = lane & 15, slot = lane >> 4;
-  int n_old = a.cnt[g];
-  n_old = n_old < 0 ? 0 : (n_old > a.H ? a.H : n_old);
-  const int total = n_old + a.T;
-  const int span = (total + a.S - 1) / a.S;
-  const int j0 = min(total, p * span), j1 = min(total, j0 + span);
   const int last_row = a.H + a.T - 1;
+  const int nwaves = (kAT / 64) * a.S, gw = (kAT / 64) * p + w;
+  const int32_t* idg = a.ids + (size_t)g * a.ids_stride;
+  const uint16_t* kg = a.k + (size_t)g * a.ks + 8 * q16;
+  const uint16_t* vg = a.v + (size_t)g * a.vs + 8 * q16;
 
   float qf[kHq][8];
 #pragma unroll
@@ -162,48 +181,54 @@ __device__ void attend_split(const AttendArgs& a, int g, int p, AttendLds& lds) 
 #pragma unroll
     for (int i = 0; i < 8; ++i) s.acc[h][i] = 0.f;
 
-  const uint16_t* kg = a.k + (size_t)g * a.ks + 8 * q16;
-  const uint16_t* vg = a.v + (size_t)g * a.vs + 8 * q16;
-  const int32_t* idg = a.ids + (size_t)g * a.ids_stride;
-
-  for (int c0 = j0; c0 < j1; c0 += kPosChunk) {
-    const int n = min(kPosChunk, j1 - c0);
-    __syncthreads();  // previous chunk's positions are consumed
-    for (int i = tid; i < n; i += kAT) {
-      const int j = c0 + i;
-      int pos = j < n_old ? idg[j] : a.H + (j - n_old);
-      lds.pos[i] = pos < 0 ? 0 : (pos > last_row ? last_row : pos);
+  __attribute__((address_space(3))) void* kdst =
+      (__attribute__((address_space(3))) void*)&lds.kv[w][0][0][0];
+  __attribute__((address_space(3))) void* vdst =
+      (__attribute__((address_space(3))) void*)&lds.kv[w][1][0][0];
+  int n_old = -1, total = 0;
+  for (int round = 0;; ++round) {
+    // row i of this lane's slot in the round: list index j[i]
+    int jr[kSlotRows], idv[kSlotRows];
+#pragma unroll
+    for (int i = 0; i < kSlotRows; ++i) {
+      const int j = gw + nwaves * (round * kWaveRows + i * 4 + slot);
+      jr[i] = j;
+      idv[i] = a.H > 0 ? idg[j < a.H ? j : a.H - 1] : 0;  // speculative: meaningful only if j < count
     }
-    __syncthreads();
-    // wave w takes steps w, w+4, ...; a step is 16 rows = 4 slots x 4 rows
-    const int steps = (n + kStepRows - 1) / kStepRows;
-    int st = w;
-    if (st >= steps) continue;
-    uint4 kc[4], vc[4];
-    auto issue = [&](int step, uint4 (&kr)[4], uint4 (&vr)[4]) {
+    if (n_old < 0) {
+      n_old = a.cnt[g];
+      n_old = n_old < 0 ? 0 : (n_old > a.H ? a.H : n_old);
+      total = n_old + a.T;
+    }
+    if (!__ballot(jr[0] < total)) break;  // rows grow with i and round: nothing left for this wave
+#pragma unroll
+    for (int i = 0; i < kSlotRows; ++i) {
+      const int j = jr[i];
+      if (j < total) {
+        int pos = j < n_old ? idv[i] : a.H + (j - n_old);
+        pos = pos < 0 ? 0 : (pos > last_row ? last_row : pos);
+        __builtin_amdgcn_global_load_lds(kg + (size_t)pos * kD, (char __attribute__((address_space(3)))*)kdst + i * 1024,
+                                         16, 0, 0);
+        __builtin_amdgcn_global_load_lds(vg + (size_t)pos * kD, (char __attribute__((address_space(3)))*)vdst + i * 1024,
+                                         16, 0, 0);
+      }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    const int base = gw + nwaves * (round * kWaveRows + slot);  // list index of row i: base + 4 * nwaves * i
+#pragma unroll 1
+    for (int st = 0; st < (kSlotRows + 3) / 4; ++st) {
+      int nv = 0;
+      uint4 kr[4], vr[4];
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        const int i = step * kStepRows + slot * 4 + b;
-        const int pos = lds.pos[i < n ? i : n - 1];
-        kr[b] = load_nt16(kg + (size_t)pos * kD);
-        vr[b] = load_nt16(vg + (size_t)pos * kD);
+        const int i = min(st * 4 + b, kSlotRows - 1);
+        nv += (st * 4 + b < kSlotRows) && (base + 4 * nwaves * (st * 4 + b) < total);
+        kr[b] = lds.kv[w][0][i][lane];
+        vr[b] = lds.kv[w][1][i][lane];
       }
-    };
-    issue(st, kc, vc);
-    for (;;) {
-      const int nxt = st + kAT / 64;
-      uint4 kn[4], vn[4];
-      if (nxt < steps) issue(nxt, kn, vn);
-      const int rem = n - (st * kStepRows + slot * 4);
-      attend_step(qf, kc, vc, rem < 0 ? 0 : (rem > 4 ? 4 : rem), s);
-      if (nxt >= steps) break;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        kc[b] = kn[b];
-        vc[b] = vn[b];
-      }
-      st = nxt;
+      if (__ballot(nv > 0)) attend_step(qf, kr, vr, nv, s);
     }
+    asm volatile("" ::: "memory");  // LDS reads of this round precede the next round's gathers
   }
 
   // gather the slot's per-head max / denominator into every lane
@@ -213,80 +238,72 @@ __device__ void attend_split(const AttendArgs& a, int g, int p, AttendLds& lds) 
     mm[h] = __shfl(s.m, (lane & 48) + h);
     zz[h] = __shfl(s.z, (lane & 48) + h);
   }
+  __syncthreads();  // every wave is done with the staging area
   const int sl = w * 4 + slot;
   if (q16 == 0) {
 #pragma unroll
     for (int h = 0; h < kHq; ++h) {
-      lds.sm[sl][h] = mm[h];
-      lds.sz[sl][h] = zz[h];
+      lds.red.sm[sl][h] = mm[h];
+      lds.red.sz[sl][h] = zz[h];
     }
   }
 #pragma unroll
   for (int h = 0; h < kHq; ++h) {
-    float4* dst = reinterpret_cast<float4*>(&lds.sacc[sl][h][8 * q16]);
+    float4* dst = reinterpret_cast<float4*>(&lds.red.sacc[sl][h][8 * q16]);
     dst[0] = make_float4(s.acc[h][0], s.acc[h][1], s.acc[h][2], s.acc[h][3]);
     dst[1] = make_float4(s.acc[h][4], s.acc[h][5], s.acc[h][6], s.acc[h][7]);
   }
   __syncthreads();
   {
-    const int h = tid >> 6, d0 = (tid & 63) * 2;
+    // thread = (head tid >> 7, dim tid & 127)
+    const int h = tid >> 7, d = tid & (kD - 1);
     float M = -INFINITY;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) M = fmaxf(M, lds.sm[k][h]);
-    float den = 0.f, v0 = 0.f, v1 = 0.f;
+    for (int k = 0; k < kSlots; ++k) M = fmaxf(M, lds.red.sm[k][h]);
+    float den = 0.f, v = 0.f;
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const float wgt = exp2_or_zero(lds.sm[k][h] == -INFINITY ? -INFINITY : lds.sm[k][h] - M);
-      den = fmaf(wgt, lds.sz[k][h], den);
-      v0 = fmaf(wgt, lds.sacc[k][h][d0], v0);
-      v1 = fmaf(wgt, lds.sacc[k][h][d0 + 1], v1);
+    for (int k = 0; k < kSlots; ++k) {
+      const float wgt = lds.red.sm[k][h] == -INFINITY ? 0.f : exp2f(lds.red.sm[k][h] - M);
+      den = fmaf(wgt, lds.red.sz[k][h], den);
+      v = fmaf(wgt, lds.red.sacc[k][h][d], v);
     }
     float* stp = a.state + (((size_t)g * kHq + h) * a.S + p) * kStateW;
-    if ((tid & 63) == 0) st_dev2(stp, M, den);
-    st_dev2(stp + 2 + d0, v0, v1);
+    if (d == 0) st_dev2(stp, M, den);
+    st_dev(stp + 2 + d, v);
   }
 }
 
-// Merges the S split states of head row hh (= g*4 + h) for dims d0, d0+1.
-// All state loads of a batch of 16 splits are issued before any is used.
-__device__ __forceinline__ void merge_head(const float* state, int S, int hh, int d0, uint16_t* out) {
-  const float* st = state + (size_t)hh * S * kStateW;
-  float M = -INFINITY;
-  for (int p0 = 0; p0 < S; p0 += 16) {
-    float mv[16];
+// Merges the S split states of group g into out[g] (thread = head tid >> 7,
+// dim tid & 127).  Splits go in batches of 32: each thread issues its 32
+// accumulator loads and each wave its 32 (max, den) loads before any is
+// used, so S <= 32 costs one memory round trip.
+__device__ void merge_group(const float* state, int S, int g, uint16_t* out, AttendLds& lds) {
+  const int tid = threadIdx.x, h = tid >> 7, d = tid & (kD - 1), w = tid >> 6, lane = tid & 63;
+  const float* st = state + (size_t)(g * kHq + h) * S * kStateW;
+  float M = -INFINITY, den = 0.f, v = 0.f;
+  for (int p0 = 0; p0 < S; p0 += 32) {
+    const int n = min(32, S - p0);
+    const float2 mz = ld_dev2(st + (size_t)(p0 + min(lane & 31, n - 1)) * kStateW);
+    float av[32];
 #pragma unroll
-    for (int i = 0; i < 16; ++i) mv[i] = p0 + i < S ? ld_dev(st + (size_t)(p0 + i) * kStateW) : -INFINITY;
+    for (int i = 0; i < 32; ++i) av[i] = ld_dev(st + (size_t)(p0 + min(i, n - 1)) * kStateW + 2 + d);
+    // online merge across batches: rescale what is accumulated when the max grows
+    const bool mine = lane < n;  // lanes 32..63 duplicate lanes 0..31 and stay out
+    const float bm = wave_max(mine ? mz.x : -INFINITY);
+    const float nM = fmaxf(M, bm);
+    const float scale = (M == -INFINITY) ? 0.f : exp2f(M - nM);
+    den *= scale;
+    v *= scale;
+    M = nM;
+    const float wgt = (mine && mz.x != -INFINITY) ? exp2f(mz.x - M) : 0.f;
+    den += wave_sum(wgt * mz.y);
+    __syncthreads();  // previous batch's weights are consumed
+    lds.wts[w][lane] = wgt;
+    __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 16; ++i) M = fmaxf(M, mv[i]);
+    for (int i = 0; i < 32; ++i) v = fmaf(lds.wts[w][i], av[i], v);
   }
-  float den = 0.f, v0 = 0.f, v1 = 0.f;
-  for (int p0 = 0; p0 < S; p0 += 16) {
-    float mv[16], zv[16];
-    float2 av[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (p0 + i < S) {
-        const float* sp = st + (size_t)(p0 + i) * kStateW;
-        const float2 mz = ld_dev2(sp);
-        mv[i] = mz.x;
-        zv[i] = mz.y;
-        av[i] = ld_dev2(sp + 2 + d0);
-      } else {
-        mv[i] = -INFINITY;
-        zv[i] = 0.f;
-        av[i] = make_float2(0.f, 0.f);
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float wgt = mv[i] == -INFINITY ? 0.f : exp2f(mv[i] - M);
-      den = fmaf(wgt, zv[i], den);
-      v0 = fmaf(wgt, av[i].x, v0);
-      v1 = fmaf(wgt, av[i].y, v1);
-    }
-  }
-  out[(size_t)hh * kD + d0] = f32_to_bf16(den > 0.f ? v0 / den : 0.f);
-  out[(size_t)hh * kD + d0 + 1] = f32_to_bf16(den > 0.f ? v1 / den : 0.f);
+  out[((size_t)g * kHq + h) * kD + d] = f32_to_bf16(den > 0.f ? v / den : 0.f);
 }
 
 __global__ __launch_bounds__(kAT) void attend_fused(AttendArgs a, unsigned* __restrict__ sync,
@@ -301,7 +318,7 @@ __global__ __launch_bounds__(kAT) void attend_fused(AttendArgs a, unsigned* __re
   __syncthreads();
   if (!is_last) return;
   if (tid == 0) st_dev(&sync[g], 0u);
-  merge_head(a.state, a.S, g * kHq + (tid >> 6), (tid & 63) * 2, out);
+  merge_group(a.state, a.S, g, out, lds);
 }
 
 __global__ __launch_bounds__(kAT) void attend_split_only(AttendArgs a) {
@@ -309,10 +326,11 @@ __global__ __launch_bounds__(kAT) void attend_split_only(AttendArgs a) {
   attend_split(a, blockIdx.y, blockIdx.x, lds);
 }
 
-// Compat merge: grid (8*4) x 64, one head row per workgroup.
-__global__ __launch_bounds__(64) void attend_merge(const float* __restrict__ state, uint16_t* __restrict__ out,
-                                                   int S) {
-  merge_head(state, S, blockIdx.x, threadIdx.x * 2, out);
+// Compat merge: one workgroup per group.
+__global__ __launch_bounds__(kAT) void attend_merge(const float* __restrict__ state, uint16_t* __restrict__ out,
+                                                    int S) {
+  __shared__ AttendLds lds;
+  merge_group(state, S, blockIdx.x, out, lds);
 }
 
 }  // namespace
@@ -354,7 +372,7 @@ int attention_tuned(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t c
                reinterpret_cast<const uint16_t*>(v), reinterpret_cast<const int32_t*>(ids),
                reinterpret_cast<const int32_t*>(cnt), KS, VS, H, H, T, S, reinterpret_cast<float*>(state)};
   hipLaunchKernelGGL(attend_split_only, dim3(S, 8), dim3(kAT), 0, (hipStream_t)stream, a);
-  hipLaunchKernelGGL(attend_merge, dim3(8 * kHq), dim3(64), 0, (hipStream_t)stream,
+  hipLaunchKernelGGL(attend_merge, dim3(8), dim3(kAT), 0, (hipStream_t)stream,
                      reinterpret_cast<const float*>(state), reinterpret_cast<uint16_t*>(out), S);
   return (int)hipGetLastError();
 }

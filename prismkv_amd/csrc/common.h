@@ -41,6 +41,16 @@ __device__ __forceinline__ uint4 load_nt16(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Per-lane select by a wave lane mask: lane i gets `if_set` when bit i of
+// `lanes` is set, else `if_clear` (one v_cndmask).  Written out so that the
+// compiler cannot fold `c ? x[a] : x[b]` over a register array into a
+// dynamically indexed array, which it lowers to long compare/select chains.
+__device__ __forceinline__ float lane_select(unsigned long long lanes, float if_set, float if_clear) {
+  float r;
+  asm("v_cndmask_b32_e64 %0, %1, %2, %3" : "=v"(r) : "v"(if_clear), "v"(if_set), "s"(lanes));
+  return r;
+}
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));

@@ -5,25 +5,29 @@
 // Semantics: src/prismkv/core.py:106-130 (router="moments"),
 //            kernels/ppu_8b/route_parallel.cu:12-32 (tie rule, padding, raw).
 //
-// Design (one launch per layer, no vendor GEMM):
+// Design (two launches per layer, no vendor GEMM):
 //   * Moment tables live in HBM as 32-bucket tiles [g][chunk][k][32] (k < 128:
-//     mean, k >= 128: variance; 128-byte tile rows).  Workgroup (chunk, g)
-//     streams its 32 KB tile with eight independent 16-byte loads per thread
-//     (thread = 4 buckets x 8 k-rows), so a launch keeps ~750 workgroups and
-//     all of their loads in flight.  The per-thread products for 2 parts x 4
-//     heads x 4 buckets are reduced across the 8 k-row lanes of a wave with a
-//     transpose-reduce (28 shuffles) and across the 4 waves in LDS, in a fixed
-//     order, so results are run-to-run identical.
+//     mean, k >= 128: variance; 128-byte tile rows).  Scoring workgroup
+//     (chunk, g) streams its 32 KB tile with eight independent 16-byte loads
+//     per thread (thread = 4 buckets x 8 k-rows), so ~750 workgroups keep the
+//     whole 24.6 MB table in flight at once.  The per-thread products for
+//     2 parts x 4 heads x 4 buckets are reduced across the 8 k-row lanes of a
+//     wave with a transpose-reduce (28 shuffles) and across the 4 waves in
+//     LDS, in a fixed order, so results are run-to-run identical.
 //   * Logit = (log(count) + mean_term / sqrt(d)) + var_term / (2d): the
-//     accumulation order of core.py:122-127.  Each workgroup stores its 4x32
-//     logits and per-head (max, sum-exp) chunk statistics.
-//   * The last workgroup of the group (device-scope counter) merges the 94
-//     chunk statistics, forms the head-averaged probabilities and selects the
-//     Top-16 with an LDS radix select on 44-bit keys (probability bits << 12 |
-//     4095 - bucket): value descending, bucket id ascending on ties, the
-//     reference order.  It restores the counter to zero, so the launch is
-//     replayable from a graph without memset nodes.  Logits and statistics
-//     cross workgroups through write-through stores, not fences.
+//     accumulation order of core.py:122-127.  Each scoring workgroup stores
+//     its 4x32 logits and per-head (max, sum-exp) chunk statistics with
+//     plain stores and exits: the kernel boundary is the only inter-workgroup
+//     synchronisation (a per-group arrival counter would serialise 94
+//     device-scope atomics on one address).
+//   * The select kernel (one workgroup per group) merges the 94 chunk
+//     statistics, forms the head-summed probabilities exp(l - M) / Z -- equal
+//     logits give bit-equal probabilities, so exact ties fall to the lower
+//     bucket id as in the reference -- and picks the Top-16 on 44-bit keys
+//     (probability bits << 12 | 4095 - bucket): value descending, bucket id
+//     ascending on ties.  The select ranks per-thread maxima with LDS
+//     broadcast reads to find a threshold, then ranks the few keys above it
+//     (no histogram atomics, no sorting network).
 #include "common.h"
 
 namespace prismkv {
@@ -31,16 +35,14 @@ namespace {
 
 constexpr int kRT = 256;                      // route workgroup size
 constexpr int kKeys = (kFP + kRT - 1) / kRT;  // 12 candidate keys per thread
-constexpr int kDigit = 11;                    // radix digit width of the Top-16 select
-constexpr int kBins = 1 << kDigit;
-constexpr int kKeyBits = 44;                  // 32 probability bits + 12 id bits
 constexpr float kSqrtD = 11.3137084989847604f;  // fp32(sqrt(128)), core.py:125
 
 struct SelectLds {
-  unsigned hist[kBins];
-  unsigned wsum[kRT / 64];
-  unsigned long long sel[kTop];
-  int nsel, live, digit, rem, stop;
+  unsigned long long tm[kRT];    // per-thread maxima
+  unsigned long long cand[kRT];  // keys >= tau
+  unsigned long long sel[kTop];  // the winners, rank order
+  unsigned long long tau;
+  int ncand;
 };
 
 __device__ __forceinline__ uint64_t make_key(float prob, int bucket) {
@@ -48,98 +50,70 @@ __device__ __forceinline__ uint64_t make_key(float prob, int bucket) {
 }
 __device__ __forceinline__ int key_bucket(uint64_t k) { return 4095 - (int)(k & 4095u); }
 
-// Selects the min(kTop, live) largest nonzero keys (unique by construction)
-// into lds.sel, unordered; returns that count.  MSB-first radix select with
-// 11-bit digits and an early stop once the boundary digit holds exactly the
-// remaining number of keys.
+// Top-16 of the nonzero keys of the workgroup (unique by construction), in
+// rank order, into lds.sel; returns how many (min(16, live)).  No histogram
+// and no sorting network: tau = the 16th largest per-thread maximum, found by
+// ranking the 256 maxima against each other with LDS broadcast reads; at
+// least 16 keys are >= tau and at most 16 threads hold such keys (15 when
+// fewer than 16 threads hold a live key and tau falls back to 1), so the
+// <= 192 candidates >= tau are ranked exactly the same way.
 __device__ int select_top(const uint64_t (&key)[kKeys], SelectLds& lds) {
   const int tid = threadIdx.x;
-  int nl = 0;
+  unsigned long long lm = 0;
 #pragma unroll
-  for (int i = 0; i < kKeys; ++i) nl += key[i] != 0;
-  nl = wave_sum_i(nl);
-  if ((tid & 63) == 0) lds.wsum[tid >> 6] = (unsigned)nl;
-  if (tid == 0) lds.nsel = 0;
-  __syncthreads();
-  int live = 0;
-#pragma unroll
-  for (int w = 0; w < kRT / 64; ++w) live += (int)lds.wsum[w];
-  const int need = live < kTop ? live : kTop;
-  uint64_t thr = 1;  // select every nonzero key >= thr
-  if (live > need) {
-    uint64_t prefix = 0;
-    unsigned rem = (unsigned)need;
-    for (int shift = kKeyBits - kDigit; shift >= 0; shift -= kDigit) {
-      __syncthreads();  // wsum / previous round's reads are complete
-#pragma unroll
-      for (int i = 0; i < kBins / kRT; ++i) lds.hist[tid + i * kRT] = 0;
-      __syncthreads();
-#pragma unroll
-      for (int i = 0; i < kKeys; ++i) {
-        const uint64_t k = key[i];
-        if (k != 0 && (k >> (shift + kDigit)) == prefix) atomicAdd(&lds.hist[(unsigned)(k >> shift) & (kBins - 1)], 1u);
-      }
-      __syncthreads();
-      // thread t owns digits 2047-8t .. 2040-8t (descending)
-      constexpr int kPer = kBins / kRT;
-      unsigned c[kPer], tot = 0;
-#pragma unroll
-      for (int u = 0; u < kPer; ++u) {
-        c[u] = lds.hist[kBins - 1 - (tid * kPer + u)];
-        tot += c[u];
-      }
-      const unsigned incl = block_incl_scan<kRT>(tot, lds.wsum);
-      unsigned run = incl - tot;
-#pragma unroll
-      for (int u = 0; u < kPer; ++u) {
-        if (run < rem && run + c[u] >= rem) {
-          lds.digit = kBins - 1 - (tid * kPer + u);
-          lds.rem = (int)(rem - run);
-          lds.stop = (c[u] == rem - run);
-        }
-        run += c[u];
-      }
-      __syncthreads();
-      prefix = (prefix << kDigit) | (uint64_t)lds.digit;
-      rem = (unsigned)lds.rem;
-      if (lds.stop || shift == 0) {
-        thr = prefix << shift;
-        break;
-      }
-    }
-  }
-#pragma unroll
-  for (int i = 0; i < kKeys; ++i) {
-    const uint64_t k = key[i];
-    if (k != 0 && k >= thr) {
-      const int s = atomicAdd(&lds.nsel, 1);
-      if (s < kTop) lds.sel[s] = k;
-    }
+  for (int i = 0; i < kKeys; ++i) lm = key[i] > lm ? key[i] : lm;
+  lds.tm[tid] = lm;
+  if (tid == 0) {
+    lds.tau = 1;  // dead keys (0) never qualify
+    lds.ncand = 0;
   }
   __syncthreads();
-  return need;
+  int r = 0;
+  const ulonglong2* tm2 = reinterpret_cast<const ulonglong2*>(lds.tm);
+#pragma unroll 8
+  for (int j = 0; j < kRT / 2; ++j) {
+    const ulonglong2 o = tm2[j];
+    r += (o.x > lm) + (o.y > lm);
+  }
+  if (r == kTop - 1 && lm > 0) lds.tau = lm;  // unique: nonzero maxima are distinct
+  __syncthreads();
+  const unsigned long long tau = lds.tau;
+  int mine = 0;
+#pragma unroll
+  for (int i = 0; i < kKeys; ++i) mine += key[i] >= tau;
+  if (mine) {
+    int at = atomicAdd(&lds.ncand, mine);
+#pragma unroll
+    for (int i = 0; i < kKeys; ++i)
+      if (key[i] >= tau && at < kRT) lds.cand[at++] = key[i];
+  }
+  __syncthreads();
+  const int nc = lds.ncand < kRT ? lds.ncand : kRT;
+  if (tid < nc) {
+    const unsigned long long k = lds.cand[tid];
+    int rk = 0;
+    for (int j = 0; j < nc; ++j) rk += lds.cand[j] > k;
+    if (rk < kTop) lds.sel[rk] = k;
+  }
+  __syncthreads();
+  return nc < kTop ? nc : kTop;
 }
 
-// Writes the selected keys in rank order: features[r] = bucket, valid[r] = 1
-// for r < need; remaining slots id 0 / valid 0 (route_parallel.cu:23,29);
+// Writes the winners (lds.sel, rank order): features[r] = bucket, valid[r] =
+// 1 for r < need; remaining slots id 0 / valid 0 (route_parallel.cu:23,29);
 // raw = sum of winner counts.
 template <typename CountT>
 __device__ void write_selection(const SelectLds& lds, int need, const CountT* counts, int64_t* features,
                                 float* valid, int* raw) {
   const int tid = threadIdx.x;
-  if (tid < need) {
-    const unsigned long long k = lds.sel[tid];
-    int r = 0;
-    for (int j = 0; j < need; ++j) r += lds.sel[j] > k;
-    features[r] = (int64_t)key_bucket(k);
-    valid[r] = 1.0f;
-  } else if (tid < kTop) {
-    features[tid] = 0;
-    valid[tid] = 0.0f;
-  }
   if (tid < 64) {
-    int n = tid < need ? (int)counts[key_bucket(lds.sel[tid])] : 0;
-    n = wave_sum_i(n);
+    const bool hit = tid < need;
+    const int b = hit ? key_bucket(lds.sel[tid]) : 0;
+    if (tid < kTop) {
+      features[tid] = b;
+      valid[tid] = hit ? 1.0f : 0.0f;
+    }
+    const int n = wave_sum_i(hit ? (int)counts[b] : 0);
     if (tid == 0) *raw = n;
   }
 }
@@ -149,37 +123,31 @@ __device__ void write_selection(const SelectLds& lds, int need, const CountT* co
 // copy of the kept half.  After the step x[0..n) holds the new partial sums.
 template <int N>
 __device__ __forceinline__ void treduce(float* x, int mask) {
-  const bool hi = (threadIdx.x & mask) != 0;
+  const unsigned long long hi = __ballot((threadIdx.x & mask) != 0);
 #pragma unroll
   for (int j = 0; j < N; ++j) {
-    const float keep = hi ? x[j + N] : x[j];
-    const float send = hi ? x[j] : x[j + N];
+    const float keep = lane_select(hi, x[j + N], x[j]);
+    const float send = lane_select(hi, x[j], x[j + N]);
     x[j] = keep + __shfl_xor(send, mask);
   }
 }
 
 // ---------------------------------------------------------------------------
-// Fused route: grid (kChunks, G) x 256.
+// Route, pass 1 (moment scoring): grid (kChunks, G) x 256.
 // ---------------------------------------------------------------------------
 struct RouteWork {
-  float* logits;    // [G][4][kFP]
-  float* stats;     // [G][kChunks][4][2] (max, sum of exp)
-  unsigned* sync;   // [G] arrival counters, zero between launches
+  float* logits;  // [G][4][kFP]
+  float* stats;   // [G][kChunks][4][2] (chunk max, chunk sum of exp)
 };
 
-__global__ __launch_bounds__(kRT) void route_kernel(const uint16_t* __restrict__ q,
-                                                    const float* __restrict__ moments,
-                                                    const int* __restrict__ counts, RouteWork work,
-                                                    int64_t* __restrict__ features, float* __restrict__ valid,
-                                                    int* __restrict__ raw) {
+__global__ __launch_bounds__(kRT) void route_score_kernel(const uint16_t* __restrict__ q,
+                                                          const float* __restrict__ moments,
+                                                          const int* __restrict__ counts, RouteWork work) {
   const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
   const int w = tid >> 6, lane = tid & 63;
   __shared__ float4 qq[kRow];                 // [k] -> 4 heads; k < 128: q, k >= 128: q*q
   __shared__ float4 red[kRT / 64][64];        // cross-wave partials
   __shared__ float dots[2][kHq][kChunk];      // [part][head][bucket]
-  __shared__ int is_last;
-  __shared__ float gmax[kHq], grz[kHq];
-  __shared__ SelectLds lds;
 
   // 16-byte tile loads first: thread = bucket quad (tid & 7) x k-row phase (tid >> 3)
   const int quad = tid & 7, r = tid >> 3;
@@ -239,28 +207,41 @@ __global__ __launch_bounds__(kRT) void route_kernel(const uint16_t* __restrict__
       const float lc = logf((float)n);
       l = (lc + dots[0][h][b] / kSqrtD) + dots[1][h][b] / (2.0f * kD);
     }
-    st_dev(&work.logits[((size_t)g * kHq + h) * kFP + bucket], l);
+    work.logits[((size_t)g * kHq + h) * kFP + bucket] = l;
     float m = l;
 #pragma unroll
     for (int o = 16; o; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
     float e = (l == -INFINITY) ? 0.f : expf(l - m);
 #pragma unroll
     for (int o = 16; o; o >>= 1) e += __shfl_xor(e, o);
-    if (b == 0) st_dev2(&work.stats[(((size_t)g * kChunks + c) * kHq + h) * 2], m, e);
+    if (b == 0) *reinterpret_cast<float2*>(&work.stats[(((size_t)g * kChunks + c) * kHq + h) * 2]) = make_float2(m, e);
   }
-  drain();
-  __syncthreads();
-  if (tid == 0) is_last = inc_dev(&work.sync[g]) == (unsigned)(kChunks - 1);
-  __syncthreads();
-  if (!is_last) return;
-  if (tid == 0) st_dev(&work.sync[g], 0u);
+}
 
+// ---------------------------------------------------------------------------
+// Route, pass 2 (normalise, aggregate, Top-16): grid G x 256.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kRT) void route_select_kernel(RouteWork work, const int* __restrict__ counts,
+                                                           int64_t* __restrict__ features,
+                                                           float* __restrict__ valid, int* __restrict__ raw) {
+  const int g = blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  __shared__ float gmax[kHq], grz[kHq];
+  __shared__ SelectLds lds;
+  // every load of the workgroup is issued before any is used
+  const float* lg = work.logits + (size_t)g * kHq * kFP;
+  float lv[kKeys][kHq];
+#pragma unroll
+  for (int i = 0; i < kKeys; ++i) {
+    const int b = min(tid + i * kRT, kFP - 1);
+#pragma unroll
+    for (int h = 0; h < kHq; ++h) lv[i][h] = lg[h * kFP + b];
+  }
   {
     // merge chunk statistics: wave h handles head h, lanes cover the 94 chunks
     const int h = w;
-    const float* st = work.stats + ((size_t)g * kChunks * kHq + h) * 2;
-    const float2 s0 = lane < kChunks ? ld_dev2(st + lane * kHq * 2) : make_float2(-INFINITY, 0.f);
-    const float2 s1 = lane + 64 < kChunks ? ld_dev2(st + (lane + 64) * kHq * 2) : make_float2(-INFINITY, 0.f);
+    const float2* st = reinterpret_cast<const float2*>(work.stats) + (size_t)g * kChunks * kHq + h;
+    const float2 s0 = lane < kChunks ? st[lane * kHq] : make_float2(-INFINITY, 0.f);
+    const float2 s1 = lane + 64 < kChunks ? st[(lane + 64) * kHq] : make_float2(-INFINITY, 0.f);
     const float m = wave_max(fmaxf(s0.x, s1.x));
     float z = (s0.x == -INFINITY ? 0.f : s0.y * expf(s0.x - m)) + (s1.x == -INFINITY ? 0.f : s1.y * expf(s1.x - m));
     z = wave_sum(z);
@@ -270,24 +251,18 @@ __global__ __launch_bounds__(kRT) void route_kernel(const uint16_t* __restrict__
     }
   }
   __syncthreads();
-
   uint64_t key[kKeys];
-  const float* lg = work.logits + (size_t)g * kHq * kFP;
 #pragma unroll
   for (int i = 0; i < kKeys; ++i) {
     const int b = tid + i * kRT;
     key[i] = 0;
-    if (b < kFP) {
-      const float l0 = ld_dev(lg + b), l1 = ld_dev(lg + kFP + b), l2 = ld_dev(lg + 2 * kFP + b),
-                  l3 = ld_dev(lg + 3 * kFP + b);
-      if (l0 != -INFINITY) {
-        // per-head softmax, then the sum over heads in head order (core.py:128)
-        const float p0 = expf(l0 - gmax[0]) * grz[0];
-        const float p1 = expf(l1 - gmax[1]) * grz[1];
-        const float p2 = expf(l2 - gmax[2]) * grz[2];
-        const float p3 = expf(l3 - gmax[3]) * grz[3];
-        key[i] = make_key(((p0 + p1) + p2) + p3, b);
-      }
+    if (b < kFP && lv[i][0] != -INFINITY) {
+      // per-head softmax exp(l - M) / Z, then the sum over heads in head order (core.py:128)
+      const float p0 = expf(lv[i][0] - gmax[0]) * grz[0];
+      const float p1 = expf(lv[i][1] - gmax[1]) * grz[1];
+      const float p2 = expf(lv[i][2] - gmax[2]) * grz[2];
+      const float p3 = expf(lv[i][3] - gmax[3]) * grz[3];
+      key[i] = make_key(((p0 + p1) + p2) + p3, b);
     }
   }
   const int need = select_top(key, lds);
@@ -373,14 +348,13 @@ __global__ void pack_kernel(const uint16_t* __restrict__ q, float* __restrict__ 
 using namespace prismkv;
 
 static size_t route_logits_bytes(int groups) { return (size_t)groups * kHq * kFP * sizeof(float); }
-static size_t route_stats_bytes(int groups) { return (size_t)groups * kChunks * kHq * sizeof(float2); }
+static size_t route_stats_bytes(int groups) { return (size_t)groups * kChunks * kHq * 2 * sizeof(float); }
 
 extern "C" {
 
 size_t prismkv_route_work_bytes(int groups) {
   if (groups < 1) return 0;
-  const size_t sync = (size_t)groups * sizeof(unsigned);
-  return route_logits_bytes(groups) + route_stats_bytes(groups) + ((sync + 255) & ~(size_t)255);
+  return route_logits_bytes(groups) + route_stats_bytes(groups);
 }
 
 int prismkv_route(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features, uint64_t valid,
@@ -388,12 +362,13 @@ int prismkv_route(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, 
   if (groups < 1 || groups > 65535) return kBadSize;
   if (!q || !moments || !counts || !work || !features || !valid || !raw) return kBadSize;
   char* base = reinterpret_cast<char*>(work);
-  RouteWork rw{reinterpret_cast<float*>(base), reinterpret_cast<float*>(base + route_logits_bytes(groups)),
-               reinterpret_cast<unsigned*>(base + route_logits_bytes(groups) + route_stats_bytes(groups))};
-  hipLaunchKernelGGL(route_kernel, dim3(kChunks, groups), dim3(kRT), 0, (hipStream_t)stream,
-                     reinterpret_cast<const uint16_t*>(q), reinterpret_cast<const float*>(moments),
-                     reinterpret_cast<const int*>(counts), rw, reinterpret_cast<int64_t*>(features),
-                     reinterpret_cast<float*>(valid), reinterpret_cast<int*>(raw));
+  RouteWork rw{reinterpret_cast<float*>(base), reinterpret_cast<float*>(base + route_logits_bytes(groups))};
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(route_score_kernel, dim3(kChunks, groups), dim3(kRT), 0, s, reinterpret_cast<const uint16_t*>(q),
+                     reinterpret_cast<const float*>(moments), reinterpret_cast<const int*>(counts), rw);
+  hipLaunchKernelGGL(route_select_kernel, dim3(groups), dim3(kRT), 0, s, rw, reinterpret_cast<const int*>(counts),
+                     reinterpret_cast<int64_t*>(features), reinterpret_cast<float*>(valid),
+                     reinterpret_cast<int*>(raw));
   return (int)hipGetLastError();
 }
 

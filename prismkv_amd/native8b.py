@@ -31,6 +31,9 @@ from . import _lib
 from .build import compile_hip  # noqa: F401  (re-exported: reference name compile_ppu)
 
 GROUPS, HEADS, DIM, FEATURES, TOPK = 8, 4, 128, 3000, 16
+# Workgroups per KV group of the sparse-attention launch (each 8 waves; one
+# per CU at 8 groups x 32 = 256): the partition the kernel is tuned for.
+ATTEND_SPLITS = 32
 CHUNK = 32
 CHUNKS = (FEATURES + CHUNK - 1) // CHUNK
 PADDED = CHUNKS * CHUNK
@@ -145,8 +148,8 @@ class Native8B:
                                       device=device)
         self.union_work = torch.zeros(self.lib.query("prismkv_union_work_bytes", GROUPS, self.capacity),
                                       dtype=torch.uint8, device=device)
-        self.state = torch.zeros(self.lib.query("prismkv_attend_work_bytes", GROUPS, 128), dtype=torch.uint8,
-                                 device=device)
+        self.state = torch.zeros(self.lib.query("prismkv_attend_work_bytes", GROUPS, ATTEND_SPLITS),
+                                 dtype=torch.uint8, device=device)
         self.out = torch.zeros(GROUPS, HEADS, DIM, dtype=torch.bfloat16, device=device)
 
     def _stream(self):
@@ -166,8 +169,10 @@ class Native8B:
                       self.row_words, self.capacity, stream=s)
 
     def attention(self, q, k, v, *, splits=64, schedule=0):
-        """Stage 3.  `schedule` (0, 1, 2) is accepted for compatibility; every
-        schedule uses contiguous per-split row ranges and gives the same result."""
+        """Stage 3.  `splits` (1..128) and `schedule` (0, 1, 2) are validated and
+        accepted for compatibility; the softmax is exact, so the partition does
+        not change the result, and the kernel always uses ATTEND_SPLITS
+        workgroups per group with rows dealt evenly to their waves."""
         if not 1 <= splits <= 128 or schedule not in (0, 1, 2):
             raise ValueError("unsupported attention partition/schedule")
         if k.shape != v.shape or k.shape[0] != GROUPS or k.shape[-1] != DIM or k.shape[1] < self.history:
@@ -184,7 +189,7 @@ class Native8B:
             raise ValueError("Q/K/V rows must be 16-byte aligned")
         self.lib.call("prismkv_attend", q.data_ptr(), k.data_ptr(), v.data_ptr(), self.ids.data_ptr(),
                       self.count.data_ptr(), self.state.data_ptr(), self.out.data_ptr(), GROUPS, self.history,
-                      k.shape[1] - self.history, k.stride(0), v.stride(0), self.capacity, splits,
+                      k.shape[1] - self.history, k.stride(0), v.stride(0), self.capacity, ATTEND_SPLITS,
                       stream=self._stream())
         return self.out
 
