@@ -9,13 +9,15 @@ Inputs are generated on the device (synthetic, seeded) and stay resident in
 HBM; 36 distinct layers (~17.7 GB) rotate so nothing is served from the
 256 MB Infinity Cache.
 
-A "step" is one decode step through all layers: for every layer route
-(moment scoring + Top-16), union (bitmap OR + compaction) and sparse AV,
-captured once in a HIP graph and replayed.  The headline value is the replay
-time per layer in microseconds (lower is better).  Per-stage times come from
-isolated-stage graphs (one launch per layer), and the roofline object reports
-the dominant kernel's algorithmic bytes per launch over its average launch
-time.  The CPU baseline times the C oracle (single thread) on a bounded
+A "step" is one decode step through all layers: for every layer the
+Native8B call (route: moment scoring + Top-16, union: bitmap OR + compaction,
+sparse AV) -- two launches per layer, moment scoring and the fused
+selection/union/attention kernel -- captured once in a HIP graph and
+replayed.  The headline value is the replay time per layer in microseconds
+(lower is better).  Per-stage times come from isolated-stage graphs (one
+launch per layer); the separate route/union/attend entry points are timed
+too.  The roofline object reports the dominant kernel's algorithmic bytes per
+launch over its average launch time.  The CPU baseline times the C oracle (single thread) on a bounded
 sample of the same layer workload.
 """
 from __future__ import annotations
@@ -43,11 +45,10 @@ def parse():
     p.add_argument("--layers", type=int, default=36)
     p.add_argument("--history", type=int, default=65536)
     p.add_argument("--tail", type=int, default=256)
-    p.add_argument("--splits", type=int, default=64)
     p.add_argument("--seed", type=int, default=2)
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--stages", default="chain,route,union,attend,copy",
+    p.add_argument("--stages", default="chain,decode,route,union,attend,copy",
                    help="comma list of timed regions (for profiling runs)")
     return p.parse_args()
 
@@ -184,26 +185,39 @@ def main():
     torch.cuda.synchronize()
     log(f"built in {time.perf_counter() - t0:.1f}s; mem {torch.cuda.memory_allocated() / 2**30:.1f} GiB")
 
-    def chain():
+    def stream():
+        return torch.cuda.current_stream().cuda_stream
+
+    def chain():  # the decode step: Native8B.__call__ = route + attention (fused path, 2 launches per layer)
         for op, q, k, v in layers:
-            op.route(q)
-            op.attention(q, k, v, splits=a.splits)
+            op(q, k, v)
+
+    def score_only():
+        for op, q, k, v in layers:
+            op.lib.call("prismkv_decode_score", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(),
+                        op.decode_work.data_ptr(), G, op.capacity, stream=stream())
+
+    def decode_attend_only():
+        for op, q, k, v in layers:
+            op.lib.call("prismkv_decode_attend", q.data_ptr(), op.n.data_ptr(), op.bits.data_ptr(), k.data_ptr(),
+                        v.data_ptr(), op.decode_work.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(),
+                        op.raw.data_ptr(), op.ids.data_ptr(), op.count.data_ptr(), op.out.data_ptr(), G, op.history,
+                        k.shape[1] - op.history, op.capacity, op.row_words, k.stride(0), v.stride(0), op.capacity,
+                        stream=stream())
 
     def route_only():
         for op, q, k, v in layers:
-            op.lib.call("prismkv_route", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(),
-                        op.route_work.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(), op.raw.data_ptr(),
-                        G, stream=torch.cuda.current_stream().cuda_stream)
+            op.route(q)
 
     def union_only():
         for op, q, k, v in layers:
             op.lib.call("prismkv_union", op.bits.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(),
                         op.union_work.data_ptr(), op.ids.data_ptr(), op.count.data_ptr(), G, op.history,
-                        op.row_words, op.capacity, stream=torch.cuda.current_stream().cuda_stream)
+                        op.row_words, op.capacity, stream=stream())
 
     def attend_only():
         for op, q, k, v in layers:
-            op.attention(q, k, v, splits=a.splits)
+            op.attention(q, k, v)
 
     result = {}
     chain()  # populate ids/count for the byte model and the stage graphs
@@ -211,13 +225,19 @@ def main():
     ms, wall, _ = graph_time(chain, a.steps, a.warmup) if "chain" in stages else (float("nan"),) * 3
     log(f"chain: {ms:.4f} ms/step events, {wall:.4f} ms/step wall")
     per_stage = {}
-    for name, fn in (("route", route_only), ("union", union_only), ("attend", attend_only)):
-        if name in stages:
+    stage_fns = (("score", score_only), ("select_union_attend", decode_attend_only), ("route", route_only),
+                 ("union", union_only), ("attend", attend_only))
+    for name, fn in stage_fns:
+        if name in stages or (name in ("score", "select_union_attend") and "decode" in stages):
             sm, _, _ = graph_time(fn, a.steps, a.warmup)
             per_stage[name] = sm * 1e3 / a.layers
             log(f"{name}: {per_stage[name]:.2f} us/launch")
+    chain()
+    torch.cuda.synchronize()
     b_route, b_union, b_av, uniq = stage_bytes([l[0] for l in layers], H, T)
-    nbytes = {"route": b_route, "union": b_union, "attend": b_av}
+    b_select = G * (HQ * 3008 * 4 + 94 * HQ * 8)  # logits + chunk statistics read back by the selection
+    nbytes = {"score": b_route, "select_union_attend": b_select + b_union + b_av, "route": b_route,
+              "union": b_union, "attend": b_av}
     stage_report = {}
     for name, us in per_stage.items():
         gbs = nbytes[name] / (us * 1e-6) / 1e9
@@ -239,7 +259,8 @@ def main():
         copy_gbs = 2 * 2 ** 30 * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9
         log(f"copy probe: {copy_gbs:.0f} GB/s (read+write)")
         del src, dst
-    dominant = max(stage_report, key=lambda n: stage_report[n]["us_per_launch"]) if stage_report else None
+    fused = [n for n in ("score", "select_union_attend") if n in stage_report]
+    dominant = max(fused or stage_report, key=lambda n: stage_report[n]["us_per_launch"]) if stage_report else None
     roofline = None
     if dominant:
         d = stage_report[dominant]
@@ -259,7 +280,7 @@ def main():
         "vs_baseline": round(value / PPU_US_PER_LAYER_64K, 4), "dtype": "fp32", "data": "synthetic",
         "config": {"workload": f"8B-geometry routed decode, {a.layers} layers x 8 KV groups x 4 Q heads, d=128, "
                                f"F=3000, Top-16, H={H} + {T} tail, bf16 KV, per-key top-8 SAE membership",
-                   "layers": a.layers, "groups": G, "history": H, "tail": T, "splits": a.splits,
+                   "layers": a.layers, "groups": G, "history": H, "tail": T,
                    "kv_dtype": "bf16", "mean_unique_ids_per_group": round(uniq, 1), "parallelism": "single GPU"},
         "wall_ms_per_step": round(wall, 4), "stages": stage_report, "copy_probe_GBps": copy_gbs and round(copy_gbs, 1),
         "roofline": roofline, "cpu_baseline": cpu,

@@ -30,6 +30,10 @@ SIGNATURES = {
     "prismkv_build_bits": ([_U64] * 3 + [_I32, _I64, _I64], True, _I32),
     "prismkv_attend_work_bytes": ([_I32, _I32], False, _SZ),
     "prismkv_attend": ([_U64] * 7 + [_I32, _I32, _I32, _I64, _I64, _I64, _I32], True, _I32),
+    "prismkv_decode_work_bytes": ([_I32, _I32], False, _SZ),
+    "prismkv_decode": ([_U64] * 13 + [_I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64], True, _I32),
+    "prismkv_decode_score": ([_U64] * 4 + [_I32, _I32], True, _I32),
+    "prismkv_decode_attend": ([_U64] * 12 + [_I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64], True, _I32),
 }
 
 _loaded: dict[str, "Library"] = {}

@@ -21,7 +21,7 @@ from pathlib import Path
 PACKAGE = Path(__file__).resolve().parent
 CSRC = PACKAGE / "csrc"
 INCLUDE = PACKAGE.parent / "include"
-SOURCES = ["route.hip", "union.hip", "attend.hip", "update.hip"]
+SOURCES = ["route.hip", "union.hip", "attend.hip", "decode.hip", "update.hip"]
 LIBRARY_NAME = "libprismkv_hip.so"
 ARCH = "gfx950"
 

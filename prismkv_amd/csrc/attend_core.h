@@ -1,0 +1,208 @@
+// Sparse-attention core shared by the attend and decode kernels: the
+// per-slot online softmax step, the workgroup state merge and the split merge.
+#pragma once
+
+#include "common.h"
+
+namespace prismkv {
+namespace {
+
+constexpr int kAT = 512;                           // 8 waves
+constexpr int kStateW = kD + 2;                    // {max, den, acc[128]}
+constexpr float kLog2eScale = 0.12751743082459868f;  // log2(e) / sqrt(128): scores in the exp2 domain
+constexpr float kSlack = 8.0f;                     // lazy-rescale threshold (log2 units)
+constexpr int kStepRows = 16;                      // rows per wave step (4 slots x 4 rows)
+
+struct AttendArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const int32_t* ids;
+  const int32_t* cnt;
+  int64_t ks, vs, ids_stride;
+  int H, T, S;
+  float* state;
+};
+
+__device__ __forceinline__ void unpack8(const uint4 r, float (&f)[8]) {
+  f[0] = bf16_lo(r.x); f[1] = bf16_hi(r.x);
+  f[2] = bf16_lo(r.y); f[3] = bf16_hi(r.y);
+  f[4] = bf16_lo(r.z); f[5] = bf16_hi(r.z);
+  f[6] = bf16_lo(r.w); f[7] = bf16_hi(r.w);
+}
+
+__device__ __forceinline__ float exp2_or_zero(float x) { return x == -INFINITY ? 0.f : exp2f(x); }
+
+constexpr int kSlotRows = 9;                 // rows per slot per round
+constexpr int kWaveRows = 4 * kSlotRows;     // rows per wave per round
+
+constexpr int kSlots = kAT / 16;             // 32 slots of 16 lanes
+
+// LDS of one workgroup: the slot merge, then the split weights of the final merge.
+struct AttendLds {
+  union {
+    struct {
+      float sm[kSlots][kHq], sz[kSlots][kHq];
+      float sacc[kSlots][kHq][kD];
+    } red;
+    float wts[kAT / 64][64];               // split weights of the final merge
+  };
+};
+
+// Per-lane running state of one slot: head-h scores live in lanes with
+// (lane & 3) == h; acc holds all 4 heads x this lane's 8 dims.
+struct SlotState {
+  float m, z;            // running max / denominator of head (lane & 3)
+  float acc[kHq][8];
+};
+
+// One step: 4 rows per slot (row b of slot = rows[b]); kr/vr hold the loaded
+// lines; ok[b] marks real rows.
+__device__ __forceinline__ void attend_step(const float (&qf)[kHq][8], const uint4 (&kr)[4], const uint4 (&vr)[4],
+                                            int nvalid, SlotState& s) {
+  const int lane = threadIdx.x & 63, q16 = lane & 15, slot0 = lane & 48;
+  float x[16];
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    float kf[8];
+    unpack8(kr[b], kf);
+#pragma unroll
+    for (int h = 0; h < kHq; ++h) {
+      float d = 0.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) d = fmaf(qf[h][i], kf[i], d);
+      x[b * 4 + h] = d;
+    }
+  }
+  // transpose-reduce over the 16 lanes of the slot: lane q16 ends with (row q16>>2, head q16&3)
+#pragma unroll
+  for (int stage = 0; stage < 4; ++stage) {
+    const int mask = 8 >> stage, n = 8 >> stage;
+    const unsigned long long hi = __ballot((q16 & mask) != 0);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j < n) {
+        const float keep = lane_select(hi, x[j + n], x[j]);
+        const float send = lane_select(hi, x[j], x[j + n]);
+        const float got = mask == 8 ? xor8(send) : mask == 4 ? xor4(send) : mask == 2 ? xor2(send) : xor1(send);
+        x[j] = keep + got;
+      }
+    }
+  }
+  float sc = ((q16 >> 2) < nvalid) ? x[0] : -INFINITY;
+  // batch max of this head over the 4 rows (lane bits 2, 3)
+  float bm = fmaxf(sc, xor4(sc));
+  bm = fmaxf(bm, xor8(bm));
+  const bool grow = bm > s.m + kSlack || (s.m == -INFINITY && bm != -INFINITY);
+  if (__ballot(grow)) {
+    const float nm = grow ? bm : s.m;
+    const float alpha = grow ? exp2_or_zero(s.m - nm) : 1.0f;
+    s.m = nm;
+    s.z *= alpha;
+#pragma unroll
+    for (int h = 0; h < kHq; ++h) {
+      const float ah = __shfl(alpha, slot0 + h);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) s.acc[h][i] *= ah;
+    }
+  }
+  const float p = sc == -INFINITY ? 0.f : exp2f(sc - s.m);
+  float ps = p + xor4(p);
+  ps += xor8(ps);
+  s.z += ps;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    if (b < nvalid) {
+      float vf[8];
+      unpack8(vr[b], vf);
+#pragma unroll
+      for (int h = 0; h < kHq; ++h) {
+        const float pb = __shfl(p, slot0 + b * 4 + h);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s.acc[h][i] = fmaf(pb, vf[i], s.acc[h][i]);
+      }
+    }
+  }
+}
+
+// Merges the 32 slot states of the workgroup in LDS and stores the result as
+// split state `stp` ((max, den, acc[128]) per head; head h at stp + h * hstride).
+__device__ void store_wg_state(const SlotState& s, AttendLds& lds, float* stp, size_t hstride) {
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, q16 = lane & 15, slot = lane >> 4;
+  __syncthreads();  // LDS shared with the caller's earlier phases is free again
+  // gather the slot's per-head max / denominator into every lane
+  float mm[kHq], zz[kHq];
+#pragma unroll
+  for (int h = 0; h < kHq; ++h) {
+    mm[h] = __shfl(s.m, (lane & 48) + h);
+    zz[h] = __shfl(s.z, (lane & 48) + h);
+  }
+  const int sl = w * 4 + slot;
+  if (q16 == 0) {
+#pragma unroll
+    for (int h = 0; h < kHq; ++h) {
+      lds.red.sm[sl][h] = mm[h];
+      lds.red.sz[sl][h] = zz[h];
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < kHq; ++h) {
+    float4* dst = reinterpret_cast<float4*>(&lds.red.sacc[sl][h][8 * q16]);
+    dst[0] = make_float4(s.acc[h][0], s.acc[h][1], s.acc[h][2], s.acc[h][3]);
+    dst[1] = make_float4(s.acc[h][4], s.acc[h][5], s.acc[h][6], s.acc[h][7]);
+  }
+  __syncthreads();
+  {
+    // thread = (head tid >> 7, dim tid & 127)
+    const int h = tid >> 7, d = tid & (kD - 1);
+    float M = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kSlots; ++k) M = fmaxf(M, lds.red.sm[k][h]);
+    float den = 0.f, v = 0.f;
+#pragma unroll
+    for (int k = 0; k < kSlots; ++k) {
+      const float wgt = lds.red.sm[k][h] == -INFINITY ? 0.f : exp2f(lds.red.sm[k][h] - M);
+      den = fmaf(wgt, lds.red.sz[k][h], den);
+      v = fmaf(wgt, lds.red.sacc[k][h][d], v);
+    }
+    float* sh = stp + (size_t)h * hstride;
+    if (d == 0) st_dev2(sh, M, den);
+    st_dev(sh + 2 + d, v);
+  }
+}
+
+// Merges the S split states of group g into out[g] (thread = head tid >> 7,
+// dim tid & 127).  Splits go in batches of 32: each thread issues its 32
+// accumulator loads and each wave its 32 (max, den) loads before any is
+// used, so S <= 32 costs one memory round trip.
+__device__ void merge_group(const float* state, int S, int g, uint16_t* out, AttendLds& lds) {
+  const int tid = threadIdx.x, h = tid >> 7, d = tid & (kD - 1), w = tid >> 6, lane = tid & 63;
+  const float* st = state + (size_t)(g * kHq + h) * S * kStateW;
+  float M = -INFINITY, den = 0.f, v = 0.f;
+  for (int p0 = 0; p0 < S; p0 += 32) {
+    const int n = min(32, S - p0);
+    const float2 mz = ld_dev2(st + (size_t)(p0 + min(lane & 31, n - 1)) * kStateW);
+    float av[32];
+#pragma unroll
+    for (int i = 0; i < 32; ++i) av[i] = ld_dev(st + (size_t)(p0 + min(i, n - 1)) * kStateW + 2 + d);
+    // online merge across batches: rescale what is accumulated when the max grows
+    const bool mine = lane < n;  // lanes 32..63 duplicate lanes 0..31 and stay out
+    const float bm = wave_max(mine ? mz.x : -INFINITY);
+    const float nM = fmaxf(M, bm);
+    const float scale = (M == -INFINITY) ? 0.f : exp2f(M - nM);
+    den *= scale;
+    v *= scale;
+    M = nM;
+    const float wgt = (mine && mz.x != -INFINITY) ? exp2f(mz.x - M) : 0.f;
+    den += wave_sum(wgt * mz.y);
+    __syncthreads();  // previous batch's weights are consumed
+    lds.wts[w][lane] = wgt;
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v = fmaf(lds.wts[w][i], av[i], v);
+  }
+  out[((size_t)g * kHq + h) * kD + d] = f32_to_bf16(den > 0.f ? v / den : 0.f);
+}
+
+}  // namespace
+}  // namespace prismkv

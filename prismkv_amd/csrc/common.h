@@ -51,16 +51,64 @@ __device__ __forceinline__ float lane_select(unsigned long long lanes, float if_
   return r;
 }
 
+// In-row (16-lane) exchanges through DPP: a few cycles instead of an LDS
+// round trip.  xor 1 / xor 2 are quad permutations, xor 8 is a rotation of
+// the row by 8; xor 4 combines a left and a right row shift by 4.
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float xor1(float v) { return dpp_f<0xB1>(v); }   // quad_perm [1,0,3,2]
+__device__ __forceinline__ float xor2(float v) { return dpp_f<0x4E>(v); }   // quad_perm [2,3,0,1]
+__device__ __forceinline__ float xor8(float v) { return dpp_f<0x128>(v); }  // row_ror:8
+__device__ __forceinline__ float xor4(float v) {
+  const float up = dpp_f<0x104>(v);    // row_shl:4: lane i reads lane i + 4
+  const float down = dpp_f<0x114>(v);  // row_shr:4: lane i reads lane i - 4
+  return (threadIdx.x & 4) ? down : up;
+}
+__device__ __forceinline__ float row_mirror(float v) { return dpp_f<0x140>(v); }       // lane i <- 15 - i
+__device__ __forceinline__ float row_half_mirror(float v) { return dpp_f<0x141>(v); }  // lane i <- 7 - i (in 8)
+
+// Wave reductions: within each 16-lane row by DPP (pairs i^1, i^2, then the
+// mirrors i <-> 7-i and i <-> 15-i), then the 4 row results by readlane.
+// Fixed order, so results are run-to-run identical; the result is uniform.
+__device__ __forceinline__ float row_max(float v) {
+  v = fmaxf(v, xor1(v));
+  v = fmaxf(v, xor2(v));
+  v = fmaxf(v, row_half_mirror(v));
+  return fmaxf(v, row_mirror(v));
+}
+__device__ __forceinline__ float row_sum(float v) {
+  v += xor1(v);
+  v += xor2(v);
+  v += row_half_mirror(v);
+  return v + row_mirror(v);
+}
+__device__ __forceinline__ float lane_bcast(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
+  v = row_max(v);
+  return fmaxf(fmaxf(lane_bcast(v, 0), lane_bcast(v, 16)), fmaxf(lane_bcast(v, 32), lane_bcast(v, 48)));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row_sum(v);
+  return (lane_bcast(v, 0) + lane_bcast(v, 16)) + (lane_bcast(v, 32) + lane_bcast(v, 48));
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
+// Exclusive prefix over the lanes of a wave for small nonnegative counts
+// (v < 2^kBits): one ballot per bit plane and a lane-masked popcount.
+template <int kBits>
+__device__ __forceinline__ int wave_excl_small(int v, int* total) {
+  int pre = 0, tot = 0;
 #pragma unroll
-  for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  for (int b = 0; b < kBits; ++b) {
+    const unsigned long long m = __ballot((v >> b) & 1);
+    pre += (int)__builtin_amdgcn_mbcnt_hi((unsigned)(m >> 32), __builtin_amdgcn_mbcnt_lo((unsigned)m, 0u)) << b;
+    tot += __popcll(m) << b;
+  }
+  *total = tot;
+  return pre;
 }
 
 __device__ __forceinline__ int wave_sum_i(int v) {

@@ -20,15 +20,17 @@
 //     plain stores and exits: the kernel boundary is the only inter-workgroup
 //     synchronisation (a per-group arrival counter would serialise 94
 //     device-scope atomics on one address).
-//   * The select kernel (one workgroup per group) merges the 94 chunk
-//     statistics, forms the head-summed probabilities exp(l - M) / Z -- equal
-//     logits give bit-equal probabilities, so exact ties fall to the lower
-//     bucket id as in the reference -- and picks the Top-16 on 44-bit keys
-//     (probability bits << 12 | 4095 - bucket): value descending, bucket id
-//     ascending on ties.  The select ranks per-thread maxima with LDS
-//     broadcast reads to find a threshold, then ranks the few keys above it
-//     (no histogram atomics, no sorting network).
-#include "common.h"
+//   * The part kernel (8 workgroups per group, 376 buckets each) merges the
+//     94 chunk statistics, forms the head-summed probabilities exp(l - M) / Z
+//     -- equal logits give bit-equal probabilities, so exact ties fall to the
+//     lower bucket id as in the reference -- and keeps its 16 best 44-bit
+//     keys (probability bits << 12 | 4095 - bucket: value descending, bucket
+//     id ascending on ties); the final kernel ranks the 128 candidates of a
+//     group.  Each select ranks per-thread maxima with LDS broadcast reads to
+//     find a threshold, then ranks the few keys above it (no histogram
+//     atomics, no sorting network).
+#include "launch.h"
+#include "select.h"
 
 namespace prismkv {
 namespace {
@@ -36,87 +38,6 @@ namespace {
 constexpr int kRT = 256;                      // route workgroup size
 constexpr int kKeys = (kFP + kRT - 1) / kRT;  // 12 candidate keys per thread
 constexpr float kSqrtD = 11.3137084989847604f;  // fp32(sqrt(128)), core.py:125
-
-struct SelectLds {
-  unsigned long long tm[kRT];    // per-thread maxima
-  unsigned long long cand[kRT];  // keys >= tau
-  unsigned long long sel[kTop];  // the winners, rank order
-  unsigned long long tau;
-  int ncand;
-};
-
-__device__ __forceinline__ uint64_t make_key(float prob, int bucket) {
-  return ((uint64_t)__float_as_uint(prob) << 12) | (uint64_t)(4095 - bucket);
-}
-__device__ __forceinline__ int key_bucket(uint64_t k) { return 4095 - (int)(k & 4095u); }
-
-// Top-16 of the nonzero keys of the workgroup (unique by construction), in
-// rank order, into lds.sel; returns how many (min(16, live)).  No histogram
-// and no sorting network: tau = the 16th largest per-thread maximum, found by
-// ranking the 256 maxima against each other with LDS broadcast reads; at
-// least 16 keys are >= tau and at most 16 threads hold such keys (15 when
-// fewer than 16 threads hold a live key and tau falls back to 1), so the
-// <= 192 candidates >= tau are ranked exactly the same way.
-__device__ int select_top(const uint64_t (&key)[kKeys], SelectLds& lds) {
-  const int tid = threadIdx.x;
-  unsigned long long lm = 0;
-#pragma unroll
-  for (int i = 0; i < kKeys; ++i) lm = key[i] > lm ? key[i] : lm;
-  lds.tm[tid] = lm;
-  if (tid == 0) {
-    lds.tau = 1;  // dead keys (0) never qualify
-    lds.ncand = 0;
-  }
-  __syncthreads();
-  int r = 0;
-  const ulonglong2* tm2 = reinterpret_cast<const ulonglong2*>(lds.tm);
-#pragma unroll 8
-  for (int j = 0; j < kRT / 2; ++j) {
-    const ulonglong2 o = tm2[j];
-    r += (o.x > lm) + (o.y > lm);
-  }
-  if (r == kTop - 1 && lm > 0) lds.tau = lm;  // unique: nonzero maxima are distinct
-  __syncthreads();
-  const unsigned long long tau = lds.tau;
-  int mine = 0;
-#pragma unroll
-  for (int i = 0; i < kKeys; ++i) mine += key[i] >= tau;
-  if (mine) {
-    int at = atomicAdd(&lds.ncand, mine);
-#pragma unroll
-    for (int i = 0; i < kKeys; ++i)
-      if (key[i] >= tau && at < kRT) lds.cand[at++] = key[i];
-  }
-  __syncthreads();
-  const int nc = lds.ncand < kRT ? lds.ncand : kRT;
-  if (tid < nc) {
-    const unsigned long long k = lds.cand[tid];
-    int rk = 0;
-    for (int j = 0; j < nc; ++j) rk += lds.cand[j] > k;
-    if (rk < kTop) lds.sel[rk] = k;
-  }
-  __syncthreads();
-  return nc < kTop ? nc : kTop;
-}
-
-// Writes the winners (lds.sel, rank order): features[r] = bucket, valid[r] =
-// 1 for r < need; remaining slots id 0 / valid 0 (route_parallel.cu:23,29);
-// raw = sum of winner counts.
-template <typename CountT>
-__device__ void write_selection(const SelectLds& lds, int need, const CountT* counts, int64_t* features,
-                                float* valid, int* raw) {
-  const int tid = threadIdx.x;
-  if (tid < 64) {
-    const bool hit = tid < need;
-    const int b = hit ? key_bucket(lds.sel[tid]) : 0;
-    if (tid < kTop) {
-      features[tid] = b;
-      valid[tid] = hit ? 1.0f : 0.0f;
-    }
-    const int n = wave_sum_i(hit ? (int)counts[b] : 0);
-    if (tid == 0) *raw = n;
-  }
-}
 
 // Transpose-reduce step: `x` holds 2n partial sums; lanes whose `mask` bit is
 // set keep the upper half, the others the lower half, and add the partner's
@@ -219,20 +140,27 @@ __global__ __launch_bounds__(kRT) void route_score_kernel(const uint16_t* __rest
 }
 
 // ---------------------------------------------------------------------------
-// Route, pass 2 (normalise, aggregate, Top-16): grid G x 256.
+// Route, pass 2 (normalise, aggregate, local Top-16): grid (kParts, G) x 256.
+// Part j of group g turns the logits of buckets [j*kPartB, (j+1)*kPartB)
+// into probabilities exp(l - M) / Z -- bit-equal for equal logits, so exact
+// ties fall to the lower bucket id as in the reference -- and keeps its 16
+// best keys; the union of the parts' bests holds the group's Top-16.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kRT) void route_select_kernel(RouteWork work, const int* __restrict__ counts,
-                                                           int64_t* __restrict__ features,
-                                                           float* __restrict__ valid, int* __restrict__ raw) {
-  const int g = blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+constexpr int kParts = 8;
+constexpr int kPartB = kFP / kParts;  // 376 buckets per part
+constexpr int kPartKeys = (kPartB + kRT - 1) / kRT;  // 2
+
+__global__ __launch_bounds__(kRT) void route_part_kernel(RouteWork work, unsigned long long* __restrict__ cand) {
+  const int part = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   __shared__ float gmax[kHq], grz[kHq];
-  __shared__ SelectLds lds;
+  __shared__ __align__(16) unsigned long long keys[kPartKeys * kRT];
+  __shared__ __align__(16) unsigned long long scratch[64 + 16 * kPartKeys * 4 + 2];
   // every load of the workgroup is issued before any is used
   const float* lg = work.logits + (size_t)g * kHq * kFP;
-  float lv[kKeys][kHq];
+  float lv[kPartKeys][kHq];
 #pragma unroll
-  for (int i = 0; i < kKeys; ++i) {
-    const int b = min(tid + i * kRT, kFP - 1);
+  for (int i = 0; i < kPartKeys; ++i) {
+    const int b = part * kPartB + min(tid + i * kRT, kPartB - 1);
 #pragma unroll
     for (int h = 0; h < kHq; ++h) lv[i][h] = lg[h * kFP + b];
   }
@@ -251,22 +179,50 @@ __global__ __launch_bounds__(kRT) void route_select_kernel(RouteWork work, const
     }
   }
   __syncthreads();
-  uint64_t key[kKeys];
 #pragma unroll
-  for (int i = 0; i < kKeys; ++i) {
-    const int b = tid + i * kRT;
-    key[i] = 0;
-    if (b < kFP && lv[i][0] != -INFINITY) {
+  for (int i = 0; i < kPartKeys; ++i) {
+    const int off = tid + i * kRT, b = part * kPartB + off;
+    uint64_t key = 0;
+    if (off < kPartB && lv[i][0] != -INFINITY) {
       // per-head softmax exp(l - M) / Z, then the sum over heads in head order (core.py:128)
       const float p0 = expf(lv[i][0] - gmax[0]) * grz[0];
       const float p1 = expf(lv[i][1] - gmax[1]) * grz[1];
       const float p2 = expf(lv[i][2] - gmax[2]) * grz[2];
       const float p3 = expf(lv[i][3] - gmax[3]) * grz[3];
-      key[i] = make_key(((p0 + p1) + p2) + p3, b);
+      key = make_key(((p0 + p1) + p2) + p3, b);
     }
+    keys[off] = key;
   }
-  const int need = select_top(key, lds);
-  write_selection(lds, need, counts + (size_t)g * kFP, features + (size_t)g * kTop, valid + (size_t)g * kTop,
+  __syncthreads();
+  // wave w keeps the 16 best of keys[128w, 128w + 128); wave 0 then the 16 best of those 64
+  __shared__ __align__(16) unsigned long long best[4 * kTop];
+  __shared__ __align__(16) unsigned long long sc[4][64 + 2 * 16 + 2];
+  wave_top16<2>(keys + 128 * w, sc[w], best + kTop * w);
+  __syncthreads();
+  if (w == 0) {
+    __shared__ __align__(16) unsigned long long win[kTop];
+    wave_top16<1>(best, scratch, win);
+    if (lane < kTop) cand[((size_t)g * kParts + part) * kTop + lane] = win[lane];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Route, pass 3: the Top-16 of the kParts x 16 candidates of each group.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(64) void route_final_kernel(const unsigned long long* __restrict__ cand,
+                                                         const int* __restrict__ counts,
+                                                         int64_t* __restrict__ features, float* __restrict__ valid,
+                                                         int* __restrict__ raw) {
+  const int g = blockIdx.x, lane = threadIdx.x;
+  __shared__ __align__(16) unsigned long long keys[kParts * kTop];
+  __shared__ __align__(16) unsigned long long scratch[64 + 2 * 16 + 2];
+  __shared__ __align__(16) unsigned long long win[kTop];
+  static_assert(kParts * kTop == 128, "two candidates per lane");
+  keys[lane] = cand[(size_t)g * kParts * kTop + lane];
+  keys[lane + 64] = cand[(size_t)g * kParts * kTop + lane + 64];
+  __syncthreads();
+  const int need = wave_top16<2>(keys, scratch, win);
+  write_selection(win, need, counts + (size_t)g * kFP, features + (size_t)g * kTop, valid + (size_t)g * kTop,
                   raw + g);
 }
 
@@ -281,7 +237,9 @@ __global__ __launch_bounds__(kRT) void norm_top_kernel(const float* __restrict__
   const int g = blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   __shared__ float red[kHq][4];
   __shared__ float hmax[kHq], hsum[kHq];
-  __shared__ SelectLds lds;
+  __shared__ __align__(16) unsigned long long keys[kKeys * kRT];
+  __shared__ __align__(16) unsigned long long sc[kRT / 64][64 + 16 * kKeys];
+  __shared__ __align__(16) unsigned long long best[kRT / 64 * kTop], win[kTop];
   const int* cg = ct + (size_t)g * kF;
   const float* lng = ln + (size_t)g * kF;
   float lv[kHq][kKeys];
@@ -318,20 +276,26 @@ __global__ __launch_bounds__(kRT) void norm_top_kernel(const float* __restrict__
   __syncthreads();
   if (tid < kHq) hsum[tid] = (red[tid][0] + red[tid][1]) + (red[tid][2] + red[tid][3]);
   __syncthreads();
-  uint64_t key[kKeys];
+  // keys laid out so that wave w's 768 keys are contiguous: slot i of thread t at 768 w + 64 i + lane
 #pragma unroll
   for (int i = 0; i < kKeys; ++i) {
     const int b = tid + i * kRT;
-    key[i] = 0;
+    uint64_t key = 0;
     if (b < kF && cg[b] > 0) {
       float a = 0.f;
 #pragma unroll
       for (int h = 0; h < kHq; ++h) a += hsum[h] > 0.f ? lv[h][i] / hsum[h] : 0.f;
-      key[i] = make_key(a, b);
+      key = make_key(a, b);
     }
+    keys[w * 64 * kKeys + 64 * i + lane] = key;
   }
-  const int need = select_top(key, lds);
-  write_selection(lds, need, cg, ids + (size_t)g * kTop, vals + (size_t)g * kTop, raw + g);
+  __syncthreads();
+  wave_top16<kKeys>(keys + w * 64 * kKeys, sc[w], best + kTop * w);
+  __syncthreads();
+  if (w == 0) {
+    const int need = wave_top16<1>(best, sc[0], win);
+    write_selection(win, need, cg, ids + (size_t)g * kTop, vals + (size_t)g * kTop, raw + g);
+  }
 }
 
 // Compat: pack (kernels/ppu_8b/pack.cu:3-4): bf16 q[32][128] -> a[32][256] = [q, q*q].
@@ -347,14 +311,22 @@ __global__ void pack_kernel(const uint16_t* __restrict__ q, float* __restrict__ 
 
 using namespace prismkv;
 
+void prismkv::launch_route_score(const uint16_t* q, const float* moments, const int* counts, float* logits,
+                                 float* stats, int groups, hipStream_t stream) {
+  hipLaunchKernelGGL(route_score_kernel, dim3(kChunks, groups), dim3(kRT), 0, stream, q, moments, counts,
+                     RouteWork{logits, stats});
+}
+
 static size_t route_logits_bytes(int groups) { return (size_t)groups * kHq * kFP * sizeof(float); }
 static size_t route_stats_bytes(int groups) { return (size_t)groups * kChunks * kHq * 2 * sizeof(float); }
 
 extern "C" {
 
+static size_t route_cand_bytes(int groups) { return (size_t)groups * kParts * kTop * sizeof(unsigned long long); }
+
 size_t prismkv_route_work_bytes(int groups) {
   if (groups < 1) return 0;
-  return route_logits_bytes(groups) + route_stats_bytes(groups);
+  return route_logits_bytes(groups) + route_stats_bytes(groups) + route_cand_bytes(groups);
 }
 
 int prismkv_route(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features, uint64_t valid,
@@ -364,9 +336,12 @@ int prismkv_route(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, 
   char* base = reinterpret_cast<char*>(work);
   RouteWork rw{reinterpret_cast<float*>(base), reinterpret_cast<float*>(base + route_logits_bytes(groups))};
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(route_score_kernel, dim3(kChunks, groups), dim3(kRT), 0, s, reinterpret_cast<const uint16_t*>(q),
-                     reinterpret_cast<const float*>(moments), reinterpret_cast<const int*>(counts), rw);
-  hipLaunchKernelGGL(route_select_kernel, dim3(groups), dim3(kRT), 0, s, rw, reinterpret_cast<const int*>(counts),
+  launch_route_score(reinterpret_cast<const uint16_t*>(q), reinterpret_cast<const float*>(moments),
+                     reinterpret_cast<const int*>(counts), rw.logits, rw.stats, groups, s);
+  unsigned long long* cand =
+      reinterpret_cast<unsigned long long*>(base + route_logits_bytes(groups) + route_stats_bytes(groups));
+  hipLaunchKernelGGL(route_part_kernel, dim3(kParts, groups), dim3(kRT), 0, s, rw, cand);
+  hipLaunchKernelGGL(route_final_kernel, dim3(groups), dim3(64), 0, s, cand, reinterpret_cast<const int*>(counts),
                      reinterpret_cast<int64_t*>(features), reinterpret_cast<float*>(valid),
                      reinterpret_cast<int*>(raw));
   return (int)hipGetLastError();

@@ -150,6 +150,8 @@ class Native8B:
                                       dtype=torch.uint8, device=device)
         self.state = torch.zeros(self.lib.query("prismkv_attend_work_bytes", GROUPS, ATTEND_SPLITS),
                                  dtype=torch.uint8, device=device)
+        self.decode_work = torch.zeros(self.lib.query("prismkv_decode_work_bytes", GROUPS, self.capacity),
+                                       dtype=torch.uint8, device=device)
         self.out = torch.zeros(GROUPS, HEADS, DIM, dtype=torch.bfloat16, device=device)
 
     def _stream(self):
@@ -168,11 +170,7 @@ class Native8B:
                       self.union_work.data_ptr(), self.ids.data_ptr(), self.count.data_ptr(), GROUPS, self.history,
                       self.row_words, self.capacity, stream=s)
 
-    def attention(self, q, k, v, *, splits=64, schedule=0):
-        """Stage 3.  `splits` (1..128) and `schedule` (0, 1, 2) are validated and
-        accepted for compatibility; the softmax is exact, so the partition does
-        not change the result, and the kernel always uses ATTEND_SPLITS
-        workgroups per group with rows dealt evenly to their waves."""
+    def _check_kv(self, q, k, v, splits, schedule):
         if not 1 <= splits <= 128 or schedule not in (0, 1, 2):
             raise ValueError("unsupported attention partition/schedule")
         if k.shape != v.shape or k.shape[0] != GROUPS or k.shape[-1] != DIM or k.shape[1] < self.history:
@@ -187,6 +185,13 @@ class Native8B:
             raise ValueError("Q/K/V must live on the index device")
         if (q.data_ptr() | k.data_ptr() | v.data_ptr() | (k.stride(0) * 2) | (v.stride(0) * 2)) % 16:
             raise ValueError("Q/K/V rows must be 16-byte aligned")
+
+    def attention(self, q, k, v, *, splits=64, schedule=0):
+        """Stage 3.  `splits` (1..128) and `schedule` (0, 1, 2) are validated and
+        accepted for compatibility; the softmax is exact, so the partition does
+        not change the result, and the kernel always uses ATTEND_SPLITS
+        workgroups per group with rows dealt evenly to their waves."""
+        self._check_kv(q, k, v, splits, schedule)
         self.lib.call("prismkv_attend", q.data_ptr(), k.data_ptr(), v.data_ptr(), self.ids.data_ptr(),
                       self.count.data_ptr(), self.state.data_ptr(), self.out.data_ptr(), GROUPS, self.history,
                       k.shape[1] - self.history, k.stride(0), v.stride(0), self.capacity, ATTEND_SPLITS,
@@ -194,8 +199,16 @@ class Native8B:
         return self.out
 
     def __call__(self, q, k, v, **kwargs):
-        self.route(q)
-        return self.attention(q, k, v, **kwargs)
+        """route + attention (src/prismkv/native8b.py:104-106) through the fused
+        decode path: two launches, identical results, every output buffer
+        (features, valid, raw, ids, count, out) written as by the two calls."""
+        self._check_kv(q, k, v, kwargs.get("splits", 64), kwargs.get("schedule", 0))
+        self.lib.call("prismkv_decode", q.data_ptr(), self.moments.data_ptr(), self.n.data_ptr(), self.bits.data_ptr(),
+                      k.data_ptr(), v.data_ptr(), self.decode_work.data_ptr(), self.features.data_ptr(),
+                      self.valid.data_ptr(), self.raw.data_ptr(), self.ids.data_ptr(), self.count.data_ptr(),
+                      self.out.data_ptr(), GROUPS, self.history, k.shape[1] - self.history, self.capacity,
+                      self.row_words, k.stride(0), v.stride(0), self.capacity, stream=self._stream())
+        return self.out
 
     def buffer_bytes(self):
         """Live tensors owned here; excludes model/KV, caller indices and build temporaries."""

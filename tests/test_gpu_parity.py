@@ -35,6 +35,18 @@ def check_case(case, splits_list=(32, 64, 128), schedules=(0, 2)):
             log(f"  splits={splits} schedule={schedule} {err}")
             assert np.isfinite(bf16_bits(out).astype(np.float32)).all()
             assert err["rel_l2"] <= AV_TOL and err["max_abs"] < 0.05, err
+    # the fused decode path (Native8B.__call__) gives the same selection and ids
+    features, valid, raw, ids, count = route_outputs(op)
+    out = op(q, k, v)
+    torch.cuda.synchronize()
+    f2, v2, r2, i2, c2 = route_outputs(op)
+    assert np.array_equal(features, f2) and np.array_equal(valid, v2) and np.array_equal(raw, r2)
+    assert np.array_equal(count, c2)
+    for g in range(8):
+        assert np.array_equal(ids[g][:count[g]], i2[g][:c2[g]]), ("fused ids", g)
+    err = expect.attention_errors(bf16_bits(out), want)
+    log(f"  fused decode {err}")
+    assert err["rel_l2"] <= AV_TOL and err["max_abs"] < 0.05, err
     return op, groups
 
 
