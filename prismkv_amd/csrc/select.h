@@ -12,18 +12,18 @@ __device__ __forceinline__ uint64_t make_key(float prob, int bucket) {
 }
 __device__ __forceinline__ int key_bucket(uint64_t k) { return 4095 - (int)(k & 4095u); }
 
-// Number of the n keys at v (n <= 2 * kPairs) that are greater than x.
-// Independent broadcast LDS reads, two keys each, all issued back to back.
-template <int kPairs>
+// Number of keys greater than x among v[0 .. 16 * ceil(n / 16)), n uniform
+// across the wave; entries past n must be zero (a zero key is never
+// greater).  Reads go in chunks of 8 pairs with no branch between them.
 __device__ __forceinline__ int count_greater(const unsigned long long* v, int n, unsigned long long x) {
-  // every pair is read (no branch between reads, so they all issue back to
-  // back); entries at or past n are masked out of the count
   const ulonglong2* v2 = reinterpret_cast<const ulonglong2*>(v);
   int r = 0;
+  for (int j0 = 0; 2 * j0 < n; j0 += 8) {
+    ulonglong2 o[8];
 #pragma unroll
-  for (int j = 0; j < kPairs; ++j) {
-    const ulonglong2 o = v2[j];
-    r += (2 * j < n && o.x > x) + (2 * j + 1 < n && o.y > x);
+    for (int j = 0; j < 8; ++j) o[j] = v2[j0 + j];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r += (o[j].x > x) + (o[j].y > x);
   }
   return r;
 }
@@ -36,7 +36,8 @@ __device__ __forceinline__ int wave_scan_i(int v) { return (int)wave_incl_scan((
 // tau = the 16th largest per-lane maximum (lane maxima ranked against each
 // other with broadcast LDS reads): at least 16 keys are >= tau and at most 16
 // lanes hold such keys, so the <= 16K candidates >= tau are ranked exactly.
-// `scratch` holds 64 + 16K keys (16-byte aligned).  Returns the number of winners.
+// `scratch` holds 64 + 16K keys rounded up to 16 (16-byte aligned).  Returns
+// the number of winners.
 template <int K>
 __device__ int wave_top16(const unsigned long long* keys, unsigned long long* scratch, unsigned long long* out) {
   const int lane = threadIdx.x & 63;
@@ -51,7 +52,7 @@ __device__ int wave_top16(const unsigned long long* keys, unsigned long long* sc
   mx[lane] = lm;
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_s_waitcnt(0);
-  const int r = lm > 0 ? count_greater<32>(mx, 64, lm) : 64;
+  const int r = lm > 0 ? count_greater(mx, 64, lm) : 64;
   const unsigned long long at15 = __ballot(r == kTop - 1);
   unsigned long long tau = 1;  // dead keys (0) never qualify
   if (at15) {
@@ -69,11 +70,12 @@ __device__ int wave_top16(const unsigned long long* keys, unsigned long long* sc
 #pragma unroll
   for (int i = 0; i < K; ++i)
     if (kk[i] >= tau) cand[at++] = kk[i];
+  for (int c = nc + lane; c < ((nc + 15) & ~15); c += 64) cand[c] = 0;  // zero tail of the last chunk
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_s_waitcnt(0);
   for (int c = lane; c < nc; c += 64) {
     const unsigned long long k = cand[c];
-    const int rk = count_greater<8 * K>(cand, nc, k);
+    const int rk = count_greater(cand, nc, k);
     if (rk < kTop) out[rk] = k;
   }
   const int need = nc < kTop ? nc : kTop;
