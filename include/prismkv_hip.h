@@ -112,6 +112,30 @@ int prismkv_decode(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits,
                    uint64_t out, int groups, int H, int T, int capacity, int64_t row_words, int64_t ks, int64_t vs,
                    int64_t ids_stride, uint64_t stream);
 
+/* ---- stage 4: incremental index update ---------------------------------
+ * append_index (src/prismkv/core.py:186-201) for all groups at once, on the
+ * device tables in place.  The new block is K rows [H, H+N) of each group
+ * (bf16, group stride `ks` elements, rows of 128).  Per group:
+ *   x = (k - center[g]) / scale[g] (fp32), a = relu(x W[g]^T + b[g])
+ *     (SharedSAE.dense, core.py:47-48), W f32 [G][3000][128], b f32 [G][3000],
+ *     center f32 [G][128] (the index's ORIGINAL center), scale f32 [G];
+ *   BatchTopK over the block (positive_global_topk, core.py:13-26) with the
+ *     budget N * key_mean: values above the budget-th largest tau, then ties
+ *     at tau in ascending flat index (token * 3000 + bucket) up to the budget,
+ *     or every positive value when fewer are positive;
+ *   bits: member (token t, bucket f) sets bit H + t of row f (columns
+ *     [H, H+N) must be zero on entry; rows of `row_words` >= (H+N+31)/32);
+ *   counts i32 [G][3008] += new members; moments (the tiled [G][94][256][32]
+ *     table) <- Chan merge of the old moments with the block's population
+ *     moments, in fp32 and the operation order of core.py:190-199.
+ * `work` is prismkv_update_work_bytes(groups, N) bytes, zero-filled once
+ * before first use and left zeroed.  N <= 4096; returns -1 on bad sizes.
+ * The caller guarantees K holds rows [0, H+N) for every group. */
+size_t prismkv_update_work_bytes(int groups, int max_block);
+int prismkv_update(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
+                   uint64_t counts, uint64_t moments, uint64_t work, int groups, int H, int N, int key_mean,
+                   int64_t ks, int64_t row_words, uint64_t stream);
+
 #ifdef __cplusplus
 }
 #endif

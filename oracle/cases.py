@@ -9,6 +9,15 @@
   reference's global BatchTopK budget 8*H (src/prismkv/core.py:92-103).
 * `topk8_case` is the 8B-geometry kernel check: bf16 K/V ~ N(0,1), every key
   joins the buckets of its top-8 ReLU activations of the same random SAE.
+* `update_case` is one append_index step (src/prismkv/core.py:186-201): an
+  index built by the reference rule over the first H keys, then a block of N
+  new keys to index with the same per-group SAE and key scale.  Its kinds
+  steer the BatchTopK branches of src/prismkv/core.py:13-26: "random"
+  (distinct values), "bias_ties" (W = 0, b = 1: every activation equals 1,
+  so ties at tau overflow the budget and the flat-index order decides),
+  "sparse" (b = -3: fewer positives than the budget, tau = 0), "dead"
+  (b = -100: no positive activation at all) and "dup" (the block's keys
+  come in identical pairs: ties of two at every value).
 
 All cases return plain numpy arrays: bf16 tensors as uint16 bit patterns,
 indices as `oracle.Index` objects.
@@ -134,3 +143,36 @@ def topk8_case(H=65536, T=256, seed=2, groups=G):
         W, b = sae_weights(seed, g)
         indices.append(index_from_lists(kf[g, :H], topk8_lists(kf[g, :H], W, b)))
     return dict(H=H, T=T, q=q, k=k, v=v, indices=indices, kind="topk8")
+
+
+UPDATE_KINDS = ("random", "bias_ties", "sparse", "dead", "dup")
+
+
+def update_sae(kind, seed, g):
+    W, b = sae_weights(seed, g)
+    if kind == "bias_ties":
+        W = np.zeros_like(W)
+        b = np.ones_like(b)
+    elif kind == "sparse":
+        b = np.full_like(b, -3.0)
+    elif kind == "dead":
+        b = np.full_like(b, -100.0)
+    return W, b
+
+
+def update_case(kind="random", H=512, N=256, T=8, seed=21, key_mean=8):
+    """Inputs of one append step for 8 groups (see the module docstring)."""
+    k = bf16_normal((seed, 0), (G, H + N + T, D))
+    if kind == "dup":
+        k[:, H + 1:H + N:2] = k[:, H:H + N - 1:2]
+    v = bf16_normal((seed, 1), (G, H + N + T, D))
+    q = bf16_normal((seed, 2), (G, HQ, D))
+    kf = bf16_to_f32(k)
+    W = np.empty((G, F, D), np.float32)
+    b = np.empty((G, F), np.float32)
+    scale = np.array([1.0 + 0.25 * g for g in range(G)], np.float32)
+    indices = []
+    for g in range(G):
+        W[g], b[g] = update_sae(kind, seed, g)
+        indices.append(build_index(kf[g, :H], W[g], b[g], float(scale[g]), key_mean=key_mean))
+    return dict(H=H, N=N, T=T, q=q, k=k, v=v, W=W, b=b, scale=scale, key_mean=key_mean, indices=indices, kind=kind)

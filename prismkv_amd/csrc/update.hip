@@ -1,0 +1,481 @@
+// Stage 4 -- incremental index update: index a block of N new keys (K rows
+// [H, H+N) of a group) with the group's SAE and merge it into the index.
+//
+// Semantics: src/prismkv/core.py:186-201 (append_index) on top of
+//   build_index  core.py:92-103  x = (k - center) / key_scale with the
+//                                ORIGINAL center; a = relu(x W^T + b)
+//                                (SharedSAE.dense, core.py:47-48);
+//   positive_global_topk core.py:13-26  budget N * key_mean over the block:
+//                                keep a > tau and a > 0, then, if tau > 0,
+//                                values == tau in ascending flat index
+//                                (token * F + feature) up to the budget;
+//   summarize    core.py:76-89   per-bucket mean / population variance of
+//                                the ORIGINAL new keys (two-pass);
+//   the merge    core.py:190-199 mean = (a m_a + b m_b) / max(a+b, 1),
+//                                var = (a v_a + b v_b) / max(a+b, 1)
+//                                      + a b / max(a+b, 1)^2 (m_a - m_b)^2,
+//                                in fp32 and in that operation order;
+//   lists        core.py:200     new members are tokens H + t: here bits
+//                                H + t of the bucket's bitmap row
+//                                (kernels/ppu_8b/pack.cu:5 bit order).
+//
+// Launches (all G groups at once; the update runs every `interval` tokens,
+// its cost is amortised):
+//   encode   LDS-tiled fp32 GEMM, 64 tokens x 64 buckets per workgroup,
+//            writes a = relu(...) [G][N][F] and a histogram of the positive
+//            values' top 11 bits (4 replicas of each global bin, so the
+//            flushes of ~750 workgroups do not queue on one address);
+//   digit    one workgroup per group picks the histogram bin holding the
+//            budget-th largest value (3 levels: bits 30..20, 19..9, 8..0);
+//   refine   re-reads a, histograms the values inside the chosen prefix;
+//   emit     sets bitmap bits for a > tau (or all positives when fewer
+//            than the budget are positive) and for a == tau when every tie
+//            fits the budget;
+//   ties     only when ties overflow the budget: one workgroup per group
+//            walks a in flat order and takes the first `need` ties;
+//   moments  per 32-bucket tile: new members from the bitmap, two-pass
+//            moments of their bf16 keys, merge, counts += new.
+#include "common.h"
+
+namespace prismkv {
+namespace {
+
+constexpr int kUT = 256;
+constexpr int kTT = 64;        // tokens per encode tile
+constexpr int kFT = 64;        // buckets per encode tile
+constexpr int kFTiles = (kF + kFT - 1) / kFT;  // 47
+constexpr int kBins = 2048;
+constexpr int kRep = 4;        // global histogram replicas
+constexpr int kLevels = 3;
+constexpr int kRefineBlocks = 256;  // workgroups per group of a pass over a
+
+// ctl words per group
+enum { kMode = 0, kPrefix, kRem, kTau, kNeed, kTies, kOrdered, kCount, kCtl = 16 };
+enum { kModeTopK = 0, kModeAllPositive = 1 };
+
+struct UpdateArgs {
+  const uint16_t* k;  // K cache; the block is rows [H, H+N) of each group
+  int64_t ks;         // group stride (elements)
+  const float* W;     // [G][F][128]
+  const float* b;     // [G][F]
+  const float* center;  // [G][128]
+  const float* scale;   // [G]
+  uint32_t* bits;
+  int64_t row_words;
+  int* counts;     // [G][kFP]
+  float* moments;  // [G][kChunks][256][32]
+  float* act;      // [G][N][F]
+  unsigned* hist;  // [G][kLevels][kRep][kBins]
+  unsigned* ctl;   // [G][kCtl]
+  int H, N;
+  long long budget;  // N * key_mean
+};
+
+__device__ __forceinline__ unsigned* hist_of(const UpdateArgs& a, int g, int level) {
+  return a.hist + ((size_t)g * kLevels + level) * kRep * kBins;
+}
+
+// ---------------------------------------------------------------------------
+// encode: grid (kFTiles, ceil(N/64), G) x 256; thread = 4 tokens x 4 buckets.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kUT) void encode_kernel(UpdateArgs a) {
+  const int ft = blockIdx.x, tt = blockIdx.y, g = blockIdx.z, tid = threadIdx.x;
+  __shared__ __align__(16) float xs[kD][kTT + 4];  // [dim][token], padded against bank conflicts
+  __shared__ __align__(16) float ws[kD][kFT + 4];  // [dim][bucket]
+  __shared__ unsigned hist[kBins];
+  const int t0 = tt * kTT, f0 = ft * kFT;
+  for (int i = tid; i < kBins; i += kUT) hist[i] = 0;
+  {
+    // x = (k - center) / key_scale in fp32 (core.py:98), 8 dims per load
+    const float sc = a.scale[g];
+    const float* cg = a.center + (size_t)g * kD;
+    for (int i = tid; i < kTT * kD / 8; i += kUT) {
+      const int tok = i / (kD / 8), d0 = (i % (kD / 8)) * 8;
+      float v[8];
+      if (t0 + tok < a.N) {
+        const uint4 r = *reinterpret_cast<const uint4*>(a.k + (size_t)g * a.ks + (size_t)(a.H + t0 + tok) * kD + d0);
+        v[0] = bf16_lo(r.x); v[1] = bf16_hi(r.x); v[2] = bf16_lo(r.y); v[3] = bf16_hi(r.y);
+        v[4] = bf16_lo(r.z); v[5] = bf16_hi(r.z); v[6] = bf16_lo(r.w); v[7] = bf16_hi(r.w);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = (v[j] - cg[d0 + j]) / sc;
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xs[d0 + j][tok] = v[j];
+    }
+    const float* wg = a.W + (size_t)g * kF * kD;
+    for (int i = tid; i < kFT * kD / 4; i += kUT) {
+      const int f = i / (kD / 4), d0 = (i % (kD / 4)) * 4;
+      float4 wv = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (f0 + f < kF) wv = *reinterpret_cast<const float4*>(wg + (size_t)(f0 + f) * kD + d0);
+      ws[d0][f] = wv.x;
+      ws[d0 + 1][f] = wv.y;
+      ws[d0 + 2][f] = wv.z;
+      ws[d0 + 3][f] = wv.w;
+    }
+  }
+  __syncthreads();
+  const int ty = tid >> 4, tx = tid & 15;  // tokens 4ty.., buckets 4tx..
+  float acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
+#pragma unroll 8
+  for (int d = 0; d < kD; ++d) {
+    const float4 xv = *reinterpret_cast<const float4*>(&xs[d][4 * ty]);
+    const float4 wv = *reinterpret_cast<const float4*>(&ws[d][4 * tx]);
+    const float xa[4] = {xv.x, xv.y, xv.z, xv.w}, wa[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(xa[i], wa[j], acc[i][j]);
+  }
+  const float* bg = a.b + (size_t)g * kF;
+  float* ag = a.act + (size_t)g * a.N * kF;
+  const int f = f0 + 4 * tx;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int tok = t0 + 4 * ty + i;
+    float v[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float x = f + j < kF ? acc[i][j] + bg[f + j] : 0.f;
+      v[j] = x > 0.f ? x : 0.f;  // relu; non-positive values are never selected
+      if (tok < a.N && f + j < kF && v[j] > 0.f) atomicAdd(&hist[__float_as_uint(v[j]) >> 20], 1u);
+    }
+    if (tok < a.N && f < kF) {  // kF is a multiple of 4: a quad is all in or all out
+      *reinterpret_cast<float4*>(ag + (size_t)tok * kF + f) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+  }
+  __syncthreads();
+  unsigned* hg = hist_of(a, g, 0) + ((ft + tt) % kRep) * kBins;
+  for (int i = tid; i < kBins; i += kUT)
+    if (hist[i]) atomicAdd(&hg[i], hist[i]);
+}
+
+// ---------------------------------------------------------------------------
+// digit: grid G x 256.  Level L consumes hist level L (all replicas, then
+// zeroes them for the next update) and narrows the threshold prefix.
+// Level widths: 11 bits (30..20), 11 bits (19..9), 9 bits (8..0); positive
+// floats order like their bit patterns, so the prefix after level 2 is the
+// exact bit pattern of tau, the budget-th largest value.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kUT) void digit_kernel(UpdateArgs a, int level) {
+  const int g = blockIdx.x, tid = threadIdx.x;
+  __shared__ unsigned wsum[kUT / 64];
+  __shared__ unsigned found_digit, found_rem, found_ties;
+  unsigned* ctl = a.ctl + (size_t)g * kCtl;
+  unsigned* h = hist_of(a, g, level);
+  constexpr int kPer = kBins / kUT;  // 8 bins per thread, descending digits
+  unsigned c[kPer], tot = 0;
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int d = kBins - 1 - (tid * kPer + u);
+    unsigned s = 0;
+#pragma unroll
+    for (int r = 0; r < kRep; ++r) {
+      s += h[r * kBins + d];
+      h[r * kBins + d] = 0;
+    }
+    c[u] = s;
+    tot += s;
+  }
+  const long long total_vals = (long long)a.N * kF;
+  const unsigned count = (unsigned)(a.budget < total_vals ? a.budget : total_vals);
+  const unsigned incl = block_incl_scan<kUT>(tot, wsum);
+  unsigned rem, prefix_in;
+  if (level == 0) {
+    // wsum holds the per-wave totals: their sum is the number of positive values
+    const unsigned npos = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    if (npos < count || count == 0) {
+      // fewer positives than the budget: tau = 0 and every positive value is
+      // kept (core.py:22-26); an empty budget keeps nothing
+      if (tid == 0) {
+        ctl[kMode] = count == 0 ? kModeTopK : kModeAllPositive;
+        ctl[kPrefix] = 0;
+        ctl[kRem] = 0;
+        ctl[kTau] = count == 0 ? 0x7f800000u : 0u;
+        ctl[kNeed] = 0;
+        ctl[kTies] = 0;
+        ctl[kOrdered] = 0;
+        ctl[kCount] = count;
+      }
+      return;
+    }
+    rem = count;
+    prefix_in = 0;
+  } else {
+    if (ctl[kMode] != kModeTopK || ctl[kTau] == 0x7f800000u) return;
+    rem = ctl[kRem];
+    prefix_in = ctl[kPrefix];
+  }
+  const int width = level < 2 ? 11 : 9;
+  unsigned run = incl - tot;
+#pragma unroll
+  for (int u = 0; u < kPer; ++u) {
+    const int d = kBins - 1 - (tid * kPer + u);
+    if (d < (1 << width) && run < rem && run + c[u] >= rem) {
+      found_digit = (unsigned)d;
+      found_rem = rem - run;
+      found_ties = c[u];
+    }
+    run += c[u];
+  }
+  __syncthreads();
+  if (tid == 0) {
+    const unsigned prefix = (prefix_in << width) | found_digit;
+    ctl[kMode] = kModeTopK;
+    ctl[kPrefix] = prefix;
+    ctl[kRem] = found_rem;
+    ctl[kCount] = count;
+    if (level == kLevels - 1) {
+      // prefix is the exact tau; found_rem of its found_ties ties are taken
+      ctl[kTau] = prefix;
+      ctl[kNeed] = found_rem;
+      ctl[kTies] = found_ties;
+      ctl[kOrdered] = found_ties > found_rem;
+    } else {
+      ctl[kTau] = 0;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// refine: grid (kRefineBlocks, G) x 256 over a; histogram of the next digit
+// of the positive values whose higher bits equal the prefix.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kUT) void refine_kernel(UpdateArgs a, int level) {
+  const int g = blockIdx.y, tid = threadIdx.x;
+  const unsigned* ctl = a.ctl + (size_t)g * kCtl;
+  if (ctl[kMode] != kModeTopK || ctl[kTau] == 0x7f800000u) return;
+  __shared__ unsigned hist[kBins];
+  for (int i = tid; i < kBins; i += kUT) hist[i] = 0;
+  __syncthreads();
+  const unsigned prefix = ctl[kPrefix];
+  const int shift_hi = level == 1 ? 20 : 9;  // bits above this level's digit
+  const int shift = level == 1 ? 9 : 0;
+  const unsigned dmask = level == 1 ? 0x7ffu : 0x1ffu;
+  const size_t n = (size_t)a.N * kF;
+  const float4* ag = reinterpret_cast<const float4*>(a.act + (size_t)g * n);
+  for (size_t i = (size_t)blockIdx.x * kUT + tid; i < n / 4; i += (size_t)gridDim.x * kUT) {
+    const float4 v4 = ag[i];
+    const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const unsigned u = __float_as_uint(vv[j]);
+      if (vv[j] > 0.f && (u >> shift_hi) == prefix) atomicAdd(&hist[(u >> shift) & dmask], 1u);
+    }
+  }
+  __syncthreads();
+  unsigned* hg = hist_of(a, g, level) + (blockIdx.x % kRep) * kBins;
+  for (int i = tid; i < kBins; i += kUT)
+    if (hist[i]) atomicAdd(&hg[i], hist[i]);
+}
+
+__device__ __forceinline__ void set_member(const UpdateArgs& a, int g, unsigned flat) {
+  const int tok = (int)(flat / kF), f = (int)(flat % kF);
+  const int t = a.H + tok;
+  atomicOr(a.bits + ((size_t)g * kF + f) * a.row_words + (t >> 5), 1u << (t & 31));
+}
+
+// ---------------------------------------------------------------------------
+// emit: grid (kRefineBlocks, G) x 256 over a.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kUT) void emit_kernel(UpdateArgs a) {
+  const int g = blockIdx.y, tid = threadIdx.x;
+  const unsigned* ctl = a.ctl + (size_t)g * kCtl;
+  const unsigned mode = ctl[kMode];
+  const float tau = __uint_as_float(ctl[kTau]);
+  const bool take_ties = mode == kModeTopK && !ctl[kOrdered] && tau > 0.f;
+  const size_t n = (size_t)a.N * kF;
+  const float4* ag = reinterpret_cast<const float4*>(a.act + (size_t)g * n);
+  for (size_t i = (size_t)blockIdx.x * kUT + tid; i < n / 4; i += (size_t)gridDim.x * kUT) {
+    const float4 v4 = ag[i];
+    const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float v = vv[j];
+      const bool sel = mode == kModeAllPositive ? v > 0.f : ((v > tau && v > 0.f) || (take_ties && v == tau));
+      if (sel) set_member(a, g, (unsigned)(4 * i + j));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// ties: grid G x 256; only when the ties at tau overflow the budget: the
+// first `need` of them in ascending flat index (core.py:23-24).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kUT) void ties_kernel(UpdateArgs a) {
+  const int g = blockIdx.x, tid = threadIdx.x;
+  const unsigned* ctl = a.ctl + (size_t)g * kCtl;
+  if (ctl[kMode] != kModeTopK || !ctl[kOrdered]) return;
+  const float tau = __uint_as_float(ctl[kTau]);
+  unsigned need = ctl[kNeed];
+  __shared__ unsigned wsum[kUT / 64];
+  const size_t n = (size_t)a.N * kF;
+  const float* ag = a.act + (size_t)g * n;
+  for (size_t base = 0; base < n && need > 0; base += kUT) {
+    const size_t i = base + tid;
+    const unsigned hit = i < n && ag[i] == tau;
+    const unsigned incl = block_incl_scan<kUT>(hit, wsum);
+    if (hit && incl <= need) set_member(a, g, (unsigned)i);
+    const unsigned taken = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    need = taken >= need ? 0u : need - taken;
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// moments: grid (kChunks, G) x 256.  Wave w handles buckets 32c + 8w + j:
+// members from the bitmap, two-pass moments of their keys; then the tile
+// merge, thread = (dim k, bucket col) pairs of mean row k and var row 128+k.
+// ---------------------------------------------------------------------------
+constexpr int kMaxBlock = 4096;  // new tokens per update (LDS member list per wave)
+
+__device__ __forceinline__ float merge_mean(float a, float b, float den, float ma, float mb) {
+#pragma clang fp contract(off)
+  return (a * ma + b * mb) / den;
+}
+__device__ __forceinline__ float merge_var(float a, float b, float den, float ma, float mb, float va, float vb) {
+#pragma clang fp contract(off)
+  const float v = (a * va + b * vb) / den;
+  const float d = ma - mb;
+  return v + ((a * b) / (den * den)) * (d * d);
+}
+
+__global__ __launch_bounds__(kUT) void moments_kernel(UpdateArgs a) {
+  const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  __shared__ float nm[kChunk][kD], nv[kChunk][kD];
+  __shared__ int nb[kChunk];
+  __shared__ int toks[kUT / 64][kMaxBlock];
+  const int w_lo = a.H >> 5, w_hi = (a.H + a.N - 1) >> 5;
+  const uint16_t* kg = a.k + (size_t)g * a.ks;
+  for (int j = 0; j < kChunk / 4; ++j) {
+    const int col = w * (kChunk / 4) + j, f = c * kChunk + col;
+    int b = 0;
+    if (f < kF) {
+      const uint32_t* row = a.bits + ((size_t)g * kF + f) * a.row_words;
+      for (int w0 = w_lo; w0 <= w_hi; w0 += 64) {
+        const int wd = w0 + lane;
+        uint32_t m = wd <= w_hi ? row[wd] : 0u;
+        if (wd == w_lo) m &= ~0u << (a.H & 31);                               // tokens before H
+        if (wd == w_hi && ((a.H + a.N) & 31)) m &= (1u << ((a.H + a.N) & 31)) - 1u;  // tokens past H+N
+        const int pc = __popc(m);
+        const int incl = (int)wave_incl_scan((unsigned)pc);
+        int at = b + incl - pc;
+        while (m) {
+          toks[w][at++] = wd * 32 + (int)__builtin_ctz(m);
+          m &= m - 1u;
+        }
+        b += __shfl(incl, 63);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_s_waitcnt(0);
+    // two-pass moments of the ORIGINAL keys (core.py:84-88); lane owns dims 2l, 2l+1
+    float s0 = 0.f, s1 = 0.f;
+#pragma unroll 4
+    for (int i = 0; i < b; ++i) {
+      const uint32_t r = *reinterpret_cast<const uint32_t*>(kg + (size_t)toks[w][i] * kD + 2 * lane);
+      s0 += bf16_lo(r);
+      s1 += bf16_hi(r);
+    }
+    const float m0 = b ? s0 / (float)b : 0.f, m1 = b ? s1 / (float)b : 0.f;
+    float q0 = 0.f, q1 = 0.f;
+#pragma unroll 4
+    for (int i = 0; i < b; ++i) {
+      const uint32_t r = *reinterpret_cast<const uint32_t*>(kg + (size_t)toks[w][i] * kD + 2 * lane);
+      const float d0 = bf16_lo(r) - m0, d1 = bf16_hi(r) - m1;
+      q0 += d0 * d0;
+      q1 += d1 * d1;
+    }
+    nm[col][2 * lane] = m0;
+    nm[col][2 * lane + 1] = m1;
+    nv[col][2 * lane] = b ? q0 / (float)b : 0.f;
+    nv[col][2 * lane + 1] = b ? q1 / (float)b : 0.f;
+    if (lane == 0) nb[col] = b;
+    __builtin_amdgcn_wave_barrier();
+  }
+  __syncthreads();
+  float* tile = a.moments + (size_t)(g * kChunks + c) * kRow * kChunk;
+  const int col = tid & (kChunk - 1), f = c * kChunk + col;
+  if (f >= kF) return;  // padding columns stay zero
+  const int na = a.counts[(size_t)g * kFP + f], nbn = nb[col];
+  const float fa = (float)na, fb = (float)nbn;
+  const float total = fa + fb, den = total < 1.f ? 1.f : total;
+  for (int k = tid >> 5; k < kD; k += kUT / kChunk) {
+    const float ma = tile[k * kChunk + col], va = tile[(kD + k) * kChunk + col];
+    const float mb = nm[col][k], vb = nv[col][k];
+    tile[k * kChunk + col] = merge_mean(fa, fb, den, ma, mb);
+    tile[(kD + k) * kChunk + col] = merge_var(fa, fb, den, ma, mb, va, vb);
+  }
+  if (tid < kChunk) a.counts[(size_t)g * kFP + f] = na + nbn;
+}
+
+}  // namespace
+}  // namespace prismkv
+
+using namespace prismkv;
+
+struct UpdateLayout {
+  size_t act, hist, ctl, total;
+  UpdateLayout(int groups, int N) {
+    size_t o = 0;
+    auto take = [&](size_t n) { const size_t at = o; o += (n + 255) & ~(size_t)255; return at; };
+    act = take((size_t)groups * N * kF * sizeof(float));
+    hist = take((size_t)groups * kLevels * kRep * kBins * sizeof(unsigned));
+    ctl = take((size_t)groups * kCtl * sizeof(unsigned));
+    total = o;
+  }
+};
+
+extern "C" {
+
+size_t prismkv_update_work_bytes(int groups, int max_block) {
+  if (groups < 1 || max_block < 1 || max_block > kMaxBlock) return 0;
+  return UpdateLayout(groups, max_block).total;
+}
+
+int prismkv_update(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
+                   uint64_t counts, uint64_t moments, uint64_t work, int groups, int H, int N, int key_mean,
+                   int64_t ks, int64_t row_words, uint64_t stream) {
+  if (groups < 1 || groups > 65535 || H < 0 || N < 1 || N > kMaxBlock || key_mean < 1 || key_mean > kF)
+    return kBadSize;
+  if (ks < (int64_t)(H + N) * kD || row_words < (H + N + 31) / 32) return kBadSize;
+  if (!k || !W || !b || !center || !scale || !bits || !counts || !moments || !work) return kBadSize;
+  const UpdateLayout L(groups, N);
+  char* w = reinterpret_cast<char*>(work);
+  UpdateArgs a;
+  a.k = reinterpret_cast<const uint16_t*>(k);
+  a.ks = ks;
+  a.W = reinterpret_cast<const float*>(W);
+  a.b = reinterpret_cast<const float*>(b);
+  a.center = reinterpret_cast<const float*>(center);
+  a.scale = reinterpret_cast<const float*>(scale);
+  a.bits = reinterpret_cast<uint32_t*>(bits);
+  a.row_words = row_words;
+  a.counts = reinterpret_cast<int*>(counts);
+  a.moments = reinterpret_cast<float*>(moments);
+  a.act = reinterpret_cast<float*>(w + L.act);
+  a.hist = reinterpret_cast<unsigned*>(w + L.hist);
+  a.ctl = reinterpret_cast<unsigned*>(w + L.ctl);
+  a.H = H;
+  a.N = N;
+  a.budget = (long long)N * key_mean;
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(encode_kernel, dim3(kFTiles, (N + kTT - 1) / kTT, groups), dim3(kUT), 0, s, a);
+  hipLaunchKernelGGL(digit_kernel, dim3(groups), dim3(kUT), 0, s, a, 0);
+  for (int level = 1; level < kLevels; ++level) {
+    hipLaunchKernelGGL(refine_kernel, dim3(kRefineBlocks, groups), dim3(kUT), 0, s, a, level);
+    hipLaunchKernelGGL(digit_kernel, dim3(groups), dim3(kUT), 0, s, a, level);
+  }
+  hipLaunchKernelGGL(emit_kernel, dim3(kRefineBlocks, groups), dim3(kUT), 0, s, a);
+  hipLaunchKernelGGL(ties_kernel, dim3(groups), dim3(kUT), 0, s, a);
+  hipLaunchKernelGGL(moments_kernel, dim3(kChunks, groups), dim3(kUT), 0, s, a);
+  return (int)hipGetLastError();
+}
+
+}  // extern "C"

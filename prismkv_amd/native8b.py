@@ -12,7 +12,12 @@ shapes as the reference binding:
 * ``.attention(q, k, v, *, splits=64, schedule=0)`` runs stage 3 and returns
   the preallocated ``out`` buffer, overwritten by the next call
   (src/prismkv/native8b.py:91-102);
-* ``__call__`` = route + attention; ``buffer_bytes()`` lists live buffers.
+* ``__call__`` = route + attention; ``buffer_bytes()`` lists live buffers;
+* ``append(k, block)`` is the reference's ``append_index``
+  (src/prismkv/core.py:186-201) for all 8 groups on the device tables in
+  place (after ``set_encoders``); ``catch_up`` is the update loop of
+  src/prismkv/hf_reference.py:209-211; ``export_indices()`` reads the tables
+  back as ``FeatureIndex`` objects.
 
 All validation happens on the host before anything is enqueued (ValueError
 for shapes/dtypes/devices/strides, RuntimeError for a nonzero launch code).
@@ -31,6 +36,9 @@ from . import _lib
 from .build import compile_hip  # noqa: F401  (re-exported: reference name compile_ppu)
 
 GROUPS, HEADS, DIM, FEATURES, TOPK = 8, 4, 128, 3000, 16
+# Largest block one `append` indexes (the reference's update interval is 4096,
+# src/prismkv/hf_reference.py:75).
+MAX_BLOCK = 4096
 # Workgroups per KV group of the sparse-attention launch (each 8 waves; one
 # per CU at 8 groups x 32 = 256): the partition the kernel is tuned for.
 ATTEND_SPLITS = 32
@@ -98,13 +106,16 @@ class Native8B:
                                  counts.long().cumsum(1)), dim=1).int()
             self._setup(h, capacity, library, counts,
                         torch.stack([torch.as_tensor(x.mean).to(device) for x in indices]),
-                        torch.stack([torch.as_tensor(x.variance).to(device) for x in indices]), csr, offsets)
+                        torch.stack([torch.as_tensor(x.variance).to(device) for x in indices]), csr, offsets,
+                        torch.stack([torch.as_tensor(x.center).to(device) for x in indices]))
 
     @classmethod
-    def from_tables(cls, history, counts, mean, variance, csr_ids, offsets, library=None, *, capacity=None):
+    def from_tables(cls, history, counts, mean, variance, csr_ids, offsets, library=None, *, capacity=None,
+                    center=None):
         """Build from device tables directly: counts [8,3000], mean/variance
         [8,3000,128] f32, csr_ids i32 [8,C] (bucket f owns columns
-        offsets[g,f] .. offsets[g,f+1]) and offsets i32 [8,3001]."""
+        offsets[g,f] .. offsets[g,f+1]), offsets i32 [8,3001] and, for
+        `append`, the indices' original centers [8,128]."""
         if counts.device.type != "cuda":
             raise ValueError("native backend requires a device tensor")
         if tuple(mean.shape) != (GROUPS, FEATURES, DIM) or mean.shape != variance.shape:
@@ -112,10 +123,10 @@ class Native8B:
         obj = cls.__new__(cls)
         with torch.cuda.device(counts.device):
             obj._setup(int(history), capacity, library, counts, mean, variance, csr_ids.int().contiguous(),
-                       offsets.int().contiguous())
+                       offsets.int().contiguous(), center)
         return obj
 
-    def _setup(self, h, capacity, library, counts, mean, variance, csr, offsets):
+    def _setup(self, h, capacity, library, counts, mean, variance, csr, offsets, center=None):
         capacity = h if capacity is None else int(capacity)
         if capacity < h or h < 1:
             raise ValueError("history must be >= 1 and capacity >= history")
@@ -153,6 +164,12 @@ class Native8B:
         self.decode_work = torch.zeros(self.lib.query("prismkv_decode_work_bytes", GROUPS, self.capacity),
                                        dtype=torch.uint8, device=device)
         self.out = torch.zeros(GROUPS, HEADS, DIM, dtype=torch.bfloat16, device=device)
+        self.center = None if center is None else center.to(device=device, dtype=torch.float32).reshape(
+            GROUPS, DIM).contiguous()
+        # encoder tables and block workspace of `append`, set by set_encoders
+        self.W_enc = self.b_enc = self.key_scale = self.update_work = None
+        self.key_mean = 0
+        self.update_block = 0
 
     def _stream(self):
         return torch.cuda.current_stream().cuda_stream
@@ -209,6 +226,107 @@ class Native8B:
                       self.out.data_ptr(), GROUPS, self.history, k.shape[1] - self.history, self.capacity,
                       self.row_words, k.stride(0), v.stride(0), self.capacity, stream=self._stream())
         return self.out
+
+    # ------------------------------------------------------------ stage 4
+
+    def set_encoders(self, saes, key_scales):
+        """Per-group encoders for `append`: `saes[g]` has W_enc [3000,128],
+        b_enc [3000] and key_mean (SharedSAE, src/prismkv/core.py:29-48) and
+        `key_scales[g]` > 0 is its key scale -- the reference's
+        encoders[(layer, group)] bundle (src/prismkv/hf_reference.py:196-211)."""
+        if len(saes) != GROUPS or len(key_scales) != GROUPS:
+            raise ValueError("one SAE and key scale per KV group required")
+        means = {int(s.key_mean) for s in saes}
+        if len(means) != 1:
+            raise ValueError("all groups must share one key_mean")
+        W = torch.stack([torch.as_tensor(s.W_enc).detach() for s in saes])
+        b = torch.stack([torch.as_tensor(s.b_enc).detach() for s in saes])
+        self.set_encoder_tables(W, b, key_scales, means.pop())
+
+    def set_encoder_tables(self, W, b, key_scale, key_mean):
+        """Encoder tables directly: W [8,3000,128], b [8,3000], key_scale [8]
+        (each > 0), key_mean in [1, 3000].  Copied to the device as f32."""
+        device = self.out.device
+        W = torch.as_tensor(W).to(device=device, dtype=torch.float32).contiguous()
+        b = torch.as_tensor(b).to(device=device, dtype=torch.float32).contiguous()
+        scale = torch.as_tensor(key_scale, dtype=torch.float32).reshape(-1).to(device)
+        if tuple(W.shape) != (GROUPS, FEATURES, DIM) or tuple(b.shape) != (GROUPS, FEATURES):
+            raise ValueError("W_enc [8,3000,128] and b_enc [8,3000] required")
+        if scale.numel() != GROUPS or not bool((scale > 0).all()):
+            raise ValueError("positive key_scale per group required")
+        if not 1 <= int(key_mean) <= FEATURES:
+            raise ValueError("invalid sparsity")
+        self.W_enc, self.b_enc, self.key_scale, self.key_mean = W, b, scale.contiguous(), int(key_mean)
+
+    def append(self, k, block):
+        """append_index (src/prismkv/core.py:186-201) for all 8 groups: index
+        K rows [history, history + block) with the encoders and the ORIGINAL
+        centers, BatchTopK over the block only (budget block * key_mean),
+        merge their moments into the tables and add their memberships; then
+        history += block.  Enqueued on the current stream; the workspace is
+        allocated on the first call with a larger block than before."""
+        if self.W_enc is None:
+            raise ValueError("set_encoders before append")
+        if self.center is None:
+            raise ValueError("the index centers are required to append")
+        block = int(block)
+        if not 1 <= block <= MAX_BLOCK:
+            raise ValueError(f"block must be in [1, {MAX_BLOCK}]")
+        if k.dtype != torch.bfloat16 or k.dim() != 3 or k.shape[0] != GROUPS or k.shape[-1] != DIM:
+            raise ValueError("BF16 K[8,total_length,128] required")
+        if k.stride(-1) != 1 or k.stride(1) != DIM or k.device != self.out.device:
+            raise ValueError("contiguous per-group K rows on the index device required")
+        if k.shape[1] < self.history + block:
+            raise ValueError("K does not hold the block to index")
+        if self.history + block > self.capacity:
+            raise ValueError("capacity exceeded: rebuild with a larger capacity")
+        if block > self.update_block:
+            self.update_work = torch.zeros(self.lib.query("prismkv_update_work_bytes", GROUPS, block),
+                                           dtype=torch.uint8, device=self.out.device)
+            self.update_block = block
+        self.lib.call("prismkv_update", k.data_ptr(), self.W_enc.data_ptr(), self.b_enc.data_ptr(),
+                      self.center.data_ptr(), self.key_scale.data_ptr(), self.bits.data_ptr(), self.n.data_ptr(),
+                      self.moments.data_ptr(), self.update_work.data_ptr(), GROUPS, self.history, block,
+                      self.key_mean, k.stride(0), self.row_words, stream=self._stream())
+        self.history += block
+
+    def update_activations(self, block):
+        """The last append's dense activations relu(x W^T + b) [8,block,3000]
+        (a view of the workspace, valid until the next append)."""
+        if self.update_work is None or not 1 <= block <= self.update_block:
+            raise ValueError("no append with this block size")
+        n = GROUPS * block * FEATURES
+        return self.update_work[:4 * n].view(torch.float32).view(GROUPS, block, FEATURES)
+
+    def catch_up(self, k, total=None, update_interval=MAX_BLOCK):
+        """Index complete old tail blocks while more than `update_interval`
+        tokens follow the history (src/prismkv/hf_reference.py:209-211);
+        returns the number of blocks appended."""
+        total = k.shape[1] if total is None else int(total)
+        blocks = 0
+        while total - self.history > update_interval:
+            self.append(k, update_interval)
+            blocks += 1
+        return blocks
+
+    def export_indices(self):
+        """The device tables as 8 FeatureIndex objects (counts i64, mean and
+        variance f32 [3000,128], centers on the device; per-bucket ascending
+        token lists as host int64 tensors).  Synchronises; allocates."""
+        mean, var = untile_moments(self.moments)
+        h = self.history
+        shifts = torch.arange(32, device=self.bits.device, dtype=torch.int32)
+        out = []
+        for g in range(GROUPS):
+            words = self.bits[g, :, :(h + 31) // 32]
+            flags = ((words.unsqueeze(-1) >> shifts) & 1).to(torch.bool).reshape(FEATURES, -1)[:, :h]
+            f, t = flags.nonzero(as_tuple=True)
+            per = torch.bincount(f, minlength=FEATURES).tolist()
+            lists = list(torch.split(t.cpu(), per))
+            center = None if self.center is None else self.center[g].clone()
+            out.append(FeatureIndex(h, center, self.n[g, :FEATURES].long().clone(), mean[g].contiguous(),
+                                    var[g].contiguous(), lists))
+        return out
 
     def buffer_bytes(self):
         """Live tensors owned here; excludes model/KV, caller indices and build temporaries."""

@@ -52,6 +52,10 @@ def test_work_size_queries(lib):
     assert lib.query("prismkv_route_work_bytes", 0) == 0
     assert lib.query("prismkv_union_work_bytes", 8, 65536) > 8
     assert lib.query("prismkv_attend_work_bytes", 8, 64) >= 8 * 4 * 64 * 130 * 4
+    # the update workspace holds the block's dense activations [G][N][3000] f32
+    assert lib.query("prismkv_update_work_bytes", 8, 4096) >= 8 * 4096 * 3000 * 4
+    assert lib.query("prismkv_update_work_bytes", 8, 4097) == 0
+    assert lib.query("prismkv_update_work_bytes", 0, 16) == 0
 
 
 def call_raw(lib, name, *args):
@@ -81,6 +85,13 @@ def test_native_error_codes(lib):
     assert call_raw(lib, "prismkv_union", *[1] * 6, 8, 100, 4, 99) == -1   # ids stride too small
     assert call_raw(lib, "prismkv_attend", *[1] * 7, 8, 10, 2, 12 * 128, 12 * 128, 10, 0) == -1  # splits
     assert call_raw(lib, "prismkv_attend", *[1] * 7, 8, 10, 2, 11 * 128, 12 * 128, 10, 4) == -1  # ks
+    # prismkv_update(k, W, b, center, scale, bits, counts, moments, work, groups, H, N, key_mean, ks, row_words)
+    good = (100 + 64) * 128
+    for G, H, N, km, ks, rw in [(8, 100, 0, 8, good, 8), (8, 100, 4097, 8, 4197 * 128, 132), (8, 100, 64, 0, good, 8),
+                                (8, 100, 64, 3001, good, 8), (8, 100, 64, 8, good - 1, 8), (8, 100, 64, 8, good, 5),
+                                (0, 100, 64, 8, good, 8), (8, -1, 64, 8, good, 8)]:
+        assert call_raw(lib, "prismkv_update", *[1] * 9, G, H, N, km, ks, rw) == -1, (G, H, N, km, ks, rw)
+    assert call_raw(lib, "prismkv_update", *[0] * 9, 8, 100, 64, 8, good, 8) == -1  # null pointers
 
 
 def test_native8b_host_validation_without_gpu():
