@@ -35,6 +35,12 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "routed decode µs/layer at 64K history (8 groups); per-stage HBM GB/s vs peak"
 PPU_US_PER_LAYER_64K = 108.3  # whole sparse chain, PPU-ZW810 (tail 8)
 G, HQ, D, F, TOPK = 8, 4, 128, 3000, 16
+# HBM bytes per launch from the two counter passes (FETCH_SIZE, WRITE_SIZE)
+# over this workload, each scaled by what the counter reads for a 1 GiB
+# streaming kernel; measured at H=65536, T=256 only.
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "decode_kernel_64k_hbm_traffic.md")
+STAGE_KERNEL = {"select_union_attend": "decode_kernel", "score": "route_score_kernel"}
 
 
 def parse():
@@ -48,7 +54,9 @@ def parse():
     p.add_argument("--seed", type=int, default=2)
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU-baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--stages", default="chain,decode,route,union,attend,copy",
+    p.add_argument("--update-blocks", default="1024,4096",
+                   help="block sizes of the amortised index-update timing (tokens per append)")
+    p.add_argument("--stages", default="chain,decode,route,union,attend,update,copy",
                    help="comma list of timed regions (for profiling runs)")
     return p.parse_args()
 
@@ -98,6 +106,18 @@ def make_layer(lib_path, layer, H, T, seed, device):
     return op, q, k, v
 
 
+def measured_traffic(stage, H, T):
+    """Counter-derived HBM bytes per launch of the stage's kernel, or None."""
+    if (H, T) != (65536, 256) or stage not in STAGE_KERNEL or not os.path.exists(TRAFFIC_PROFILE):
+        return None
+    with open(TRAFFIC_PROFILE) as fh:
+        for line in fh:
+            parts = line.split()
+            if len(parts) == 3 and parts[0] == "traffic_bytes_per_launch" and parts[1] == STAGE_KERNEL[stage]:
+                return int(parts[2])
+    return None
+
+
 def graph_time(fn, steps, warmup):
     """Capture fn once, replay; returns (ms per replay by events, ms per replay wall)."""
     cur = torch.cuda.current_stream()
@@ -136,6 +156,50 @@ def stage_bytes(ops, H, T):
         avs.append(int(((u + T) * 2 * D * 2 + u * 4 + 4).sum() + 2 * G * HQ * D * 2))
         uniq.append(u.mean())
     return route, float(np.mean(unions)), float(np.mean(avs)), float(np.mean(uniq))
+
+
+@torch.no_grad()
+def update_timing(lib_path, H, blocks, steps, warmup, seed, device):
+    """Amortised index update: one prismkv_update launch sequence per replay
+    (encode, BatchTopK threshold, bitmap append, moment merge for 8 groups),
+    indexing a block of N keys at history H - N of a dedicated table (so the
+    decode tables are untouched).  Every replay indexes the same block."""
+    from prismkv_amd import Native8B
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed * 7919)
+    out = {}
+    N_max = max(blocks)
+    k = torch.randn(G, H, D, generator=gen, device=device).to(torch.bfloat16)
+    W = torch.randn(G, F, D, generator=gen, device=device) / D ** 0.5
+    b = torch.zeros(G, F, device=device)
+    for N in blocks:
+        h0 = H - N
+        counts = torch.full((G, F), 8, dtype=torch.int64, device=device)
+        mean = torch.randn(G, F, D, generator=gen, device=device) * 0.1
+        var = torch.rand(G, F, D, generator=gen, device=device)
+        csr = torch.zeros(G, 1, dtype=torch.int32, device=device)
+        offs = torch.zeros(G, F + 1, dtype=torch.int32, device=device)
+        op = Native8B.from_tables(h0, counts, mean, var, csr, offs, lib_path, capacity=H,
+                                  center=k[:, :h0].float().mean(1))
+        op.set_encoder_tables(W, b, torch.ones(G), 8)
+        op.append(k, N)  # allocates the workspace; history -> H
+        torch.cuda.synchronize()
+
+        def once():
+            op.lib.call("prismkv_update", k.data_ptr(), op.W_enc.data_ptr(), op.b_enc.data_ptr(),
+                        op.center.data_ptr(), op.key_scale.data_ptr(), op.bits.data_ptr(), op.n.data_ptr(),
+                        op.moments.data_ptr(), op.update_work.data_ptr(), G, h0, N, 8, k.stride(0), op.row_words,
+                        stream=torch.cuda.current_stream().cuda_stream)
+        ms, _, _ = graph_time(once, steps, warmup)
+        us = ms * 1e3
+        flops = 2.0 * G * N * F * D
+        out[str(N)] = dict(us_per_block=round(us, 2), us_per_token_per_layer=round(us / N, 4),
+                           encode_gflop=round(flops / 1e9, 2), encode_tflops_if_alone=round(flops / (us * 1e-6) / 1e12, 2))
+        log(f"update N={N}: {us:.1f} us per block ({us / N:.3f} us per token per layer, amortised)")
+        del op
+    del k, W, b
+    torch.cuda.empty_cache()
+    return out
 
 
 def cpu_baseline(op, q, k, v, H, budget_s):
@@ -245,27 +309,34 @@ def main():
                                   achieved_GBps=round(gbs, 1), frac_of_peak=round(gbs / HBM_PEAK_GBS, 4))
     copy_gbs = None
     if "copy" in stages:
-        src = torch.empty(2 ** 30, dtype=torch.uint8, device=device)
+        # a plain streaming kernel of known size (1 GiB read + 1 GiB written): the
+        # attainable-bandwidth probe, and the reference for HBM byte counters
+        src = torch.ones(2 ** 28, dtype=torch.float32, device=device)
         dst = torch.empty_like(src)
         for _ in range(3):
-            dst.copy_(src)
+            torch.neg(src, out=dst)
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(10):
-            dst.copy_(src)
+            torch.neg(src, out=dst)
         e1.record()
         torch.cuda.synchronize()
         copy_gbs = 2 * 2 ** 30 * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9
         log(f"copy probe: {copy_gbs:.0f} GB/s (read+write)")
         del src, dst
+    update = None
+    if "update" in stages:
+        blocks = [int(x) for x in a.update_blocks.split(",") if x]
+        update = update_timing(lib_path, H, blocks, a.steps, a.warmup, a.seed, device)
     fused = [n for n in ("score", "select_union_attend") if n in stage_report]
     dominant = max(fused or stage_report, key=lambda n: stage_report[n]["us_per_launch"]) if stage_report else None
     roofline = None
     if dominant:
         d = stage_report[dominant]
         roofline = dict(bound="hbm", achieved=d["achieved_GBps"], peak=HBM_PEAK_GBS, unit="GB/s",
-                        frac=d["frac_of_peak"], traffic=None, kernel=dominant)
+                        frac=d["frac_of_peak"], traffic=measured_traffic(dominant, H, T),
+                        kernel=STAGE_KERNEL.get(dominant, dominant), algorithmic_bytes=d["algorithmic_bytes"])
     cpu = None
     if not a.no_cpu_baseline:
         op, q, k, v = layers[0]
@@ -283,7 +354,7 @@ def main():
                    "layers": a.layers, "groups": G, "history": H, "tail": T,
                    "kv_dtype": "bf16", "mean_unique_ids_per_group": round(uniq, 1), "parallelism": "single GPU"},
         "wall_ms_per_step": round(wall, 4), "stages": stage_report, "copy_probe_GBps": copy_gbs and round(copy_gbs, 1),
-        "roofline": roofline, "cpu_baseline": cpu,
+        "update": update, "roofline": roofline, "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
 

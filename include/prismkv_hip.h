@@ -67,7 +67,8 @@ int attention_tuned(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t c
 /* ---- MI355X-native entry points ---- */
 
 /* Stage 1 (replaces pack + torch.bmm + fused_norm_top, src/prismkv/native8b.py:85-87;
- * semantics src/prismkv/core.py:106-130): one launch for G groups. */
+ * semantics src/prismkv/core.py:106-130): moment scoring, per-part Top-16
+ * candidates and the final Top-16, three launches for G groups. */
 size_t prismkv_route_work_bytes(int groups);
 int prismkv_route(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
                   uint64_t valid, uint64_t raw, int groups, uint64_t stream);
