@@ -79,6 +79,15 @@ size_t prismkv_union_work_bytes(int groups, int H);
 int prismkv_union(uint64_t bits, uint64_t features, uint64_t valid, uint64_t work, uint64_t ids,
                   uint64_t count, int groups, int H, int64_t row_words, int64_t ids_stride, uint64_t stream);
 
+/* Stage 2, strict unique-ID budget (src/prismkv/core.py:149-163, select_buckets
+ * with unique_cap): walks the ranked buckets (rows with valid > 0, in rank
+ * order) and keeps a bucket only if the union of the kept buckets stays within
+ * `limit` = floor(H * unique_cap) tokens, skipping one that would overflow;
+ * rewrites features / valid / raw with the kept buckets compacted to the front
+ * in rank order (then run prismkv_union).  H <= 2^20; counts i32 [G][3008]. */
+int prismkv_select_cap(uint64_t bits, uint64_t counts, uint64_t features, uint64_t valid, uint64_t raw, int groups,
+                       int H, int64_t limit, int64_t row_words, uint64_t stream);
+
 /* Bitmap build from CSR (replaces build_bits, src/prismkv/native8b.py:66-70):
  * ids i32 [G][cap], offsets i32 [G][3001]; bits must be zeroed by the caller. */
 int prismkv_build_bits(uint64_t ids, uint64_t offsets, uint64_t bits, int groups, int64_t cap,

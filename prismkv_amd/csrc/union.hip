@@ -251,6 +251,157 @@ __global__ __launch_bounds__(256) void bits_kernel(const int* __restrict__ ids, 
   }
 }
 
+// Strict unique-ID budget (src/prismkv/core.py:149-163): walk the ranked
+// buckets (rows with valid > 0, in rank order) and accept a bucket only if
+// the tokens it adds to the running union keep the union within `limit`;
+// a bucket that would overflow is skipped and the walk continues.  Rewrites
+// features / valid / raw with the accepted buckets compacted to the front in
+// rank order (unused slots id 0, valid 0), which the union then consumes.
+//
+// One workgroup of kCapT threads per group.  Thread tid owns bitmap words
+// tid + kCapT u (u < WPT) of every row and keeps its slice of the running
+// union in registers; each bucket costs one block-wide popcount reduction.
+// With kAhead the next bucket's words are requested before the current
+// bucket's reduction, so the row loads overlap the decisions.
+template <int kCapT, int WPT, bool kAhead>
+__global__ __launch_bounds__(kCapT) void cap_kernel(const uint32_t* __restrict__ bits, int64_t row_words,
+                                                    const int* __restrict__ counts, int64_t* features, float* valid,
+                                                    int* raw, int H, long long limit) {
+  const int g = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  __shared__ int sel[kTop], nsel_s;
+  __shared__ int part[2][kCapT / 64];
+  if (tid == 0) {
+    int n = 0;
+    for (int j = 0; j < kTop; ++j) {
+      const int64_t f = features[(size_t)g * kTop + j];
+      if (valid[(size_t)g * kTop + j] > 0.f && f >= 0 && f < kF) sel[n++] = (int)f;
+    }
+    nsel_s = n;
+  }
+  __syncthreads();
+  const int n = nsel_s;
+  const int nw = (H + 31) >> 5;
+  const uint32_t tail_mask = (H & 31) ? (1u << (H & 31)) - 1u : ~0u;
+  const uint32_t* bg = bits + (size_t)g * kF * row_words;
+  auto load_row = [&](int j, uint32_t (&r)[WPT]) {
+    const uint32_t* row = bg + (size_t)sel[j] * row_words;
+#pragma unroll
+    for (int u = 0; u < WPT; ++u) {
+      const int wd = tid + u * kCapT;
+      const uint32_t m = wd < nw ? row[wd] : 0u;
+      r[u] = wd == nw - 1 ? (m & tail_mask) : m;
+    }
+  };
+  uint32_t chosen[WPT], cur[WPT], nxt[WPT];
+#pragma unroll
+  for (int u = 0; u < WPT; ++u) chosen[u] = cur[u] = nxt[u] = 0u;
+  if (kAhead && n > 0) load_row(0, cur);
+  long long total = 0;
+  int raw_sum = 0;
+  unsigned accepted = 0;
+  for (int j = 0; j < n; ++j) {
+    if (kAhead) {
+      if (j + 1 < n) load_row(j + 1, nxt);
+    } else {
+      load_row(j, cur);
+    }
+    int c = 0;
+#pragma unroll
+    for (int u = 0; u < WPT; ++u) c += __popc(cur[u] & ~chosen[u]);
+    c = wave_sum_i(c);
+    if (lane == 0) part[j & 1][w] = c;
+    __syncthreads();
+    // part[j & 1] is rewritten two buckets later, after the next barrier
+    long long add = 0;
+#pragma unroll
+    for (int i = 0; i < kCapT / 64; ++i) add += part[j & 1][i];
+    if (total + add <= limit) {  // uniform: every thread holds the same sums
+#pragma unroll
+      for (int u = 0; u < WPT; ++u) chosen[u] |= cur[u];
+      total += add;
+      raw_sum += counts[(size_t)g * kFP + sel[j]];
+      accepted |= 1u << j;
+    }
+    if (kAhead) {
+#pragma unroll
+      for (int u = 0; u < WPT; ++u) cur[u] = nxt[u];
+    }
+  }
+  if (tid == 0) {
+    int at = 0;
+    for (int j = 0; j < n; ++j)
+      if (accepted >> j & 1u) features[(size_t)g * kTop + at++] = sel[j];
+    for (int j = 0; j < kTop; ++j) {
+      if (j >= at) features[(size_t)g * kTop + j] = 0;
+      valid[(size_t)g * kTop + j] = j < at ? 1.f : 0.f;
+    }
+    raw[g] = raw_sum;
+  }
+}
+
+// The same walk for histories up to 2^20 tokens: the running union lives in
+// LDS (up to 32768 words) and an accepted bucket's words are read a second
+// time (from L2) to merge them in.
+constexpr int kCapBigT = 1024;
+constexpr int kCapMaxWords = 32768;
+
+__global__ __launch_bounds__(kCapBigT) void cap_big_kernel(const uint32_t* __restrict__ bits, int64_t row_words,
+                                                           const int* __restrict__ counts, int64_t* features,
+                                                           float* valid, int* raw, int H, long long limit) {
+  const int g = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  __shared__ int sel[kTop], nsel_s;
+  __shared__ int part[2][kCapBigT / 64];
+  __shared__ uint32_t chosen[kCapMaxWords];
+  const int nw = (H + 31) >> 5;
+  for (int i = tid; i < nw; i += kCapBigT) chosen[i] = 0u;
+  if (tid == 0) {
+    int n = 0;
+    for (int j = 0; j < kTop; ++j) {
+      const int64_t f = features[(size_t)g * kTop + j];
+      if (valid[(size_t)g * kTop + j] > 0.f && f >= 0 && f < kF) sel[n++] = (int)f;
+    }
+    nsel_s = n;
+  }
+  __syncthreads();
+  const int n = nsel_s;
+  const uint32_t tail_mask = (H & 31) ? (1u << (H & 31)) - 1u : ~0u;
+  const uint32_t* bg = bits + (size_t)g * kF * row_words;
+  long long total = 0;
+  int raw_sum = 0;
+  unsigned accepted = 0;
+  for (int j = 0; j < n; ++j) {
+    const uint32_t* row = bg + (size_t)sel[j] * row_words;
+    int c = 0;
+    for (int i = tid; i < nw; i += kCapBigT) {
+      const uint32_t m = i == nw - 1 ? (row[i] & tail_mask) : row[i];
+      c += __popc(m & ~chosen[i]);
+    }
+    c = wave_sum_i(c);
+    if (lane == 0) part[j & 1][w] = c;
+    __syncthreads();
+    long long add = 0;
+#pragma unroll
+    for (int i = 0; i < kCapBigT / 64; ++i) add += part[j & 1][i];
+    if (total + add <= limit) {  // uniform
+      // each thread merges exactly the words it counted: no other thread touches them
+      for (int i = tid; i < nw; i += kCapBigT) chosen[i] |= i == nw - 1 ? (row[i] & tail_mask) : row[i];
+      total += add;
+      raw_sum += counts[(size_t)g * kFP + sel[j]];
+      accepted |= 1u << j;
+    }
+  }
+  if (tid == 0) {
+    int at = 0;
+    for (int j = 0; j < n; ++j)
+      if (accepted >> j & 1u) features[(size_t)g * kTop + at++] = sel[j];
+    for (int j = 0; j < kTop; ++j) {
+      if (j >= at) features[(size_t)g * kTop + j] = 0;
+      valid[(size_t)g * kTop + j] = j < at ? 1.f : 0.f;
+    }
+    raw[g] = raw_sum;
+  }
+}
+
 }  // namespace
 }  // namespace prismkv
 
@@ -266,6 +417,28 @@ static int union_wpt(int H, int64_t row_words) {
 }
 
 extern "C" {
+
+int prismkv_select_cap(uint64_t bits, uint64_t counts, uint64_t features, uint64_t valid, uint64_t raw, int groups,
+                       int H, int64_t limit, int64_t row_words, uint64_t stream) {
+  if (groups < 1 || groups > 65535 || H < 1 || H > (1 << 20) || limit < 0) return kBadSize;
+  if (row_words < (H + 31) / 32) return kBadSize;
+  if (!bits || !counts || !features || !valid || !raw) return kBadSize;
+  const int nw = (H + 31) / 32;
+  const uint32_t* b = reinterpret_cast<const uint32_t*>(bits);
+  const int* c = reinterpret_cast<const int*>(counts);
+  int64_t* f = reinterpret_cast<int64_t*>(features);
+  float* v = reinterpret_cast<float*>(valid);
+  int* r = reinterpret_cast<int*>(raw);
+  hipStream_t s = (hipStream_t)stream;
+  const long long lim = (long long)limit;
+  if (nw <= 2 * 1024)
+    hipLaunchKernelGGL((cap_kernel<1024, 2, true>), dim3(groups), dim3(1024), 0, s, b, row_words, c, f, v, r, H, lim);
+  else if (nw <= 8 * 1024)
+    hipLaunchKernelGGL((cap_kernel<1024, 8, true>), dim3(groups), dim3(1024), 0, s, b, row_words, c, f, v, r, H, lim);
+  else  // up to 2^20 tokens
+    hipLaunchKernelGGL(cap_big_kernel, dim3(groups), dim3(kCapBigT), 0, s, b, row_words, c, f, v, r, H, lim);
+  return (int)hipGetLastError();
+}
 
 size_t prismkv_union_work_bytes(int groups, int H) {
   if (groups < 1 || H < 1) return 0;

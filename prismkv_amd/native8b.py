@@ -13,6 +13,11 @@ shapes as the reference binding:
   the preallocated ``out`` buffer, overwritten by the next call
   (src/prismkv/native8b.py:91-102);
 * ``__call__`` = route + attention; ``buffer_bytes()`` lists live buffers;
+* ``unique_cap`` (constructor keyword or attribute, default None) applies the
+  strict unique-ID budget of ``select_buckets`` (src/prismkv/core.py:149-163):
+  ranked buckets that would push the union past floor(history * unique_cap)
+  tokens are skipped, and ``features`` / ``valid`` / ``raw`` list the kept
+  buckets in rank order;
 * ``append(k, block)`` is the reference's ``append_index``
   (src/prismkv/core.py:186-201) for all 8 groups on the device tables in
   place (after ``set_encoders``); ``catch_up`` is the update loop of
@@ -28,6 +33,7 @@ constructor raises.
 """
 from __future__ import annotations
 
+import math
 from dataclasses import dataclass
 
 import torch
@@ -86,7 +92,7 @@ def bitmap_row_words(capacity: int) -> int:
 
 
 class Native8B:
-    def __init__(self, indices, library=None, *, capacity=None):
+    def __init__(self, indices, library=None, *, capacity=None, unique_cap=None):
         if len(indices) != GROUPS:
             raise ValueError("native specialization requires 8 KV groups")
         h = int(indices[0].history)
@@ -108,10 +114,11 @@ class Native8B:
                         torch.stack([torch.as_tensor(x.mean).to(device) for x in indices]),
                         torch.stack([torch.as_tensor(x.variance).to(device) for x in indices]), csr, offsets,
                         torch.stack([torch.as_tensor(x.center).to(device) for x in indices]))
+        self.unique_cap = unique_cap
 
     @classmethod
     def from_tables(cls, history, counts, mean, variance, csr_ids, offsets, library=None, *, capacity=None,
-                    center=None):
+                    center=None, unique_cap=None):
         """Build from device tables directly: counts [8,3000], mean/variance
         [8,3000,128] f32, csr_ids i32 [8,C] (bucket f owns columns
         offsets[g,f] .. offsets[g,f+1]), offsets i32 [8,3001] and, for
@@ -124,6 +131,7 @@ class Native8B:
         with torch.cuda.device(counts.device):
             obj._setup(int(history), capacity, library, counts, mean, variance, csr_ids.int().contiguous(),
                        offsets.int().contiguous(), center)
+        obj.unique_cap = unique_cap
         return obj
 
     def _setup(self, h, capacity, library, counts, mean, variance, csr, offsets, center=None):
@@ -174,6 +182,17 @@ class Native8B:
     def _stream(self):
         return torch.cuda.current_stream().cuda_stream
 
+    @property
+    def unique_cap(self):
+        return self.__dict__.get("_unique_cap")
+
+    @unique_cap.setter
+    def unique_cap(self, cap):
+        # same check and message as src/prismkv/core.py:149-150
+        if cap is not None and not 0 <= cap <= 1:
+            raise ValueError("unique_cap must be a fraction in [0,1]")
+        self.__dict__["_unique_cap"] = cap
+
     def route(self, q):
         if tuple(q.shape) != (GROUPS, HEADS, DIM) or q.dtype != torch.bfloat16 or not q.is_contiguous():
             raise ValueError("contiguous BF16 Q[8,4,128] required")
@@ -183,6 +202,11 @@ class Native8B:
         self.lib.call("prismkv_route", q.data_ptr(), self.moments.data_ptr(), self.n.data_ptr(),
                       self.route_work.data_ptr(), self.features.data_ptr(), self.valid.data_ptr(),
                       self.raw.data_ptr(), GROUPS, stream=s)
+        if self.unique_cap is not None:
+            limit = math.floor(self.history * self.unique_cap)
+            self.lib.call("prismkv_select_cap", self.bits.data_ptr(), self.n.data_ptr(), self.features.data_ptr(),
+                          self.valid.data_ptr(), self.raw.data_ptr(), GROUPS, self.history, limit, self.row_words,
+                          stream=s)
         self.lib.call("prismkv_union", self.bits.data_ptr(), self.features.data_ptr(), self.valid.data_ptr(),
                       self.union_work.data_ptr(), self.ids.data_ptr(), self.count.data_ptr(), GROUPS, self.history,
                       self.row_words, self.capacity, stream=s)
@@ -220,6 +244,9 @@ class Native8B:
         decode path: two launches, identical results, every output buffer
         (features, valid, raw, ids, count, out) written as by the two calls."""
         self._check_kv(q, k, v, kwargs.get("splits", 64), kwargs.get("schedule", 0))
+        if self.unique_cap is not None:  # the budgeted walk runs between selection and union
+            self.route(q)
+            return self.attention(q, k, v, **kwargs)
         self.lib.call("prismkv_decode", q.data_ptr(), self.moments.data_ptr(), self.n.data_ptr(), self.bits.data_ptr(),
                       k.data_ptr(), v.data_ptr(), self.decode_work.data_ptr(), self.features.data_ptr(),
                       self.valid.data_ptr(), self.raw.data_ptr(), self.ids.data_ptr(), self.count.data_ptr(),

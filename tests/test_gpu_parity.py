@@ -8,6 +8,7 @@ import numpy as np
 import pytest
 import torch
 
+import oracle
 from oracle import cases, expect
 from tests.gpu_util import bf16_bits, log, operator, route_outputs
 
@@ -144,3 +145,48 @@ def test_graph_replay_matches_eager():
 def test_union_262k_history():
     # H beyond the reference union limit (131072): 8 groups x 262144 tokens
     check_case(cases.native_case(262144, 64, "random", seed=5), splits_list=(128,), schedules=(0,))
+
+
+@pytest.mark.parametrize("H,tail,kind,cap", [(65, 7, "few", 0.3), (1025, 3, "random", 0.01),
+                                             (65536, 17, "random", 0.002), (262144, 5, "random", 0.01),
+                                             (300000, 7, "random", 0.005)])
+def test_strict_unique_cap(H, tail, kind, cap):
+    # src/prismkv/core.py:149-163: with a cap, a ranked bucket whose new ids would
+    # push the union past floor(H * cap) is skipped and the walk goes on.  The
+    # device's own ranked order (checked against the oracle first) is fed to the
+    # oracle's select_buckets, so the budgeted walk is checked bit-exactly.
+    # The three walk variants: up to 2048 bitmap words (H <= 65536), up to 8192
+    # (H = 262144, the stress history) and the LDS-union one (H = 300000).
+    case = cases.native_case(H, tail, kind)
+    log(f"cap case kind={kind} H={H} T={tail} cap={cap}")
+    op, q, k, v = operator(case)
+    op.route(q)
+    groups = expect.expected(case)
+    identical, near = expect.compare_route(groups, *route_outputs(op))
+    assert identical + near == 8
+    features, valid, _, _, _ = route_outputs(op)
+    orders = [features[g][valid[g] > 0] for g in range(8)]
+    op.unique_cap = cap
+    op.route(q)
+    f2, v2, r2, i2, c2 = route_outputs(op)
+    want = []
+    skipped = 0
+    for g in range(8):
+        ids, meta = oracle.select_buckets(orders[g], case["indices"][g].lists, H, cap)
+        nf = len(meta["features"])
+        skipped += len(orders[g]) - nf
+        assert f2[g][:nf].tolist() == meta["features"], ("kept buckets", g)
+        assert not f2[g][nf:].any() and v2[g].tolist() == [1.0] * nf + [0.0] * (16 - nf), ("padding", g)
+        assert int(r2[g]) == meta["raw"] and int(c2[g]) == len(ids) <= meta["limit"], ("raw/count", g)
+        assert np.array_equal(i2[g][:len(ids)].astype(np.int64), ids), ("ids", g)
+        want.append(dict(ids=ids))
+    log(f"  {skipped} ranked buckets skipped by the budget across 8 groups")
+    expected = expect.expected_attention(case, want)
+    out = op.attention(q, k, v)
+    torch.cuda.synchronize()
+    first = bf16_bits(out).copy()
+    err = expect.attention_errors(first, expected)
+    assert err["rel_l2"] <= AV_TOL and err["max_abs"] < 0.05, err
+    out = op(q, k, v)  # __call__ with a cap: same kernels, same bits
+    torch.cuda.synchronize()
+    assert np.array_equal(bf16_bits(out), first)
