@@ -11,14 +11,14 @@ HBM; 36 distinct layers (~17.7 GB) rotate so nothing is served from the
 
 A "step" is one decode step through all layers: for every layer the
 Native8B call (route: moment scoring + Top-16, union: bitmap OR + compaction,
-sparse AV) -- two launches per layer, moment scoring and the fused
-selection/union/attention kernel -- captured once in a HIP graph and
-replayed.  The headline value is the replay time per layer in microseconds
-(lower is better).  Per-stage times come from isolated-stage graphs (one
-launch per layer); the separate route/union/attend entry points are timed
-too.  The roofline object reports the dominant kernel's algorithmic bytes per
-launch over its average launch time.  The CPU baseline times the C oracle (single thread) on a bounded
-sample of the same layer workload.
+sparse AV) -- ONE launch per layer, the fused decode kernel -- captured once
+in a HIP graph and replayed.  The headline value is the replay time per
+layer in microseconds (lower is better); since every layer is one launch of
+the decode kernel, it is also that kernel's average launch time, which the
+roofline object divides the algorithmic bytes by.  The separate
+route/union/attend entry points are timed in isolated-stage graphs too.  The
+CPU baseline times the C oracle (single thread) on a bounded sample of the
+same layer workload.
 """
 from __future__ import annotations
 
@@ -40,7 +40,7 @@ G, HQ, D, F, TOPK = 8, 4, 128, 3000, 16
 # streaming kernel; measured at H=65536, T=256 only.
 TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                "decode_kernel_64k_hbm_traffic.md")
-STAGE_KERNEL = {"select_union_attend": "decode_kernel", "score": "route_score_kernel"}
+STAGE_KERNEL = {"decode": "decode_kernel"}
 
 
 def parse():
@@ -56,7 +56,7 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--update-blocks", default="1024,4096",
                    help="block sizes of the amortised index-update timing (tokens per append)")
-    p.add_argument("--stages", default="chain,decode,route,union,attend,update,copy",
+    p.add_argument("--stages", default="chain,route,union,attend,update,copy",
                    help="comma list of timed regions (for profiling runs)")
     return p.parse_args()
 
@@ -252,22 +252,9 @@ def main():
     def stream():
         return torch.cuda.current_stream().cuda_stream
 
-    def chain():  # the decode step: Native8B.__call__ = route + attention (fused path, 2 launches per layer)
+    def chain():  # the decode step: Native8B.__call__ = route + attention (fused path, 1 launch per layer)
         for op, q, k, v in layers:
             op(q, k, v)
-
-    def score_only():
-        for op, q, k, v in layers:
-            op.lib.call("prismkv_decode_score", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(),
-                        op.decode_work.data_ptr(), G, op.capacity, stream=stream())
-
-    def decode_attend_only():
-        for op, q, k, v in layers:
-            op.lib.call("prismkv_decode_attend", q.data_ptr(), op.n.data_ptr(), op.bits.data_ptr(), k.data_ptr(),
-                        v.data_ptr(), op.decode_work.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(),
-                        op.raw.data_ptr(), op.ids.data_ptr(), op.count.data_ptr(), op.out.data_ptr(), G, op.history,
-                        k.shape[1] - op.history, op.capacity, op.row_words, k.stride(0), v.stride(0), op.capacity,
-                        stream=stream())
 
     def route_only():
         for op, q, k, v in layers:
@@ -289,19 +276,18 @@ def main():
     ms, wall, _ = graph_time(chain, a.steps, a.warmup) if "chain" in stages else (float("nan"),) * 3
     log(f"chain: {ms:.4f} ms/step events, {wall:.4f} ms/step wall")
     per_stage = {}
-    stage_fns = (("score", score_only), ("select_union_attend", decode_attend_only), ("route", route_only),
-                 ("union", union_only), ("attend", attend_only))
+    if "chain" in stages:
+        per_stage["decode"] = ms * 1e3 / a.layers  # one decode_kernel launch per layer
+    stage_fns = (("route", route_only), ("union", union_only), ("attend", attend_only))
     for name, fn in stage_fns:
-        if name in stages or (name in ("score", "select_union_attend") and "decode" in stages):
+        if name in stages:
             sm, _, _ = graph_time(fn, a.steps, a.warmup)
             per_stage[name] = sm * 1e3 / a.layers
             log(f"{name}: {per_stage[name]:.2f} us/launch")
     chain()
     torch.cuda.synchronize()
     b_route, b_union, b_av, uniq = stage_bytes([l[0] for l in layers], H, T)
-    b_select = G * (HQ * 3008 * 4 + 94 * HQ * 8)  # logits + chunk statistics read back by the selection
-    nbytes = {"score": b_route, "select_union_attend": b_select + b_union + b_av, "route": b_route,
-              "union": b_union, "attend": b_av}
+    nbytes = {"decode": b_route + b_union + b_av, "route": b_route, "union": b_union, "attend": b_av}
     stage_report = {}
     for name, us in per_stage.items():
         gbs = nbytes[name] / (us * 1e-6) / 1e9
@@ -329,7 +315,7 @@ def main():
     if "update" in stages:
         blocks = [int(x) for x in a.update_blocks.split(",") if x]
         update = update_timing(lib_path, H, blocks, a.steps, a.warmup, a.seed, device)
-    fused = [n for n in ("score", "select_union_attend") if n in stage_report]
+    fused = [n for n in ("decode",) if n in stage_report]
     dominant = max(fused or stage_report, key=lambda n: stage_report[n]["us_per_launch"]) if stage_report else None
     roofline = None
     if dominant:

@@ -102,21 +102,16 @@ int prismkv_attend(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t co
                    int splits, uint64_t stream);
 
 /* Stages 1-3 fused (replaces Native8B.__call__ = route + attention,
- * src/prismkv/native8b.py:104-106): one moment-scoring launch plus one
- * launch for selection, union and sparse attention; writes the same
- * features / valid / raw / ids / count as prismkv_route + prismkv_union and
- * the same out as prismkv_attend.  `work` is sized for the largest history
- * the caller will use (`capacity` >= H) by prismkv_decode_work_bytes and is
- * zero-filled once before first use. */
+ * src/prismkv/native8b.py:104-106): ONE launch per layer for moment scoring,
+ * selection, union and sparse attention; writes the same features / valid /
+ * raw / ids / count as prismkv_route + prismkv_union and the same out as
+ * prismkv_attend.  H <= 524288.  `work` is sized for the largest history the
+ * caller will use (`capacity` >= H) by prismkv_decode_work_bytes and is
+ * zero-filled once before first use; its first 32-bit word is the error word
+ * (nonzero if a bounded inter-workgroup wait gave up).  The workgroups of one
+ * group wait on each other: it returns -1 if one group's
+ * max(32, ceil(H/2048)) workgroups cannot be resident on the device at once. */
 size_t prismkv_decode_work_bytes(int groups, int capacity);
-/* The two halves of prismkv_decode, for callers that time or overlap them:
- * moment scoring into `work`, then selection + union + attention from it. */
-int prismkv_decode_score(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, int groups, int capacity,
-                         uint64_t stream);
-int prismkv_decode_attend(uint64_t q, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v, uint64_t work,
-                          uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count, uint64_t out,
-                          int groups, int H, int T, int capacity, int64_t row_words, int64_t ks, int64_t vs,
-                          int64_t ids_stride, uint64_t stream);
 int prismkv_decode(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
                    uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
                    uint64_t out, int groups, int H, int T, int capacity, int64_t row_words, int64_t ks, int64_t vs,

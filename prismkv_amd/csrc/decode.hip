@@ -1,37 +1,53 @@
-// Fused routed decode of one layer: bucket selection (stages 1b), bitmap
-// union (stage 2) and sparse attention (stage 3) in ONE launch after the
-// moment-scoring launch of route.hip.  Same results as prismkv_route +
-// prismkv_union + prismkv_attend; it exists because every kernel boundary in
-// a HIP graph costs ~1.75 us on MI355X, more than most of these stages' work.
+// Fused routed decode of one layer in ONE launch: moment scoring (stage 1a),
+// bucket selection (stage 1b), bitmap union (stage 2) and sparse attention
+// (stage 3).  Same results as prismkv_route + prismkv_union + prismkv_attend;
+// it exists because every kernel boundary in a HIP graph costs ~1.75 us on
+// MI355X, more than most of these stages' work, and because the selection
+// is cheapest when each workgroup ranks only the buckets it scored.
 //
 // Semantics: src/prismkv/core.py:106-183 (route, union, attend), the tie and
 // padding rules of kernels/ppu_8b/route_parallel.cu:12,23,29 and the ascending
 // emission of kernels/ppu_8b/union.cu:26.
 //
-// Grid (S, G) x 512, S = ceil(ceil(H/32) / 64): workgroup p of group g owns
+// Grid (S, G) x 512, S = clamp(ceil(ceil(H/32) / 64), 32, 256).  Workgroup p
+// of group g owns moment tiles p, p + S, p + 2S, ... (at most 3 of the 94),
 // bitmap words [64p, 64p + 64) (tokens [2048p, 2048p + 2048)) and tail rows
 // [p * ceil(T/S), ...).  Phases:
-//   1. every workgroup turns the group's logits into head-summed
-//      probabilities and selects the Top-16 itself (~1 us of VALU per
-//      workgroup; the same bits everywhere, so all agree) -- cheaper than
-//      handing candidates between workgroups; workgroup 0 writes
-//      features / valid / raw;
-//   2. union tile: one wave ORs the selected rows over its 64 words and
+//   1. score its tiles (two 256-thread scorers side by side, every tile load
+//      issued up front) into LDS logits; publish each tile's per-head
+//      (max, sum-exp) statistics;
+//   2. read the group's 94 chunk statistics as they land and merge them into
+//      the per-head (M, 1/Z) -- every workgroup merges the same 94 pairs in
+//      the same order, so all hold the same bits;
+//   3. rank its own buckets' keys (head-summed probability, bucket id) and
+//      publish its 16 best;
+//   4. read the group's S x 16 candidates as they land and rank them: the
+//      group's Top-16 is among them, and every workgroup computes the same
+//      winners; workgroup 0 writes features / valid / raw;
+//   5. union tile: one wave ORs the selected rows over its 64 words and
 //      compacts the set bits into an LDS token list, publishing the tile's
-//      count;
-//   3. attention over the tile's tokens plus its tail share, 36 rows per
+//      count (and requesting the lower tiles' counts);
+//   6. attention over the tile's tokens plus its tail share, 36 rows per
 //      wave per round, every load of a round in flight at once;
-//   4. the tile's ids go to ids[g][prefix ...], prefix = sum of the counts of
-//      the lower tiles (published in phase 2, long before; lower-numbered
-//      workgroups are dispatched earlier, so the bounded wait ends);
-//   5. the last workgroup of the group (arrival counter) merges the S split
-//      states into out[g] and clears the counters, so the launch can be
-//      replayed from a graph without memset nodes.
+//   7. the tile's ids offset: prefix = sum of the counts of the lower tiles;
+//   8. its split state (per head max, denominator, acc[128]) is published,
+//      then the tile's ids go to ids[g][prefix ...];
+//   9. workgroup 0 reads the S split states as they land, merges them into
+//      out[g], and clears every published word of the group, so the launch
+//      replays from a graph without memset nodes.
+// Published words hold the bitwise complement of their value, so a zero
+// word (as cleared, or as the zero-filled workspace starts) reads as "not
+// yet written": readers poll the data itself, one memory round trip after
+// the writer's store, with no flags and no drains.  Waits only involve the
+// workgroups of one group, which the in-order dispatcher starts back to back
+// (S <= 256 fit on the GPU at once); every wait is bounded and reports
+// through the error word instead of hanging.  Data crosses workgroups only
+// through write-through (agent-scope) stores and loads, never through
+// device-scope fences.
 #include <algorithm>
 
 #include "attend_core.h"
-#include "launch.h"
-#include "select.h"
+#include "score.h"
 
 namespace prismkv {
 namespace {
@@ -39,23 +55,26 @@ namespace {
 constexpr int kDT = kAT;           // 512 threads, 8 waves
 constexpr int kTileWords = 64;     // bitmap words per workgroup
 constexpr int kTileTokens = 32 * kTileWords;
+constexpr int kMinSplits = 32;     // at least one workgroup per CU for the scoring
+constexpr int kMaxSplits = 256;    // one group's workgroups must fit on the GPU at once
+constexpr int kMaxOwn = (kChunks + kMinSplits - 1) / kMinSplits;  // moment tiles per workgroup (3)
 constexpr unsigned kReady = 1u << 31;
 
 struct DecodeArgs {
   const uint16_t* q;
-  const float* logits;  // [G][4][kFP] from the scoring launch
-  const float* stats;   // [G][kChunks][4][2]
-  const int* counts;    // [G][kFP]
+  const float* moments;  // [G][94][256][32]
+  const int* counts;     // [G][kFP]
   const uint32_t* bits;
   int64_t row_words;
   const uint16_t* k;
   const uint16_t* v;
   int64_t ks, vs;
   int H, T, S, tail_per;
-  unsigned* status;          // [G][S] kReady | tile count
-  unsigned* sync;            // [G]
+  unsigned long long* stats;  // [G][kChunks][4] published (max, sum-exp) per chunk and head
+  unsigned long long* cand;   // [G][S][16] published best keys of each workgroup
+  unsigned* status;           // [G][S] kReady | tile count
   unsigned* err;
-  float* state;  // [G*4][S][130]
+  float* state;  // [G*4][S][130] published split states
   int64_t* features;
   float* valid;
   int* raw;
@@ -67,16 +86,19 @@ struct DecodeArgs {
 
 struct DecodeLds {
   int rows[kTileTokens];  // the tile's selected tokens, ascending
+  float tl[kMaxOwn][kHq][kChunk];  // logits of this workgroup's moment tiles
   alignas(16) unsigned long long win[kTop];
   int sel_rows[kTop];
   int need, nsel, base;
-  int is_last;
   float gmax[kHq], grz[kHq];
   union alignas(16) {
     struct {
-      alignas(16) unsigned long long keys[kDT * 6];   // 6 keys per thread
-      unsigned long long best[kDT / 64 * kTop];
-      unsigned long long sc[kDT / 64][64 + 16 * 6];
+      float4 qq[kRow];
+      TileLds tile[2];
+    } score;
+    struct {
+      alignas(16) unsigned long long own[2 * 64];  // this workgroup's keys (<= 96 used)
+      alignas(16) unsigned long long best[kDT / 64 * kTop];
     } sel;
     AttendLds att;
   };
@@ -96,73 +118,134 @@ __device__ __forceinline__ void wait_all(Pred pred, unsigned* err) {
   }
 }
 
-// Phases 1-2: the group's Top-16 (rank order) into lds.win / lds.sel_rows /
-// lds.need, computed by this workgroup alone from the scoring launch's logits
-// and chunk statistics: probabilities exp(l - M) / Z summed over heads in head
-// order (core.py:128), keys value-descending / id-ascending.  Every
-// workgroup of the group computes the same bits, so all of them agree.
-constexpr int kSelKeys = (kFP + kDT - 1) / kDT;  // 6 buckets per thread
+// Published words: the complement of the value's bits, so 0 = not yet.
+__device__ __forceinline__ void pub(float* p, float v) { st_dev(reinterpret_cast<unsigned*>(p), ~__float_as_uint(v)); }
+__device__ __forceinline__ void pub2(unsigned long long* p, float a, float b) {
+  st_dev(p, ~(((unsigned long long)__float_as_uint(b) << 32) | (unsigned long long)__float_as_uint(a)));
+}
+__device__ __forceinline__ float2 unpub2(unsigned long long r) {
+  r = ~r;
+  return make_float2(__uint_as_float((unsigned)r), __uint_as_float((unsigned)(r >> 32)));
+}
 
-__device__ void decode_select(const DecodeArgs& a, int g, DecodeLds& lds) {
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  const float* lg = a.logits + (size_t)g * kHq * kFP;
-  float lv[kSelKeys][kHq];
+// Phase 4 for KW sets of 64 candidates per wave: wave w polls the published
+// keys [64 KW w, 64 KW (w + 1)) straight into registers (each 16-lane row is
+// one workgroup's list, already in rank order), keeps their top 16; wave 0
+// then merges the 8 waves' lists into the group's Top-16.
+template <int KW>
+__device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, DecodeLds& lds) {
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nk = a.S * kTop;
+  const unsigned long long* cg = a.cand + (size_t)g * a.S * kTop;
+  unsigned long long v[KW];
 #pragma unroll
-  for (int i = 0; i < kSelKeys; ++i) {
-    const int b = min(tid + kDT * i, kFP - 1);
-#pragma unroll
-    for (int h = 0; h < kHq; ++h) lv[i][h] = lg[h * kFP + b];
+  for (int k = 0; k < KW; ++k) {
+    const int i = (w * KW + k) * 64 + lane;
+    unsigned long long r = 0;
+    wait_all([&] {
+      if (i < nk && r == 0) r = ld_dev(cg + i);
+      return i >= nk || r != 0;
+    }, a.err);
+    v[k] = i < nk ? ~r : 0ull;
   }
-  if (w < kHq) {
-    // merge chunk statistics: wave h handles head h, lanes cover the 94 chunks
-    const int h = w;
-    const float2* st = reinterpret_cast<const float2*>(a.stats) + (size_t)g * kChunks * kHq + h;
-    const float2 s0 = lane < kChunks ? st[lane * kHq] : make_float2(-INFINITY, 0.f);
-    const float2 s1 = lane + 64 < kChunks ? st[(lane + 64) * kHq] : make_float2(-INFINITY, 0.f);
-    const float m = wave_max(fmaxf(s0.x, s1.x));
-    float z = (s0.x == -INFINITY ? 0.f : s0.y * expf(s0.x - m)) + (s1.x == -INFINITY ? 0.f : s1.y * expf(s1.x - m));
-    z = wave_sum(z);
-    if (lane == 0) {
-      lds.gmax[h] = m;
-      lds.grz[h] = z > 0.f ? 1.0f / z : 0.f;
-    }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int i = 0; i < kSelKeys; ++i) {
-    const int b = tid + kDT * i;
-    uint64_t key = 0;
-    if (b < kFP && lv[i][0] != -INFINITY) {
-      const float p0 = expf(lv[i][0] - lds.gmax[0]) * lds.grz[0];
-      const float p1 = expf(lv[i][1] - lds.gmax[1]) * lds.grz[1];
-      const float p2 = expf(lv[i][2] - lds.gmax[2]) * lds.grz[2];
-      const float p3 = expf(lv[i][3] - lds.gmax[3]) * lds.grz[3];
-      key = make_key(((p0 + p1) + p2) + p3, b);
-    }
-    lds.sel.keys[w * 64 * kSelKeys + 64 * i + lane] = key;  // wave w's keys contiguous
-  }
-  __syncthreads();
-  wave_top16<kSelKeys>(lds.sel.keys + w * 64 * kSelKeys, lds.sel.sc[w], lds.sel.best + kTop * w);
+  const unsigned long long best = sorted_rows_top16<KW>(v);
+  if (lane < kTop) lds.sel.best[kTop * w + lane] = best;
   __syncthreads();
   if (w == 0) {
-    const int need = wave_top16<2>(lds.sel.best, lds.sel.sc[0], lds.win);
-    if (lane < kTop) lds.sel_rows[lane] = key_bucket(lds.win[lane < need ? lane : 0]);
+    unsigned long long u[2] = {lds.sel.best[lane], lds.sel.best[64 + lane]};
+    const unsigned long long win = sorted_rows_top16<2>(u);
+    const int need = __popcll(__ballot(lane < kTop && win != 0));
+    if (lane < kTop) {
+      lds.win[lane] = win;
+      lds.sel_rows[lane] = lane < need ? key_bucket(win) : 0;  // the union reads rows < need only
+    }
     if (lane == 0) lds.need = need;
   }
   __syncthreads();
+}
+
+// Phases 1-4: the group's Top-16 (rank order) into lds.win / lds.sel_rows /
+// lds.need.
+__device__ void decode_select(const DecodeArgs& a, int g, int p, DecodeLds& lds) {
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int S = a.S;
+  const int own = (kChunks - p + S - 1) / S;  // tiles p, p + S, ... below 94
+  // ---- 1. score the own tiles: half 0 takes tiles 0 and 2, half 1 tile 1
+  {
+    const int half = tid >> 8, t = tid & 255;
+    float4 m4[2][8];
+    load_tile(a.moments, g, p + S * half, t, half < own, m4[0]);
+    load_tile(a.moments, g, p + S * 2, t, half == 0 && own > 2, m4[1]);
+    stage_query(a.q, g, lds.score.qq, tid, kDT);
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      if (r == 1 && own <= 2) break;  // uniform
+      const int j = r == 0 ? half : 2;
+      const bool has = r == 0 ? half < own : half == 0;
+      if (r == 1) __syncthreads();  // the first round's LDS reads are done
+      const float l = tile_logit(lds.score.qq, m4[r], t, lds.score.tile[half], a.counts, g, p + S * j, has);
+      if (t < kHq * kChunk && has) {
+        const int h = t >> 5, b = t & 31;
+        lds.tl[j][h][b] = l;
+        const float2 st = chunk_stats(l);
+        if (b == 0) pub2(&a.stats[((size_t)g * kChunks + p + S * j) * kHq + h], st.x, st.y);
+      }
+    }
+  }
+  __syncthreads();
+  // ---- 2. the group's per-head (M, 1/Z), from the statistics as they land
+  if (w < kHq) {
+    const int h = w;
+    const unsigned long long* st = a.stats + (size_t)g * kChunks * kHq + h;
+    unsigned long long r0 = 0, r1 = 0;
+    wait_all([&] {
+      if (lane < kChunks && r0 == 0) r0 = ld_dev(st + lane * kHq);
+      if (lane + 64 < kChunks && r1 == 0) r1 = ld_dev(st + (lane + 64) * kHq);
+      return (lane >= kChunks || r0 != 0) && (lane + 64 >= kChunks || r1 != 0);
+    }, a.err);
+    const float2 mz = merge_chunk_stats([&](int ch) { return unpub2(ch == lane ? r0 : r1); });
+    if (lane == 0) {
+      lds.gmax[h] = mz.x;
+      lds.grz[h] = mz.y;
+    }
+  }
+  __syncthreads();
+  // ---- 3. this workgroup's 16 best keys
+  if (tid < 2 * 64) {
+    const int j = tid >> 5, b = tid & 31;
+    uint64_t key = 0;
+    if (j < own) {
+      const float lv[kHq] = {lds.tl[j][0][b], lds.tl[j][1][b], lds.tl[j][2][b], lds.tl[j][3][b]};
+      key = bucket_key(lv, lds.gmax, lds.grz, (p + S * j) * kChunk + b);
+    }
+    lds.sel.own[tid] = key;
+  }
+  __syncthreads();
+  if (w == 0) {
+    unsigned long long v[2] = {lds.sel.own[lane], lds.sel.own[64 + lane]};
+    const unsigned long long best = bitonic_top16<2>(v);  // lane j < 16: rank j
+    if (lane < kTop) st_dev(&a.cand[((size_t)g * S + p) * kTop + lane], ~best);
+  }
+  // ---- 4. the group's Top-16 from its S x 16 candidates, as they land
+  const int kw = S <= 32 ? 1 : S <= 64 ? 2 : S <= 128 ? 4 : 8;  // 64-key sets per wave
+  if (kw == 1) final_top16<1>(a, g, lds);
+  else if (kw == 2) final_top16<2>(a, g, lds);
+  else if (kw == 4) final_top16<4>(a, g, lds);
+  else final_top16<8>(a, g, lds);
 }
 
 __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   const int p = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   __shared__ DecodeLds lds;
 
-  // ---- 1-2. the group's Top-16, computed here
-  decode_select(a, g, lds);
+  // ---- 1-4. the group's Top-16
+  decode_select(a, g, p, lds);
   if (p == 0 && w == 0)
     write_selection(lds.win, lds.need, a.counts + (size_t)g * kFP, a.features + (size_t)g * kTop,
                     a.valid + (size_t)g * kTop, a.raw + g);
 
-  // ---- 3. union tile: OR the selected rows over words [64p, 64p + 64), compact
+  // ---- 5. union tile: OR the selected rows over words [64p, 64p + 64), compact
   const int nw = (a.H + 31) / 32;
   const int nr = lds.need;
   if (w == 0) {
@@ -191,8 +274,13 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     }
   }
   __syncthreads();
+  // the lower tiles' counts, requested once this workgroup's first K/V loads
+  // are in flight and used after the attention (no barrier in between)
+  unsigned lower[kMaxSplits / 64];  // 0 = not loaded yet (a workgroup without rows never prefetches)
+#pragma unroll
+  for (int c = 0; c < kMaxSplits / 64; ++c) lower[c] = (64 * c + lane < p) ? 0u : kReady;
 
-  // ---- 4. attention over the tile's tokens, then its tail rows
+  // ---- 6. attention over the tile's tokens, then its tail rows
   const int n_sel = lds.nsel;
   const int t_lo = min(a.T, p * a.tail_per), t_hi = min(a.T, t_lo + a.tail_per);
   const int n_rows = n_sel + (t_hi - t_lo);
@@ -230,6 +318,13 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
         vr[i] = load_nt16(vg + (size_t)pos * kD);
         if ((i & 3) == 3) asm volatile("" ::: "memory");  // issue the rows step by step, in order
       }
+      if (round == 0 && w == 0) {
+#pragma unroll
+        for (int c = 0; c < kMaxSplits / 64; ++c) {
+          const int qq = 64 * c + lane;
+          if (qq < p) lower[c] = ld_dev(&a.status[(size_t)g * a.S + qq]);
+        }
+      }
 #pragma unroll
       for (int st = 0; st < (kSlotRows + 3) / 4; ++st) {
         int nv = 0;
@@ -244,38 +339,46 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
         if (__ballot(nv > 0)) attend_step(qf, ks, vs, nv, s);
       }
     }
-    store_wg_state(s, lds.att, a.state + ((size_t)g * kHq * a.S + p) * kStateW, (size_t)a.S * kStateW);
-  }
 
-  // ---- 5. the tile's ids at their global offset
-  if (w == 0) {
-    const unsigned* st = a.status + (size_t)g * a.S;
-    unsigned prefix = 0;
-    for (int c0 = 0; c0 < p; c0 += 64) {
-      const int qq = c0 + lane;
-      wait_all([&] { return qq >= p || (ld_dev(st + qq) & kReady) != 0u; }, a.err);
-      prefix += (unsigned)wave_sum_i(qq < p ? (int)(ld_dev(st + qq) & ~kReady) : 0);
+    // ---- 7. the tile's global ids offset (ids are written after phase 8)
+    if (w == 0) {
+      const unsigned* st = a.status + (size_t)g * a.S;
+      unsigned prefix = 0;
+#pragma unroll
+      for (int c = 0; c < kMaxSplits / 64; ++c) {
+        const int qq = 64 * c + lane;
+        unsigned v = lower[c];
+        wait_all([&] {
+          if (qq < p && !(v & kReady)) v = ld_dev(st + qq);
+          return (v & kReady) != 0u;
+        }, a.err);
+        prefix += (unsigned)wave_sum_i(qq < p ? (int)(v & ~kReady) : 0);
+      }
+      if (lane == 0) {
+        lds.base = (int)prefix;
+        if (p == a.S - 1) a.count[g] = (int32_t)(prefix + (unsigned)n_sel);
+      }
     }
-    if (lane == 0) {
-      lds.base = (int)prefix;
-      if (p == a.S - 1) a.count[g] = (int32_t)(prefix + (unsigned)n_sel);
-    }
+
+    // ---- 8. the split state (after the look-back: its publication tells
+    // workgroup 0 that this workgroup no longer reads any published word);
+    // its barriers also publish lds.base to every wave
+    store_wg_state(s, lds.att, a.state + ((size_t)g * kHq * a.S + p) * kStateW, (size_t)a.S * kStateW, true);
   }
-  __syncthreads();
   {
     int32_t* dst = a.ids + (size_t)g * a.ids_stride + lds.base;
     for (int i = tid; i < n_sel; i += kDT) dst[i] = lds.rows[i];
   }
 
-  // ---- 6. arrival; the last workgroup merges and resets
-  drain();
-  __syncthreads();
-  if (tid == 0) lds.is_last = inc_dev(&a.sync[g]) == (unsigned)(a.S - 1);
-  __syncthreads();
-  if (!lds.is_last) return;
+  // ---- 9. workgroup 0 merges the split states and clears the group's words
+  if (p != 0) return;
+  merge_group(a.state, a.S, g, a.out, lds.att, a.err);
+  __syncthreads();  // every state word this workgroup reads has been consumed
+  for (int i = tid; i < kChunks * kHq; i += kDT) st_dev(&a.stats[(size_t)g * kChunks * kHq + i], 0ull);
+  for (int i = tid; i < a.S * kTop; i += kDT) st_dev(&a.cand[(size_t)g * a.S * kTop + i], 0ull);
   for (int i = tid; i < a.S; i += kDT) st_dev(&a.status[(size_t)g * a.S + i], 0u);
-  if (tid == 0) st_dev(&a.sync[g], 0u);
-  merge_group(a.state, a.S, g, a.out, lds.att);
+  unsigned* sw = reinterpret_cast<unsigned*>(a.state + (size_t)g * kHq * a.S * kStateW);
+  for (int i = tid; i < kHq * a.S * kStateW; i += kDT) st_dev(&sw[i], 0u);
 }
 
 }  // namespace
@@ -283,59 +386,66 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
 
 using namespace prismkv;
 
-static int decode_tiles(int H) { return std::max(1, ((H + 31) / 32 + kTileWords - 1) / kTileWords); }
+static int decode_splits(int H) {
+  return std::min(kMaxSplits, std::max(kMinSplits, ((H + 31) / 32 + kTileWords - 1) / kTileWords));
+}
+static constexpr int kFusedMaxHistory = kMaxSplits * kTileTokens;  // 524288
 
-// Work layout (bytes): route logits | route stats | status | sync | err | state
+// Work layout (bytes), sized for the largest split count the buffer serves:
+// err | stats | candidates | status | state
 struct DecodeWorkLayout {
-  size_t logits, stats, status, sync, err, state, total;
+  size_t err, stats, cand, status, state, total;
   DecodeWorkLayout(int groups, int S) {
     size_t o = 0;
     auto take = [&](size_t n) { const size_t at = o; o += (n + 255) & ~(size_t)255; return at; };
-    logits = take((size_t)groups * kHq * kFP * sizeof(float));
-    stats = take((size_t)groups * kChunks * kHq * 2 * sizeof(float));
-    status = take((size_t)groups * S * sizeof(unsigned));
-    sync = take((size_t)groups * sizeof(unsigned));
     err = take(sizeof(unsigned));
+    stats = take((size_t)groups * kChunks * kHq * sizeof(unsigned long long));
+    cand = take((size_t)groups * S * kTop * sizeof(unsigned long long));
+    status = take((size_t)groups * S * sizeof(unsigned));
     state = take((size_t)groups * kHq * S * kStateW * sizeof(float));
     total = o;
   }
 };
 
+// Workgroups of decode_kernel resident on device `dev` at once (CUs x blocks
+// per CU), queried once per device.
+static int resident_workgroups() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cached[dev] == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel, kDT, 0) != hipSuccess) return 0;
+    cached[dev] = cus * per_cu;
+  }
+  return cached[dev];
+}
+
 extern "C" {
 
 size_t prismkv_decode_work_bytes(int groups, int capacity) {
   if (groups < 1 || capacity < 1) return 0;
-  return DecodeWorkLayout(groups, decode_tiles(capacity)).total;
+  return DecodeWorkLayout(groups, decode_splits(capacity)).total;
 }
 
-int prismkv_decode_score(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, int groups, int capacity,
-                         uint64_t stream) {
-  if (groups < 1 || groups > 65535 || capacity < 1) return kBadSize;
-  if (!q || !moments || !counts || !work) return kBadSize;
-  const DecodeWorkLayout L(groups, decode_tiles(capacity));
-  char* w = reinterpret_cast<char*>(work);
-  launch_route_score(reinterpret_cast<const uint16_t*>(q), reinterpret_cast<const float*>(moments),
-                     reinterpret_cast<const int*>(counts), reinterpret_cast<float*>(w + L.logits),
-                     reinterpret_cast<float*>(w + L.stats), groups, (hipStream_t)stream);
-  return (int)hipGetLastError();
-}
-
-int prismkv_decode_attend(uint64_t q, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v, uint64_t work,
-                          uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count, uint64_t out,
-                          int groups, int H, int T, int capacity, int64_t row_words, int64_t ks, int64_t vs,
-                          int64_t ids_stride, uint64_t stream) {
-  if (groups < 1 || groups > 65535 || H < 1 || T < 0 || capacity < H) return kBadSize;
+int prismkv_decode(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
+                   uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
+                   uint64_t out, int groups, int H, int T, int capacity, int64_t row_words, int64_t ks, int64_t vs,
+                   int64_t ids_stride, uint64_t stream) {
+  if (groups < 1 || groups > 65535 || H < 1 || H > kFusedMaxHistory || T < 0 || capacity < H) return kBadSize;
   if (row_words < (H + 31) / 32 || ids_stride < H) return kBadSize;
   if (ks < (int64_t)(H + T) * kD || vs < (int64_t)(H + T) * kD) return kBadSize;
-  if (!q || !counts || !bits || !k || !v || !work || !features || !valid || !raw || !ids || !count || !out)
+  if (!q || !moments || !counts || !bits || !k || !v || !work || !features || !valid || !raw || !ids || !count ||
+      !out)
     return kBadSize;
-  const int S = decode_tiles(H);
-  const DecodeWorkLayout L(groups, decode_tiles(capacity));
+  const int S = decode_splits(H);
+  if (S > resident_workgroups()) return kBadSize;  // a group's workgroups must be resident together
+  const DecodeWorkLayout L(groups, decode_splits(capacity));
   char* w = reinterpret_cast<char*>(work);
   DecodeArgs a;
   a.q = reinterpret_cast<const uint16_t*>(q);
-  a.logits = reinterpret_cast<const float*>(w + L.logits);
-  a.stats = reinterpret_cast<const float*>(w + L.stats);
+  a.moments = reinterpret_cast<const float*>(moments);
   a.counts = reinterpret_cast<const int*>(counts);
   a.bits = reinterpret_cast<const uint32_t*>(bits);
   a.row_words = row_words;
@@ -347,8 +457,9 @@ int prismkv_decode_attend(uint64_t q, uint64_t counts, uint64_t bits, uint64_t k
   a.T = T;
   a.S = S;
   a.tail_per = (T + S - 1) / S;
+  a.stats = reinterpret_cast<unsigned long long*>(w + L.stats);
+  a.cand = reinterpret_cast<unsigned long long*>(w + L.cand);
   a.status = reinterpret_cast<unsigned*>(w + L.status);
-  a.sync = reinterpret_cast<unsigned*>(w + L.sync);
   a.err = reinterpret_cast<unsigned*>(w + L.err);
   a.state = reinterpret_cast<float*>(w + L.state);
   a.features = reinterpret_cast<int64_t*>(features);
@@ -360,20 +471,6 @@ int prismkv_decode_attend(uint64_t q, uint64_t counts, uint64_t bits, uint64_t k
   a.out = reinterpret_cast<uint16_t*>(out);
   hipLaunchKernelGGL(decode_kernel, dim3(S, groups), dim3(kDT), 0, (hipStream_t)stream, a);
   return (int)hipGetLastError();
-}
-
-int prismkv_decode(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
-                   uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
-                   uint64_t out, int groups, int H, int T, int capacity, int64_t row_words, int64_t ks, int64_t vs,
-                   int64_t ids_stride, uint64_t stream) {
-  if (groups < 1 || groups > 65535 || H < 1 || T < 0 || capacity < H) return kBadSize;
-  if (row_words < (H + 31) / 32 || ids_stride < H) return kBadSize;
-  if (ks < (int64_t)(H + T) * kD || vs < (int64_t)(H + T) * kD) return kBadSize;
-  if (!moments) return kBadSize;
-  const int rc = prismkv_decode_score(q, moments, counts, work, groups, capacity, stream);
-  if (rc) return rc;
-  return prismkv_decode_attend(q, counts, bits, k, v, work, features, valid, raw, ids, count, out, groups, H, T,
-                               capacity, row_words, ks, vs, ids_stride, stream);
 }
 
 }  // extern "C"

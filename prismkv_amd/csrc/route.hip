@@ -29,29 +29,13 @@
 //     group.  Each select ranks per-thread maxima with LDS broadcast reads to
 //     find a threshold, then ranks the few keys above it (no histogram
 //     atomics, no sorting network).
-#include "launch.h"
-#include "select.h"
+#include "score.h"
 
 namespace prismkv {
 namespace {
 
 constexpr int kRT = 256;                      // route workgroup size
 constexpr int kKeys = (kFP + kRT - 1) / kRT;  // 12 candidate keys per thread
-constexpr float kSqrtD = 11.3137084989847604f;  // fp32(sqrt(128)), core.py:125
-
-// Transpose-reduce step: `x` holds 2n partial sums; lanes whose `mask` bit is
-// set keep the upper half, the others the lower half, and add the partner's
-// copy of the kept half.  After the step x[0..n) holds the new partial sums.
-template <int N>
-__device__ __forceinline__ void treduce(float* x, int mask) {
-  const unsigned long long hi = __ballot((threadIdx.x & mask) != 0);
-#pragma unroll
-  for (int j = 0; j < N; ++j) {
-    const float keep = lane_select(hi, x[j + N], x[j]);
-    const float send = lane_select(hi, x[j], x[j + N]);
-    x[j] = keep + __shfl_xor(send, mask);
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Route, pass 1 (moment scoring): grid (kChunks, G) x 256.
@@ -65,77 +49,19 @@ __global__ __launch_bounds__(kRT) void route_score_kernel(const uint16_t* __rest
                                                           const float* __restrict__ moments,
                                                           const int* __restrict__ counts, RouteWork work) {
   const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
-  const int w = tid >> 6, lane = tid & 63;
-  __shared__ float4 qq[kRow];                 // [k] -> 4 heads; k < 128: q, k >= 128: q*q
-  __shared__ float4 red[kRT / 64][64];        // cross-wave partials
-  __shared__ float dots[2][kHq][kChunk];      // [part][head][bucket]
-
-  // 16-byte tile loads first: thread = bucket quad (tid & 7) x k-row phase (tid >> 3)
-  const int quad = tid & 7, r = tid >> 3;
-  const float4* tile = reinterpret_cast<const float4*>(moments + (size_t)(g * kChunks + c) * kRow * kChunk);
+  __shared__ float4 qq[kRow];  // [k] -> 4 heads; k < 128: q, k >= 128: q*q
+  __shared__ TileLds lds;
   float4 m4[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tile + (r + 32 * i) * (kChunk / 4) + quad));
-    m4[i] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
-  }
-  for (int i = tid; i < kHq * kD; i += kRT) {
-    const int h = i >> 7, k = i & (kD - 1);
-    const float x = bf16_to_f32(q[((size_t)g * kHq + h) * kD + k]);
-    reinterpret_cast<float*>(&qq[k])[h] = x;
-    reinterpret_cast<float*>(&qq[kD + k])[h] = x * x;  // core.py:127 q.square() in fp32
-  }
+  load_tile(moments, g, c, tid, true, m4);  // 16-byte tile loads first
+  stage_query(q, g, qq, tid, kRT);
   __syncthreads();
-
-  // acc[part*16 + head*4 + j]: part 0 = mean rows, 1 = variance rows
-  float acc[32];
-#pragma unroll
-  for (int i = 0; i < 32; ++i) acc[i] = 0.f;
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float4 qv = qq[r + 32 * i];
-    const float* hq = reinterpret_cast<const float*>(&qv);
-    const float* mv = reinterpret_cast<const float*>(&m4[i]);
-    const int part = i >> 2;
-#pragma unroll
-    for (int h = 0; h < kHq; ++h)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[part * 16 + h * 4 + j] = fmaf(hq[h], mv[j], acc[part * 16 + h * 4 + j]);
-  }
-  // reduce over the 8 k-row lanes of the wave (lane bits 5,4,3)
-  treduce<16>(acc, 32);
-  treduce<8>(acc, 16);
-  treduce<4>(acc, 8);
-  // lane now holds part (lane>>5)&1, head (lane>>3)&3, buckets 4*quad .. +3
-  red[w][lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-  __syncthreads();
-  {
-    const int l = tid >> 2, j = tid & 3;
-    const float s = ((reinterpret_cast<const float*>(&red[0][l])[j] + reinterpret_cast<const float*>(&red[1][l])[j]) +
-                     reinterpret_cast<const float*>(&red[2][l])[j]) +
-                    reinterpret_cast<const float*>(&red[3][l])[j];
-    dots[(l >> 5) & 1][(l >> 3) & 3][4 * (l & 7) + j] = s;
-  }
-  __syncthreads();
-
+  const float l = tile_logit(qq, m4, tid, lds, counts, g, c, true);
   if (tid < kHq * kChunk) {
     // thread = (head tid>>5, bucket tid&31); 32 lanes per head
-    const int h = tid >> 5, b = tid & 31, bucket = c * kChunk + b;
-    const int n = counts[(size_t)g * kFP + bucket];
-    float l = -INFINITY;
-    if (n > 0) {
-      // core.py:122-127: log(count) + (q @ mean^T) / sqrt(d) + (q^2 @ var^T) / (2d)
-      const float lc = logf((float)n);
-      l = (lc + dots[0][h][b] / kSqrtD) + dots[1][h][b] / (2.0f * kD);
-    }
-    work.logits[((size_t)g * kHq + h) * kFP + bucket] = l;
-    float m = l;
-#pragma unroll
-    for (int o = 16; o; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
-    float e = (l == -INFINITY) ? 0.f : expf(l - m);
-#pragma unroll
-    for (int o = 16; o; o >>= 1) e += __shfl_xor(e, o);
-    if (b == 0) *reinterpret_cast<float2*>(&work.stats[(((size_t)g * kChunks + c) * kHq + h) * 2]) = make_float2(m, e);
+    const int h = tid >> 5, b = tid & 31;
+    work.logits[((size_t)g * kHq + h) * kFP + c * kChunk + b] = l;
+    const float2 st = chunk_stats(l);
+    if (b == 0) *reinterpret_cast<float2*>(&work.stats[(((size_t)g * kChunks + c) * kHq + h) * 2]) = st;
   }
 }
 
@@ -168,29 +94,17 @@ __global__ __launch_bounds__(kRT) void route_part_kernel(RouteWork work, unsigne
     // merge chunk statistics: wave h handles head h, lanes cover the 94 chunks
     const int h = w;
     const float2* st = reinterpret_cast<const float2*>(work.stats) + (size_t)g * kChunks * kHq + h;
-    const float2 s0 = lane < kChunks ? st[lane * kHq] : make_float2(-INFINITY, 0.f);
-    const float2 s1 = lane + 64 < kChunks ? st[(lane + 64) * kHq] : make_float2(-INFINITY, 0.f);
-    const float m = wave_max(fmaxf(s0.x, s1.x));
-    float z = (s0.x == -INFINITY ? 0.f : s0.y * expf(s0.x - m)) + (s1.x == -INFINITY ? 0.f : s1.y * expf(s1.x - m));
-    z = wave_sum(z);
+    const float2 mz = merge_chunk_stats([&](int ch) { return st[ch * kHq]; });
     if (lane == 0) {
-      gmax[h] = m;
-      grz[h] = z > 0.f ? 1.0f / z : 0.f;
+      gmax[h] = mz.x;
+      grz[h] = mz.y;
     }
   }
   __syncthreads();
 #pragma unroll
   for (int i = 0; i < kPartKeys; ++i) {
     const int off = tid + i * kRT, b = part * kPartB + off;
-    uint64_t key = 0;
-    if (off < kPartB && lv[i][0] != -INFINITY) {
-      // per-head softmax exp(l - M) / Z, then the sum over heads in head order (core.py:128)
-      const float p0 = expf(lv[i][0] - gmax[0]) * grz[0];
-      const float p1 = expf(lv[i][1] - gmax[1]) * grz[1];
-      const float p2 = expf(lv[i][2] - gmax[2]) * grz[2];
-      const float p3 = expf(lv[i][3] - gmax[3]) * grz[3];
-      key = make_key(((p0 + p1) + p2) + p3, b);
-    }
+    const uint64_t key = off < kPartB ? bucket_key(lv[i], gmax, grz, b) : 0;
     keys[off] = key;
   }
   __syncthreads();
@@ -311,8 +225,8 @@ __global__ void pack_kernel(const uint16_t* __restrict__ q, float* __restrict__ 
 
 using namespace prismkv;
 
-void prismkv::launch_route_score(const uint16_t* q, const float* moments, const int* counts, float* logits,
-                                 float* stats, int groups, hipStream_t stream) {
+static void launch_route_score(const uint16_t* q, const float* moments, const int* counts, float* logits,
+                               float* stats, int groups, hipStream_t stream) {
   hipLaunchKernelGGL(route_score_kernel, dim3(kChunks, groups), dim3(kRT), 0, stream, q, moments, counts,
                      RouteWork{logits, stats});
 }

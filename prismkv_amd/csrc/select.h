@@ -85,6 +85,92 @@ __device__ int wave_top16(const unsigned long long* keys, unsigned long long* sc
   return need;
 }
 
+// ---------------------------------------------------------------------------
+// Register-resident Top-16 by bitonic networks.  A wave holds 64 keys per
+// "set" (one per lane); rows are the four 16-lane groups.  Exchanges within a
+// row go through DPP (a few cycles), across rows through a lane permute, so
+// a Top-16 of 64 keys is ~20 dependent compare-exchange steps and touches
+// no LDS.  Keys are unique except 0 (empty), which sorts last.
+// ---------------------------------------------------------------------------
+template <int kCtrl>
+__device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
+  const int lo = __builtin_amdgcn_mov_dpp((int)(unsigned)v, kCtrl, 0xF, 0xF, false);
+  const int hi = __builtin_amdgcn_mov_dpp((int)(unsigned)(v >> 32), kCtrl, 0xF, 0xF, false);
+  return ((unsigned long long)(unsigned)hi << 32) | (unsigned long long)(unsigned)lo;
+}
+__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int m) {
+  const int lo = __shfl_xor((int)(unsigned)v, m);
+  const int hi = __shfl_xor((int)(unsigned)(v >> 32), m);
+  return ((unsigned long long)(unsigned)hi << 32) | (unsigned long long)(unsigned)lo;
+}
+// The key of lane (lane ^ D) for D in {1, 2, 4, 8} (within the row).
+template <int D>
+__device__ __forceinline__ unsigned long long xor_lane_u64(unsigned long long v) {
+  if constexpr (D == 1) return dpp_u64<0xB1>(v);   // quad_perm [1,0,3,2]
+  if constexpr (D == 2) return dpp_u64<0x4E>(v);   // quad_perm [2,3,0,1]
+  if constexpr (D == 8) return dpp_u64<0x128>(v);  // row_ror:8
+  if constexpr (D == 4) {
+    const unsigned long long up = dpp_u64<0x104>(v);    // row_shl:4: lane i reads lane i + 4
+    const unsigned long long down = dpp_u64<0x114>(v);  // row_shr:4: lane i reads lane i - 4
+    return (threadIdx.x & 4) ? down : up;
+  }
+  return v;
+}
+// Compare-exchange with lane ^ D: keep the larger key where keep_max, else the smaller.
+template <int D>
+__device__ __forceinline__ unsigned long long cx_u64(unsigned long long v, bool keep_max) {
+  const unsigned long long o = xor_lane_u64<D>(v);
+  return ((v > o) == keep_max) ? v : o;
+}
+// Bitonic sequence in each row -> descending row (lane 16r + j holds rank j).
+__device__ __forceinline__ unsigned long long row_merge_desc(unsigned long long v) {
+  const int i = threadIdx.x & 15;
+  v = cx_u64<8>(v, (i & 8) == 0);
+  v = cx_u64<4>(v, (i & 4) == 0);
+  v = cx_u64<2>(v, (i & 2) == 0);
+  return cx_u64<1>(v, (i & 1) == 0);
+}
+// Any keys -> each row sorted descending.
+__device__ __forceinline__ unsigned long long row_sort_desc(unsigned long long v) {
+  const int i = threadIdx.x & 15;
+  v = cx_u64<1>(v, ((i & 1) == 0) == ((i & 2) == 0));
+  v = cx_u64<2>(v, ((i & 2) == 0) == ((i & 4) == 0));
+  v = cx_u64<1>(v, ((i & 1) == 0) == ((i & 4) == 0));
+  v = cx_u64<4>(v, ((i & 4) == 0) == ((i & 8) == 0));
+  v = cx_u64<2>(v, ((i & 2) == 0) == ((i & 8) == 0));
+  v = cx_u64<1>(v, ((i & 1) == 0) == ((i & 8) == 0));
+  return row_merge_desc(v);
+}
+// Two descending 16-lists a, b (same lanes) -> the descending top 16 of both.
+__device__ __forceinline__ unsigned long long merge_top16(unsigned long long a, unsigned long long b) {
+  const unsigned long long r = dpp_u64<0x140>(b);  // row_mirror: b ascending along the row
+  return row_merge_desc(a > r ? a : r);
+}
+// Rows sorted descending -> every row holds the descending top 16 of the wave.
+__device__ __forceinline__ unsigned long long rows_top16(unsigned long long v) {
+  v = merge_top16(v, shfl_xor_u64(v, 16));
+  return merge_top16(v, shfl_xor_u64(v, 32));
+}
+// Top-16 of K sets of 64 keys whose rows are already sorted descending:
+// lane j < 16 of every row ends with the rank-j key (0 if fewer keys).
+template <int K>
+__device__ __forceinline__ unsigned long long sorted_rows_top16(unsigned long long (&v)[K]) {
+#pragma unroll
+  for (int k = 0; k < K; ++k) v[k] = rows_top16(v[k]);
+#pragma unroll
+  for (int w = 1; w < K; w *= 2)
+#pragma unroll
+    for (int k = 0; k + w < K; k += 2 * w) v[k] = merge_top16(v[k], v[k + w]);
+  return v[0];
+}
+// Top-16 of K sets of 64 arbitrary keys.
+template <int K>
+__device__ __forceinline__ unsigned long long bitonic_top16(unsigned long long (&v)[K]) {
+#pragma unroll
+  for (int k = 0; k < K; ++k) v[k] = row_sort_desc(v[k]);
+  return sorted_rows_top16<K>(v);
+}
+
 // Writes the winners (sel, rank order) from one wave: features[r] = bucket,
 // valid[r] = 1 for r < need; remaining slots id 0 / valid 0
 // (route_parallel.cu:23,29); raw = sum of winner counts.

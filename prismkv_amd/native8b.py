@@ -42,6 +42,9 @@ from . import _lib
 from .build import compile_hip  # noqa: F401  (re-exported: reference name compile_ppu)
 
 GROUPS, HEADS, DIM, FEATURES, TOPK = 8, 4, 128, 3000, 16
+# Largest history the single-launch decode serves (256 workgroups per group
+# of 2048 tokens each); longer histories take route + attention.
+FUSED_MAX_HISTORY = 524288
 # Largest block one `append` indexes (the reference's update interval is 4096,
 # src/prismkv/hf_reference.py:75).
 MAX_BLOCK = 4096
@@ -241,10 +244,12 @@ class Native8B:
 
     def __call__(self, q, k, v, **kwargs):
         """route + attention (src/prismkv/native8b.py:104-106) through the fused
-        decode path: two launches, identical results, every output buffer
+        decode path: one launch, identical results, every output buffer
         (features, valid, raw, ids, count, out) written as by the two calls."""
         self._check_kv(q, k, v, kwargs.get("splits", 64), kwargs.get("schedule", 0))
-        if self.unique_cap is not None:  # the budgeted walk runs between selection and union
+        if self.unique_cap is not None or self.history > FUSED_MAX_HISTORY:
+            # the budgeted walk runs between selection and union; very long histories
+            # exceed one launch's group size
             self.route(q)
             return self.attention(q, k, v, **kwargs)
         self.lib.call("prismkv_decode", q.data_ptr(), self.moments.data_ptr(), self.n.data_ptr(), self.bits.data_ptr(),
@@ -354,6 +359,11 @@ class Native8B:
             out.append(FeatureIndex(h, center, self.n[g, :FEATURES].long().clone(), mean[g].contiguous(),
                                     var[g].contiguous(), lists))
         return out
+
+    def decode_errors(self):
+        """Error word of the single-launch decode (nonzero if a bounded
+        inter-workgroup wait gave up); synchronises."""
+        return int(self.decode_work[:4].view(torch.int32).item())
 
     def buffer_bytes(self):
         """Live tensors owned here; excludes model/KV, caller indices and build temporaries."""
