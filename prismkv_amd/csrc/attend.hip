@@ -122,7 +122,7 @@ __global__ __launch_bounds__(kAT) void attend_fused(AttendArgs a, unsigned* __re
   __syncthreads();
   if (!is_last) return;
   if (tid == 0) st_dev(&sync[g], 0u);
-  merge_group(a.state, a.S, g, out, lds);
+  merge_group(a.state, a.S, g, out, lds.wts);
 }
 
 __global__ __launch_bounds__(kAT) void attend_split_only(AttendArgs a) {
@@ -134,7 +134,7 @@ __global__ __launch_bounds__(kAT) void attend_split_only(AttendArgs a) {
 __global__ __launch_bounds__(kAT) void attend_merge(const float* __restrict__ state, uint16_t* __restrict__ out,
                                                     int S) {
   __shared__ AttendLds lds;
-  merge_group(state, S, blockIdx.x, out, lds);
+  merge_group(state, S, blockIdx.x, out, lds.wts);
 }
 
 }  // namespace

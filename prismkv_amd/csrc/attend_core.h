@@ -196,7 +196,7 @@ __device__ void store_wg_state(const SlotState& s, AttendLds& lds, float* stp, s
 // used, so S <= 32 costs one memory round trip.  With `err`, the states are
 // published words (complemented bits, 0 = not yet): loads are repeated until
 // every word has landed, a bounded wait that reports through *err.
-__device__ void merge_group(const float* state, int S, int g, uint16_t* out, AttendLds& lds,
+__device__ void merge_group(const float* state, int S, int g, uint16_t* out, float (&wts)[kAT / 64][64],
                             unsigned* err = nullptr) {
   const int tid = threadIdx.x, h = tid >> 7, d = tid & (kD - 1), w = tid >> 6, lane = tid & 63;
   const float* st = state + (size_t)(g * kHq + h) * S * kStateW;
@@ -247,10 +247,10 @@ __device__ void merge_group(const float* state, int S, int g, uint16_t* out, Att
     const float wgt = (mine && mz.x != -INFINITY) ? exp2f(mz.x - M) : 0.f;
     den += wave_sum(wgt * mz.y);
     __syncthreads();  // previous batch's weights are consumed
-    lds.wts[w][lane] = wgt;
+    wts[w][lane] = wgt;
     __syncthreads();
 #pragma unroll
-    for (int i = 0; i < 32; ++i) v = fmaf(lds.wts[w][i], av[i], v);
+    for (int i = 0; i < 32; ++i) v = fmaf(wts[w][i], av[i], v);
   }
   out[((size_t)g * kHq + h) * kD + d] = f32_to_bf16(den > 0.f ? v / den : 0.f);
 }

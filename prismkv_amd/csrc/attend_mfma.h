@@ -1,0 +1,262 @@
+// Sparse attention of one wave on the matrix cores: 32 rows per block,
+// QK^T and PV both as v_mfma_f32_16x16x32_bf16, online softmax in fp32.
+//
+// Semantics: src/prismkv/core.py:170-183 (exact softmax over the selected
+// rows and the tail, scale 1/sqrt(d)): scores are fp32 sums of exact bf16
+// products; probabilities stay fp32 up to the PV product, where each is
+// split into a bf16 head and a bf16 remainder (two products), so P.V carries
+// ~16 significant bits of P instead of bf16's 8; accumulation is fp32.
+//
+// Operand layout of 16x16x32 (lane l, j = l % 16, q = l / 16): A[i][k] with
+// i = j, k = 8q + t; B[k][jj] with jj = j, k = 8q + t; D[i][jj] with
+// i = 4q + r, jj = j (t = 0..7 bf16 elements, r = 0..3 fp32 results).
+//   QK:  D[row][head] = K . Q^T over 4 chunks of 32 dims.  Lane l supplies
+//        row j of each 16-row group, dims 32c + 8q .. +8 -- one 16-byte load
+//        per chunk of its own row -- and Q[head j] (zero for j >= 4).  The
+//        scores of rows 4q + r (group 0) and 16 + 4q + r (group 1) for head j
+//        land in lane l.
+//   PV:  D[head][dim] = P . V with the reduction index k = 8q + t mapped to
+//        the rows the lane already scored (t < 4: row 4q + t, t >= 4: row
+//        16 + 4q + t - 4), so P needs no lane exchange; the 8 column blocks
+//        n map dim 8j + n to column j, so lane l reads its 8 rows at dims
+//        8j .. 8j + 8 (16-byte loads; each load instruction covers 4 whole
+//        rows) and pairs them per dim with v_perm.  Lanes 0-15 end with
+//        out[head r][8j + n] in acc[n][r].
+#pragma once
+
+#include "attend_core.h"
+
+namespace prismkv {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBlockRows = 32;
+
+struct MfmaAttn {
+  bf16x8 qop[4];  // Q^T operand per 32-dim chunk (zero in lanes with j >= 4)
+  f32x4 acc[8];   // PV accumulators
+  float m;        // running max (exp2 domain) of head j (lanes with j < 4)
+  float z;        // this lane's share of head j's denominator
+};
+
+// Per-wave states of a workgroup, merged in LDS.
+template <int kWaves>
+struct MfmaLds {
+  float sm[kWaves][kHq], sz[kWaves][kHq], wt[kWaves][kHq], mx[kHq];
+  float sacc[kWaves][kHq][kD];
+};
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) {
+  const u32x4 u = {v.x, v.y, v.z, v.w};
+  return __builtin_bit_cast(bf16x8, u);
+}
+
+__device__ __forceinline__ void mfma_init(MfmaAttn& st, const uint16_t* qg) {
+  const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (j < kHq) v = *reinterpret_cast<const uint4*>(qg + j * kD + 32 * c + 8 * q);
+    st.qop[c] = as_bf16x8(v);
+  }
+#pragma unroll
+  for (int n = 0; n < 8; ++n) st.acc[n] = f32x4{0.f, 0.f, 0.f, 0.f};
+  st.m = -INFINITY;
+  st.z = 0.f;
+}
+
+// bf16 pair (lo = a's dim n, hi = b's dim n) of two 8-dim rows.
+template <int N>
+__device__ __forceinline__ unsigned dim_pair(const uint4& a, const uint4& b) {
+  const unsigned wa = (N >> 1) == 0 ? a.x : (N >> 1) == 1 ? a.y : (N >> 1) == 2 ? a.z : a.w;
+  const unsigned wb = (N >> 1) == 0 ? b.x : (N >> 1) == 1 ? b.y : (N >> 1) == 2 ? b.z : b.w;
+  return __builtin_amdgcn_perm(wb, wa, (N & 1) ? 0x07060302u : 0x05040100u);
+}
+
+template <int N>
+__device__ __forceinline__ bf16x8 v_operand(const uint4 (&vr)[8]) {
+  const u32x4 u = {dim_pair<N>(vr[0], vr[1]), dim_pair<N>(vr[2], vr[3]), dim_pair<N>(vr[4], vr[5]),
+                   dim_pair<N>(vr[6], vr[7])};
+  return __builtin_bit_cast(bf16x8, u);
+}
+
+// One block of 32 rows.  kr[4g + c]: lane's row j of group g, dims 32c + 8q;
+// vr[4g + t]: row 16g + 4q + t, dims 8j .. 8j + 8.  Rows >= nvalid are
+// masked (their loads may repeat any valid row).
+__device__ __forceinline__ void mfma_block(MfmaAttn& st, const uint4 (&kr)[8], const uint4 (&vr)[8], int nvalid) {
+  const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
+  f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    d0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kr[c]), st.qop[c], d0, 0, 0, 0);
+    d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kr[4 + c]), st.qop[c], d1, 0, 0, 0);
+  }
+  float s[8];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    s[r] = (j < kHq && 4 * q + r < nvalid) ? d0[r] * kLog2eScale : -INFINITY;
+    s[4 + r] = (j < kHq && 16 + 4 * q + r < nvalid) ? d1[r] * kLog2eScale : -INFINITY;
+  }
+  float bm = s[0];
+#pragma unroll
+  for (int t = 1; t < 8; ++t) bm = fmaxf(bm, s[t]);
+  bm = fmaxf(bm, __shfl_xor(bm, 16));
+  bm = fmaxf(bm, __shfl_xor(bm, 32));
+  // lazy rescale: the running max moves only when a score exceeds it by kSlack
+  const bool grow = bm > st.m + kSlack || (st.m == -INFINITY && bm != -INFINITY);
+  if (__ballot(grow)) {
+    const float nm = grow ? bm : st.m;
+    const float alpha = grow ? exp2_or_zero(st.m - nm) : 1.0f;
+    st.m = nm;
+    st.z *= alpha;
+    float ah[kHq];
+#pragma unroll
+    for (int r = 0; r < kHq; ++r) ah[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), r));
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+#pragma unroll
+      for (int r = 0; r < kHq; ++r) st.acc[n][r] *= ah[r];
+  }
+  float p[8];
+  float zs = 0.f;
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    p[t] = s[t] == -INFINITY ? 0.f : exp2f(s[t] - st.m);
+    zs += p[t];
+  }
+  st.z += zs;
+  // P = head + remainder, both bf16: head = the top 16 bits, remainder rounded to nearest
+  unsigned hi[8], lo[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) {
+    const unsigned b = __float_as_uint(p[t]);
+    hi[t] = b >> 16;
+    lo[t] = f32_to_bf16(p[t] - __uint_as_float(b & 0xffff0000u));
+  }
+  const u32x4 uh = {hi[0] | hi[1] << 16, hi[2] | hi[3] << 16, hi[4] | hi[5] << 16, hi[6] | hi[7] << 16};
+  const u32x4 ul = {lo[0] | lo[1] << 16, lo[2] | lo[3] << 16, lo[4] | lo[5] << 16, lo[6] | lo[7] << 16};
+  const bf16x8 ph = __builtin_bit_cast(bf16x8, uh), pl = __builtin_bit_cast(bf16x8, ul);
+#define PRISMKV_PV(N)                                                              \
+  {                                                                                \
+    const bf16x8 vb = v_operand<N>(vr);                                            \
+    st.acc[N] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, vb, st.acc[N], 0, 0, 0); \
+    st.acc[N] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl, vb, st.acc[N], 0, 0, 0); \
+  }
+  PRISMKV_PV(0) PRISMKV_PV(1) PRISMKV_PV(2) PRISMKV_PV(3) PRISMKV_PV(4) PRISMKV_PV(5) PRISMKV_PV(6) PRISMKV_PV(7)
+#undef PRISMKV_PV
+}
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// One block of 16 rows: QK as above (one group), PV as 16x16x16 products
+// whose reduction index k = 4q + t is exactly the lane's scored rows 4q + t.
+// kr[c]: lane's row j, dims 32c + 8q; vr[t]: row 4q + t, dims 8j .. 8j + 8.
+__device__ __forceinline__ void mfma_block16(MfmaAttn& st, const uint4 (&kr)[4], const uint4 (&vr)[4], int nvalid) {
+  const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
+  f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int c = 0; c < 4; ++c) d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kr[c]), st.qop[c], d, 0, 0, 0);
+  float s[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) s[r] = (j < kHq && 4 * q + r < nvalid) ? d[r] * kLog2eScale : -INFINITY;
+  float bm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+  bm = fmaxf(bm, __shfl_xor(bm, 16));
+  bm = fmaxf(bm, __shfl_xor(bm, 32));
+  const bool grow = bm > st.m + kSlack || (st.m == -INFINITY && bm != -INFINITY);
+  if (__ballot(grow)) {
+    const float nm = grow ? bm : st.m;
+    const float alpha = grow ? exp2_or_zero(st.m - nm) : 1.0f;
+    st.m = nm;
+    st.z *= alpha;
+    float ah[kHq];
+#pragma unroll
+    for (int r = 0; r < kHq; ++r) ah[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), r));
+#pragma unroll
+    for (int n = 0; n < 8; ++n)
+#pragma unroll
+      for (int r = 0; r < kHq; ++r) st.acc[n][r] *= ah[r];
+  }
+  float p[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) p[t] = s[t] == -INFINITY ? 0.f : exp2f(s[t] - st.m);
+  st.z += (p[0] + p[1]) + (p[2] + p[3]);
+  unsigned hi[4], lo[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const unsigned b = __float_as_uint(p[t]);
+    hi[t] = b >> 16;
+    lo[t] = f32_to_bf16(p[t] - __uint_as_float(b & 0xffff0000u));
+  }
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  const u32x2 uh = {hi[0] | hi[1] << 16, hi[2] | hi[3] << 16};
+  const u32x2 ul = {lo[0] | lo[1] << 16, lo[2] | lo[3] << 16};
+  const s16x4 ph = __builtin_bit_cast(s16x4, uh), pl = __builtin_bit_cast(s16x4, ul);
+#define PRISMKV_PV16(N)                                                                  \
+  {                                                                                      \
+    const u32x2 vu = {dim_pair<N>(vr[0], vr[1]), dim_pair<N>(vr[2], vr[3])};             \
+    const s16x4 vb = __builtin_bit_cast(s16x4, vu);                                      \
+    st.acc[N] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ph, vb, st.acc[N], 0, 0, 0);   \
+    st.acc[N] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pl, vb, st.acc[N], 0, 0, 0);   \
+  }
+  PRISMKV_PV16(0) PRISMKV_PV16(1) PRISMKV_PV16(2) PRISMKV_PV16(3)
+  PRISMKV_PV16(4) PRISMKV_PV16(5) PRISMKV_PV16(6) PRISMKV_PV16(7)
+#undef PRISMKV_PV16
+}
+
+// Writes wave w's state (max, denominator, acc[4][128]) into LDS.
+template <int kWaves>
+__device__ __forceinline__ void mfma_stash(const MfmaAttn& st, MfmaLds<kWaves>& lds, int w) {
+  const int lane = threadIdx.x & 63;
+  float zt = st.z + __shfl_xor(st.z, 16);
+  zt += __shfl_xor(zt, 32);
+  if (lane < kHq) {
+    lds.sm[w][lane] = st.m;
+    lds.sz[w][lane] = zt;
+  }
+  if (lane < 16) {
+#pragma unroll
+    for (int r = 0; r < kHq; ++r) {
+      float4* dst = reinterpret_cast<float4*>(&lds.sacc[w][r][8 * lane]);
+      dst[0] = make_float4(st.acc[0][r], st.acc[1][r], st.acc[2][r], st.acc[3][r]);
+      dst[1] = make_float4(st.acc[4][r], st.acc[5][r], st.acc[6][r], st.acc[7][r]);
+    }
+  }
+}
+
+// Merges the kWaves wave states (after a barrier) into one split state per
+// head, published at stp + h * hstride as complemented words: (max, den) as
+// one 64-bit word, then acc[128].  Thread = (head tid >> 7, dim tid & 127).
+template <int kWaves>
+__device__ __forceinline__ void mfma_publish(MfmaLds<kWaves>& lds, float* stp, size_t hstride) {
+  const int tid = threadIdx.x;
+  __syncthreads();
+  if (tid < kWaves * kHq) {
+    const int k = tid >> 2, h = tid & 3;
+    float M = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) M = fmaxf(M, lds.sm[i][h]);
+    const float m = lds.sm[k][h];
+    lds.wt[k][h] = m == -INFINITY ? 0.f : exp2f(m - M);
+    if (k == 0) lds.mx[h] = M;
+  }
+  __syncthreads();
+  const int h = tid >> 7, d = tid & (kD - 1);
+  const float M = lds.mx[h];
+  float den = 0.f, v = 0.f;
+#pragma unroll
+  for (int k = 0; k < kWaves; ++k) {
+    const float wgt = lds.wt[k][h];
+    den = fmaf(wgt, lds.sz[k][h], den);
+    v = fmaf(wgt, lds.sacc[k][h][d], v);
+  }
+  float* sh = stp + (size_t)h * hstride;
+  if (d == 0)
+    st_dev(reinterpret_cast<unsigned long long*>(sh),
+           ~(((unsigned long long)__float_as_uint(den) << 32) | (unsigned long long)__float_as_uint(M)));
+  st_dev(reinterpret_cast<unsigned*>(sh + 2 + d), ~__float_as_uint(v));
+}
+
+}  // namespace
+}  // namespace prismkv

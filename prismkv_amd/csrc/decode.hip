@@ -46,7 +46,7 @@
 // device-scope fences.
 #include <algorithm>
 
-#include "attend_core.h"
+#include "attend_mfma.h"
 #include "score.h"
 
 namespace prismkv {
@@ -100,7 +100,8 @@ struct DecodeLds {
       alignas(16) unsigned long long own[2 * 64];  // this workgroup's keys (<= 96 used)
       alignas(16) unsigned long long best[kDT / 64 * kTop];
     } sel;
-    AttendLds att;
+    MfmaLds<kDT / 64> mf;
+    float wts[kDT / 64][64];  // split weights of the final merge
   };
 };
 
@@ -280,45 +281,45 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
 #pragma unroll
   for (int c = 0; c < kMaxSplits / 64; ++c) lower[c] = (64 * c + lane < p) ? 0u : kReady;
 
-  // ---- 6. attention over the tile's tokens, then its tail rows
+  // ---- 6. attention over the tile's tokens, then its tail rows: wave w
+  // takes the contiguous range [w * per, (w + 1) * per), per = ceil(rows / 8),
+  // in 16-row blocks, four blocks per round with every K/V load of the round
+  // issued up front
   const int n_sel = lds.nsel;
   const int t_lo = min(a.T, p * a.tail_per), t_hi = min(a.T, t_lo + a.tail_per);
   const int n_rows = n_sel + (t_hi - t_lo);
   {
-    const int q16 = lane & 15, slot = lane >> 4;
+    const int j = lane & 15, qd = lane >> 4;
     const int last_row = a.H + a.T - 1;
-    const uint16_t* kg = a.k + (size_t)g * a.ks + 8 * q16;
-    const uint16_t* vg = a.v + (size_t)g * a.vs + 8 * q16;
-    float qf[kHq][8];
+    const uint16_t* kg = a.k + (size_t)g * a.ks;
+    const uint16_t* vg = a.v + (size_t)g * a.vs;
+    const int per = (n_rows + kDT / 64 - 1) / (kDT / 64);
+    const int r0 = min(n_rows, w * per), r1 = min(n_rows, r0 + per);
+    // position of row r of the workgroup's list; rows past the wave's range
+    // repeat the range's first row (masked, same lines)
+    auto row_pos = [&](int r) {
+      r = r < r1 ? r : r0;
+      int pos = r < n_sel ? lds.rows[r] : a.H + t_lo + (r - n_sel);
+      return pos < 0 ? 0 : (pos > last_row ? last_row : pos);
+    };
+    MfmaAttn st;
+    mfma_init(st, a.q + (size_t)g * kHq * kD);
+    constexpr int kPerRound = 4;
+    for (int b0 = r0; b0 < r1; b0 += kPerRound * 16) {
+      uint4 kr[kPerRound][4], vr[kPerRound][4];
 #pragma unroll
-    for (int h = 0; h < kHq; ++h) {
-      unpack8(*reinterpret_cast<const uint4*>(a.q + ((size_t)g * kHq + h) * kD + 8 * q16), qf[h]);
+      for (int i = 0; i < kPerRound; ++i) {
+        const int base = b0 + 16 * i;
+        if (base < r1) {  // uniform per wave
+          const uint16_t* kp = kg + (size_t)row_pos(base + j) * kD + 8 * qd;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) qf[h][i] *= kLog2eScale;
-    }
-    SlotState s;
-    s.m = -INFINITY;
-    s.z = 0.f;
+          for (int c = 0; c < 4; ++c) kr[i][c] = load_nt16(kp + 32 * c);
 #pragma unroll
-    for (int h = 0; h < kHq; ++h)
-#pragma unroll
-      for (int i = 0; i < 8; ++i) s.acc[h][i] = 0.f;
-    // row r of the workgroup's list: wave w takes r = w + 8 (36 round + 4 i + slot)
-    for (int round = 0; round * (kDT / 64) * kWaveRows < n_rows; ++round) {
-      const int base = w + (kDT / 64) * (round * kWaveRows + slot);
-      uint4 kr[kSlotRows], vr[kSlotRows];
-#pragma unroll
-      for (int i = 0; i < kSlotRows; ++i) {
-        const int r = base + (kDT / 64) * 4 * i;
-        int pos = 0;
-        if (r < n_sel) pos = lds.rows[r];
-        else if (r < n_rows) pos = a.H + t_lo + (r - n_sel);
-        pos = pos < 0 ? 0 : (pos > last_row ? last_row : pos);
-        kr[i] = load_nt16(kg + (size_t)pos * kD);
-        vr[i] = load_nt16(vg + (size_t)pos * kD);
-        if ((i & 3) == 3) asm volatile("" ::: "memory");  // issue the rows step by step, in order
+          for (int t = 0; t < 4; ++t) vr[i][t] = load_nt16(vg + (size_t)row_pos(base + 4 * qd + t) * kD + 8 * j);
+        }
       }
-      if (round == 0 && w == 0) {
+      asm volatile("" ::: "memory");  // every load of the round is in flight before any is used
+      if (b0 == r0 && w == 0) {
 #pragma unroll
         for (int c = 0; c < kMaxSplits / 64; ++c) {
           const int qq = 64 * c + lane;
@@ -326,30 +327,22 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
         }
       }
 #pragma unroll
-      for (int st = 0; st < (kSlotRows + 3) / 4; ++st) {
-        int nv = 0;
-        uint4 ks[4], vs[4];
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const int i = st * 4 + b;
-          nv += (i < kSlotRows) && (base + (kDT / 64) * 4 * i < n_rows);
-          ks[b] = kr[i < kSlotRows ? i : kSlotRows - 1];
-          vs[b] = vr[i < kSlotRows ? i : kSlotRows - 1];
-        }
-        if (__ballot(nv > 0)) attend_step(qf, ks, vs, nv, s);
+      for (int i = 0; i < kPerRound; ++i) {
+        const int base = b0 + 16 * i;
+        if (base < r1) mfma_block16(st, kr[i], vr[i], min(16, r1 - base));
       }
     }
 
     // ---- 7. the tile's global ids offset (ids are written after phase 8)
     if (w == 0) {
-      const unsigned* st = a.status + (size_t)g * a.S;
+      const unsigned* tiles = a.status + (size_t)g * a.S;
       unsigned prefix = 0;
 #pragma unroll
       for (int c = 0; c < kMaxSplits / 64; ++c) {
         const int qq = 64 * c + lane;
         unsigned v = lower[c];
         wait_all([&] {
-          if (qq < p && !(v & kReady)) v = ld_dev(st + qq);
+          if (qq < p && !(v & kReady)) v = ld_dev(tiles + qq);
           return (v & kReady) != 0u;
         }, a.err);
         prefix += (unsigned)wave_sum_i(qq < p ? (int)(v & ~kReady) : 0);
@@ -363,7 +356,9 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     // ---- 8. the split state (after the look-back: its publication tells
     // workgroup 0 that this workgroup no longer reads any published word);
     // its barriers also publish lds.base to every wave
-    store_wg_state(s, lds.att, a.state + ((size_t)g * kHq * a.S + p) * kStateW, (size_t)a.S * kStateW, true);
+    __syncthreads();  // the LDS union is free (rows[] and base stay)
+    mfma_stash(st, lds.mf, w);
+    mfma_publish(lds.mf, a.state + ((size_t)g * kHq * a.S + p) * kStateW, (size_t)a.S * kStateW);
   }
   {
     int32_t* dst = a.ids + (size_t)g * a.ids_stride + lds.base;
@@ -372,7 +367,7 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
 
   // ---- 9. workgroup 0 merges the split states and clears the group's words
   if (p != 0) return;
-  merge_group(a.state, a.S, g, a.out, lds.att, a.err);
+  merge_group(a.state, a.S, g, a.out, lds.wts, a.err);
   __syncthreads();  // every state word this workgroup reads has been consumed
   for (int i = tid; i < kChunks * kHq; i += kDT) st_dev(&a.stats[(size_t)g * kChunks * kHq + i], 0ull);
   for (int i = tid; i < a.S * kTop; i += kDT) st_dev(&a.cand[(size_t)g * a.S * kTop + i], 0ull);
