@@ -102,8 +102,8 @@ __device__ __forceinline__ void mfma_block(MfmaAttn& st, const uint4 (&kr)[8], c
   float bm = s[0];
 #pragma unroll
   for (int t = 1; t < 8; ++t) bm = fmaxf(bm, s[t]);
-  bm = fmaxf(bm, __shfl_xor(bm, 16));
-  bm = fmaxf(bm, __shfl_xor(bm, 32));
+  bm = fmaxf(bm, xor16(bm));
+  bm = fmaxf(bm, xor32(bm));
   // lazy rescale: the running max moves only when a score exceeds it by kSlack
   const bool grow = bm > st.m + kSlack || (st.m == -INFINITY && bm != -INFINITY);
   if (__ballot(grow)) {
@@ -162,8 +162,8 @@ __device__ __forceinline__ void mfma_block16(MfmaAttn& st, const uint4 (&kr)[4],
 #pragma unroll
   for (int r = 0; r < 4; ++r) s[r] = (j < kHq && 4 * q + r < nvalid) ? d[r] * kLog2eScale : -INFINITY;
   float bm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-  bm = fmaxf(bm, __shfl_xor(bm, 16));
-  bm = fmaxf(bm, __shfl_xor(bm, 32));
+  bm = fmaxf(bm, xor16(bm));
+  bm = fmaxf(bm, xor32(bm));
   const bool grow = bm > st.m + kSlack || (st.m == -INFINITY && bm != -INFINITY);
   if (__ballot(grow)) {
     const float nm = grow ? bm : st.m;
@@ -209,8 +209,8 @@ __device__ __forceinline__ void mfma_block16(MfmaAttn& st, const uint4 (&kr)[4],
 template <int kWaves>
 __device__ __forceinline__ void mfma_stash(const MfmaAttn& st, MfmaLds<kWaves>& lds, int w) {
   const int lane = threadIdx.x & 63;
-  float zt = st.z + __shfl_xor(st.z, 16);
-  zt += __shfl_xor(zt, 32);
+  float zt = st.z + xor16(st.z);
+  zt += xor32(zt);
   if (lane < kHq) {
     lds.sm[w][lane] = st.m;
     lds.sz[w][lane] = zt;

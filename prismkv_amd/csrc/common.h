@@ -69,6 +69,37 @@ __device__ __forceinline__ float xor4(float v) {
 __device__ __forceinline__ float row_mirror(float v) { return dpp_f<0x140>(v); }       // lane i <- 15 - i
 __device__ __forceinline__ float row_half_mirror(float v) { return dpp_f<0x141>(v); }  // lane i <- 7 - i (in 8)
 
+// Exchanges across rows through the gfx950 permlane swaps (VALU, no LDS).
+// permlane32_swap(a, b) returns {a', b'}: a' = a in lanes 0-31 and b of lane
+// l - 32 in lanes 32-63; b' = a of lane l + 32 in lanes 0-31 and b in lanes
+// 32-63.  permlane16_swap does the same between rows 0/1 and 2/3.
+__device__ __forceinline__ unsigned xor32_u(unsigned v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return (threadIdx.x & 32) ? r[0] : r[1];
+}
+__device__ __forceinline__ unsigned xor16_u(unsigned v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  return (threadIdx.x & 16) ? r[0] : r[1];
+}
+__device__ __forceinline__ float xor32(float v) { return __uint_as_float(xor32_u(__float_as_uint(v))); }
+__device__ __forceinline__ float xor16(float v) { return __uint_as_float(xor16_u(__float_as_uint(v))); }
+// Transpose-reduce step across lane bit 5 (M = 32) or 4 (M = 16): lanes with
+// the bit clear return lo + lo of lane l ^ M, lanes with it set hi + hi of
+// lane l ^ M (own term first).
+template <int M>
+__device__ __forceinline__ float swap_add(float lo, float hi) {
+  const unsigned a = __float_as_uint(lo), b = __float_as_uint(hi);
+  if constexpr (M == 32) {
+    const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+    return (threadIdx.x & 32) ? __uint_as_float(r[1]) + __uint_as_float(r[0])
+                              : __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+    return (threadIdx.x & 16) ? __uint_as_float(r[1]) + __uint_as_float(r[0])
+                              : __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+}
+
 // Wave reductions: within each 16-lane row by DPP (pairs i^1, i^2, then the
 // mirrors i <-> 7-i and i <-> 15-i), then the 4 row results by readlane.
 // Fixed order, so results are run-to-run identical; the result is uniform.

@@ -95,6 +95,7 @@ struct DecodeLds {
     struct {
       float4 qq[kRow];
       TileLds tile[2];
+      SplitLds split;
     } score;
     struct {
       alignas(16) unsigned long long own[2 * 64];  // this workgroup's keys (<= 96 used)
@@ -171,27 +172,47 @@ __device__ void decode_select(const DecodeArgs& a, int g, int p, DecodeLds& lds)
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int S = a.S;
   const int own = (kChunks - p + S - 1) / S;  // tiles p, p + S, ... below 94
-  // ---- 1. score the own tiles: half 0 takes tiles 0 and 2, half 1 tile 1
+  // ---- 1. score the own tiles: half 0 takes tile 0, half 1 tile 1, then
+  // both halves tile 2 (half h its part h).  Loads go out in one batch with
+  // no branch: q first (so staging it waits for nothing else), then the
+  // tiles (a missing tile repeats a valid one), then the bucket sizes.
   {
     const int half = tid >> 8, t = tid & 255;
-    float4 m4[2][8];
-    load_tile(a.moments, g, p + S * half, t, half < own, m4[0]);
-    load_tile(a.moments, g, p + S * 2, t, half == 0 && own > 2, m4[1]);
-    stage_query(a.q, g, lds.score.qq, tid, kDT);
+    unsigned qv = load_query512(a.q, g, tid);
+    const int c0 = min(p + S * half, kChunks - 1), c2 = min(p + S * 2, kChunks - 1);
+    float4 m4[8], m2[4];
+    load_tile(a.moments, g, c0, t, m4);
+    load_half_tile(a.moments, g, c2, half, t, m2);
+    const int* cg = a.counts + (size_t)g * kFP + (t & 31);
+    const int n0 = cg[c0 * kChunk], n2 = cg[c2 * kChunk];
+    // every load above is issued before q is first used (the asm takes q as
+    // an operand, so even its conversion cannot move up between the loads)
+    asm volatile("" : "+v"(qv) :: "memory");
+    store_query512(qv, lds.score.qq, tid);
     __syncthreads();
-#pragma unroll
-    for (int r = 0; r < 2; ++r) {
-      if (r == 1 && own <= 2) break;  // uniform
-      const int j = r == 0 ? half : 2;
-      const bool has = r == 0 ? half < own : half == 0;
-      if (r == 1) __syncthreads();  // the first round's LDS reads are done
-      const float l = tile_logit(lds.score.qq, m4[r], t, lds.score.tile[half], a.counts, g, p + S * j, has);
+    // the statistics are published after both rounds: a store issued between
+    // the second tile's loads and their use would make that wait cover the
+    // store's write-through as well (stores count in the same counter)
+    float2 st0 = make_float2(0.f, 0.f), st2 = make_float2(0.f, 0.f);
+    {
+      const bool has = half < own;
+      const float l = tile_logit(lds.score.qq, m4, t, lds.score.tile[half], n0, has);
       if (t < kHq * kChunk && has) {
-        const int h = t >> 5, b = t & 31;
-        lds.tl[j][h][b] = l;
-        const float2 st = chunk_stats(l);
-        if (b == 0) pub2(&a.stats[((size_t)g * kChunks + p + S * j) * kHq + h], st.x, st.y);
+        lds.tl[half][t >> 5][t & 31] = l;
+        st0 = chunk_stats(l);
       }
+    }
+    if (own > 2) {  // uniform; its LDS is disjoint from the first round's
+      const float l = tile_logit_split(lds.score.qq, m2, tid, lds.score.split, n2, true);
+      if (tid < kHq * kChunk) {
+        lds.tl[2][tid >> 5][tid & 31] = l;
+        st2 = chunk_stats(l);
+      }
+    }
+    if (t < kHq * kChunk && (t & 31) == 0) {
+      const int h = t >> 5;
+      if (half < own) pub2(&a.stats[((size_t)g * kChunks + p + S * half) * kHq + h], st0.x, st0.y);
+      if (half == 0 && own > 2) pub2(&a.stats[((size_t)g * kChunks + p + S * 2) * kHq + h], st2.x, st2.y);
     }
   }
   __syncthreads();

@@ -52,10 +52,11 @@ __global__ __launch_bounds__(kRT) void route_score_kernel(const uint16_t* __rest
   __shared__ float4 qq[kRow];  // [k] -> 4 heads; k < 128: q, k >= 128: q*q
   __shared__ TileLds lds;
   float4 m4[8];
-  load_tile(moments, g, c, tid, true, m4);  // 16-byte tile loads first
+  load_tile(moments, g, c, tid, m4);  // 16-byte tile loads first
+  const int n = tid < kHq * kChunk ? counts[(size_t)g * kFP + c * kChunk + (tid & 31)] : 0;
   stage_query(q, g, qq, tid, kRT);
   __syncthreads();
-  const float l = tile_logit(qq, m4, tid, lds, counts, g, c, true);
+  const float l = tile_logit(qq, m4, tid, lds, n, true);
   if (tid < kHq * kChunk) {
     // thread = (head tid>>5, bucket tid&31); 32 lanes per head
     const int h = tid >> 5, b = tid & 31;

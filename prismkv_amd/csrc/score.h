@@ -22,17 +22,23 @@ namespace {
 
 constexpr float kSqrtD = 11.3137084989847604f;  // fp32(sqrt(128)), core.py:125
 
-// Transpose-reduce step: `x` holds 2n partial sums; lanes whose `mask` bit is
-// set keep the upper half, the others the lower half, and add the partner's
-// copy of the kept half.  After the step x[0..n) holds the new partial sums.
-template <int N>
-__device__ __forceinline__ void treduce(float* x, int mask) {
-  const unsigned long long hi = __ballot((threadIdx.x & mask) != 0);
+// Transpose-reduce step over lane bit M (32, 16 or 8): `x` holds 2N partial
+// sums; lanes with the bit set keep the upper half, the others the lower
+// half, and add the partner's copy of the kept half (own term first).  After
+// the step x[0..N) holds the new partial sums.
+template <int N, int M>
+__device__ __forceinline__ void treduce(float* x) {
+  if constexpr (M == 32 || M == 16) {
 #pragma unroll
-  for (int j = 0; j < N; ++j) {
-    const float keep = lane_select(hi, x[j + N], x[j]);
-    const float send = lane_select(hi, x[j], x[j + N]);
-    x[j] = keep + __shfl_xor(send, mask);
+    for (int j = 0; j < N; ++j) x[j] = swap_add<M>(x[j], x[j + N]);
+  } else {
+    const unsigned long long hi = __ballot((threadIdx.x & M) != 0);
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const float keep = lane_select(hi, x[j + N], x[j]);
+      const float send = lane_select(hi, x[j], x[j + N]);
+      x[j] = keep + xor8(send);
+    }
   }
 }
 
@@ -52,25 +58,38 @@ __device__ __forceinline__ void stage_query(const uint16_t* q, int g, float4* qq
     reinterpret_cast<float*>(&qq[kD + k])[h] = x * x;  // core.py:127 q.square() in fp32
   }
 }
+// The same for exactly 512 threads, split so the caller can issue the q load
+// before its tile loads (its wait then leaves those in flight): the raw bf16
+// bits are loaded first and converted only in store_query512.
+__device__ __forceinline__ unsigned load_query512(const uint16_t* q, int g, int t) {
+  return q[((size_t)g * kHq + (t >> 7)) * kD + (t & (kD - 1))];
+}
+__device__ __forceinline__ void store_query512(unsigned bits, float4* qq, int t) {
+  const float x = __uint_as_float(bits << 16);
+  const int h = t >> 7, k = t & (kD - 1);
+  reinterpret_cast<float*>(&qq[k])[h] = x;
+  reinterpret_cast<float*>(&qq[kD + k])[h] = x * x;  // core.py:127 q.square() in fp32
+}
 
-// The 16-byte loads of tile (g, c) for thread t (0..255); zeros if !has.
-__device__ __forceinline__ void load_tile(const float* moments, int g, int c, int t, bool has, float4 (&m4)[8]) {
+// The 16-byte loads of tile (g, c) for thread t (0..255); c must be a valid
+// tile (no branch, so every load of the caller stays in flight together).
+__device__ __forceinline__ void load_tile(const float* moments, int g, int c, int t, float4 (&m4)[8]) {
   const int quad = t & 7, r = t >> 3;
   const float4* tile = reinterpret_cast<const float4*>(moments + (size_t)(g * kChunks + c) * kRow * kChunk);
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (has) v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tile + (r + 32 * i) * (kChunk / 4) + quad));
+    const u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(tile + (r + 32 * i) * (kChunk / 4) + quad));
     m4[i] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
   }
 }
 
 // Products and reductions of one tile; returns, in thread t < 128, the logit
-// of head t >> 5 for bucket 32c + (t & 31) (-inf for a dead bucket).  Every
-// thread of the workgroup must call it (two barriers); t is the thread's
-// index within its 256-thread scorer, whose 4 waves are consecutive.
-__device__ __forceinline__ float tile_logit(const float4* qq, const float4 (&m4)[8], int t, TileLds& s,
-                                            const int* counts, int g, int c, bool has) {
+// of head t >> 5 for bucket 32c + (t & 31) whose size is `n` (loaded by the
+// caller with the tile, so no load waits here; -inf for a dead bucket).
+// Every thread of the workgroup must call it (two barriers); t is the
+// thread's index within its 256-thread scorer, whose 4 waves are consecutive.
+__device__ __forceinline__ float tile_logit(const float4* qq, const float4 (&m4)[8], int t, TileLds& s, int n,
+                                            bool has) {
   const int r = t >> 3, w = t >> 6, lane = t & 63;
   // acc[part*16 + head*4 + j]: part 0 = mean rows, 1 = variance rows
   float acc[32];
@@ -88,9 +107,9 @@ __device__ __forceinline__ float tile_logit(const float4* qq, const float4 (&m4)
       for (int j = 0; j < 4; ++j) acc[part * 16 + h * 4 + j] = fmaf(hq[h], mv[j], acc[part * 16 + h * 4 + j]);
   }
   // reduce over the 8 row lanes of the wave (lane bits 5,4,3)
-  treduce<16>(acc, 32);
-  treduce<8>(acc, 16);
-  treduce<4>(acc, 8);
+  treduce<16, 32>(acc);
+  treduce<8, 16>(acc);
+  treduce<4, 8>(acc);
   // lane now holds part (lane>>5)&1, head (lane>>3)&3, buckets 4*quad .. +3
   s.red[w][lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
   __syncthreads();
@@ -105,7 +124,73 @@ __device__ __forceinline__ float tile_logit(const float4* qq, const float4 (&m4)
   float l = -INFINITY;
   if (t < kHq * kChunk && has) {
     const int h = t >> 5, b = t & 31;
-    const int n = counts[(size_t)g * kFP + c * kChunk + b];
+    if (n > 0) {
+      // core.py:122-127: log(count) + (q @ mean^T) / sqrt(d) + (q^2 @ var^T) / (2d)
+      const float lc = logf((float)n);
+      l = (lc + s.dots[0][h][b] / kSqrtD) + s.dots[1][h][b] / (2.0f * kD);
+    }
+  }
+  return l;
+}
+
+// One tile scored by both halves of a 512-thread workgroup: half h takes
+// part h (h = 0: mean rows 0..127, 1: variance rows 128..255) with 4 loads
+// per thread.  Every dot product is the same tree of additions as in
+// tile_logit (row lanes paired by lane bit 5, then 4, then 3; each pair sum
+// is commutative; then the 4 waves in order), so the logits are bit-identical.
+struct SplitLds {
+  float2 red[2][4][64];
+  float dots[2][kHq][kChunk];
+};
+
+__device__ __forceinline__ void load_half_tile(const float* moments, int g, int c, int part, int t, float4 (&m4)[4]) {
+  const int quad = t & 7, r = t >> 3;
+  const float4* tile = reinterpret_cast<const float4*>(moments + (size_t)(g * kChunks + c) * kRow * kChunk);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const u32x4 v = __builtin_nontemporal_load(
+        reinterpret_cast<const u32x4*>(tile + (r + 32 * i + 128 * part) * (kChunk / 4) + quad));
+    m4[i] = make_float4(__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w));
+  }
+}
+
+// Returns the logit in threads tid < 128 (head tid >> 5, bucket 32c + (tid & 31),
+// size n); every thread of the 512 must call it (two barriers).
+__device__ __forceinline__ float tile_logit_split(const float4* qq, const float4 (&m4)[4], int tid, SplitLds& s, int n,
+                                                  bool has) {
+  const int half = tid >> 8, t = tid & 255, r = t >> 3, w = t >> 6, lane = t & 63;
+  float acc[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float4 qv = qq[r + 32 * i + 128 * half];
+    const float* hq = reinterpret_cast<const float*>(&qv);
+    const float* mv = reinterpret_cast<const float*>(&m4[i]);
+#pragma unroll
+    for (int h = 0; h < kHq; ++h)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[h * 4 + j] = fmaf(hq[h], mv[j], acc[h * 4 + j]);
+  }
+  // lane bit 5 -> head bit 1, bit 4 -> head bit 0, bit 3 -> bucket bit 1
+  treduce<8, 32>(acc);
+  treduce<4, 16>(acc);
+  treduce<2, 8>(acc);
+  s.red[half][w][lane] = make_float2(acc[0], acc[1]);
+  __syncthreads();
+  if (t < kHq * kChunk) {
+    const int h = t >> 5, b = t & 31;
+    const int L = ((h >> 1) << 5) | ((h & 1) << 4) | (((b & 3) >> 1) << 3) | (b >> 2);
+    const bool hi = b & 1;
+    const float v = (((hi ? s.red[half][0][L].y : s.red[half][0][L].x) + (hi ? s.red[half][1][L].y : s.red[half][1][L].x)) +
+                     (hi ? s.red[half][2][L].y : s.red[half][2][L].x)) +
+                    (hi ? s.red[half][3][L].y : s.red[half][3][L].x);
+    s.dots[half][h][b] = v;
+  }
+  __syncthreads();
+  float l = -INFINITY;
+  if (tid < kHq * kChunk && has) {
+    const int h = tid >> 5, b = tid & 31;
     if (n > 0) {
       // core.py:122-127: log(count) + (q @ mean^T) / sqrt(d) + (q^2 @ var^T) / (2d)
       const float lc = logf((float)n);
@@ -119,11 +204,17 @@ __device__ __forceinline__ float tile_logit(const float4* qq, const float4 (&m4)
 // 32-63 of a wave, all active).
 __device__ __forceinline__ float2 chunk_stats(float l) {
   float m = l;
-#pragma unroll
-  for (int o = 16; o; o >>= 1) m = fmaxf(m, __shfl_xor(m, o));
+  m = fmaxf(m, xor16(m));
+  m = fmaxf(m, xor8(m));
+  m = fmaxf(m, xor4(m));
+  m = fmaxf(m, xor2(m));
+  m = fmaxf(m, xor1(m));
   float e = (l == -INFINITY) ? 0.f : expf(l - m);
-#pragma unroll
-  for (int o = 16; o; o >>= 1) e += __shfl_xor(e, o);
+  e += xor16(e);
+  e += xor8(e);
+  e += xor4(e);
+  e += xor2(e);
+  e += xor1(e);
   return make_float2(m, e);
 }
 

@@ -98,10 +98,12 @@ __device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
   const int hi = __builtin_amdgcn_mov_dpp((int)(unsigned)(v >> 32), kCtrl, 0xF, 0xF, false);
   return ((unsigned long long)(unsigned)hi << 32) | (unsigned long long)(unsigned)lo;
 }
-__device__ __forceinline__ unsigned long long shfl_xor_u64(unsigned long long v, int m) {
-  const int lo = __shfl_xor((int)(unsigned)v, m);
-  const int hi = __shfl_xor((int)(unsigned)(v >> 32), m);
-  return ((unsigned long long)(unsigned)hi << 32) | (unsigned long long)(unsigned)lo;
+// The key of lane (lane ^ M) for M = 16 or 32 (permlane swaps, no LDS).
+template <int M>
+__device__ __forceinline__ unsigned long long xor_rows_u64(unsigned long long v) {
+  const unsigned lo = M == 32 ? xor32_u((unsigned)v) : xor16_u((unsigned)v);
+  const unsigned hi = M == 32 ? xor32_u((unsigned)(v >> 32)) : xor16_u((unsigned)(v >> 32));
+  return ((unsigned long long)hi << 32) | (unsigned long long)lo;
 }
 // The key of lane (lane ^ D) for D in {1, 2, 4, 8} (within the row).
 template <int D>
@@ -148,8 +150,8 @@ __device__ __forceinline__ unsigned long long merge_top16(unsigned long long a, 
 }
 // Rows sorted descending -> every row holds the descending top 16 of the wave.
 __device__ __forceinline__ unsigned long long rows_top16(unsigned long long v) {
-  v = merge_top16(v, shfl_xor_u64(v, 16));
-  return merge_top16(v, shfl_xor_u64(v, 32));
+  v = merge_top16(v, xor_rows_u64<16>(v));
+  return merge_top16(v, xor_rows_u64<32>(v));
 }
 // Top-16 of K sets of 64 keys whose rows are already sorted descending:
 // lane j < 16 of every row ends with the rank-j key (0 if fewer keys).
