@@ -59,6 +59,9 @@ constexpr int kMinSplits = 32;     // at least one workgroup per CU for the scor
 constexpr int kMaxSplits = 256;    // one group's workgroups must fit on the GPU at once
 constexpr int kMaxOwn = (kChunks + kMinSplits - 1) / kMinSplits;  // moment tiles per workgroup (3)
 constexpr unsigned kReady = 1u << 31;
+constexpr int kSlices = 4;                    // 32-dim slices of a head's output
+constexpr int kSliceW = 2 + kD / kSlices;     // {max, den, acc[32]} per (split, head, slice)
+constexpr int kMergers = kHq * kSlices;       // workgroups 0..15 each merge one (head, slice)
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -74,7 +77,7 @@ struct DecodeArgs {
   unsigned long long* cand;   // [G][S][16] published best keys of each workgroup
   unsigned* status;           // [G][S] kReady | tile count
   unsigned* err;
-  float* state;  // [G*4][S][130] published split states
+  float* state;  // [G][S][4 heads][4 slices][34] published split states
   int64_t* features;
   float* valid;
   int* raw;
@@ -102,7 +105,11 @@ struct DecodeLds {
       alignas(16) unsigned long long best[kDT / 64 * kTop];
     } sel;
     MfmaLds<kDT / 64> mf;
-    float wts[kDT / 64][64];  // split weights of the final merge
+    struct {
+      float2 mz[kMaxSplits];                 // (max, den) of every split
+      float red[kDT / 64];                    // per-wave partial max / den
+      float part[kDT / 32][kD / kSlices];    // per split-group partial sums
+    } fin;
   };
 };
 
@@ -128,6 +135,122 @@ __device__ __forceinline__ void pub2(unsigned long long* p, float a, float b) {
 __device__ __forceinline__ float2 unpub2(unsigned long long r) {
   r = ~r;
   return make_float2(__uint_as_float((unsigned)r), __uint_as_float((unsigned)(r >> 32)));
+}
+
+// Phase 8: merges the 8 wave states in LDS (as mfma_publish) and publishes
+// them per (head, 32-dim slice) as complemented words {max, den, acc[32]}:
+// each slice has its own copy of (max, den), so every published word has
+// exactly one reader.  Thread = (head tid >> 7, dim tid & 127).
+__device__ __forceinline__ void publish_sliced(MfmaLds<kDT / 64>& lds, float* stp) {
+  const int tid = threadIdx.x;
+  __syncthreads();
+  if (tid < (kDT / 64) * kHq) {
+    const int k = tid >> 2, h = tid & 3;
+    float M = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kDT / 64; ++i) M = fmaxf(M, lds.sm[i][h]);
+    const float m = lds.sm[k][h];
+    lds.wt[k][h] = m == -INFINITY ? 0.f : exp2f(m - M);
+    if (k == 0) lds.mx[h] = M;
+  }
+  __syncthreads();
+  const int h = tid >> 7, d = tid & (kD - 1);
+  const float M = lds.mx[h];
+  float den = 0.f, v = 0.f;
+#pragma unroll
+  for (int k = 0; k < kDT / 64; ++k) {
+    const float wgt = lds.wt[k][h];
+    den = fmaf(wgt, lds.sz[k][h], den);
+    v = fmaf(wgt, lds.sacc[k][h][d], v);
+  }
+  float* sl = stp + (h * kSlices + (d >> 5)) * kSliceW;
+  if ((d & 31) == 0)
+    st_dev(reinterpret_cast<unsigned long long*>(sl),
+           ~(((unsigned long long)__float_as_uint(den) << 32) | (unsigned long long)__float_as_uint(M)));
+  st_dev(reinterpret_cast<unsigned*>(sl + 2 + (d & 31)), ~__float_as_uint(v));
+}
+
+// Phase 9 for (head h, slice c): polls the S published (max, den) pairs and
+// the S x 32 accumulators of the slice, merges them exactly
+// (out = sum_k e^(m_k - M) acc_k / sum_k e^(m_k - M) den_k, 0 if the
+// denominator is 0), writes out[g][h][32c .. 32c + 32) and clears the words.
+// Thread = (dim tid & 31, split group tid >> 5): splits k = group + 16 i.
+__device__ __forceinline__ void merge_slice(const DecodeArgs& a, int g, int h, int c, DecodeLds& lds) {
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, d = tid & 31, sg = tid >> 5;
+  const int S = a.S;
+  constexpr int kGroups = kDT / 32;  // 16
+  const size_t stride = (size_t)kHq * kSlices * kSliceW;  // floats per split
+  float* base = a.state + (size_t)g * S * stride + (h * kSlices + c) * kSliceW;
+  // every load of the merge is issued together and repeated until it has landed
+  unsigned long long rmz = 0;
+  unsigned racc[kMaxSplits / kGroups];
+#pragma unroll
+  for (int i = 0; i < kMaxSplits / kGroups; ++i) racc[i] = 0u;
+  for (int spins = 0;; ++spins) {
+    bool ok = true;
+    if (tid < S) {
+      if (rmz == 0) rmz = ld_dev(reinterpret_cast<const unsigned long long*>(base + (size_t)tid * stride));
+      ok = rmz != 0;
+    }
+#pragma unroll
+    for (int i = 0; i < kMaxSplits / kGroups; ++i) {
+      const int k = sg + kGroups * i;
+      if (k < S) {
+        if (racc[i] == 0u) racc[i] = ld_dev(reinterpret_cast<const unsigned*>(base + (size_t)k * stride + 2 + d));
+        ok = ok && racc[i] != 0u;
+      }
+    }
+    if (__syncthreads_and(ok)) break;
+    if (spins >= kSpinLimit) {
+      if (tid == 0) atomicOr(a.err, 1u);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  // M = max over splits, den = sum of weighted denominators (fixed order)
+  float2 mz = make_float2(-INFINITY, 0.f);
+  if (tid < S) {
+    const unsigned long long r = ~rmz;
+    mz = make_float2(__uint_as_float((unsigned)r), __uint_as_float((unsigned)(r >> 32)));
+    lds.fin.mz[tid] = mz;
+  }
+  float m = wave_max(mz.x);
+  if (lane == 0) lds.fin.red[w] = m;
+  __syncthreads();
+  float M = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < kDT / 64; ++i) M = fmaxf(M, lds.fin.red[i]);
+  const float wk = (tid < S && mz.x != -INFINITY) ? exp2f(mz.x - M) : 0.f;
+  const float dsum = wave_sum(wk * mz.y);
+  __syncthreads();  // everyone has read red[] as maxima
+  if (lane == 0) lds.fin.red[w] = dsum;
+  // weighted accumulators of this thread's splits
+  float v = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxSplits / kGroups; ++i) {
+    const int k = sg + kGroups * i;
+    if (k < S) {
+      const float mk = lds.fin.mz[k].x;
+      const float wgt = mk == -INFINITY ? 0.f : exp2f(mk - M);
+      v = fmaf(wgt, __uint_as_float(~racc[i]), v);
+    }
+  }
+  lds.fin.part[sg][d] = v;
+  __syncthreads();
+  if (tid < 32) {
+    float den = 0.f;
+#pragma unroll
+    for (int i = 0; i < kDT / 64; ++i) den += lds.fin.red[i];
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < kGroups; ++i) acc += lds.fin.part[i][tid];
+    a.out[((size_t)g * kHq + h) * kD + c * (kD / kSlices) + tid] = f32_to_bf16(den > 0.f ? acc / den : 0.f);
+  }
+  // every word read above has been consumed (the barrier follows the last use)
+  for (int i = tid; i < S * kSliceW; i += kDT) {
+    const int k = i / kSliceW, e = i - k * kSliceW;
+    st_dev(reinterpret_cast<unsigned*>(base + (size_t)k * stride + e), 0u);
+  }
 }
 
 // Phase 4 for KW sets of 64 candidates per wave: wave w polls the published
@@ -379,22 +502,24 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     // its barriers also publish lds.base to every wave
     __syncthreads();  // the LDS union is free (rows[] and base stay)
     mfma_stash(st, lds.mf, w);
-    mfma_publish(lds.mf, a.state + ((size_t)g * kHq * a.S + p) * kStateW, (size_t)a.S * kStateW);
+    publish_sliced(lds.mf, a.state + (size_t)(g * a.S + p) * kHq * kSlices * kSliceW);
   }
   {
     int32_t* dst = a.ids + (size_t)g * a.ids_stride + lds.base;
     for (int i = tid; i < n_sel; i += kDT) dst[i] = lds.rows[i];
   }
 
-  // ---- 9. workgroup 0 merges the split states and clears the group's words
-  if (p != 0) return;
-  merge_group(a.state, a.S, g, a.out, lds.wts, a.err);
-  __syncthreads();  // every state word this workgroup reads has been consumed
-  for (int i = tid; i < kChunks * kHq; i += kDT) st_dev(&a.stats[(size_t)g * kChunks * kHq + i], 0ull);
-  for (int i = tid; i < a.S * kTop; i += kDT) st_dev(&a.cand[(size_t)g * a.S * kTop + i], 0ull);
-  for (int i = tid; i < a.S; i += kDT) st_dev(&a.status[(size_t)g * a.S + i], 0u);
-  unsigned* sw = reinterpret_cast<unsigned*>(a.state + (size_t)g * kHq * a.S * kStateW);
-  for (int i = tid; i < kHq * a.S * kStateW; i += kDT) st_dev(&sw[i], 0u);
+  // ---- 9. workgroups 0..15 each merge one (head, 32-dim slice) of the S
+  // split states into out[g] and clear the words they read; workgroup 0
+  // also clears the group's statistics, candidates and tile counts (every
+  // workgroup has published its state, so none reads them any more)
+  if (p >= kMergers) return;
+  merge_slice(a, g, p >> 2, p & 3, lds);
+  if (p == 0) {
+    for (int i = tid; i < kChunks * kHq; i += kDT) st_dev(&a.stats[(size_t)g * kChunks * kHq + i], 0ull);
+    for (int i = tid; i < a.S * kTop; i += kDT) st_dev(&a.cand[(size_t)g * a.S * kTop + i], 0ull);
+    for (int i = tid; i < a.S; i += kDT) st_dev(&a.status[(size_t)g * a.S + i], 0u);
+  }
 }
 
 }  // namespace
@@ -418,7 +543,7 @@ struct DecodeWorkLayout {
     stats = take((size_t)groups * kChunks * kHq * sizeof(unsigned long long));
     cand = take((size_t)groups * S * kTop * sizeof(unsigned long long));
     status = take((size_t)groups * S * sizeof(unsigned));
-    state = take((size_t)groups * kHq * S * kStateW * sizeof(float));
+    state = take((size_t)groups * S * kHq * kSlices * kSliceW * sizeof(float));
     total = o;
   }
 };
