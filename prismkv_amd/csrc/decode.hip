@@ -10,7 +10,8 @@
 // emission of kernels/ppu_8b/union.cu:26.
 //
 // Grid (S, G) x 512, S = clamp(ceil(ceil(H/32) / 64), 32, 256).  Workgroup p
-// of group g owns moment tiles p, p + S, p + 2S, ... (at most 3 of the 94),
+// of group g owns the contiguous moment tiles kp .. kp + k - 1 of the 94
+// (k = ceil(94 / S) <= 3: one 96 KB stream per workgroup),
 // bitmap words [64p, 64p + 64) (tokens [2048p, 2048p + 2048)) and tail rows
 // [p * ceil(T/S), ...).  Phases:
 //   1. score its tiles (two 256-thread scorers side by side, every tile load
@@ -294,7 +295,10 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, DecodeLd
 __device__ void decode_select(const DecodeArgs& a, int g, int p, DecodeLds& lds) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int S = a.S;
-  const int own = (kChunks - p + S - 1) / S;  // tiles p, p + S, ... below 94
+  // moment tiles kper * p + j, j < own: contiguous 32 KB tiles, one stream per workgroup
+  const int kper = (kChunks + S - 1) / S;
+  const int own = max(0, min(kper, kChunks - kper * p));
+  auto tile = [&](int j) { return kper * p + j; };
   // ---- 1. score the own tiles: half 0 takes tile 0, half 1 tile 1, then
   // both halves tile 2 (half h its part h).  Loads go out in one batch with
   // no branch: q first (so staging it waits for nothing else), then the
@@ -302,7 +306,7 @@ __device__ void decode_select(const DecodeArgs& a, int g, int p, DecodeLds& lds)
   {
     const int half = tid >> 8, t = tid & 255;
     unsigned qv = load_query512(a.q, g, tid);
-    const int c0 = min(p + S * half, kChunks - 1), c2 = min(p + S * 2, kChunks - 1);
+    const int c0 = min(tile(half), kChunks - 1), c2 = min(tile(2), kChunks - 1);
     float4 m4[8], m2[4];
     load_tile(a.moments, g, c0, t, m4);
     load_half_tile(a.moments, g, c2, half, t, m2);
@@ -334,8 +338,8 @@ __device__ void decode_select(const DecodeArgs& a, int g, int p, DecodeLds& lds)
     }
     if (t < kHq * kChunk && (t & 31) == 0) {
       const int h = t >> 5;
-      if (half < own) pub2(&a.stats[((size_t)g * kChunks + p + S * half) * kHq + h], st0.x, st0.y);
-      if (half == 0 && own > 2) pub2(&a.stats[((size_t)g * kChunks + p + S * 2) * kHq + h], st2.x, st2.y);
+      if (half < own) pub2(&a.stats[((size_t)g * kChunks + tile(half)) * kHq + h], st0.x, st0.y);
+      if (half == 0 && own > 2) pub2(&a.stats[((size_t)g * kChunks + tile(2)) * kHq + h], st2.x, st2.y);
     }
   }
   __syncthreads();
@@ -362,7 +366,7 @@ __device__ void decode_select(const DecodeArgs& a, int g, int p, DecodeLds& lds)
     uint64_t key = 0;
     if (j < own) {
       const float lv[kHq] = {lds.tl[j][0][b], lds.tl[j][1][b], lds.tl[j][2][b], lds.tl[j][3][b]};
-      key = bucket_key(lv, lds.gmax, lds.grz, (p + S * j) * kChunk + b);
+      key = bucket_key(lv, lds.gmax, lds.grz, tile(j) * kChunk + b);
     }
     lds.sel.own[tid] = key;
   }
