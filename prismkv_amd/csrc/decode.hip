@@ -28,14 +28,16 @@
 //   5. union tile: one wave ORs the selected rows over its 64 words and
 //      compacts the set bits into an LDS token list, publishing the tile's
 //      count (and requesting the lower tiles' counts);
-//   6. attention over the tile's tokens plus its tail share, 36 rows per
-//      wave per round, every load of a round in flight at once;
+//   6. attention over the tile's tokens plus its tail share: wave w takes a
+//      contiguous eighth of the rows in 16-row MFMA blocks, with the K/V
+//      loads of four blocks in flight at once;
 //   7. the tile's ids offset: prefix = sum of the counts of the lower tiles;
 //   8. its split state (per head max, denominator, acc[128]) is published,
 //      then the tile's ids go to ids[g][prefix ...];
-//   9. workgroup 0 reads the S split states as they land, merges them into
-//      out[g], and clears every published word of the group, so the launch
-//      replays from a graph without memset nodes.
+//   9. workgroups 0..15 each read one (head, 32-dim slice) of the S split
+//      states as they land, merge it into out[g] and clear the words they
+//      read; workgroup 0 also clears the group's statistics, candidates and
+//      tile counts, so the launch replays from a graph without memset nodes.
 // Published words hold the bitwise complement of their value, so a zero
 // word (as cleared, or as the zero-filled workspace starts) reads as "not
 // yet written": readers poll the data itself, one memory round trip after

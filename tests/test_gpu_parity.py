@@ -144,6 +144,21 @@ def test_graph_replay_matches_eager():
         _ = (torch.randn(1000, device="cuda") * 2).sum().item()   # unrelated eager work between replays
 
 
+def test_no_tail_and_uneven_split_count():
+    # T = 0 (the step right after an index update) and H = 81920: 40 workgroups
+    # per group, 3 moment tiles each, 640 candidates per group
+    check_case(cases.native_case(4096, 0, "random", seed=7), splits_list=(32,), schedules=(0,))
+    check_case(cases.native_case(81920, 9, "random", seed=8), splits_list=(64,), schedules=(0,))
+
+
+def test_long_history_uses_split_path(monkeypatch):
+    # beyond the single-launch limit Native8B.__call__ runs route + attention;
+    # the limit is lowered here so a small case takes that branch
+    import prismkv_amd.native8b as nb
+    monkeypatch.setattr(nb, "FUSED_MAX_HISTORY", 1000)
+    check_case(cases.native_case(1025, 3, "random"), splits_list=(32,), schedules=(0,))
+
+
 def test_union_262k_history():
     # H beyond the reference union limit (131072): 8 groups x 262144 tokens
     check_case(cases.native_case(262144, 64, "random", seed=5), splits_list=(128,), schedules=(0,))
