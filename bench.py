@@ -56,7 +56,7 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--update-blocks", default="1024,4096",
                    help="block sizes of the amortised index-update timing (tokens per append)")
-    p.add_argument("--stages", default="chain,route,union,attend,update,copy",
+    p.add_argument("--stages", default="chain,route,union,attend,update,build,copy",
                    help="comma list of timed regions (for profiling runs)")
     return p.parse_args()
 
@@ -202,6 +202,37 @@ def update_timing(lib_path, H, blocks, steps, warmup, seed, device):
     return out
 
 
+@torch.no_grad()
+def build_timing(lib_path, H, steps, warmup, seed, device):
+    """Prefill index build of one layer: one prismkv_build per replay (center,
+    bitmap clear, encode, exact BatchTopK with budget 8 H, bitmap set,
+    per-bucket two-pass moments) for the 8 groups' K rows [0, H), into the
+    tables of a dedicated instance."""
+    from prismkv_amd import Native8B
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed * 104729)
+    k = torch.randn(G, H, D, generator=gen, device=device).to(torch.bfloat16)
+    W = torch.randn(G, F, D, generator=gen, device=device) / D ** 0.5
+    b = torch.zeros(G, F, device=device)
+    op = Native8B.from_keys(k, H, W, b, torch.ones(G), 8, lib_path, keep_activations=True)
+    torch.cuda.synchronize()
+
+    def once():
+        op.lib.call("prismkv_build", k.data_ptr(), op.W_enc.data_ptr(), op.b_enc.data_ptr(), op.center.data_ptr(),
+                    op.key_scale.data_ptr(), op.bits.data_ptr(), op.n.data_ptr(), op.moments.data_ptr(),
+                    op.build_work.data_ptr(), G, op.build_batch, H, 8, 1, k.stride(0), op.row_words,
+                    stream=torch.cuda.current_stream().cuda_stream)
+    ms, _, _ = graph_time(once, max(2, steps // 4), max(1, warmup // 4))
+    flops = 2.0 * G * H * F * D
+    out = dict(history=H, ms_per_layer=round(ms, 3), groups_per_batch=op.build_batch,
+               memberships_per_group=int(op.n[0].sum()), encode_gflop=round(flops / 1e9, 1),
+               encode_tflops_if_alone=round(flops / (ms * 1e-3) / 1e12, 2))
+    log(f"build H={H}: {ms:.2f} ms per layer (8 groups)")
+    del op, k, W, b
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(op, q, k, v, H, budget_s):
     """C oracle (single thread) on layer 0: route + union + AV for 8 groups."""
     import oracle
@@ -317,6 +348,7 @@ def main():
     if "update" in stages:
         blocks = [int(x) for x in a.update_blocks.split(",") if x]
         update = update_timing(lib_path, H, blocks, a.steps, a.warmup, a.seed, device)
+    build = build_timing(lib_path, H, a.steps, a.warmup, a.seed, device) if "build" in stages else None
     fused = [n for n in ("decode",) if n in stage_report]
     dominant = max(fused or stage_report, key=lambda n: stage_report[n]["us_per_launch"]) if stage_report else None
     roofline = None
@@ -342,7 +374,7 @@ def main():
                    "layers": a.layers, "groups": G, "history": H, "tail": T,
                    "kv_dtype": "bf16", "mean_unique_ids_per_group": round(uniq, 1), "parallelism": "single GPU"},
         "wall_ms_per_step": round(wall, 4), "stages": stage_report, "copy_probe_GBps": copy_gbs and round(copy_gbs, 1),
-        "update": update, "roofline": roofline, "cpu_baseline": cpu,
+        "update": update, "build": build, "roofline": roofline, "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
 

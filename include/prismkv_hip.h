@@ -141,6 +141,26 @@ int prismkv_update(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t
                    uint64_t counts, uint64_t moments, uint64_t work, int groups, int H, int N, int key_mean,
                    int64_t ks, int64_t row_words, uint64_t stream);
 
+/* ---- prefill index build -----------------------------------------------
+ * build_index (src/prismkv/core.py:92-103) of every group from K rows
+ * [0, H) (replaces the host build before Native8B(indices), i.e.
+ * src/prismkv/hf_reference.py:196-198 followed by src/prismkv/native8b.py:35-74).
+ * Per group: center[g] = mean of the rows (computed when flags & 1, else an
+ * input); x = (k - center[g]) / scale[g]; a = relu(x W[g]^T + b[g]); BatchTopK
+ * over all H keys with the budget H * key_mean (the same rule as
+ * prismkv_update); the bitmap rows are cleared and member (t, f) sets bit t
+ * of row f; counts[g][f] = members and the tiled moments get each bucket's
+ * population mean and variance of the ORIGINAL keys (core.py:76-89), written
+ * directly.  Groups are processed `batch` at a time; `work` is
+ * prismkv_build_work_bytes(batch, H) bytes (H x 3000 fp32 activations per
+ * group of a batch), zero-filled once before first use and left zeroed.
+ * H <= 2^20, row_words a multiple of 4 and >= (H+31)/32, bits and K rows
+ * 16-byte aligned; -1 on bad sizes, -2 on unknown flags. */
+size_t prismkv_build_work_bytes(int batch, int H);
+int prismkv_build(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
+                  uint64_t counts, uint64_t moments, uint64_t work, int groups, int batch, int H, int key_mean,
+                  int flags, int64_t ks, int64_t row_words, uint64_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,6 +18,9 @@
   "sparse" (b = -3: fewer positives than the budget, tau = 0), "dead"
   (b = -100: no positive activation at all) and "dup" (the block's keys
   come in identical pairs: ties of two at every value).
+* `build_case` is one prefill index build (src/prismkv/core.py:92-103) of
+  the first H keys of each group with the SAEs and kinds of `update_case`,
+  plus V, Q and a T-row tail for a decode step on the built index.
 
 All cases return plain numpy arrays: bf16 tensors as uint16 bit patterns,
 indices as `oracle.Index` objects.
@@ -176,3 +179,18 @@ def update_case(kind="random", H=512, N=256, T=8, seed=21, key_mean=8):
         W[g], b[g] = update_sae(kind, seed, g)
         indices.append(build_index(kf[g, :H], W[g], b[g], float(scale[g]), key_mean=key_mean))
     return dict(H=H, N=N, T=T, q=q, k=k, v=v, W=W, b=b, scale=scale, key_mean=key_mean, indices=indices, kind=kind)
+
+
+def build_case(kind="random", H=1024, T=8, seed=51, key_mean=8):
+    """Inputs of one prefill index build for 8 groups (see the module docstring)."""
+    k = bf16_normal((seed, 0), (G, H + T, D))
+    if kind == "dup":
+        k[:, 1:H:2] = k[:, 0:H - 1:2]
+    v = bf16_normal((seed, 1), (G, H + T, D))
+    q = bf16_normal((seed, 2), (G, HQ, D))
+    W = np.empty((G, F, D), np.float32)
+    b = np.empty((G, F), np.float32)
+    for g in range(G):
+        W[g], b[g] = update_sae(kind, seed, g)
+    scale = np.array([1.0 + 0.25 * g for g in range(G)], np.float32)
+    return dict(H=H, T=T, q=q, k=k, v=v, W=W, b=b, scale=scale, key_mean=key_mean, kind=kind)

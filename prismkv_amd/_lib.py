@@ -35,6 +35,8 @@ SIGNATURES = {
     "prismkv_select_cap": ([_U64] * 5 + [_I32, _I32, _I64, _I64], True, _I32),
     "prismkv_update_work_bytes": ([_I32, _I32], False, _SZ),
     "prismkv_update": ([_U64] * 9 + [_I32] * 4 + [_I64, _I64], True, _I32),
+    "prismkv_build_work_bytes": ([_I32, _I32], False, _SZ),
+    "prismkv_build": ([_U64] * 9 + [_I32] * 5 + [_I64, _I64], True, _I32),
 }
 
 _loaded: dict[str, "Library"] = {}

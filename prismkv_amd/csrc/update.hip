@@ -1,16 +1,20 @@
-// Stage 4 -- incremental index update: index a block of N new keys (K rows
-// [H, H+N) of a group) with the group's SAE and merge it into the index.
+// Stage 4 -- the index update (append_index) and the prefill index build
+// (build_index): encode keys with the group's SAE, take the exact batch-wide
+// positive Top-k of the activations, set the members' bitmap bits and
+// (re)compute the bucket moments.
 //
 // Semantics: src/prismkv/core.py:186-201 (append_index) on top of
-//   build_index  core.py:92-103  x = (k - center) / key_scale with the
-//                                ORIGINAL center; a = relu(x W^T + b)
-//                                (SharedSAE.dense, core.py:47-48);
-//   positive_global_topk core.py:13-26  budget N * key_mean over the block:
-//                                keep a > tau and a > 0, then, if tau > 0,
-//                                values == tau in ascending flat index
-//                                (token * F + feature) up to the budget;
+//   build_index  core.py:92-103  center = keys.float().mean(0) unless given
+//                                (append: the ORIGINAL center);
+//                                x = (k - center) / key_scale;
+//                                a = relu(x W^T + b) (SharedSAE.dense,
+//                                core.py:47-48);
+//   positive_global_topk core.py:13-26  budget N * key_mean over the keys
+//                                indexed: keep a > tau and a > 0, then, if
+//                                tau > 0, values == tau in ascending flat
+//                                index (token * F + feature) up to the budget;
 //   summarize    core.py:76-89   per-bucket mean / population variance of
-//                                the ORIGINAL new keys (two-pass);
+//                                the ORIGINAL keys (two-pass);
 //   the merge    core.py:190-199 mean = (a m_a + b m_b) / max(a+b, 1),
 //                                var = (a v_a + b v_b) / max(a+b, 1)
 //                                      + a b / max(a+b, 1)^2 (m_a - m_b)^2,
@@ -19,8 +23,8 @@
 //                                H + t of the bucket's bitmap row
 //                                (kernels/ppu_8b/pack.cu:5 bit order).
 //
-// Launches (all G groups at once; the update runs every `interval` tokens,
-// its cost is amortised):
+// Launches of one update (all G groups at once; the update runs every
+// `interval` tokens, its cost is amortised):
 //   encode   LDS-tiled fp32 GEMM, 64 tokens x 64 buckets per workgroup,
 //            writes a = relu(...) [G][N][F] and a histogram of the positive
 //            values' top 11 bits (4 replicas of each global bin, so the
@@ -31,10 +35,16 @@
 //   emit     sets bitmap bits for a > tau (or all positives when fewer
 //            than the budget are positive) and for a == tau when every tie
 //            fits the budget;
-//   ties     only when ties overflow the budget: one workgroup per group
-//            walks a in flat order and takes the first `need` ties;
+//   ties     only when ties overflow the budget: per contiguous range of a,
+//            count the ties, then take the first `need` in flat order;
 //   moments  per 32-bucket tile: new members from the bitmap, two-pass
 //            moments of their bf16 keys, merge, counts += new.
+// The build runs the same selection over all H keys of a group (in batches
+// of groups, so the activations of one batch fit the workspace) after a
+// center pass and a bitmap clear, and computes every bucket's moments from
+// scratch (build_moments: one workgroup per bucket, any member count).
+#include <algorithm>
+
 #include "common.h"
 
 namespace prismkv {
@@ -48,6 +58,11 @@ constexpr int kBins = 2048;
 constexpr int kRep = 4;        // global histogram replicas
 constexpr int kLevels = 3;
 constexpr int kRefineBlocks = 256;  // workgroups per group of a pass over a
+constexpr int kMaxTieBlocks = 4096;  // contiguous ranges of a per group for the ordered ties
+constexpr int kTieMinLen = 65536;    // values per range at least (multiple of 4 * kUT)
+constexpr int kCenterParts = 64;     // row ranges of the center sum
+constexpr int kMaxBuild = 1 << 20;   // keys per group of a build (N * F < 2^32 flat indices)
+constexpr int kBuildCenter = 1;      // prismkv_build flag: compute the center (else it is an input)
 
 // ctl words per group
 enum { kMode = 0, kPrefix, kRem, kTau, kNeed, kTies, kOrdered, kCount, kCtl = 16 };
@@ -67,8 +82,11 @@ struct UpdateArgs {
   float* act;      // [G][N][F]
   unsigned* hist;  // [G][kLevels][kRep][kBins]
   unsigned* ctl;   // [G][kCtl]
-  int H, N;
+  unsigned* tcount;  // [G][tie_blocks] ties per contiguous range of a
+  int H, N;          // first key row / bitmap column, keys indexed
   long long budget;  // N * key_mean
+  int tie_blocks;
+  long long tie_len;  // values per range, a multiple of 4 * kUT
 };
 
 __device__ __forceinline__ unsigned* hist_of(const UpdateArgs& a, int g, int level) {
@@ -305,26 +323,65 @@ __global__ __launch_bounds__(kUT) void emit_kernel(UpdateArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// ties: grid G x 256; only when the ties at tau overflow the budget: the
-// first `need` of them in ascending flat index (core.py:23-24).
+// ties, only when the ties at tau overflow the budget: the first `need` of
+// them in ascending flat index (core.py:23-24).  Workgroup r of a group owns
+// the contiguous range [r L, (r + 1) L) of a.  tie_count_kernel counts the
+// range's ties; tie_take_kernel skips the ties of the lower ranges and takes
+// its own in flat order (4 consecutive values per thread) while the budget
+// lasts.  Grid (tie_blocks, G) x 256 each.
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(kUT) void ties_kernel(UpdateArgs a) {
-  const int g = blockIdx.x, tid = threadIdx.x;
+__device__ __forceinline__ bool ordered_ties(const UpdateArgs& a, int g) {
   const unsigned* ctl = a.ctl + (size_t)g * kCtl;
-  if (ctl[kMode] != kModeTopK || !ctl[kOrdered]) return;
-  const float tau = __uint_as_float(ctl[kTau]);
-  unsigned need = ctl[kNeed];
+  return ctl[kMode] == kModeTopK && ctl[kOrdered];
+}
+
+__global__ __launch_bounds__(kUT) void tie_count_kernel(UpdateArgs a) {
+  const int r = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+  if (!ordered_ties(a, g)) return;
   __shared__ unsigned wsum[kUT / 64];
+  const float tau = __uint_as_float(a.ctl[(size_t)g * kCtl + kTau]);
   const size_t n = (size_t)a.N * kF;
-  const float* ag = a.act + (size_t)g * n;
-  for (size_t base = 0; base < n && need > 0; base += kUT) {
+  const size_t lo = min(n, (size_t)r * a.tie_len), hi = min(n, lo + a.tie_len);
+  const float4* ag = reinterpret_cast<const float4*>(a.act + (size_t)g * n);
+  unsigned c = 0;
+  for (size_t i = lo / 4 + tid; i < hi / 4; i += kUT) {
+    const float4 v = ag[i];
+    c += (unsigned)(v.x == tau) + (unsigned)(v.y == tau) + (unsigned)(v.z == tau) + (unsigned)(v.w == tau);
+  }
+  block_incl_scan<kUT>(c, wsum);
+  if (tid == 0) a.tcount[(size_t)g * a.tie_blocks + r] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+}
+
+__global__ __launch_bounds__(kUT) void tie_take_kernel(UpdateArgs a) {
+  const int r = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+  if (!ordered_ties(a, g)) return;
+  __shared__ unsigned wsum[kUT / 64];
+  const unsigned* ctl = a.ctl + (size_t)g * kCtl;
+  const float tau = __uint_as_float(ctl[kTau]);  // > 0: only positive values reach the histogram
+  const unsigned need = ctl[kNeed];
+  unsigned below = 0;
+  for (int j = tid; j < r; j += kUT) below += a.tcount[(size_t)g * a.tie_blocks + j];
+  block_incl_scan<kUT>(below, wsum);
+  unsigned taken = wsum[0] + wsum[1] + wsum[2] + wsum[3];  // ties of the lower ranges, all ranked first
+  __syncthreads();  // every thread has read wsum before the loop's first scan rewrites it
+  const size_t n = (size_t)a.N * kF;
+  const size_t lo = min(n, (size_t)r * a.tie_len), hi = min(n, lo + a.tie_len);
+  const float4* ag = reinterpret_cast<const float4*>(a.act + (size_t)g * n);
+  for (size_t base = lo / 4; base < hi / 4 && taken < need; base += kUT) {  // uniform condition
     const size_t i = base + tid;
-    const unsigned hit = i < n && ag[i] == tau;
-    const unsigned incl = block_incl_scan<kUT>(hit, wsum);
-    if (hit && incl <= need) set_member(a, g, (unsigned)i);
-    const unsigned taken = wsum[0] + wsum[1] + wsum[2] + wsum[3];
-    need = taken >= need ? 0u : need - taken;
-    __syncthreads();
+    const float4 v = i < hi / 4 ? ag[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    const bool h[4] = {v.x == tau, v.y == tau, v.z == tau, v.w == tau};
+    const unsigned c = (unsigned)h[0] + (unsigned)h[1] + (unsigned)h[2] + (unsigned)h[3];
+    const unsigned incl = block_incl_scan<kUT>(c, wsum);
+    unsigned rank = taken + incl - c;  // rank of this thread's first tie among all ties
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (h[j]) {
+        if (rank < need) set_member(a, g, (unsigned)(4 * i + j));
+        ++rank;
+      }
+    taken += wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    __syncthreads();  // wsum is rewritten by the next scan
   }
 }
 
@@ -415,38 +472,218 @@ __global__ __launch_bounds__(kUT) void moments_kernel(UpdateArgs a) {
   if (tid < kChunk) a.counts[(size_t)g * kFP + f] = na + nbn;
 }
 
+// ---------------------------------------------------------------------------
+// Build-only kernels.
+// center (build without a given center, core.py:95): keys.float().mean(0)
+// over K rows [H, H + N).  center_part_kernel: grid (kCenterParts, G) x 256,
+// part p sums rows [p R, (p + 1) R), R = ceil(N / kCenterParts), in double
+// (thread = row step tid >> 4 of 16, dims 8 (tid & 15) ..);
+// center_final_kernel: grid G x 128 adds the parts in order, divides by N.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kUT) void center_part_kernel(UpdateArgs a, double* part) {
+  const int p = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+  __shared__ double red[kUT / 16][kD];
+  const int R = (a.N + kCenterParts - 1) / kCenterParts;
+  const int lo = min(a.N, p * R), hi = min(a.N, lo + R);
+  const int r = tid >> 4, d0 = (tid & 15) * 8;
+  const uint16_t* kg = a.k + (size_t)g * a.ks + (size_t)a.H * kD;
+  double acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.0;
+  for (int t = lo + r; t < hi; t += kUT / 16) {
+    const uint4 v = *reinterpret_cast<const uint4*>(kg + (size_t)t * kD + d0);
+    acc[0] += bf16_lo(v.x); acc[1] += bf16_hi(v.x); acc[2] += bf16_lo(v.y); acc[3] += bf16_hi(v.y);
+    acc[4] += bf16_lo(v.z); acc[5] += bf16_hi(v.z); acc[6] += bf16_lo(v.w); acc[7] += bf16_hi(v.w);
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) red[r][d0 + j] = acc[j];
+  __syncthreads();
+  if (tid < kD) {
+    double t = 0.0;
+#pragma unroll
+    for (int i = 0; i < kUT / 16; ++i) t += red[i][tid];
+    part[((size_t)g * kCenterParts + p) * kD + tid] = t;
+  }
+}
+
+__global__ __launch_bounds__(kD) void center_final_kernel(UpdateArgs a, const double* part, float* center) {
+  const int g = blockIdx.x, d = threadIdx.x;
+  double t = 0.0;
+  for (int p = 0; p < kCenterParts; ++p) t += part[((size_t)g * kCenterParts + p) * kD + d];
+  center[(size_t)g * kD + d] = (float)(t / (double)a.N);
+}
+
+// clear: grid (blocks, G) x 256 zeroes the group's F bitmap rows (row_words
+// is a multiple of 4 words and the rows are 16-byte aligned).
+__global__ __launch_bounds__(kUT) void clear_bits_kernel(UpdateArgs a) {
+  const int g = blockIdx.y;
+  const size_t n4 = (size_t)kF * a.row_words / 4;
+  uint4* bg = reinterpret_cast<uint4*>(a.bits + (size_t)g * kF * a.row_words);
+  for (size_t i = (size_t)blockIdx.x * kUT + threadIdx.x; i < n4; i += (size_t)gridDim.x * kUT)
+    bg[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+// ---------------------------------------------------------------------------
+// build_moments: grid (F, G) x 256, one workgroup per bucket f, any member
+// count.  Members are the set bits of the bucket's bitmap row below N (a
+// build indexes K rows = bitmap columns [0, N)).  Chunks of 256 words (one
+// per thread) are compacted into an LDS token list; while the whole list
+// fits in kList tokens it is kept and both passes read it, otherwise each
+// pass re-scans the row chunk by chunk.  Thread = (member slot tid >> 4 of
+// 16, dims 8 (tid & 15) ..): 16 key rows per step with 16-byte loads,
+// double accumulation, fixed order.  mean = sum / n rounded to fp32; var =
+// sum (x - mean)^2 / n with that rounded mean; empty bucket -> 0
+// (core.py:84-88).  Counts and moments are written, not merged.
+// ---------------------------------------------------------------------------
+constexpr int kList = 8192;
+constexpr int kSlots = kUT / 16;
+
+struct BuildMomentsLds {
+  int toks[kList];
+  double red[kSlots][kD];
+  unsigned wsum[kUT / 64];
+  float mean[kD];
+};
+
+// Members among words [w0, w0 + 256) of the row -> toks[at ..] when they all
+// fit below kList.  Returns the chunk's member count (uniform); the caller
+// barriers before the list is read and before the next chunk.
+__device__ __forceinline__ unsigned compact_chunk(const uint32_t* row, int w0, int nw, int N, int* toks, unsigned at,
+                                                  unsigned* wsum) {
+  const int wd = w0 + threadIdx.x;
+  uint32_t m = wd < nw ? row[wd] : 0u;
+  if (wd == nw - 1 && (N & 31)) m &= (1u << (N & 31)) - 1u;
+  const unsigned pc = (unsigned)__popc(m);
+  const unsigned incl = block_incl_scan<kUT>(pc, wsum);
+  const unsigned total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+  if (at + total <= (unsigned)kList) {
+    unsigned p = at + incl - pc;
+    while (m) {
+      toks[p++] = wd * 32 + (int)__builtin_ctz(m);
+      m &= m - 1u;
+    }
+  }
+  return total;
+}
+
+template <bool kDev>
+__device__ __forceinline__ void accumulate_rows(const uint16_t* kg, const int* toks, unsigned n, int slot, int d0,
+                                                const float (&m)[8], double (&acc)[8]) {
+#pragma unroll 4
+  for (unsigned i = slot; i < n; i += kSlots) {
+    const uint4 v = *reinterpret_cast<const uint4*>(kg + (size_t)toks[i] * kD + d0);
+    const float x[8] = {bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y),
+                        bf16_lo(v.z), bf16_hi(v.z), bf16_lo(v.w), bf16_hi(v.w)};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if constexpr (kDev) {
+        const double t = (double)x[j] - (double)m[j];
+        acc[j] += t * t;
+      } else {
+        acc[j] += (double)x[j];
+      }
+    }
+  }
+}
+
+// One pass over the members (kDev: squared deviations from m), reduced over
+// the slots into red[0][..] order-fixed sums for tid < kD (returned).
+template <bool kDev>
+__device__ double bucket_pass(BuildMomentsLds& L, const uint32_t* row, const uint16_t* kg, int nw, int N, bool kept,
+                              unsigned n, const float (&m)[8]) {
+  const int tid = threadIdx.x, slot = tid >> 4, d0 = (tid & 15) * 8;
+  double acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.0;
+  if (kept) {
+    accumulate_rows<kDev>(kg, L.toks, n, slot, d0, m, acc);
+  } else {
+    for (int w0 = 0; w0 < nw; w0 += kUT) {
+      __syncthreads();  // the previous chunk's list has been read
+      const unsigned c = compact_chunk(row, w0, nw, N, L.toks, 0u, L.wsum);  // <= 8192: always fits
+      __syncthreads();
+      accumulate_rows<kDev>(kg, L.toks, c, slot, d0, m, acc);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) L.red[slot][d0 + j] = acc[j];
+  __syncthreads();
+  double t = 0.0;
+  if (tid < kD)
+#pragma unroll
+    for (int i = 0; i < kSlots; ++i) t += L.red[i][tid];
+  __syncthreads();  // red is free again
+  return t;
+}
+
+__global__ __launch_bounds__(kUT) void build_moments_kernel(UpdateArgs a) {
+  const int f = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+  __shared__ BuildMomentsLds L;
+  const uint32_t* row = a.bits + ((size_t)g * kF + f) * a.row_words;
+  const uint16_t* kg = a.k + (size_t)g * a.ks;
+  const int nw = (a.N + 31) >> 5;
+  // count the members, keeping the list while it fits
+  unsigned n = 0;
+  bool kept = true;
+  for (int w0 = 0; w0 < nw; w0 += kUT) {
+    const unsigned c = compact_chunk(row, w0, nw, a.N, L.toks, n, L.wsum);
+    __syncthreads();
+    if (n + c > (unsigned)kList) {
+      kept = false;
+      n = 0;
+      for (int w1 = 0; w1 < nw; w1 += kUT) {  // count only: the list is rebuilt per chunk in the passes
+        const int wd = w1 + tid;
+        uint32_t m = wd < nw ? row[wd] : 0u;
+        if (wd == nw - 1 && (a.N & 31)) m &= (1u << (a.N & 31)) - 1u;
+        block_incl_scan<kUT>((unsigned)__popc(m), L.wsum);
+        n += L.wsum[0] + L.wsum[1] + L.wsum[2] + L.wsum[3];
+        __syncthreads();
+      }
+      break;
+    }
+    n += c;
+  }
+  float zero[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) zero[j] = 0.f;
+  const double sum = bucket_pass<false>(L, row, kg, nw, a.N, kept, n, zero);
+  if (tid < kD) L.mean[tid] = n ? (float)(sum / (double)n) : 0.f;
+  __syncthreads();
+  float m[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) m[j] = L.mean[(tid & 15) * 8 + j];
+  const double dev = bucket_pass<true>(L, row, kg, nw, a.N, kept, n, m);
+  if (tid < kD) {
+    float* tile = a.moments + (size_t)(g * kChunks + f / kChunk) * kRow * kChunk;
+    const int col = f % kChunk;
+    tile[tid * kChunk + col] = L.mean[tid];
+    tile[(kD + tid) * kChunk + col] = n ? (float)(dev / (double)n) : 0.f;
+  }
+  if (tid == 0) a.counts[(size_t)g * kFP + f] = (int)n;
+}
+
 }  // namespace
 }  // namespace prismkv
 
 using namespace prismkv;
 
 struct UpdateLayout {
-  size_t act, hist, ctl, total;
+  size_t act, hist, ctl, tcount, part, total;
   UpdateLayout(int groups, int N) {
     size_t o = 0;
     auto take = [&](size_t n) { const size_t at = o; o += (n + 255) & ~(size_t)255; return at; };
     act = take((size_t)groups * N * kF * sizeof(float));
     hist = take((size_t)groups * kLevels * kRep * kBins * sizeof(unsigned));
     ctl = take((size_t)groups * kCtl * sizeof(unsigned));
+    tcount = take((size_t)groups * kMaxTieBlocks * sizeof(unsigned));
+    part = take((size_t)groups * kCenterParts * kD * sizeof(double));
     total = o;
   }
 };
 
-extern "C" {
-
-size_t prismkv_update_work_bytes(int groups, int max_block) {
-  if (groups < 1 || max_block < 1 || max_block > kMaxBlock) return 0;
-  return UpdateLayout(groups, max_block).total;
-}
-
-int prismkv_update(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
-                   uint64_t counts, uint64_t moments, uint64_t work, int groups, int H, int N, int key_mean,
-                   int64_t ks, int64_t row_words, uint64_t stream) {
-  if (groups < 1 || groups > 65535 || H < 0 || N < 1 || N > kMaxBlock || key_mean < 1 || key_mean > kF)
-    return kBadSize;
-  if (ks < (int64_t)(H + N) * kD || row_words < (H + N + 31) / 32) return kBadSize;
-  if (!k || !W || !b || !center || !scale || !bits || !counts || !moments || !work) return kBadSize;
-  const UpdateLayout L(groups, N);
+static UpdateArgs make_args(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
+                            uint64_t counts, uint64_t moments, uint64_t work, int groups, int H, int N, int key_mean,
+                            int64_t ks, int64_t row_words, const UpdateLayout& L) {
   char* w = reinterpret_cast<char*>(work);
   UpdateArgs a;
   a.k = reinterpret_cast<const uint16_t*>(k);
@@ -462,19 +699,97 @@ int prismkv_update(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t
   a.act = reinterpret_cast<float*>(w + L.act);
   a.hist = reinterpret_cast<unsigned*>(w + L.hist);
   a.ctl = reinterpret_cast<unsigned*>(w + L.ctl);
+  a.tcount = reinterpret_cast<unsigned*>(w + L.tcount);
   a.H = H;
   a.N = N;
   a.budget = (long long)N * key_mean;
-  hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(encode_kernel, dim3(kFTiles, (N + kTT - 1) / kTT, groups), dim3(kUT), 0, s, a);
+  // ordered-tie ranges: at most kMaxTieBlocks per group, each a multiple of 4 * kUT values
+  const long long n = (long long)N * kF;
+  long long len = std::max<long long>(kTieMinLen, (n + kMaxTieBlocks - 1) / kMaxTieBlocks);
+  len = (len + 4 * kUT - 1) / (4 * kUT) * (4 * kUT);
+  a.tie_len = len;
+  a.tie_blocks = (int)((n + len - 1) / len);
+  (void)groups;
+  return a;
+}
+
+// encode .. ties: the exact batch-wide positive Top-k of the N keys' activations
+// and their bitmap bits.
+static void launch_selection(const UpdateArgs& a, int groups, hipStream_t s) {
+  hipLaunchKernelGGL(encode_kernel, dim3(kFTiles, (a.N + kTT - 1) / kTT, groups), dim3(kUT), 0, s, a);
   hipLaunchKernelGGL(digit_kernel, dim3(groups), dim3(kUT), 0, s, a, 0);
   for (int level = 1; level < kLevels; ++level) {
     hipLaunchKernelGGL(refine_kernel, dim3(kRefineBlocks, groups), dim3(kUT), 0, s, a, level);
     hipLaunchKernelGGL(digit_kernel, dim3(groups), dim3(kUT), 0, s, a, level);
   }
   hipLaunchKernelGGL(emit_kernel, dim3(kRefineBlocks, groups), dim3(kUT), 0, s, a);
-  hipLaunchKernelGGL(ties_kernel, dim3(groups), dim3(kUT), 0, s, a);
+  hipLaunchKernelGGL(tie_count_kernel, dim3(a.tie_blocks, groups), dim3(kUT), 0, s, a);
+  hipLaunchKernelGGL(tie_take_kernel, dim3(a.tie_blocks, groups), dim3(kUT), 0, s, a);
+}
+
+static bool aligned16(uint64_t p, int64_t stride_elems) { return ((p | (uint64_t)(stride_elems * 2)) & 15u) == 0; }
+
+extern "C" {
+
+size_t prismkv_update_work_bytes(int groups, int max_block) {
+  if (groups < 1 || max_block < 1 || max_block > kMaxBlock) return 0;
+  return UpdateLayout(groups, max_block).total;
+}
+
+int prismkv_update(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
+                   uint64_t counts, uint64_t moments, uint64_t work, int groups, int H, int N, int key_mean,
+                   int64_t ks, int64_t row_words, uint64_t stream) {
+  if (groups < 1 || groups > 65535 || H < 0 || N < 1 || N > kMaxBlock || key_mean < 1 || key_mean > kF)
+    return kBadSize;
+  if (ks < (int64_t)(H + N) * kD || row_words < (H + N + 31) / 32) return kBadSize;
+  if (!k || !W || !b || !center || !scale || !bits || !counts || !moments || !work) return kBadSize;
+  if (!aligned16(k, ks)) return kBadSize;
+  const UpdateLayout L(groups, N);
+  const UpdateArgs a = make_args(k, W, b, center, scale, bits, counts, moments, work, groups, H, N, key_mean, ks,
+                                 row_words, L);
+  hipStream_t s = (hipStream_t)stream;
+  launch_selection(a, groups, s);
   hipLaunchKernelGGL(moments_kernel, dim3(kChunks, groups), dim3(kUT), 0, s, a);
+  return (int)hipGetLastError();
+}
+
+size_t prismkv_build_work_bytes(int batch, int H) {
+  if (batch < 1 || batch > 65535 || H < 1 || H > kMaxBuild) return 0;
+  return UpdateLayout(batch, H).total;
+}
+
+int prismkv_build(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
+                  uint64_t counts, uint64_t moments, uint64_t work, int groups, int batch, int H, int key_mean,
+                  int flags, int64_t ks, int64_t row_words, uint64_t stream) {
+  if (groups < 1 || groups > 65535 || batch < 1 || batch > groups || H < 1 || H > kMaxBuild || key_mean < 1 ||
+      key_mean > kF)
+    return kBadSize;
+  if (flags & ~kBuildCenter) return kBadMode;
+  if (ks < (int64_t)H * kD || row_words < (H + 31) / 32 || (row_words & 3)) return kBadSize;
+  if (!k || !W || !b || !center || !scale || !bits || !counts || !moments || !work) return kBadSize;
+  if (!aligned16(k, ks) || (bits & 15u)) return kBadSize;
+  const UpdateLayout L(batch, H);
+  hipStream_t s = (hipStream_t)stream;
+  for (int g0 = 0; g0 < groups; g0 += batch) {
+    const int nb = std::min(batch, groups - g0);
+    const uint64_t kg = k + (uint64_t)g0 * ks * sizeof(uint16_t);
+    const uint64_t cg = center + (uint64_t)g0 * kD * sizeof(float);
+    UpdateArgs a = make_args(kg, W + (uint64_t)g0 * kF * kD * sizeof(float), b + (uint64_t)g0 * kF * sizeof(float),
+                             cg, scale + (uint64_t)g0 * sizeof(float),
+                             bits + (uint64_t)g0 * kF * row_words * sizeof(uint32_t),
+                             counts + (uint64_t)g0 * kFP * sizeof(int),
+                             moments + (uint64_t)g0 * kChunks * kRow * kChunk * sizeof(float), work, nb, 0, H,
+                             key_mean, ks, row_words, L);
+    if (flags & kBuildCenter) {
+      double* part = reinterpret_cast<double*>(reinterpret_cast<char*>(work) + L.part);
+      hipLaunchKernelGGL(center_part_kernel, dim3(kCenterParts, nb), dim3(kUT), 0, s, a, part);
+      hipLaunchKernelGGL(center_final_kernel, dim3(nb), dim3(kD), 0, s, a, (const double*)part,
+                         reinterpret_cast<float*>(cg));
+    }
+    hipLaunchKernelGGL(clear_bits_kernel, dim3(512, nb), dim3(kUT), 0, s, a);
+    launch_selection(a, nb, s);
+    hipLaunchKernelGGL(build_moments_kernel, dim3(kF, nb), dim3(kUT), 0, s, a);
+  }
   return (int)hipGetLastError();
 }
 

@@ -48,6 +48,12 @@ FUSED_MAX_HISTORY = 524288
 # Largest block one `append` indexes (the reference's update interval is 4096,
 # src/prismkv/hf_reference.py:75).
 MAX_BLOCK = 4096
+# Largest history one device index build covers (flat activation indices
+# history * 3000 stay below 2^32).
+MAX_BUILD = 1 << 20
+# Workspace budget of a build: groups are indexed in batches whose dense
+# activations (history x 3000 fp32 per group) fit in it.
+BUILD_WORK_LIMIT = 8 << 30
 # Workgroups per KV group of the sparse-attention launch (each 8 waves; one
 # per CU at 8 groups x 32 = 256): the partition the kernel is tuned for.
 ATTEND_SPLITS = 32
@@ -94,6 +100,18 @@ def bitmap_row_words(capacity: int) -> int:
     return ((capacity + 31) // 32 + 3) // 4 * 4
 
 
+def _encoder_tables(saes, key_scales):
+    """Stacked W_enc [8,3000,128], b_enc [8,3000] and the shared key_mean of 8 SAEs."""
+    if len(saes) != GROUPS or len(key_scales) != GROUPS:
+        raise ValueError("one SAE and key scale per KV group required")
+    means = {int(s.key_mean) for s in saes}
+    if len(means) != 1:
+        raise ValueError("all groups must share one key_mean")
+    W = torch.stack([torch.as_tensor(s.W_enc).detach() for s in saes])
+    b = torch.stack([torch.as_tensor(s.b_enc).detach() for s in saes])
+    return W, b, means.pop()
+
+
 class Native8B:
     def __init__(self, indices, library=None, *, capacity=None, unique_cap=None):
         if len(indices) != GROUPS:
@@ -137,7 +155,86 @@ class Native8B:
         obj.unique_cap = unique_cap
         return obj
 
+    @classmethod
+    def from_keys(cls, k, history, W, b, key_scale, key_mean=8, library=None, *, center=None, capacity=None,
+                  unique_cap=None, work_limit=BUILD_WORK_LIMIT, keep_activations=False):
+        """build_index (src/prismkv/core.py:92-103) of all 8 groups on the
+        device: K rows [0, history) of each group are encoded with its SAE
+        (W [8,3000,128], b [8,3000], key_scale [8] > 0), the batch-wide
+        positive Top-k with budget history * key_mean selects the
+        memberships (flat-index tie rule, core.py:13-26), and every bucket's
+        population mean and variance of the ORIGINAL keys fill the tables.
+        The center is the mean of those K rows unless `center` [8,128] is
+        given.  Returns a decode-ready instance whose encoders are set for
+        `append`.  Groups are indexed in batches whose activations (history
+        x 3000 fp32 each) fit in `work_limit` bytes; with keep_activations
+        the last batch's activations stay readable (build_activations)."""
+        if k.device.type != "cuda":
+            raise ValueError("native backend requires a device tensor")
+        history = int(history)
+        if not 1 <= history <= MAX_BUILD:
+            raise ValueError(f"history must be in [1, {MAX_BUILD}]")
+        if k.dtype != torch.bfloat16 or k.dim() != 3 or k.shape[0] != GROUPS or k.shape[-1] != DIM:
+            raise ValueError("BF16 K[8,total_length,128] required")
+        if k.stride(-1) != 1 or k.stride(1) != DIM or k.shape[1] < history:
+            raise ValueError("contiguous per-group K rows covering the history required")
+        if (k.data_ptr() | (k.stride(0) * 2)) % 16:
+            raise ValueError("K rows must be 16-byte aligned")
+        obj = cls.__new__(cls)
+        with torch.cuda.device(k.device):
+            obj._allocate(history, capacity, library, k.device, center)
+            obj.set_encoder_tables(W, b, key_scale, key_mean)
+            flags = 0
+            if obj.center is None:
+                obj.center = torch.zeros(GROUPS, DIM, dtype=torch.float32, device=k.device)
+                flags = 1  # the device computes the centers
+            per_group = obj.lib.query("prismkv_build_work_bytes", 1, history)
+            batch = max(1, min(GROUPS, int(work_limit) // per_group))
+            work = torch.zeros(obj.lib.query("prismkv_build_work_bytes", batch, history), dtype=torch.uint8,
+                               device=k.device)
+            obj.lib.call("prismkv_build", k.data_ptr(), obj.W_enc.data_ptr(), obj.b_enc.data_ptr(),
+                         obj.center.data_ptr(), obj.key_scale.data_ptr(), obj.bits.data_ptr(), obj.n.data_ptr(),
+                         obj.moments.data_ptr(), work.data_ptr(), GROUPS, batch, history, obj.key_mean, flags,
+                         k.stride(0), obj.row_words, stream=obj._stream())
+            obj.build_work = work if keep_activations else None
+            obj.build_batch = batch
+        obj.unique_cap = unique_cap
+        return obj
+
+    @classmethod
+    def build_index(cls, k, saes, key_scales, history=None, library=None, **kwargs):
+        """from_keys with the reference's encoder objects: `saes[g]` has
+        W_enc [3000,128], b_enc [3000] and key_mean (SharedSAE,
+        src/prismkv/core.py:29-48); history defaults to all rows of k."""
+        W, b, key_mean = _encoder_tables(saes, key_scales)
+        return cls.from_keys(k, k.shape[1] if history is None else history, W, b, key_scales, key_mean, library,
+                             **kwargs)
+
+    def build_activations(self):
+        """Dense activations relu(x W^T + b) [batch, history, 3000] of the
+        last group batch of from_keys(keep_activations=True): groups
+        8 - batch .. 7."""
+        if getattr(self, "build_work", None) is None:
+            raise ValueError("build with keep_activations=True first")
+        n = self.build_batch * self.history * FEATURES
+        return self.build_work[:4 * n].view(torch.float32).view(self.build_batch, self.history, FEATURES)
+
     def _setup(self, h, capacity, library, counts, mean, variance, csr, offsets, center=None):
+        if csr.numel() and (int(csr.max()) >= h or int(csr.min()) < 0):
+            raise ValueError("bucket lists must address tokens in [0, history)")
+        if offsets.shape != (GROUPS, FEATURES + 1) or int(offsets[:, -1].max()) > csr.shape[1]:
+            raise ValueError("offsets must be [8,3001] within the list width")
+        device = counts.device
+        self._allocate(h, capacity, library, device, center)
+        self.n[:, :FEATURES] = counts.int()
+        self.moments.copy_(tile_moments(mean, variance))
+        self.lib.call("prismkv_build_bits", csr.data_ptr(), offsets.data_ptr(), self.bits.data_ptr(), GROUPS,
+                      csr.shape[1], self.row_words, stream=self._stream())
+        # Temporary CSR storage may be freed after this build barrier.
+        torch.cuda.synchronize(device)
+
+    def _allocate(self, h, capacity, library, device, center=None):
+        """Zeroed tables and buffers for history h (ids and bitmap columns for `capacity`)."""
         capacity = h if capacity is None else int(capacity)
         if capacity < h or h < 1:
             raise ValueError("history must be >= 1 and capacity >= history")
@@ -146,15 +243,8 @@ class Native8B:
         self.lib = _lib.load(library)
         if self.lib.missing:
             raise RuntimeError(f"{self.lib.path.name} lacks entry points {self.lib.missing}; rebuild it")
-        device = counts.device
-        if csr.numel() and (int(csr.max()) >= h or int(csr.min()) < 0):
-            raise ValueError("bucket lists must address tokens in [0, history)")
-        if offsets.shape != (GROUPS, FEATURES + 1) or int(offsets[:, -1].max()) > csr.shape[1]:
-            raise ValueError("offsets must be [8,3001] within the list width")
-        stream = torch.cuda.current_stream().cuda_stream
         self.n = torch.zeros(GROUPS, PADDED, dtype=torch.int32, device=device)
-        self.n[:, :FEATURES] = counts.int()
-        self.moments = tile_moments(mean, variance)
+        self.moments = torch.zeros(GROUPS, CHUNKS, 2 * DIM, CHUNK, dtype=torch.float32, device=device)
         self.features = torch.zeros(GROUPS, TOPK, dtype=torch.int64, device=device)
         self.valid = torch.zeros(GROUPS, TOPK, device=device)
         self.raw = torch.zeros(GROUPS, dtype=torch.int32, device=device)
@@ -162,10 +252,6 @@ class Native8B:
         self.count = torch.zeros(GROUPS, dtype=torch.int32, device=device)
         self.row_words = bitmap_row_words(self.capacity)
         self.bits = torch.zeros(GROUPS, FEATURES, self.row_words, dtype=torch.int32, device=device)
-        self.lib.call("prismkv_build_bits", csr.data_ptr(), offsets.data_ptr(), self.bits.data_ptr(), GROUPS,
-                      csr.shape[1], self.row_words, stream=stream)
-        # Temporary CSR storage may be freed after this build barrier.
-        torch.cuda.synchronize(device)
         self.route_work = torch.zeros(self.lib.query("prismkv_route_work_bytes", GROUPS), dtype=torch.uint8,
                                       device=device)
         self.union_work = torch.zeros(self.lib.query("prismkv_union_work_bytes", GROUPS, self.capacity),
@@ -266,14 +352,8 @@ class Native8B:
         b_enc [3000] and key_mean (SharedSAE, src/prismkv/core.py:29-48) and
         `key_scales[g]` > 0 is its key scale -- the reference's
         encoders[(layer, group)] bundle (src/prismkv/hf_reference.py:196-211)."""
-        if len(saes) != GROUPS or len(key_scales) != GROUPS:
-            raise ValueError("one SAE and key scale per KV group required")
-        means = {int(s.key_mean) for s in saes}
-        if len(means) != 1:
-            raise ValueError("all groups must share one key_mean")
-        W = torch.stack([torch.as_tensor(s.W_enc).detach() for s in saes])
-        b = torch.stack([torch.as_tensor(s.b_enc).detach() for s in saes])
-        self.set_encoder_tables(W, b, key_scales, means.pop())
+        W, b, key_mean = _encoder_tables(saes, key_scales)
+        self.set_encoder_tables(W, b, key_scales, key_mean)
 
     def set_encoder_tables(self, W, b, key_scale, key_mean):
         """Encoder tables directly: W [8,3000,128], b [8,3000], key_scale [8]

@@ -56,6 +56,11 @@ def test_work_size_queries(lib):
     assert lib.query("prismkv_update_work_bytes", 8, 4096) >= 8 * 4096 * 3000 * 4
     assert lib.query("prismkv_update_work_bytes", 8, 4097) == 0
     assert lib.query("prismkv_update_work_bytes", 0, 16) == 0
+    # the build workspace holds one batch's activations [batch][H][3000] f32
+    assert lib.query("prismkv_build_work_bytes", 8, 65536) >= 8 * 65536 * 3000 * 4
+    assert lib.query("prismkv_build_work_bytes", 1, 1 << 20) >= (1 << 20) * 3000 * 4
+    assert lib.query("prismkv_build_work_bytes", 1, (1 << 20) + 1) == 0
+    assert lib.query("prismkv_build_work_bytes", 0, 16) == 0
 
 
 def call_raw(lib, name, *args):
@@ -92,6 +97,18 @@ def test_native_error_codes(lib):
                                 (0, 100, 64, 8, good, 8), (8, -1, 64, 8, good, 8)]:
         assert call_raw(lib, "prismkv_update", *[1] * 9, G, H, N, km, ks, rw) == -1, (G, H, N, km, ks, rw)
     assert call_raw(lib, "prismkv_update", *[0] * 9, 8, 100, 64, 8, good, 8) == -1  # null pointers
+    # prismkv_build(k, W, b, center, scale, bits, counts, moments, work, groups, batch, H, key_mean, flags, ks,
+    # row_words): 16-byte aligned fake pointers, so only the sizes decide
+    good = 100 * 128
+    for G, B, H, km, fl, ks, rw in [(0, 1, 100, 8, 0, good, 4), (8, 0, 100, 8, 0, good, 4), (8, 9, 100, 8, 0, good, 4),
+                                    (8, 8, 0, 8, 0, good, 4), (8, 8, (1 << 20) + 1, 8, 0, 1 << 28, 32772),
+                                    (8, 8, 100, 0, 0, good, 4), (8, 8, 100, 3001, 0, good, 4),
+                                    (8, 8, 100, 8, 0, good - 128, 4), (8, 8, 100, 8, 0, good, 3),
+                                    (8, 8, 100, 8, 0, good, 5)]:
+        assert call_raw(lib, "prismkv_build", *[16] * 9, G, B, H, km, fl, ks, rw) == -1, (G, B, H, km, fl, ks, rw)
+    assert call_raw(lib, "prismkv_build", *[16] * 9, 8, 8, 100, 8, 2, good, 4) == -2  # unknown flag
+    assert call_raw(lib, "prismkv_build", *[0] * 9, 8, 8, 100, 8, 0, good, 4) == -1   # null pointers
+    assert call_raw(lib, "prismkv_build", *[18] + [16] * 8, 8, 8, 100, 8, 0, good, 4) == -1  # misaligned K
 
 
 def test_native8b_host_validation_without_gpu():

@@ -1,0 +1,234 @@
+"""GPU parity of the prefill index build (build_index,
+src/prismkv/core.py:92-103) against the CPU oracle.
+
+For every group of each case:
+  * the device center equals the exact mean of the K rows rounded to fp32
+    (to one ulp);
+  * activations relu((k - center)/scale W^T + b) match the oracle's
+    double-accumulated encode (with the device center) within fp32 rounding;
+  * the device's memberships equal the oracle's BatchTopK applied to the
+    device's own activations -- bit-exact, including the flat-index tie rule
+    (src/prismkv/core.py:13-26) -- and differ from the oracle's selection on
+    its own activations only at values within the encode error of tau;
+  * counts equal the list lengths and the moments equal the oracle's
+    summarize (src/prismkv/core.py:76-89) over the device's lists;
+  * the decode path on the built tables matches the oracle's route and
+    attention over the exported index.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import bf16_to_f32, cases, expect
+from tests.gpu_util import bf16_bits, bf16_tensor, log, route_outputs
+
+pytestmark = pytest.mark.gpu
+
+F = 3000
+
+
+def run_build(case, **kwargs):
+    from prismkv_amd import Native8B
+    k = bf16_tensor(case["k"])
+    kwargs.setdefault("keep_activations", True)
+    op = Native8B.from_keys(k, case["H"], torch.from_numpy(case["W"]), torch.from_numpy(case["b"]),
+                            torch.from_numpy(case["scale"]), case["key_mean"], capacity=case["H"] + case["T"],
+                            **kwargs)
+    torch.cuda.synchronize()
+    return op, k
+
+
+def lists_from_flat(flat, H):
+    tok, feat = flat // F, flat % F
+    order = np.lexsort((tok, feat))
+    return np.split(tok[order], np.cumsum(np.bincount(feat, minlength=F))[:-1])
+
+
+def check_center(case, g, center):
+    kf = bf16_to_f32(case["k"][g, :case["H"]])
+    exact = kf.astype(np.float64).mean(0)
+    err = np.abs(center.astype(np.float64) - exact)
+    assert (err <= np.spacing(np.abs(exact).astype(np.float32)) + 1e-30).all(), ("center", g, float(err.max()))
+
+
+def check_selection(case, g, act, got, ref=None):
+    """Exact BatchTopK on the device activations; returns (selected, moved)."""
+    H, km = case["H"], case["key_mean"]
+    count = min(H * km, H * F)
+    flat = oracle.positive_global_topk(act, count)
+    want = lists_from_flat(flat, H)
+    for f in range(F):
+        have = got.lists[f].numpy()
+        if not np.array_equal(have, want[f]):
+            raise AssertionError(f"group {g} bucket {f}: lists differ ({len(have)} vs {len(want[f])})")
+    moved = 0
+    if ref is not None:
+        ref_index, act_ref, err = ref
+        ref_sel = np.zeros(H * F, bool)
+        for f, l in enumerate(ref_index.lists):
+            ref_sel[np.asarray(l) * F + f] = True
+        dev_sel = np.zeros(H * F, bool)
+        dev_sel[flat] = True
+        idx = np.flatnonzero(ref_sel != dev_sel)
+        moved = len(idx)
+        if moved:
+            vals = act_ref.reshape(-1)
+            tau = np.partition(vals, vals.size - count)[vals.size - count]
+            assert np.abs(vals[idx] - tau).max() <= 2 * err + 1e-7, ("selection moved away from tau", g)
+    return len(flat), moved
+
+
+def check_moments(case, g, got):
+    kf = bf16_to_f32(case["k"][g, :case["H"]])
+    lists = [l.numpy() for l in got.lists]
+    c, m, v = oracle.summarize(kf, lists)
+    assert np.array_equal(got.counts.cpu().numpy(), c), ("counts", g)
+    s = max(1.0, float(np.abs(kf).max()))
+    gm, gv = got.mean.cpu().numpy(), got.variance.cpu().numpy()
+    assert np.allclose(gm, m, rtol=1e-6, atol=1e-7 * s), ("mean", g, float(np.abs(gm - m).max()))
+    assert np.allclose(gv, v, rtol=1e-6, atol=1e-7 * s * s), ("var", g, float(np.abs(gv - v).max()))
+
+
+def check_decode(case, op, k, got):
+    H = case["H"]
+    idx = [oracle.Index(H, i.center.cpu().numpy(), i.counts.cpu().numpy(), i.mean.cpu().numpy(),
+                        i.variance.cpu().numpy(), [l.numpy() for l in i.lists]) for i in got]
+    case2 = dict(H=H, T=case["T"], q=case["q"], k=case["k"], v=case["v"], indices=idx, kind=case["kind"])
+    q, v = bf16_tensor(case["q"]), bf16_tensor(case["v"])
+    out = op(q, k, v)
+    torch.cuda.synchronize()
+    assert op.decode_errors() == 0
+    groups = expect.expected(case2)
+    identical, near = expect.compare_route(groups, *route_outputs(op))
+    assert identical + near == 8
+    err = expect.attention_errors(bf16_bits(out), expect.expected_attention(case2, groups))
+    log(f"  decode on the built index: {identical} identical, {near} near-tie; {err}")
+    assert err["rel_l2"] <= 2e-3 and err["max_abs"] < 0.05, err
+
+
+def full_check(case, op, k, center_given=False):
+    H, km = case["H"], case["key_mean"]
+    act = op.build_activations().cpu().numpy()
+    centers = op.center.cpu().numpy()
+    got = op.export_indices()
+    for g in range(8):
+        if not center_given:
+            check_center(case, g, centers[g])
+        kf = bf16_to_f32(case["k"][g, :H])
+        ref_index, act_ref = oracle.build_index(kf, case["W"][g], case["b"][g], float(case["scale"][g]), km,
+                                                center=centers[g], return_act=True)
+        err = float(np.abs(act[g] - act_ref).max())
+        bound = 2e-6 * max(1.0, float(np.abs(act_ref).max()))
+        assert err <= bound, ("activation error", g, err, bound)
+        sel, moved = check_selection(case, g, act[g], got[g], (ref_index, act_ref, err))
+        check_moments(case, g, got[g])
+        log(f"  group {g}: selected={sel} moved_at_tau={moved} act_err={err:.2e}")
+        if case["kind"] == "bias_ties":
+            assert sel == min(H * km, H * F)
+        if case["kind"] == "dead":
+            assert sel == 0
+    return got
+
+
+@pytest.mark.parametrize("kind", cases.UPDATE_KINDS)
+def test_build_kinds(kind):
+    case = cases.build_case(kind, H=600, T=5, seed=61)
+    log(f"build case kind={kind} H={case['H']}")
+    op, k = run_build(case)
+    got = full_check(case, op, k)
+    if kind != "dead":
+        check_decode(case, op, k, got)
+
+
+@pytest.mark.parametrize("H", [1, 33, 2048])
+def test_build_sizes(H):
+    # one key (budget 8 of 3000 values; a computed center would equal the key
+    # and zero every activation, so it gets a zero center), a partial bitmap
+    # word, and a 4-chunk row
+    case = cases.build_case("random", H=H, T=3, seed=70 + H)
+    log(f"build case kind=random H={H}")
+    center = torch.zeros(8, 128, device="cuda") if H == 1 else None
+    op, k = run_build(case, center=center)
+    got = full_check(case, op, k, center_given=center is not None)
+    assert all(x.memberships == 8 * H for x in got)
+
+
+def test_build_given_center_and_batches():
+    # center supplied by the caller (flags 0), and groups indexed one batch at a
+    # time: the tables equal those of an all-groups batch bit for bit
+    case = cases.build_case("random", H=700, T=4, seed=81)
+    center = torch.from_numpy(np.linspace(-0.1, 0.1, 8 * 128, dtype=np.float32).reshape(8, 128)).cuda()
+    op1, k = run_build(case, center=center, keep_activations=False)
+    assert op1.build_batch == 8
+    assert torch.equal(op1.center, center)
+    per_group = op1.lib.query("prismkv_build_work_bytes", 1, case["H"])
+    op2, _ = run_build(case, center=center, work_limit=3 * per_group, keep_activations=False)
+    assert op2.build_batch == 3
+    torch.cuda.synchronize()
+    for name in ("bits", "n", "moments", "center"):
+        assert torch.equal(getattr(op1, name), getattr(op2, name)), name
+    # against the oracle with the same center
+    got = op1.export_indices()
+    for g in (0, 5):
+        kf = bf16_to_f32(case["k"][g, :case["H"]])
+        ref = oracle.build_index(kf, case["W"][g], case["b"][g], float(case["scale"][g]), case["key_mean"],
+                                 center=center[g].cpu().numpy())
+        margin = oracle.topk_margin(oracle.sae_dense((kf - center[g].cpu().numpy()) / case["scale"][g],
+                                                     case["W"][g], case["b"][g]), case["H"] * case["key_mean"])
+        same = all(np.array_equal(a.numpy(), b) for a, b in zip(got[g].lists, ref.lists))
+        log(f"  group {g}: lists identical to the oracle build={same} margin={margin:.2e}")
+        assert same or margin < 1e-5
+
+
+def test_build_then_append():
+    # build_index over H keys, then append_index of one block: the oracle's two steps
+    from prismkv_amd.native8b import MAX_BLOCK
+    H, N, T = 900, 256, 6
+    case = cases.build_case("random", H=H + N, T=T, seed=91)
+    case_b = dict(case, H=H, T=N + T)
+    op, k = run_build(case_b, keep_activations=False)
+    op.append(k, N)
+    torch.cuda.synchronize()
+    assert op.history == H + N and N <= MAX_BLOCK
+    got = op.export_indices()
+    kf = bf16_to_f32(case["k"])
+    for g in range(8):
+        W, b, s = case["W"][g], case["b"][g], float(case["scale"][g])
+        idx0 = oracle.build_index(kf[g, :H], W, b, s, case["key_mean"], center=op.center[g].cpu().numpy())
+        idx1, act = oracle.append_index(idx0, kf[g, H:H + N], W, b, s, case["key_mean"], return_act=True)
+        same = all(np.array_equal(a.numpy(), b_) for a, b_ in zip(got[g].lists, idx1.lists))
+        log(f"  group {g}: lists identical={same}")
+        assert same or oracle.topk_margin(act, N * case["key_mean"]) < 1e-5
+        if same:
+            assert np.array_equal(got[g].counts.cpu().numpy(), idx1.counts)
+            assert np.allclose(got[g].mean.cpu().numpy(), idx1.mean, rtol=1e-4, atol=1e-5)
+            assert np.allclose(got[g].variance.cpu().numpy(), idx1.variance, rtol=1e-4, atol=1e-5)
+
+
+def test_build_64k():
+    # the 8B geometry's history: 65536 keys per group, 8 groups in one batch
+    # (6.3 GB of activations); activations checked on a row sample, selection
+    # exact on the device activations of three groups, moments of all groups
+    H = 65536
+    case = cases.build_case("random", H=H, T=32, seed=101)
+    log(f"build case kind=random H={H}")
+    op, k = run_build(case)
+    assert op.build_batch == 8
+    centers = op.center.cpu().numpy()
+    got = op.export_indices()
+    rows = np.random.default_rng(5).choice(H, 256, replace=False)
+    for g in range(8):
+        check_center(case, g, centers[g])
+        kf = bf16_to_f32(case["k"][g, :H])
+        x = (kf[rows] - centers[g]) / case["scale"][g]
+        act_rows = op.build_activations()[g, torch.from_numpy(rows).cuda()].cpu().numpy()
+        ref_rows = oracle.sae_dense(x, case["W"][g], case["b"][g])
+        err = float(np.abs(act_rows - ref_rows).max())
+        assert err <= 2e-6 * max(1.0, float(np.abs(ref_rows).max())), ("activation error", g, err)
+        if g in (0, 3, 7):
+            sel, _ = check_selection(case, g, op.build_activations()[g].cpu().numpy(), got[g])
+            assert sel == H * case["key_mean"]
+        check_moments(case, g, got[g])
+        log(f"  group {g}: memberships={got[g].memberships} act_err={err:.2e}")
+    check_decode(case, op, k, got)
