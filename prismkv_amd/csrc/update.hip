@@ -60,6 +60,7 @@ constexpr int kLevels = 3;
 constexpr int kRefineBlocks = 256;  // workgroups per group of a pass over a
 constexpr int kMaxTieBlocks = 4096;  // contiguous ranges of a per group for the ordered ties
 constexpr int kTieMinLen = 65536;    // values per range at least (multiple of 4 * kUT)
+constexpr int kTieGrid = 256;        // workgroups per group of the tie kernels
 constexpr int kCenterParts = 64;     // row ranges of the center sum
 constexpr int kMaxBuild = 1 << 20;   // keys per group of a build (N * F < 2^32 flat indices)
 constexpr int kBuildCenter = 1;      // prismkv_build flag: compute the center (else it is an input)
@@ -324,11 +325,12 @@ __global__ __launch_bounds__(kUT) void emit_kernel(UpdateArgs a) {
 
 // ---------------------------------------------------------------------------
 // ties, only when the ties at tau overflow the budget: the first `need` of
-// them in ascending flat index (core.py:23-24).  Workgroup r of a group owns
-// the contiguous range [r L, (r + 1) L) of a.  tie_count_kernel counts the
-// range's ties; tie_take_kernel skips the ties of the lower ranges and takes
-// its own in flat order (4 consecutive values per thread) while the budget
-// lasts.  Grid (tie_blocks, G) x 256 each.
+// them in ascending flat index (core.py:23-24).  The activations of a group
+// are cut into tie_blocks contiguous ranges [r L, (r + 1) L), dealt to the
+// workgroups r = x, x + kTieGrid, ...  tie_count_kernel counts each range's
+// ties; tie_take_kernel skips the ties of the lower ranges and takes the
+// range's own in flat order (4 consecutive values per thread) while the
+// budget lasts.  Grid (min(tie_blocks, kTieGrid), G) x 256 each.
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ bool ordered_ties(const UpdateArgs& a, int g) {
   const unsigned* ctl = a.ctl + (size_t)g * kCtl;
@@ -336,52 +338,57 @@ __device__ __forceinline__ bool ordered_ties(const UpdateArgs& a, int g) {
 }
 
 __global__ __launch_bounds__(kUT) void tie_count_kernel(UpdateArgs a) {
-  const int r = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+  const int g = blockIdx.y, tid = threadIdx.x;
   if (!ordered_ties(a, g)) return;
   __shared__ unsigned wsum[kUT / 64];
   const float tau = __uint_as_float(a.ctl[(size_t)g * kCtl + kTau]);
   const size_t n = (size_t)a.N * kF;
-  const size_t lo = min(n, (size_t)r * a.tie_len), hi = min(n, lo + a.tie_len);
   const float4* ag = reinterpret_cast<const float4*>(a.act + (size_t)g * n);
-  unsigned c = 0;
-  for (size_t i = lo / 4 + tid; i < hi / 4; i += kUT) {
-    const float4 v = ag[i];
-    c += (unsigned)(v.x == tau) + (unsigned)(v.y == tau) + (unsigned)(v.z == tau) + (unsigned)(v.w == tau);
+  for (int r = blockIdx.x; r < a.tie_blocks; r += gridDim.x) {  // uniform
+    const size_t lo = min(n, (size_t)r * a.tie_len), hi = min(n, lo + a.tie_len);
+    unsigned c = 0;
+    for (size_t i = lo / 4 + tid; i < hi / 4; i += kUT) {
+      const float4 v = ag[i];
+      c += (unsigned)(v.x == tau) + (unsigned)(v.y == tau) + (unsigned)(v.z == tau) + (unsigned)(v.w == tau);
+    }
+    block_incl_scan<kUT>(c, wsum);
+    if (tid == 0) a.tcount[(size_t)g * a.tie_blocks + r] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    __syncthreads();  // wsum is rewritten by the next range's scan
   }
-  block_incl_scan<kUT>(c, wsum);
-  if (tid == 0) a.tcount[(size_t)g * a.tie_blocks + r] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
 }
 
 __global__ __launch_bounds__(kUT) void tie_take_kernel(UpdateArgs a) {
-  const int r = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
+  const int g = blockIdx.y, tid = threadIdx.x;
   if (!ordered_ties(a, g)) return;
   __shared__ unsigned wsum[kUT / 64];
   const unsigned* ctl = a.ctl + (size_t)g * kCtl;
   const float tau = __uint_as_float(ctl[kTau]);  // > 0: only positive values reach the histogram
   const unsigned need = ctl[kNeed];
-  unsigned below = 0;
-  for (int j = tid; j < r; j += kUT) below += a.tcount[(size_t)g * a.tie_blocks + j];
-  block_incl_scan<kUT>(below, wsum);
-  unsigned taken = wsum[0] + wsum[1] + wsum[2] + wsum[3];  // ties of the lower ranges, all ranked first
-  __syncthreads();  // every thread has read wsum before the loop's first scan rewrites it
   const size_t n = (size_t)a.N * kF;
-  const size_t lo = min(n, (size_t)r * a.tie_len), hi = min(n, lo + a.tie_len);
   const float4* ag = reinterpret_cast<const float4*>(a.act + (size_t)g * n);
-  for (size_t base = lo / 4; base < hi / 4 && taken < need; base += kUT) {  // uniform condition
-    const size_t i = base + tid;
-    const float4 v = i < hi / 4 ? ag[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-    const bool h[4] = {v.x == tau, v.y == tau, v.z == tau, v.w == tau};
-    const unsigned c = (unsigned)h[0] + (unsigned)h[1] + (unsigned)h[2] + (unsigned)h[3];
-    const unsigned incl = block_incl_scan<kUT>(c, wsum);
-    unsigned rank = taken + incl - c;  // rank of this thread's first tie among all ties
+  for (int r = blockIdx.x; r < a.tie_blocks; r += gridDim.x) {  // uniform
+    unsigned below = 0;
+    for (int j = tid; j < r; j += kUT) below += a.tcount[(size_t)g * a.tie_blocks + j];
+    block_incl_scan<kUT>(below, wsum);
+    unsigned taken = wsum[0] + wsum[1] + wsum[2] + wsum[3];  // ties of the lower ranges, all ranked first
+    __syncthreads();  // every thread has read wsum before the next scan rewrites it
+    const size_t lo = min(n, (size_t)r * a.tie_len), hi = min(n, lo + a.tie_len);
+    for (size_t base = lo / 4; base < hi / 4 && taken < need; base += kUT) {  // uniform condition
+      const size_t i = base + tid;
+      const float4 v = i < hi / 4 ? ag[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const bool h[4] = {v.x == tau, v.y == tau, v.z == tau, v.w == tau};
+      const unsigned c = (unsigned)h[0] + (unsigned)h[1] + (unsigned)h[2] + (unsigned)h[3];
+      const unsigned incl = block_incl_scan<kUT>(c, wsum);
+      unsigned rank = taken + incl - c;  // rank of this thread's first tie among all ties
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (h[j]) {
-        if (rank < need) set_member(a, g, (unsigned)(4 * i + j));
-        ++rank;
-      }
-    taken += wsum[0] + wsum[1] + wsum[2] + wsum[3];
-    __syncthreads();  // wsum is rewritten by the next scan
+      for (int j = 0; j < 4; ++j)
+        if (h[j]) {
+          if (rank < need) set_member(a, g, (unsigned)(4 * i + j));
+          ++rank;
+        }
+      taken += wsum[0] + wsum[1] + wsum[2] + wsum[3];
+      __syncthreads();  // wsum is rewritten by the next scan
+    }
   }
 }
 
@@ -723,8 +730,9 @@ static void launch_selection(const UpdateArgs& a, int groups, hipStream_t s) {
     hipLaunchKernelGGL(digit_kernel, dim3(groups), dim3(kUT), 0, s, a, level);
   }
   hipLaunchKernelGGL(emit_kernel, dim3(kRefineBlocks, groups), dim3(kUT), 0, s, a);
-  hipLaunchKernelGGL(tie_count_kernel, dim3(a.tie_blocks, groups), dim3(kUT), 0, s, a);
-  hipLaunchKernelGGL(tie_take_kernel, dim3(a.tie_blocks, groups), dim3(kUT), 0, s, a);
+  const int tie_grid = std::min(a.tie_blocks, kTieGrid);
+  hipLaunchKernelGGL(tie_count_kernel, dim3(tie_grid, groups), dim3(kUT), 0, s, a);
+  hipLaunchKernelGGL(tie_take_kernel, dim3(tie_grid, groups), dim3(kUT), 0, s, a);
 }
 
 static bool aligned16(uint64_t p, int64_t stride_elems) { return ((p | (uint64_t)(stride_elems * 2)) & 15u) == 0; }

@@ -232,3 +232,26 @@ def test_build_64k():
         check_moments(case, g, got[g])
         log(f"  group {g}: memberships={got[g].memberships} act_err={err:.2e}")
     check_decode(case, op, k, got)
+
+
+def test_build_ties_over_many_ranges():
+    # W = 0, b = 1 on buckets 0..8 only: every key has exactly 9 positive
+    # activations, all equal to 1, against a budget of 8 per key, so tau = 1
+    # and the ties overflow.  The first 8 H ties in flat order (token * 3000 +
+    # bucket, core.py:23-24) are all 9 buckets of tokens t < 8H // 9 and the
+    # first 8H mod 9 buckets of token 8H // 9.  At H = 8192 the ties span 333
+    # of the 375 contiguous ranges the tie kernels cut the activations into,
+    # more than one workgroup per range.
+    H = 8192
+    case = cases.build_case("bias_ties", H=H, T=2, seed=111)
+    case["b"][:] = 0.0
+    case["b"][:, :9] = 1.0
+    op, k = run_build(case, keep_activations=False)
+    got = op.export_indices()
+    full, part = divmod(8 * H, 9)
+    for g in range(8):
+        for f in range(3000):
+            want = np.arange(full + (1 if f < part else 0)) if f < 9 else np.zeros(0, np.int64)
+            assert np.array_equal(got[g].lists[f].numpy(), want), (g, f)
+        check_moments(case, g, got[g])
+    log(f"  ties over many ranges: {got[0].memberships} memberships per group")
