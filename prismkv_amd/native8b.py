@@ -421,6 +421,24 @@ class Native8B:
             blocks += 1
         return blocks
 
+    def grow(self, capacity):
+        """Extend the id and bitmap capacity to `capacity` tokens, keeping
+        every membership (bitmap columns are copied into wider rows; the
+        workspaces are reallocated zeroed).  Enqueued on the current stream."""
+        capacity = int(capacity)
+        if capacity <= self.capacity:
+            return
+        device = self.out.device
+        rw = bitmap_row_words(capacity)
+        bits = torch.zeros(GROUPS, FEATURES, rw, dtype=torch.int32, device=device)
+        bits[:, :, :self.row_words] = self.bits
+        self.bits, self.row_words, self.capacity = bits, rw, capacity
+        self.ids = torch.zeros(GROUPS, capacity, dtype=torch.int32, device=device)
+        self.union_work = torch.zeros(self.lib.query("prismkv_union_work_bytes", GROUPS, capacity),
+                                      dtype=torch.uint8, device=device)
+        self.decode_work = torch.zeros(self.lib.query("prismkv_decode_work_bytes", GROUPS, capacity),
+                                       dtype=torch.uint8, device=device)
+
     def export_indices(self):
         """The device tables as 8 FeatureIndex objects (counts i64, mean and
         variance f32 [3000,128], centers on the device; per-bucket ascending

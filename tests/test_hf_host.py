@@ -1,0 +1,85 @@
+"""Host-side checks of the encoder bundle format (src/prismkv/weights.py:18-70)
+and of the native Hugging Face session's plumbing (registration, argument
+checks, prefill through the model's own attention) -- no GPU needed."""
+import json
+
+import pytest
+import torch
+
+from prismkv_amd.weights import Encoder, SharedSAE, layer_tables, load_encoders, save_encoders
+
+
+def encoders(layers=1, seed=0):
+    torch.manual_seed(seed)
+    return {(l, g): Encoder(SharedSAE(), 1.0 + 0.5 * g, 2.0) for l in range(layers) for g in range(8)}
+
+
+def test_bundle_round_trip(tmp_path):
+    enc = encoders(2)
+    save_encoders(enc, tmp_path / "b", metadata={"model": "tiny"})
+    got, manifest = load_encoders(tmp_path / "b")
+    assert manifest["schema"] == 1 and manifest["metadata"] == {"model": "tiny"}
+    assert set(got) == set(enc)
+    for unit, e in enc.items():
+        assert torch.equal(got[unit].sae.W_enc, e.sae.W_enc) and torch.equal(got[unit].sae.b_enc, e.sae.b_enc)
+        assert got[unit].key_scale == e.key_scale and got[unit].query_scale == e.query_scale
+    W, b, scale, key_mean = layer_tables(got, 1)
+    assert W.shape == (8, 3000, 128) and b.shape == (8, 3000) and key_mean == 8
+    assert torch.equal(scale, torch.tensor([1.0 + 0.5 * g for g in range(8)]))
+    with pytest.raises(FileExistsError):  # never overwrite
+        save_encoders(enc, tmp_path / "b")
+
+
+def test_bundle_rejects_tampering(tmp_path):
+    save_encoders(encoders(1), tmp_path / "b")
+    (tmp_path / "b" / "l00_g03.pt").write_bytes(b"not the saved tensors")
+    with pytest.raises(ValueError, match="hash"):
+        load_encoders(tmp_path / "b")
+    save_encoders(encoders(1), tmp_path / "c")
+    m = json.loads((tmp_path / "c" / "manifest.json").read_text())
+    m["schema"] = 2
+    (tmp_path / "c" / "manifest.json").write_text(json.dumps(m))
+    with pytest.raises(ValueError, match="schema"):
+        load_encoders(tmp_path / "c")
+
+
+def test_load_keeps_the_rng_stream(tmp_path):
+    save_encoders(encoders(1), tmp_path / "b")
+    torch.manual_seed(7)
+    want = torch.rand(3)
+    torch.manual_seed(7)
+    load_encoders(tmp_path / "b")
+    assert torch.equal(torch.rand(3), want)
+
+
+def tiny_qwen3(layers=1):
+    from transformers import Qwen3Config, Qwen3ForCausalLM
+    cfg = Qwen3Config(vocab_size=128, hidden_size=64, intermediate_size=128, num_hidden_layers=layers,
+                      num_attention_heads=32, num_key_value_heads=8, head_dim=128, max_position_embeddings=4096)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(0)
+    return Qwen3ForCausalLM(cfg).eval()
+
+
+def test_session_plumbing_on_host():
+    from prismkv_amd.hf import HFNative
+    model = tiny_qwen3()
+    with pytest.raises(ValueError, match="missing"):
+        HFNative(model, {})
+    with pytest.raises(NotImplementedError, match="moments"):
+        HFNative(model, encoders(1), router="q_activation")
+    with pytest.raises(ValueError, match="unique cap"):
+        HFNative(model, encoders(1), unique_cap=1.5)
+    ids = torch.randint(0, 128, (1, 12))
+    with torch.no_grad():
+        dense = model(ids).logits
+    session = HFNative(model, encoders(1))
+    assert model.config._attn_implementation == "prismkv_native"
+    with torch.no_grad():
+        prefill = model(ids).logits  # prefill runs the model's own SDPA attention
+    assert torch.equal(prefill, dense)
+    assert session.prefix_lengths == {0: 12}
+    with pytest.raises(ValueError, match="already has"):
+        HFNative(model, encoders(1))
+    session.close()
+    assert model.config._attn_implementation == "sdpa"
