@@ -2,9 +2,13 @@
 
 `Native8B` is the drop-in for the reference's `prismkv.native8b.Native8B`;
 the HIP kernels behind it live in `csrc/` and are reached through the C ABI
-declared in `include/prismkv_hip.h`.
+declared in `include/prismkv_hip.h`.  `prismkv_amd.weights` reads and writes
+the reference's encoder bundles; `prismkv_amd.hf.HFNative` is the Hugging
+Face decode backend over `Native8B` (imports transformers when used).
 """
 from .native8b import FeatureIndex, Native8B, compile_hip, tile_moments, untile_moments
 from ._lib import load as load_library
+from .weights import Encoder, SharedSAE, load_encoders, save_encoders
 
-__all__ = ["FeatureIndex", "Native8B", "compile_hip", "load_library", "tile_moments", "untile_moments"]
+__all__ = ["Encoder", "FeatureIndex", "Native8B", "SharedSAE", "compile_hip", "load_encoders", "load_library",
+           "save_encoders", "tile_moments", "untile_moments"]
