@@ -95,82 +95,109 @@ __device__ __forceinline__ unsigned* hist_of(const UpdateArgs& a, int g, int lev
 }
 
 // ---------------------------------------------------------------------------
-// encode: grid (kFTiles, ceil(N/64), G) x 256; thread = 4 tokens x 4 buckets.
+// encode: grid (kFTiles, Y, G) x 256.  Workgroup (ft, y) keeps W of buckets
+// [64 ft, 64 ft + 64) in LDS (fp32 [bucket][dim]); each wave walks its own
+// 16-token tiles 4 y + w, 4 y + w + 4 Y, ... with no workgroup barrier, so
+// the histogram is flushed once per workgroup.  Products run on fp32 MFMA
+// (v_mfma_f32_16x16x4f32: lane l feeds A[i = l % 16][k], B[k][j = l % 16]
+// and holds D[4 (l / 16) + r][l % 16]).  Lane (i, q) = (l % 16, l / 16)
+// supplies the dims 16 kb + 4 q + t of dim block kb to step t: its A values
+// are x = (k - center) / scale of token row i at those 32 dims, loaded from
+// K straight into registers (the next tile's while the current one is
+// multiplied), and its B values one 16-byte LDS read per bucket tile and
+// block.  A and B always pair the same dim, so the steps only reorder the
+// sum over the 128 dims.
 // ---------------------------------------------------------------------------
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+constexpr int kEncodeTileWgs = 128;  // token-tile workgroups per (bucket tile, group) at most
+constexpr int kRowTile = 16;         // tokens per wave tile
+
+// K chunk kb (4 bf16 dims 16 kb + 4 q ..) of token row t0 + i for lane (i, q).
+__device__ __forceinline__ uint2 key_chunk(const UpdateArgs& a, int g, int t0, int kb) {
+  const int li = threadIdx.x & 15, lq = (threadIdx.x >> 4) & 3;
+  const int row = min(t0 + li, a.N - 1);  // rows past the block repeat the last one (masked at the store)
+  return *reinterpret_cast<const uint2*>(a.k + (size_t)g * a.ks + (size_t)(a.H + row) * kD + 16 * kb + 4 * lq);
+}
+
 __global__ __launch_bounds__(kUT) void encode_kernel(UpdateArgs a) {
-  const int ft = blockIdx.x, tt = blockIdx.y, g = blockIdx.z, tid = threadIdx.x;
-  __shared__ __align__(16) float xs[kD][kTT + 4];  // [dim][token], padded against bank conflicts
-  __shared__ __align__(16) float ws[kD][kFT + 4];  // [dim][bucket]
+  const int ft = blockIdx.x, g = blockIdx.z, tid = threadIdx.x;
+  const int w = tid >> 6, lane = tid & 63, li = lane & 15, lq = lane >> 4;
+  __shared__ __align__(16) float ws[kFT][kD + 4];  // [bucket][dim], padded against bank conflicts
+  __shared__ __align__(16) float cs[kD];           // center
   __shared__ unsigned hist[kBins];
-  const int t0 = tt * kTT, f0 = ft * kFT;
+  const int f0 = ft * kFT;
+  const int tiles = (a.N + kRowTile - 1) / kRowTile;
+  const int first = blockIdx.y * (kUT / 64) + w, stride = gridDim.y * (kUT / 64);
+  uint2 kr[kD / 16];
+  if (first < tiles)
+#pragma unroll
+    for (int kb = 0; kb < kD / 16; ++kb) kr[kb] = key_chunk(a, g, first * kRowTile, kb);
   for (int i = tid; i < kBins; i += kUT) hist[i] = 0;
+  if (tid < kD) cs[tid] = a.center[(size_t)g * kD + tid];
   {
-    // x = (k - center) / key_scale in fp32 (core.py:98), 8 dims per load
-    const float sc = a.scale[g];
-    const float* cg = a.center + (size_t)g * kD;
-    for (int i = tid; i < kTT * kD / 8; i += kUT) {
-      const int tok = i / (kD / 8), d0 = (i % (kD / 8)) * 8;
-      float v[8];
-      if (t0 + tok < a.N) {
-        const uint4 r = *reinterpret_cast<const uint4*>(a.k + (size_t)g * a.ks + (size_t)(a.H + t0 + tok) * kD + d0);
-        v[0] = bf16_lo(r.x); v[1] = bf16_hi(r.x); v[2] = bf16_lo(r.y); v[3] = bf16_hi(r.y);
-        v[4] = bf16_lo(r.z); v[5] = bf16_hi(r.z); v[6] = bf16_lo(r.w); v[7] = bf16_hi(r.w);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = (v[j] - cg[d0 + j]) / sc;
-      } else {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = 0.f;
-      }
-#pragma unroll
-      for (int j = 0; j < 8; ++j) xs[d0 + j][tok] = v[j];
-    }
     const float* wg = a.W + (size_t)g * kF * kD;
     for (int i = tid; i < kFT * kD / 4; i += kUT) {
       const int f = i / (kD / 4), d0 = (i % (kD / 4)) * 4;
       float4 wv = make_float4(0.f, 0.f, 0.f, 0.f);
       if (f0 + f < kF) wv = *reinterpret_cast<const float4*>(wg + (size_t)(f0 + f) * kD + d0);
-      ws[d0][f] = wv.x;
-      ws[d0 + 1][f] = wv.y;
-      ws[d0 + 2][f] = wv.z;
-      ws[d0 + 3][f] = wv.w;
+      *reinterpret_cast<float4*>(&ws[f][d0]) = wv;
     }
   }
-  __syncthreads();
-  const int ty = tid >> 4, tx = tid & 15;  // tokens 4ty.., buckets 4tx..
-  float acc[4][4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = 0.f;
-#pragma unroll 8
-  for (int d = 0; d < kD; ++d) {
-    const float4 xv = *reinterpret_cast<const float4*>(&xs[d][4 * ty]);
-    const float4 wv = *reinterpret_cast<const float4*>(&ws[d][4 * tx]);
-    const float xa[4] = {xv.x, xv.y, xv.z, xv.w}, wa[4] = {wv.x, wv.y, wv.z, wv.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(xa[i], wa[j], acc[i][j]);
-  }
+  const float sc = a.scale[g];
   const float* bg = a.b + (size_t)g * kF;
   float* ag = a.act + (size_t)g * a.N * kF;
-  const int f = f0 + 4 * tx;
+  float bias[kFT / 16];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int tok = t0 + 4 * ty + i;
-    float v[4];
+  for (int j = 0; j < kFT / 16; ++j) bias[j] = f0 + 16 * j + li < kF ? bg[f0 + 16 * j + li] : 0.f;
+  __syncthreads();
+  for (int tt = first; tt < tiles; tt += stride) {  // uniform per wave
+    const bool more = tt + stride < tiles;
+    f32x4 acc[kFT / 16];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float x = f + j < kF ? acc[i][j] + bg[f + j] : 0.f;
-      v[j] = x > 0.f ? x : 0.f;  // relu; non-positive values are never selected
-      if (tok < a.N && f + j < kF && v[j] > 0.f) atomicAdd(&hist[__float_as_uint(v[j]) >> 20], 1u);
+    for (int j = 0; j < kFT / 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < kD / 16; ++kb) {
+      // x = (k - center) / key_scale in fp32 (core.py:98) for this lane's 4 dims
+      const uint2 r = kr[kb];
+      const float4 c = *reinterpret_cast<const float4*>(&cs[16 * kb + 4 * lq]);
+      const float4 xa = make_float4((bf16_lo(r.x) - c.x) / sc, (bf16_hi(r.x) - c.y) / sc,
+                                    (bf16_lo(r.y) - c.z) / sc, (bf16_hi(r.y) - c.w) / sc);
+      if (more) kr[kb] = key_chunk(a, g, (tt + stride) * kRowTile, kb);  // next tile, in flight meanwhile
+      float4 bv[kFT / 16];
+#pragma unroll
+      for (int j = 0; j < kFT / 16; ++j) bv[j] = *reinterpret_cast<const float4*>(&ws[16 * j + li][16 * kb + 4 * lq]);
+      // the four accumulators interleaved: no MFMA waits on the one before it
+#pragma unroll
+      for (int j = 0; j < kFT / 16; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.x, bv[j].x, acc[j], 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < kFT / 16; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.y, bv[j].y, acc[j], 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < kFT / 16; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.z, bv[j].z, acc[j], 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < kFT / 16; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.w, bv[j].w, acc[j], 0, 0, 0);
+      // keep each block's B reads next to its MFMAs (hoisting all of them
+      // costs 128 registers and halves the waves per SIMD)
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (tok < a.N && f < kF) {  // kF is a multiple of 4: a quad is all in or all out
-      *reinterpret_cast<float4*>(ag + (size_t)tok * kF + f) = make_float4(v[0], v[1], v[2], v[3]);
+    // bias, relu, histogram of the positive values, store: lane (i, q) holds
+    // buckets f0 + 16 j + i of tokens 16 tt + 4 q + r
+#pragma unroll
+    for (int j = 0; j < kFT / 16; ++j) {
+      const int f = f0 + 16 * j + li;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int tok = tt * kRowTile + 4 * lq + r;
+        const float x = acc[j][r] + bias[j];
+        const float v = x > 0.f ? x : 0.f;  // relu; non-positive values are never selected
+        if (tok < a.N && f < kF) {
+          ag[(size_t)tok * kF + f] = v;
+          if (v > 0.f) atomicAdd(&hist[__float_as_uint(v) >> 20], 1u);
+        }
+      }
     }
   }
   __syncthreads();
-  unsigned* hg = hist_of(a, g, 0) + ((ft + tt) % kRep) * kBins;
+  unsigned* hg = hist_of(a, g, 0) + ((ft + blockIdx.y) % kRep) * kBins;
   for (int i = tid; i < kBins; i += kUT)
     if (hist[i]) atomicAdd(&hg[i], hist[i]);
 }
@@ -347,9 +374,19 @@ __global__ __launch_bounds__(kUT) void tie_count_kernel(UpdateArgs a) {
   for (int r = blockIdx.x; r < a.tie_blocks; r += gridDim.x) {  // uniform
     const size_t lo = min(n, (size_t)r * a.tie_len), hi = min(n, lo + a.tie_len);
     unsigned c = 0;
-    for (size_t i = lo / 4 + tid; i < hi / 4; i += kUT) {
-      const float4 v = ag[i];
-      c += (unsigned)(v.x == tau) + (unsigned)(v.y == tau) + (unsigned)(v.z == tau) + (unsigned)(v.w == tau);
+    constexpr int kU = 8;  // loads in flight per thread
+    for (size_t i0 = lo / 4 + tid; i0 < hi / 4; i0 += kU * kUT) {
+      float4 v[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const size_t i = i0 + (size_t)u * kUT;
+        v[u] = ag[i < hi / 4 ? i : i0];  // a repeated value is not counted twice below
+      }
+#pragma unroll
+      for (int u = 0; u < kU; ++u)
+        if (i0 + (size_t)u * kUT < hi / 4)
+          c += (unsigned)(v[u].x == tau) + (unsigned)(v[u].y == tau) + (unsigned)(v[u].z == tau) +
+               (unsigned)(v[u].w == tau);
     }
     block_incl_scan<kUT>(c, wsum);
     if (tid == 0) a.tcount[(size_t)g * a.tie_blocks + r] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
@@ -723,7 +760,9 @@ static UpdateArgs make_args(uint64_t k, uint64_t W, uint64_t b, uint64_t center,
 // encode .. ties: the exact batch-wide positive Top-k of the N keys' activations
 // and their bitmap bits.
 static void launch_selection(const UpdateArgs& a, int groups, hipStream_t s) {
-  hipLaunchKernelGGL(encode_kernel, dim3(kFTiles, (a.N + kTT - 1) / kTT, groups), dim3(kUT), 0, s, a);
+  const int wave_tiles = (a.N + kRowTile - 1) / kRowTile;
+  const int wgs = std::min((wave_tiles + kUT / 64 - 1) / (kUT / 64), kEncodeTileWgs);
+  hipLaunchKernelGGL(encode_kernel, dim3(kFTiles, wgs, groups), dim3(kUT), 0, s, a);
   hipLaunchKernelGGL(digit_kernel, dim3(groups), dim3(kUT), 0, s, a, 0);
   for (int level = 1; level < kLevels; ++level) {
     hipLaunchKernelGGL(refine_kernel, dim3(kRefineBlocks, groups), dim3(kUT), 0, s, a, level);
