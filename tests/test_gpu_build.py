@@ -255,3 +255,34 @@ def test_build_ties_over_many_ranges():
             assert np.array_equal(got[g].lists[f].numpy(), want), (g, f)
         check_moments(case, g, got[g])
     log(f"  ties over many ranges: {got[0].memberships} memberships per group")
+
+
+def test_long_history_with_updates():
+    # H = 131072 built on the device (two group batches within the 8 GiB
+    # workspace), then the tail grows 0 -> 4096 with an update every 1024
+    # tokens (src/prismkv/hf_reference.py:209-211 with interval 1024): decode
+    # at several tail lengths against the oracle on the exported index
+    H, T = 131072, 4096
+    case = cases.build_case("random", H=H, T=T, seed=131)
+    op, k = run_build(dict(case, T=T), keep_activations=False)
+    assert op.build_batch == 5
+    v, q = bf16_tensor(case["v"]), bf16_tensor(case["q"])
+    for tail in (0, 1, 1025, 3000, 4096):
+        total = H + tail
+        op.catch_up(k[:, :total], total, update_interval=1024)
+        want = H + max(0, (tail - 1) // 1024) * 1024
+        assert op.history == want, (tail, op.history, want)
+        out = op(q, k[:, :total], v[:, :total])
+        torch.cuda.synchronize()
+        assert op.decode_errors() == 0
+        got = op.export_indices()
+        idx = [oracle.Index(op.history, i.center.cpu().numpy(), i.counts.cpu().numpy(), i.mean.cpu().numpy(),
+                            i.variance.cpu().numpy(), [l.numpy() for l in i.lists]) for i in got]
+        c2 = dict(H=op.history, T=total - op.history, q=case["q"], k=case["k"][:, :total],
+                  v=case["v"][:, :total], indices=idx, kind="random")
+        groups = expect.expected(c2)
+        identical, near = expect.compare_route(groups, *route_outputs(op))
+        assert identical + near == 8
+        err = expect.attention_errors(bf16_bits(out), expect.expected_attention(c2, groups))
+        log(f"  tail {tail}: history={op.history} {identical} identical, {near} near-tie; {err}")
+        assert err["rel_l2"] <= 2e-3 and err["max_abs"] < 0.05, err
