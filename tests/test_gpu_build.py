@@ -286,3 +286,56 @@ def test_long_history_with_updates():
         err = expect.attention_errors(bf16_bits(out), expect.expected_attention(c2, groups))
         log(f"  tail {tail}: history={op.history} {identical} identical, {near} near-tie; {err}")
         assert err["rel_l2"] <= 2e-3 and err["max_abs"] < 0.05, err
+
+
+def test_stress_mixture_keys_with_cap():
+    # the stress configuration: H = 262144 keys per group drawn from a
+    # 64-component Gaussian mixture (centers ~ N(0, I), sigma = 0.3), indexed
+    # on the device (4 batches of 2 groups within the 8 GiB workspace), then
+    # routed with the strict unique-ID cap floor(H / 16) = 16384
+    # (src/prismkv/core.py:149-163): the device's ranked order is checked
+    # against the oracle, then fed to the oracle's budgeted walk, which the
+    # device's kept buckets / raw / ids must equal bit for bit
+    H, T, cap = 262144, 16, 1 / 16
+    gen = torch.Generator(device="cuda").manual_seed(151)
+    centers = torch.randn(8, 64, 128, generator=gen, device="cuda")
+    comp = torch.randint(0, 64, (8, H + T), generator=gen, device="cuda")
+    noise = torch.randn(8, H + T, 128, generator=gen, device="cuda") * 0.3
+    k = (torch.gather(centers, 1, comp[..., None].expand(-1, -1, 128)) + noise).to(torch.bfloat16)
+    v = torch.randn(8, H + T, 128, generator=gen, device="cuda").to(torch.bfloat16)
+    q = torch.randn(8, 4, 128, generator=gen, device="cuda").to(torch.bfloat16)
+    del noise
+    base = cases.build_case("random", H=1, T=0, seed=152)  # per-group SAE tables and scales
+    from prismkv_amd import Native8B
+    op = Native8B.from_keys(k, H, torch.from_numpy(base["W"]), torch.from_numpy(base["b"]),
+                            torch.from_numpy(base["scale"]), 8, capacity=H + T)
+    torch.cuda.synchronize()
+    assert op.build_batch == 2
+    got = op.export_indices()
+    idx = [oracle.Index(H, i.center.cpu().numpy(), i.counts.cpu().numpy(), i.mean.cpu().numpy(),
+                        i.variance.cpu().numpy(), [l.numpy() for l in i.lists]) for i in got]
+    case = dict(H=H, T=T, q=bf16_bits(q), k=bf16_bits(k), v=bf16_bits(v), indices=idx, kind="mixture")
+    op.route(q)
+    identical, near = expect.compare_route(expect.expected(case), *route_outputs(op))
+    assert identical + near == 8
+    features, valid, _, _, _ = route_outputs(op)
+    orders = [features[g][valid[g] > 0] for g in range(8)]
+    op.unique_cap = cap
+    out = op(q, k, v)
+    torch.cuda.synchronize()
+    f2, v2, r2, i2, c2 = route_outputs(op)
+    want, skipped = [], 0
+    for g in range(8):
+        ids, meta = oracle.select_buckets(orders[g], idx[g].lists, H, cap)
+        nf = len(meta["features"])
+        skipped += len(orders[g]) - nf
+        assert meta["limit"] == 16384
+        assert f2[g][:nf].tolist() == meta["features"], ("kept buckets", g)
+        assert int(r2[g]) == meta["raw"] and int(c2[g]) == len(ids), ("raw/count", g)
+        assert np.array_equal(i2[g][:len(ids)].astype(np.int64), ids), ("ids", g)
+        want.append(dict(ids=ids))
+    sizes = [max(len(l) for l in i.lists) for i in idx]
+    log(f"  largest bucket per group {sizes}; {skipped} ranked buckets skipped by the cap; unique {c2.tolist()}")
+    err = expect.attention_errors(bf16_bits(out), expect.expected_attention(case, want))
+    log(f"  capped decode {err}")
+    assert err["rel_l2"] <= 2e-3 and err["max_abs"] < 0.05, err
