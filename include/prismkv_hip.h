@@ -161,6 +161,32 @@ int prismkv_build(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t 
                   uint64_t counts, uint64_t moments, uint64_t work, int groups, int batch, int H, int key_mean,
                   int flags, int64_t ks, int64_t row_words, uint64_t stream);
 
+/* ---- the prismkv.core surface (src/prismkv/core.py) ---------------------
+ * Stage 1 with the score vector of bucket_scores (core.py:106-130): as
+ * prismkv_route, and scores f32 [G][3000] <- the per-head softmax
+ * probabilities' mean over the 4 heads (0 for a dead bucket). */
+int prismkv_route_scores(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
+                         uint64_t valid, uint64_t raw, uint64_t scores, int groups, uint64_t stream);
+
+/* positive_global_topk (core.py:13-26) of a device matrix act f32 [N][3000]
+ * (16-byte aligned, N <= 2^20) with budget `count`: out i64 [min(count,
+ * 3000 N)] <- every value above the budget-th largest tau (and above 0) in
+ * ascending flat index (row * 3000 + column), then the values equal to
+ * tau > 0 in ascending flat index up to the budget (every positive value when
+ * fewer are positive); out_len i32 [1] <- how many were written.  `work` is
+ * prismkv_topk_work_bytes() bytes, zero-filled once and left zeroed. */
+size_t prismkv_topk_work_bytes(void);
+int prismkv_topk(uint64_t act, uint64_t out, uint64_t out_len, uint64_t work, int N, int64_t count, uint64_t stream);
+
+/* summarize (core.py:76-89) of every group from its bitmap rows: counts and
+ * the tiled moments get each bucket's member count and the population mean
+ * and variance of the member K rows (bit t of row f: row t of K, t < H);
+ * center[g] <- mean of K rows [0, H) when flags & 1.  `work` is
+ * prismkv_summarize_work_bytes(groups) bytes, zero-filled once. */
+size_t prismkv_summarize_work_bytes(int groups);
+int prismkv_summarize(uint64_t k, uint64_t bits, uint64_t center, uint64_t counts, uint64_t moments, uint64_t work,
+                      int groups, int H, int flags, int64_t ks, int64_t row_words, uint64_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -37,6 +37,11 @@ SIGNATURES = {
     "prismkv_update": ([_U64] * 9 + [_I32] * 4 + [_I64, _I64], True, _I32),
     "prismkv_build_work_bytes": ([_I32, _I32], False, _SZ),
     "prismkv_build": ([_U64] * 9 + [_I32] * 5 + [_I64, _I64], True, _I32),
+    "prismkv_route_scores": ([_U64] * 8 + [_I32], True, _I32),
+    "prismkv_topk_work_bytes": ([], False, _SZ),
+    "prismkv_topk": ([_U64] * 4 + [_I32, _I64], True, _I32),
+    "prismkv_summarize_work_bytes": ([_I32], False, _SZ),
+    "prismkv_summarize": ([_U64] * 6 + [_I32, _I32, _I32, _I64, _I64], True, _I32),
 }
 
 _loaded: dict[str, "Library"] = {}

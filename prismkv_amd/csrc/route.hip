@@ -77,7 +77,8 @@ constexpr int kParts = 8;
 constexpr int kPartB = kFP / kParts;  // 376 buckets per part
 constexpr int kPartKeys = (kPartB + kRT - 1) / kRT;  // 2
 
-__global__ __launch_bounds__(kRT) void route_part_kernel(RouteWork work, unsigned long long* __restrict__ cand) {
+__global__ __launch_bounds__(kRT) void route_part_kernel(RouteWork work, unsigned long long* __restrict__ cand,
+                                                         float* __restrict__ scores) {
   const int part = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   __shared__ float gmax[kHq], grz[kHq];
   __shared__ __align__(16) unsigned long long keys[kPartKeys * kRT];
@@ -107,6 +108,8 @@ __global__ __launch_bounds__(kRT) void route_part_kernel(RouteWork work, unsigne
     const int off = tid + i * kRT, b = part * kPartB + off;
     const uint64_t key = off < kPartB ? bucket_key(lv[i], gmax, grz, b) : 0;
     keys[off] = key;
+    // optional: the head-mean score of core.py:128 (the key's probability sum / 4)
+    if (scores && off < kPartB && b < kF) scores[(size_t)g * kF + b] = __uint_as_float((unsigned)(key >> 12)) * 0.25f;
   }
   __syncthreads();
   // wave w keeps the 16 best of keys[128w, 128w + 128); wave 0 then the 16 best of those 64
@@ -244,8 +247,8 @@ size_t prismkv_route_work_bytes(int groups) {
   return route_logits_bytes(groups) + route_stats_bytes(groups) + route_cand_bytes(groups);
 }
 
-int prismkv_route(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features, uint64_t valid,
-                  uint64_t raw, int groups, uint64_t stream) {
+static int route_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
+                      uint64_t valid, uint64_t raw, float* scores, int groups, uint64_t stream) {
   if (groups < 1 || groups > 65535) return kBadSize;
   if (!q || !moments || !counts || !work || !features || !valid || !raw) return kBadSize;
   char* base = reinterpret_cast<char*>(work);
@@ -255,11 +258,23 @@ int prismkv_route(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, 
                      reinterpret_cast<const int*>(counts), rw.logits, rw.stats, groups, s);
   unsigned long long* cand =
       reinterpret_cast<unsigned long long*>(base + route_logits_bytes(groups) + route_stats_bytes(groups));
-  hipLaunchKernelGGL(route_part_kernel, dim3(kParts, groups), dim3(kRT), 0, s, rw, cand);
+  hipLaunchKernelGGL(route_part_kernel, dim3(kParts, groups), dim3(kRT), 0, s, rw, cand, scores);
   hipLaunchKernelGGL(route_final_kernel, dim3(groups), dim3(64), 0, s, cand, reinterpret_cast<const int*>(counts),
                      reinterpret_cast<int64_t*>(features), reinterpret_cast<float*>(valid),
                      reinterpret_cast<int*>(raw));
   return (int)hipGetLastError();
+}
+
+int prismkv_route(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features, uint64_t valid,
+                  uint64_t raw, int groups, uint64_t stream) {
+  return route_impl(q, moments, counts, work, features, valid, raw, nullptr, groups, stream);
+}
+
+int prismkv_route_scores(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
+                         uint64_t valid, uint64_t raw, uint64_t scores, int groups, uint64_t stream) {
+  if (!scores) return kBadSize;
+  return route_impl(q, moments, counts, work, features, valid, raw, reinterpret_cast<float*>(scores), groups,
+                    stream);
 }
 
 int pack(uint64_t q, uint64_t a, uint64_t stream) {

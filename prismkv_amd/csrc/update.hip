@@ -706,6 +706,149 @@ __global__ __launch_bounds__(kUT) void build_moments_kernel(UpdateArgs a) {
   if (tid == 0) a.counts[(size_t)g * kFP + f] = (int)n;
 }
 
+// ---------------------------------------------------------------------------
+// positive_global_topk on a given [N][F] fp32 matrix (core.py:13-26), for
+// callers of the Python surface: the same threshold kernels (digit / refine)
+// after a level-0 histogram, then the flat indices in the reference's order
+// -- every strict value (a > tau and a > 0; every positive one when fewer
+// than the budget are positive) in ascending flat index, then the first
+// `need` values equal to tau in ascending flat index.  The matrix is cut
+// into the contiguous ranges of the tie kernels; flat_count_kernel counts
+// each range's strict values and ties (tcount[2r], tcount[2r + 1]),
+// flat_emit_kernel writes them after the lower ranges' ones.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kUT) void hist0_kernel(UpdateArgs a) {
+  const int g = blockIdx.y, tid = threadIdx.x;
+  __shared__ unsigned hist[kBins];
+  for (int i = tid; i < kBins; i += kUT) hist[i] = 0;
+  __syncthreads();
+  const size_t n = (size_t)a.N * kF;
+  const float4* ag = reinterpret_cast<const float4*>(a.act + (size_t)g * n);
+  for (size_t i = (size_t)blockIdx.x * kUT + tid; i < n / 4; i += (size_t)gridDim.x * kUT) {
+    const float4 v4 = ag[i];
+    const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (vv[j] > 0.f) atomicAdd(&hist[__float_as_uint(vv[j]) >> 20], 1u);
+  }
+  __syncthreads();
+  unsigned* hg = hist_of(a, g, 0) + (blockIdx.x % kRep) * kBins;
+  for (int i = tid; i < kBins; i += kUT)
+    if (hist[i]) atomicAdd(&hg[i], hist[i]);
+}
+
+struct FlatRule {
+  float tau;
+  bool all_pos, ties;
+  __device__ bool strict(float v) const { return all_pos ? v > 0.f : (v > tau && v > 0.f); }
+  __device__ bool tie(float v) const { return ties && v == tau; }
+};
+
+__device__ __forceinline__ FlatRule flat_rule(const UpdateArgs& a, int g) {
+  const unsigned* ctl = a.ctl + (size_t)g * kCtl;
+  FlatRule r;
+  r.tau = __uint_as_float(ctl[kTau]);  // +inf (nothing) for an empty budget
+  r.all_pos = ctl[kMode] == kModeAllPositive;
+  r.ties = !r.all_pos && r.tau > 0.f && ctl[kTau] != 0x7f800000u;
+  return r;
+}
+
+__global__ __launch_bounds__(kUT) void flat_count_kernel(UpdateArgs a) {
+  const int g = blockIdx.y, tid = threadIdx.x;
+  __shared__ unsigned wsum[kUT / 64];
+  const FlatRule rule = flat_rule(a, g);
+  const size_t n = (size_t)a.N * kF;
+  const float4* ag = reinterpret_cast<const float4*>(a.act + (size_t)g * n);
+  for (int r = blockIdx.x; r < a.tie_blocks; r += gridDim.x) {  // uniform
+    const size_t lo = min(n, (size_t)r * a.tie_len), hi = min(n, lo + a.tie_len);
+    unsigned cs = 0, ct = 0;
+    for (size_t i = lo / 4 + tid; i < hi / 4; i += kUT) {
+      const float4 v = ag[i];
+      const float vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        cs += rule.strict(vv[j]);
+        ct += rule.tie(vv[j]);
+      }
+    }
+    block_incl_scan<kUT>(cs, wsum);
+    if (tid == 0) a.tcount[((size_t)g * a.tie_blocks + r) * 2] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    __syncthreads();
+    block_incl_scan<kUT>(ct, wsum);
+    if (tid == 0) a.tcount[((size_t)g * a.tie_blocks + r) * 2 + 1] = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    __syncthreads();
+  }
+}
+
+__global__ __launch_bounds__(kUT) void flat_emit_kernel(UpdateArgs a, int64_t* out, int* out_len) {
+  const int g = blockIdx.y, tid = threadIdx.x;
+  __shared__ unsigned wsum[kUT / 64];
+  const FlatRule rule = flat_rule(a, g);
+  const unsigned need = rule.ties ? a.ctl[(size_t)g * kCtl + kNeed] : 0u;
+  const unsigned* tc = a.tcount + (size_t)g * a.tie_blocks * 2;
+  // all strict values come first: their total over every range
+  unsigned all_s = 0, all_t = 0;
+  for (int j = tid; j < a.tie_blocks; j += kUT) {
+    all_s += tc[2 * j];
+    all_t += tc[2 * j + 1];
+  }
+  block_incl_scan<kUT>(all_s, wsum);
+  const unsigned strict_total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+  __syncthreads();
+  block_incl_scan<kUT>(all_t, wsum);
+  const unsigned ties_total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+  __syncthreads();
+  if (blockIdx.x == 0 && tid == 0) out_len[g] = (int)(strict_total + min(ties_total, need));
+  const size_t n = (size_t)a.N * kF;
+  const float4* ag = reinterpret_cast<const float4*>(a.act + (size_t)g * n);
+  for (int r = blockIdx.x; r < a.tie_blocks; r += gridDim.x) {  // uniform
+    unsigned bs = 0, bt = 0;
+    for (int j = tid; j < r; j += kUT) {
+      bs += tc[2 * j];
+      bt += tc[2 * j + 1];
+    }
+    block_incl_scan<kUT>(bs, wsum);
+    unsigned at_s = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    __syncthreads();
+    block_incl_scan<kUT>(bt, wsum);
+    unsigned at_t = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+    __syncthreads();
+    const size_t lo = min(n, (size_t)r * a.tie_len), hi = min(n, lo + a.tie_len);
+    for (size_t base = lo / 4; base < hi / 4; base += kUT) {  // uniform
+      const size_t i = base + tid;
+      const float4 v = i < hi / 4 ? ag[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float vv[4] = {v.x, v.y, v.z, v.w};
+      bool hs[4], ht[4];
+      unsigned cs = 0, ct = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        hs[j] = i < hi / 4 && rule.strict(vv[j]);
+        ht[j] = i < hi / 4 && rule.tie(vv[j]);
+        cs += hs[j];
+        ct += ht[j];
+      }
+      const unsigned is = block_incl_scan<kUT>(cs, wsum);
+      const unsigned ts = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+      __syncthreads();
+      const unsigned it = block_incl_scan<kUT>(ct, wsum);
+      const unsigned tt = wsum[0] + wsum[1] + wsum[2] + wsum[3];
+      __syncthreads();
+      unsigned ks = at_s + is - cs, kt = at_t + it - ct;  // ranks of this thread's first strict value / tie
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t flat = (int64_t)(4 * i + j);
+        if (hs[j]) out[ks++] = flat;
+        if (ht[j]) {
+          if (kt < need) out[strict_total + kt] = flat;
+          ++kt;
+        }
+      }
+      at_s += ts;
+      at_t += tt;
+    }
+  }
+}
+
 }  // namespace
 }  // namespace prismkv
 
@@ -719,7 +862,7 @@ struct UpdateLayout {
     act = take((size_t)groups * N * kF * sizeof(float));
     hist = take((size_t)groups * kLevels * kRep * kBins * sizeof(unsigned));
     ctl = take((size_t)groups * kCtl * sizeof(unsigned));
-    tcount = take((size_t)groups * kMaxTieBlocks * sizeof(unsigned));
+    tcount = take((size_t)groups * kMaxTieBlocks * 2 * sizeof(unsigned));
     part = take((size_t)groups * kCenterParts * kD * sizeof(double));
     total = o;
   }
@@ -837,6 +980,55 @@ int prismkv_build(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t 
     launch_selection(a, nb, s);
     hipLaunchKernelGGL(build_moments_kernel, dim3(kF, nb), dim3(kUT), 0, s, a);
   }
+  return (int)hipGetLastError();
+}
+
+size_t prismkv_topk_work_bytes(void) { return UpdateLayout(1, 0).total; }
+
+int prismkv_topk(uint64_t act, uint64_t out, uint64_t out_len, uint64_t work, int N, int64_t count,
+                 uint64_t stream) {
+  if (N < 1 || N > kMaxBuild || count < 0) return kBadSize;
+  if (!act || !out || !out_len || !work || (act & 15u)) return kBadSize;
+  const UpdateLayout L(1, 0);
+  const int64_t n = (int64_t)N * kF;
+  UpdateArgs a = make_args(0, 0, 0, 0, 0, 0, 0, 0, work, 1, 0, N, 1, 0, 0, L);
+  a.act = reinterpret_cast<float*>(act);  // read only here
+  a.budget = count < n ? count : n;
+  hipStream_t s = (hipStream_t)stream;
+  hipLaunchKernelGGL(hist0_kernel, dim3(kRefineBlocks, 1), dim3(kUT), 0, s, a);
+  hipLaunchKernelGGL(digit_kernel, dim3(1), dim3(kUT), 0, s, a, 0);
+  for (int level = 1; level < kLevels; ++level) {
+    hipLaunchKernelGGL(refine_kernel, dim3(kRefineBlocks, 1), dim3(kUT), 0, s, a, level);
+    hipLaunchKernelGGL(digit_kernel, dim3(1), dim3(kUT), 0, s, a, level);
+  }
+  const int grid = std::min(a.tie_blocks, kTieGrid);
+  hipLaunchKernelGGL(flat_count_kernel, dim3(grid, 1), dim3(kUT), 0, s, a);
+  hipLaunchKernelGGL(flat_emit_kernel, dim3(grid, 1), dim3(kUT), 0, s, a, reinterpret_cast<int64_t*>(out),
+                     reinterpret_cast<int*>(out_len));
+  return (int)hipGetLastError();
+}
+
+size_t prismkv_summarize_work_bytes(int groups) {
+  if (groups < 1 || groups > 65535) return 0;
+  return UpdateLayout(groups, 0).total;
+}
+
+int prismkv_summarize(uint64_t k, uint64_t bits, uint64_t center, uint64_t counts, uint64_t moments, uint64_t work,
+                      int groups, int H, int flags, int64_t ks, int64_t row_words, uint64_t stream) {
+  if (groups < 1 || groups > 65535 || H < 1 || H > kMaxBuild) return kBadSize;
+  if (flags & ~kBuildCenter) return kBadMode;
+  if (ks < (int64_t)H * kD || row_words < (H + 31) / 32) return kBadSize;
+  if (!k || !bits || !center || !counts || !moments || !work || !aligned16(k, ks)) return kBadSize;
+  const UpdateLayout L(groups, 0);
+  const UpdateArgs a = make_args(k, 0, 0, center, 0, bits, counts, moments, work, groups, 0, H, 1, ks, row_words, L);
+  hipStream_t s = (hipStream_t)stream;
+  if (flags & kBuildCenter) {
+    double* part = reinterpret_cast<double*>(reinterpret_cast<char*>(work) + L.part);
+    hipLaunchKernelGGL(center_part_kernel, dim3(kCenterParts, groups), dim3(kUT), 0, s, a, part);
+    hipLaunchKernelGGL(center_final_kernel, dim3(groups), dim3(kD), 0, s, a, (const double*)part,
+                       reinterpret_cast<float*>(center));
+  }
+  hipLaunchKernelGGL(build_moments_kernel, dim3(kF, groups), dim3(kUT), 0, s, a);
   return (int)hipGetLastError();
 }
 
