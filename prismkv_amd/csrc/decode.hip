@@ -294,7 +294,8 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, DecodeLd
 
 // Phases 1-4: the group's Top-16 (rank order) into lds.win / lds.sel_rows /
 // lds.need.
-__device__ void decode_select(const DecodeArgs& a, int g, int p, DecodeLds& lds) {
+template <int KW>
+__device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p, DecodeLds& lds) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int S = a.S;
   // moment tiles kper * p + j, j < own: contiguous 32 KB tiles, one stream per workgroup
@@ -379,19 +380,18 @@ __device__ void decode_select(const DecodeArgs& a, int g, int p, DecodeLds& lds)
     if (lane < kTop) st_dev(&a.cand[((size_t)g * S + p) * kTop + lane], ~best);
   }
   // ---- 4. the group's Top-16 from its S x 16 candidates, as they land
-  const int kw = S <= 32 ? 1 : S <= 64 ? 2 : S <= 128 ? 4 : 8;  // 64-key sets per wave
-  if (kw == 1) final_top16<1>(a, g, lds);
-  else if (kw == 2) final_top16<2>(a, g, lds);
-  else if (kw == 4) final_top16<4>(a, g, lds);
-  else final_top16<8>(a, g, lds);
+  final_top16<KW>(a, g, lds);
 }
 
+// KW = 64-key candidate sets per wave, ceil(S / 32): one instantiation per
+// range of S, so a launch carries only the selection code it runs.
+template <int KW>
 __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   const int p = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   __shared__ DecodeLds lds;
 
   // ---- 1-4. the group's Top-16
-  decode_select(a, g, p, lds);
+  decode_select<KW>(a, g, p, lds);
   if (p == 0 && w == 0)
     write_selection(lds.win, lds.need, a.counts + (size_t)g * kFP, a.features + (size_t)g * kTop,
                     a.valid + (size_t)g * kTop, a.raw + g);
@@ -563,7 +563,15 @@ static int resident_workgroups() {
   if (cached[dev] == 0) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, decode_kernel, kDT, 0) != hipSuccess) return 0;
+    // the instantiations differ only in the selection code; take the least resident
+    int least = 1 << 30;
+    const void* fns[] = {reinterpret_cast<const void*>(decode_kernel<1>), reinterpret_cast<const void*>(decode_kernel<2>),
+                         reinterpret_cast<const void*>(decode_kernel<4>), reinterpret_cast<const void*>(decode_kernel<8>)};
+    for (const void* fn : fns) {
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kDT, 0) != hipSuccess) return 0;
+      least = std::min(least, per_cu);
+    }
+    per_cu = least;
     cached[dev] = cus * per_cu;
   }
   return cached[dev];
@@ -616,7 +624,12 @@ int prismkv_decode(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits,
   a.ids_stride = ids_stride;
   a.count = reinterpret_cast<int32_t*>(count);
   a.out = reinterpret_cast<uint16_t*>(out);
-  hipLaunchKernelGGL(decode_kernel, dim3(S, groups), dim3(kDT), 0, (hipStream_t)stream, a);
+  const dim3 grid(S, groups), block(kDT);
+  hipStream_t s = (hipStream_t)stream;
+  if (S <= 32) hipLaunchKernelGGL(decode_kernel<1>, grid, block, 0, s, a);
+  else if (S <= 64) hipLaunchKernelGGL(decode_kernel<2>, grid, block, 0, s, a);
+  else if (S <= 128) hipLaunchKernelGGL(decode_kernel<4>, grid, block, 0, s, a);
+  else hipLaunchKernelGGL(decode_kernel<8>, grid, block, 0, s, a);
   return (int)hipGetLastError();
 }
 

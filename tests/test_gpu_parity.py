@@ -159,6 +159,12 @@ def test_long_history_uses_split_path(monkeypatch):
     check_case(cases.native_case(1025, 3, "random"), splits_list=(32,), schedules=(0,))
 
 
+def test_fused_decode_beyond_128_splits():
+    # H = 300000: 147 workgroups per group, 8 candidate sets of 64 per wave in
+    # the single-launch selection
+    check_case(cases.native_case(300000, 3, "random", seed=9), splits_list=(128,), schedules=(0,))
+
+
 def test_union_262k_history():
     # H beyond the reference union limit (131072): 8 groups x 262144 tokens
     check_case(cases.native_case(262144, 64, "random", seed=5), splits_list=(128,), schedules=(0,))
