@@ -168,6 +168,26 @@ int prismkv_build(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t 
 int prismkv_route_scores(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
                          uint64_t valid, uint64_t raw, uint64_t scores, int groups, uint64_t stream);
 
+/* Stage 1 by query activations (router "q_activation", core.py:131-139):
+ * a = relu((q / qscale[g]) W[g]^T + b[g]) for the 4 heads (W f32 [G][3000][128],
+ * b f32 [G][3000], qscale f32 [G]); per head the 16 largest activations
+ * (value descending, bucket ascending), weights val / max(sum, 1e-20) / 4;
+ * score = the weights of a bucket summed in head order; the selection is the
+ * buckets of positive score and nonzero size by score descending, bucket
+ * ascending: features i64 [G][64], valid f32 [G][64], raw i32 [G]; scores
+ * f32 [G][3000] (optional, 0 to skip).  Then prismkv_union_n / _select_cap_n
+ * with width 64. */
+size_t prismkv_route_qact_work_bytes(int groups);
+int prismkv_route_qact(uint64_t q, uint64_t W, uint64_t b, uint64_t qscale, uint64_t counts, uint64_t work,
+                       uint64_t features, uint64_t valid, uint64_t raw, uint64_t scores, int groups, uint64_t stream);
+
+/* prismkv_union / prismkv_select_cap over selections of `width` rows per
+ * group (features / valid [G][width]), width 16 or 64. */
+int prismkv_union_n(uint64_t bits, uint64_t features, uint64_t valid, uint64_t work, uint64_t ids, uint64_t count,
+                    int groups, int H, int64_t row_words, int64_t ids_stride, int width, uint64_t stream);
+int prismkv_select_cap_n(uint64_t bits, uint64_t counts, uint64_t features, uint64_t valid, uint64_t raw, int groups,
+                         int H, int64_t limit, int64_t row_words, int width, uint64_t stream);
+
 /* positive_global_topk (core.py:13-26) of a device matrix act f32 [N][3000]
  * (16-byte aligned, N <= 2^20) with budget `count`: out i64 [min(count,
  * 3000 N)] <- every value above the budget-th largest tau (and above 0) in

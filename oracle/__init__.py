@@ -64,6 +64,7 @@ def _declare(L):
         "orc_build_index": ([P, I64, I32, P, P, I32, I32, F32, P, P, P, P, P, P, P, P], I64),
         "orc_merge_moments": ([I32, I32, P, P, P, P, P, P, P, P, P], None),
         "orc_bucket_scores": ([P, I32, I32, P, P, P, I32, I32, I32, P, P, P, P], I32),
+        "orc_qact_scores": ([P, I32, I32, P, P, I32, F32, P, I32, P, P, P], I32),
         "orc_norm_top": ([P, P, P, I32, I32, I32, P, P, P, P, P], I32),
         "orc_pack": ([P, I32, I32, P], None),
         "orc_select_buckets": ([P, I32, P, P, I64, F64, P, P, P, P, P], I64),
@@ -248,6 +249,20 @@ def bucket_scores(q, counts, mean, var, topk=16, terms=("count", "mean", "varian
     k = lib().orc_bucket_scores(_ptr(q), Hq, d, _ptr(counts), _ptr(_c(mean, np.float32)), _ptr(_c(var, np.float32)),
                                 F, mask, topk, _ptr(score), _ptr(order), ctypes.byref(margin), ctypes.byref(ties))
     return score, order[:k].copy(), margin.value, ties.value
+
+
+def qact_scores(q, W, b, query_scale, counts, topk=16):
+    """src/prismkv/core.py:131-139 (router="q_activation") -> (score f32[F], order i64, margin)."""
+    q = _c(q, np.float32)
+    Hq, d = q.shape
+    W = _c(W, np.float32)
+    F = W.shape[0]
+    score = np.empty(F, np.float32)
+    order = np.empty(max(F, 1), np.int64)
+    margin = ctypes.c_double()
+    n = lib().orc_qact_scores(_ptr(q), Hq, d, _ptr(W), _ptr(_c(b, np.float32)), F, float(query_scale),
+                              _ptr(_c(counts, np.int64)), topk, _ptr(score), _ptr(order), ctypes.byref(margin))
+    return score, order[:n].copy(), margin.value
 
 
 def norm_top(prod, ln, ct, topk=16):

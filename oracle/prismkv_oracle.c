@@ -477,6 +477,77 @@ int orc_norm_top(const float *prod, const float *ln, const int32_t *ct, int Hq, 
     return k;
 }
 
+/*
+ * bucket_scores(router="q_activation") -- src/prismkv/core.py:131-139.
+ * a = relu((q / query_scale) W^T + b) per query row (x in fp32, the dot
+ * product accumulated in double and rounded to fp32, as orc_sae_dense);
+ * per row the `topk` largest activations (value descending, index ascending:
+ * the stable descending argsort); weights val / max(sum val, 1e-20) / Hq in
+ * fp32 with the sum taken in rank order (torch's own 16-element summation
+ * order is not fixed by the reference); score[f] = the weights of f added
+ * in the flattened [Hq][topk] order, from 0, in fp32; order = buckets with
+ * score > 0 and counts > 0, score descending, index ascending.  Writes
+ * score[F]; returns the order length.  *margin = the smallest relative gap
+ * that decides the result: between a row's topk-th and next activation
+ * (when positive) and between consecutive ordered scores.
+ */
+int orc_qact_scores(const float *q, int Hq, int d, const float *W, const float *b, int F, float query_scale,
+                    const int64_t *counts, int topk, float *score, int64_t *order, double *margin)
+{
+    float *x = (float *)malloc(sizeof(float) * Hq * d);
+    float *a = (float *)malloc(sizeof(float) * Hq * F);
+    scored_t *s = (scored_t *)malloc(sizeof(scored_t) * (F > 0 ? F : 1));
+    for (int i = 0; i < Hq * d; ++i)
+        x[i] = q[i] / query_scale;
+    orc_sae_dense(x, Hq, d, W, b, F, a);
+    double gap = INFINITY;
+    for (int f = 0; f < F; ++f)
+        score[f] = 0.0f;
+    int k = topk < F ? topk : F;
+    for (int h = 0; h < Hq; ++h) {
+        for (int f = 0; f < F; ++f) {
+            s[f].v = a[(int64_t)h * F + f];
+            s[f].id = f;
+        }
+        qsort(s, F, sizeof(scored_t), cmp_scored_desc);
+        if (k < F && s[k - 1].v > 0.0) {
+            double g = (s[k - 1].v - s[k].v) / fabs(s[k - 1].v);
+            if (g < gap)
+                gap = g;
+        }
+        float sum = 0.0f;
+        for (int r = 0; r < k; ++r)
+            sum += (float)s[r].v;
+        if (sum < 1e-20f)
+            sum = 1e-20f;
+        for (int r = 0; r < k; ++r) {
+            float c = ((float)s[r].v / sum) / (float)Hq;
+            score[s[r].id] += c;
+        }
+    }
+    int n = 0;
+    for (int f = 0; f < F; ++f)
+        if (score[f] > 0.0f && counts[f] > 0) {
+            s[n].v = score[f];
+            s[n].id = f;
+            ++n;
+        }
+    qsort(s, n, sizeof(scored_t), cmp_scored_desc);
+    for (int i = 0; i < n; ++i) {
+        order[i] = s[i].id;
+        if (i + 1 < n) {
+            double g = (s[i].v - s[i + 1].v) / fabs(s[i].v);
+            if (g < gap)
+                gap = g;
+        }
+    }
+    *margin = gap;
+    free(x);
+    free(a);
+    free(s);
+    return n;
+}
+
 /* pack -- kernels/ppu_8b/pack.cu:3: a[r] = [q_r, q_r * q_r] in fp32. */
 void orc_pack(const uint16_t *q, int rows, int d, float *a)
 {

@@ -42,6 +42,10 @@ SIGNATURES = {
     "prismkv_topk": ([_U64] * 4 + [_I32, _I64], True, _I32),
     "prismkv_summarize_work_bytes": ([_I32], False, _SZ),
     "prismkv_summarize": ([_U64] * 6 + [_I32, _I32, _I32, _I64, _I64], True, _I32),
+    "prismkv_route_qact_work_bytes": ([_I32], False, _SZ),
+    "prismkv_route_qact": ([_U64] * 10 + [_I32], True, _I32),
+    "prismkv_union_n": ([_U64] * 6 + [_I32, _I32, _I64, _I64, _I32], True, _I32),
+    "prismkv_select_cap_n": ([_U64] * 5 + [_I32, _I32, _I64, _I64, _I32], True, _I32),
 }
 
 _loaded: dict[str, "Library"] = {}

@@ -287,6 +287,27 @@ def _check_q(q):
     return q.contiguous().reshape(1, HEADS, DIM)
 
 
+QA_WIDTH = 64  # the q_activation selection: up to 4 heads x 16 buckets
+
+
+def _route_qact(q, index, sae, query_scale, scores):
+    t = _tables(index)
+    q1 = _check_q(q)
+    _check_sae(sae)
+    lib = _lib_()
+    device = q1.device
+    W, b = _encoder(sae, device)
+    qs = torch.tensor([float(query_scale)], dtype=torch.float32, device=device)
+    features = torch.zeros(1, QA_WIDTH, dtype=torch.int64, device=device)
+    valid = torch.zeros(1, QA_WIDTH, device=device)
+    raw = torch.zeros(1, dtype=torch.int32, device=device)
+    work = _work("route_qact", lib.query("prismkv_route_qact_work_bytes", 1), device)
+    lib.call("prismkv_route_qact", q1.data_ptr(), W.data_ptr(), b.data_ptr(), qs.data_ptr(), t.n.data_ptr(),
+             work.data_ptr(), features.data_ptr(), valid.data_ptr(), raw.data_ptr(), scores.data_ptr(), 1,
+             stream=_stream())
+    return t, features, valid, raw
+
+
 def _route(q, index, scores):
     t = _tables(index)
     q1 = _check_q(q)
@@ -301,23 +322,34 @@ def _route(q, index, scores):
     return t, features, valid, raw
 
 
-@torch.no_grad()
-def bucket_scores(q, index, *, router="moments", sae=None, query_scale=None, query_topk=16,
+def _check_router(router="moments", sae=None, query_scale=None, query_topk=16,
                   terms=("count", "mean", "variance")):
-    """src/prismkv/core.py:106-130 (router "moments") on the device: the
-    head-mean softmax scores of the 3000 buckets and the live buckets of the
-    top 16 (score descending, bucket ascending on ties)."""
+    """The argument checks of core.py:118-120,131-132, then the native limits."""
     if router == "moments":
         if not terms or set(terms) - {"count", "mean", "variance"}:
             raise ValueError("specify exact estimator components")
         _native(set(terms) == {"count", "mean", "variance"}, "the full count/mean/variance estimator")
-        _native(query_topk == TOPK, "16 selected buckets")
-        scores = torch.zeros(1, FEATURES, device=q.device)
-        _, features, valid, _ = _route(q, index, scores)
-        return scores[0], features[0][valid[0] > 0]
-    if router != "q_activation" or sae is None or query_scale is None or query_scale <= 0:
+    elif router != "q_activation" or sae is None or query_scale is None or query_scale <= 0:
         raise ValueError("q_activation requires SAE and saved positive query scale")
-    raise NotImplementedError("the MI355X path routes by moments (router='moments')")
+    _native(query_topk == TOPK, "16 buckets per query (router q_activation) or in all (router moments)")
+    return router
+
+
+@torch.no_grad()
+def bucket_scores(q, index, *, router="moments", sae=None, query_scale=None, query_topk=16,
+                  terms=("count", "mean", "variance")):
+    """src/prismkv/core.py:106-139 on the device.  "moments": the head-mean
+    softmax scores of the 3000 buckets and the live buckets of the top 16
+    (score descending, bucket ascending on ties).  "q_activation": the
+    scores of the 4 queries' top-16 SAE activations, normalised per query,
+    and every live bucket of positive score (up to 64), same order."""
+    _check_router(router, sae, query_scale, query_topk, terms)
+    scores = torch.zeros(1, FEATURES, device=q.device)
+    if router == "moments":
+        _, features, valid, _ = _route(q, index, scores)
+    else:
+        _, features, valid, _ = _route_qact(q, index, sae, query_scale, scores)
+    return scores[0], features[0][valid[0] > 0]
 
 
 @torch.no_grad()
@@ -325,37 +357,35 @@ def select_buckets(q, index, *, unique_cap=None, **kwargs):
     """src/prismkv/core.py:142-167 on the device: the union of the selected
     buckets' lists (ascending int64 ids) and meta (features, raw, unique,
     limit, candidate_buckets, scores); with a cap, a ranked bucket whose new
-    ids would overflow floor(history * unique_cap) is skipped."""
+    ids would overflow floor(history * unique_cap) is skipped.  Both routers
+    of bucket_scores."""
     if unique_cap is not None and not 0 <= unique_cap <= 1:
         raise ValueError("unique_cap must be a fraction in [0,1]")
-    router = kwargs.get("router", "moments")
-    if router != "moments":
-        bucket_scores(q, index, **kwargs)  # the reference's argument checks, then NotImplementedError
-    _native(kwargs.get("query_topk", TOPK) == TOPK, "16 selected buckets")
-    terms = kwargs.get("terms", ("count", "mean", "variance"))
-    if not terms or set(terms) - {"count", "mean", "variance"}:
-        raise ValueError("specify exact estimator components")
-    _native(set(terms) == {"count", "mean", "variance"}, "the full count/mean/variance estimator")
+    router = _check_router(**kwargs)
     H = index.history
     scores = torch.zeros(1, FEATURES, device=q.device)
-    t, features, valid, raw = _route(q, index, scores)
+    if router == "q_activation":
+        t, features, valid, raw = _route_qact(q, index, kwargs["sae"], kwargs["query_scale"], scores)
+        width = QA_WIDTH
+    else:
+        t, features, valid, raw = _route(q, index, scores)
+        width = TOPK
     candidates = int((valid[0] > 0).sum())
     limit = H if unique_cap is None else math.floor(H * unique_cap)
     lib = _lib_()
     if unique_cap is not None:
-        lib.call("prismkv_select_cap", t.bits.data_ptr(), t.n.data_ptr(), features.data_ptr(), valid.data_ptr(),
-                 raw.data_ptr(), 1, H, limit, t.row_words, stream=_stream())
+        lib.call("prismkv_select_cap_n", t.bits.data_ptr(), t.n.data_ptr(), features.data_ptr(), valid.data_ptr(),
+                 raw.data_ptr(), 1, H, limit, t.row_words, width, stream=_stream())
     ids = torch.zeros(1, max(H, 1), dtype=torch.int32, device=q.device)
     count = torch.zeros(1, dtype=torch.int32, device=q.device)
     work = _work("union", lib.query("prismkv_union_work_bytes", 1, H), q.device)
-    lib.call("prismkv_union", t.bits.data_ptr(), features.data_ptr(), valid.data_ptr(), work.data_ptr(),
-             ids.data_ptr(), count.data_ptr(), 1, H, t.row_words, ids.shape[1], stream=_stream())
+    lib.call("prismkv_union_n", t.bits.data_ptr(), features.data_ptr(), valid.data_ptr(), work.data_ptr(),
+             ids.data_ptr(), count.data_ptr(), 1, H, t.row_words, ids.shape[1], width, stream=_stream())
     n = int(count.item())
     kept = features[0][valid[0] > 0].tolist()
-    out = ids[0, :n].long()
     assert n <= limit
-    return out, dict(features=kept, raw=int(raw.item()), unique=n, limit=limit, candidate_buckets=candidates,
-                     scores=scores[0])
+    return ids[0, :n].long(), dict(features=kept, raw=int(raw.item()), unique=n, limit=limit,
+                                   candidate_buckets=candidates, scores=scores[0])
 
 
 @torch.no_grad()

@@ -145,6 +145,124 @@ __global__ __launch_bounds__(64) void route_final_kernel(const unsigned long lon
 }
 
 // ---------------------------------------------------------------------------
+// Route by query activations (router "q_activation", core.py:131-139):
+//   a = relu((q / query_scale) W^T + b), the SAE encode of the 4 queries;
+//   per head the 16 largest activations (value descending, bucket ascending:
+//   the stable descending argsort), weights val / max(sum val, 1e-20) / 4
+//   with the sum taken in rank order; score[bucket] = the weights of the
+//   bucket summed in head order (scatter_add over the flattened [4][16]
+//   lists); the order = buckets of positive score and nonzero size, by score
+//   descending and bucket ascending -- up to 64.
+// qact_part_kernel: grid (12, G) x 256: workgroup j encodes buckets
+//   [256 j, 256 j + 256) for the 4 heads (thread = bucket, fp32 dot products
+//   in dim order) and keeps each head's 16 best keys;
+// qact_final_kernel: grid G x 256: wave h ranks head h's 12 x 16 candidates;
+//   wave 0 forms the weights and scores, keeps the first entry of each bucket,
+//   sorts and writes the selection (features / valid [G][64], raw) and the
+//   score vector.
+// ---------------------------------------------------------------------------
+constexpr int kQaParts = (kF + kRT - 1) / kRT;  // 12
+constexpr int kQaSel = kHq * kTop;               // 64
+
+__global__ __launch_bounds__(kRT) void qact_part_kernel(const uint16_t* __restrict__ q, const float* __restrict__ W,
+                                                        const float* __restrict__ b, const float* __restrict__ qscale,
+                                                        unsigned long long* __restrict__ cand) {
+  const int j = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  __shared__ float xs[kHq][kD];
+  __shared__ __align__(16) unsigned long long keys[kHq][kRT];
+  const float qs = qscale[g];
+  for (int i = tid; i < kHq * kD; i += kRT) xs[i / kD][i % kD] = bf16_to_f32(q[(size_t)g * kHq * kD + i]) / qs;
+  __syncthreads();
+  const int f = j * kRT + tid;
+  float acc[kHq] = {0.f, 0.f, 0.f, 0.f};
+  if (f < kF) {
+    const float4* wr = reinterpret_cast<const float4*>(W + ((size_t)g * kF + f) * kD);
+#pragma unroll 8
+    for (int d4 = 0; d4 < kD / 4; ++d4) {
+      const float4 wv = wr[d4];
+#pragma unroll
+      for (int h = 0; h < kHq; ++h) {
+        acc[h] = fmaf(xs[h][4 * d4], wv.x, acc[h]);
+        acc[h] = fmaf(xs[h][4 * d4 + 1], wv.y, acc[h]);
+        acc[h] = fmaf(xs[h][4 * d4 + 2], wv.z, acc[h]);
+        acc[h] = fmaf(xs[h][4 * d4 + 3], wv.w, acc[h]);
+      }
+    }
+  }
+  const float bias = f < kF ? b[(size_t)g * kF + f] : 0.f;
+#pragma unroll
+  for (int h = 0; h < kHq; ++h) {
+    const float x = acc[h] + bias;
+    keys[h][tid] = f < kF ? make_key(x > 0.f ? x : 0.f, f) : 0ull;  // relu; slots past F stay empty
+  }
+  __syncthreads();
+  if (w < kHq) {
+    unsigned long long v[kRT / 64];
+#pragma unroll
+    for (int k = 0; k < kRT / 64; ++k) v[k] = keys[w][64 * k + lane];
+    const unsigned long long best = bitonic_top16<kRT / 64>(v);
+    if (lane < kTop) cand[(((size_t)g * kHq + w) * kQaParts + j) * kTop + lane] = best;
+  }
+}
+
+__global__ __launch_bounds__(kRT) void qact_final_kernel(const unsigned long long* __restrict__ cand,
+                                                         const int* __restrict__ counts, int64_t* __restrict__ features,
+                                                         float* __restrict__ valid, int* __restrict__ raw,
+                                                         float* __restrict__ scores) {
+  const int g = blockIdx.x, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  __shared__ __align__(16) unsigned long long top[kHq][kTop];
+  __shared__ float sc_lds[kFP];
+  __shared__ int ent_b[kQaSel];
+  __shared__ float ent_c[kQaSel];
+  for (int i = tid; i < kFP; i += kRT) sc_lds[i] = 0.f;
+  static_assert(kQaParts * kTop == 3 * 64, "three 64-key sets per head");
+  if (w < kHq) {
+    unsigned long long v[3];
+#pragma unroll
+    for (int k = 0; k < 3; ++k) v[k] = cand[((size_t)g * kHq + w) * kQaParts * kTop + 64 * k + lane];
+    const unsigned long long best = sorted_rows_top16<3>(v);  // each 16-lane row is one part's ranked list
+    if (lane < kTop) top[w][lane] = best;
+  }
+  __syncthreads();
+  if (w == 0) {
+    // entry e = 16 h + r: head h's rank-r activation (the flattened order of core.py:136-137)
+    const int h = lane >> 4, r = lane & 15;
+    const unsigned long long key = top[h][r];  // never 0: every part holds at least 16 real buckets
+    const float val = __uint_as_float((unsigned)(key >> 12));
+    const int bucket = key ? key_bucket(key) : 0;
+    float s = 0.f;
+#pragma unroll
+    for (int rr = 0; rr < kTop; ++rr) s += __uint_as_float((unsigned)(top[h][rr] >> 12));
+    s = fmaxf(s, 1e-20f);
+    const float c = (val / s) / (float)kHq;
+    ent_b[lane] = bucket;
+    ent_c[lane] = c;
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_s_waitcnt(0);
+    // the bucket's score: its entries' weights added in entry order, from 0
+    float sc = 0.f;
+    bool first = true;
+    for (int e = 0; e < kQaSel; ++e)
+      if (ent_b[e] == bucket) {
+        sc += ent_c[e];
+        first = first && e >= lane;
+      }
+    if (first) sc_lds[bucket] = sc;
+    const bool keep = first && sc > 0.f && counts[(size_t)g * kFP + bucket] > 0;
+    const unsigned long long k2 = wave_sort_desc(keep ? make_key(sc, bucket) : 0ull);
+    const int n = __popcll(__ballot(k2 != 0));
+    const int fb = k2 ? key_bucket(k2) : 0;
+    features[(size_t)g * kQaSel + lane] = lane < n ? fb : 0;
+    valid[(size_t)g * kQaSel + lane] = lane < n ? 1.f : 0.f;
+    const int rs = wave_sum_i(lane < n ? counts[(size_t)g * kFP + fb] : 0);
+    if (lane == 0) raw[g] = rs;
+  }
+  __syncthreads();
+  if (scores)
+    for (int i = tid; i < kF; i += kRT) scores[(size_t)g * kF + i] = sc_lds[i];
+}
+
+// ---------------------------------------------------------------------------
 // Compat: fused_norm_top (kernels/ppu_8b/route_parallel.cu:13-35).
 // prod f32 [8][4][3000], ln f32 [8][3000], ct i32 [8][3000] -> ids i64 [8][16],
 // vals f32 [8][16], raw i32 [8].  One workgroup per group.
@@ -275,6 +393,26 @@ int prismkv_route_scores(uint64_t q, uint64_t moments, uint64_t counts, uint64_t
   if (!scores) return kBadSize;
   return route_impl(q, moments, counts, work, features, valid, raw, reinterpret_cast<float*>(scores), groups,
                     stream);
+}
+
+size_t prismkv_route_qact_work_bytes(int groups) {
+  if (groups < 1 || groups > 65535) return 0;
+  return (size_t)groups * kHq * kQaParts * kTop * sizeof(unsigned long long);
+}
+
+int prismkv_route_qact(uint64_t q, uint64_t W, uint64_t b, uint64_t qscale, uint64_t counts, uint64_t work,
+                       uint64_t features, uint64_t valid, uint64_t raw, uint64_t scores, int groups, uint64_t stream) {
+  if (groups < 1 || groups > 65535) return kBadSize;
+  if (!q || !W || !b || !qscale || !counts || !work || !features || !valid || !raw || (W & 15u)) return kBadSize;
+  hipStream_t s = (hipStream_t)stream;
+  unsigned long long* cand = reinterpret_cast<unsigned long long*>(work);
+  hipLaunchKernelGGL(qact_part_kernel, dim3(kQaParts, groups), dim3(kRT), 0, s, reinterpret_cast<const uint16_t*>(q),
+                     reinterpret_cast<const float*>(W), reinterpret_cast<const float*>(b),
+                     reinterpret_cast<const float*>(qscale), cand);
+  hipLaunchKernelGGL(qact_final_kernel, dim3(groups), dim3(kRT), 0, s, cand, reinterpret_cast<const int*>(counts),
+                     reinterpret_cast<int64_t*>(features), reinterpret_cast<float*>(valid),
+                     reinterpret_cast<int*>(raw), reinterpret_cast<float*>(scores));
+  return (int)hipGetLastError();
 }
 
 int pack(uint64_t q, uint64_t a, uint64_t stream) {

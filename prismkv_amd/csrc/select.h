@@ -173,6 +173,39 @@ __device__ __forceinline__ unsigned long long bitonic_top16(unsigned long long (
   return sorted_rows_top16<K>(v);
 }
 
+// Full descending sort of one wave's 64 keys (lane r ends with rank r):
+// the bitonic network over the lane index, exchanges with lane ^ j through
+// DPP (j < 16) or a lane permute (j = 16, 32).
+template <int J>
+__device__ __forceinline__ unsigned long long xor_any_u64(unsigned long long v) {
+  if constexpr (J >= 16) return xor_rows_u64<J>(v);
+  else return xor_lane_u64<J>(v);
+}
+template <int K, int J>
+__device__ __forceinline__ unsigned long long sort_step(unsigned long long v) {
+  const int lane = threadIdx.x & 63;
+  const bool keep_max = ((lane & K) == 0) == ((lane & J) == 0);  // descending blocks of K
+  const unsigned long long o = xor_any_u64<J>(v);
+  return ((v > o) == keep_max) ? v : o;
+}
+template <int K>
+__device__ __forceinline__ unsigned long long sort_merge(unsigned long long v) {
+  if constexpr (K >= 64) v = sort_step<K, 32>(v);
+  if constexpr (K >= 32) v = sort_step<K, 16>(v);
+  if constexpr (K >= 16) v = sort_step<K, 8>(v);
+  if constexpr (K >= 8) v = sort_step<K, 4>(v);
+  if constexpr (K >= 4) v = sort_step<K, 2>(v);
+  return sort_step<K, 1>(v);
+}
+__device__ __forceinline__ unsigned long long wave_sort_desc(unsigned long long v) {
+  v = sort_merge<2>(v);
+  v = sort_merge<4>(v);
+  v = sort_merge<8>(v);
+  v = sort_merge<16>(v);
+  v = sort_merge<32>(v);
+  return sort_merge<64>(v);
+}
+
 // Writes the winners (sel, rank order) from one wave: features[r] = bucket,
 // valid[r] = 1 for r < need; remaining slots id 0 / valid 0
 // (route_parallel.cu:23,29); raw = sum of winner counts.

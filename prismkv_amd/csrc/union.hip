@@ -98,14 +98,15 @@ __device__ unsigned look_back(unsigned* st, int t, unsigned total, unsigned* err
   return prefix;
 }
 
-template <int WPT>
+template <int WPT, int kSel>
 __global__ __launch_bounds__(kUT) void union_kernel(const uint32_t* __restrict__ bits, int64_t row_words,
                                                     const int64_t* __restrict__ features,
                                                     const float* __restrict__ valid, int32_t* __restrict__ ids,
                                                     int64_t ids_stride, int32_t* __restrict__ count, UnionWork work,
                                                     int H, int tiles) {
+  static_assert(kSel % kTop == 0 && kSel <= 64, "selections of up to 64 rows, 16 at a time");
   const int t = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
-  __shared__ int rows[kTop];
+  __shared__ int rows[kSel];
   __shared__ int nrows;
   __shared__ unsigned wsum[kUT / 64];
   __shared__ unsigned base;
@@ -114,8 +115,8 @@ __global__ __launch_bounds__(kUT) void union_kernel(const uint32_t* __restrict__
     // wave 0 compacts the valid, in-range selections (an out-of-range id selects nothing)
     bool ok = false;
     int f = 0;
-    if (tid < kTop && valid[(size_t)g * kTop + tid] > 0.f) {
-      const int64_t fe = features[(size_t)g * kTop + tid];
+    if (tid < kSel && valid[(size_t)g * kSel + tid] > 0.f) {
+      const int64_t fe = features[(size_t)g * kSel + tid];
       ok = fe >= 0 && fe < kF;
       f = (int)fe;
     }
@@ -133,13 +134,18 @@ __global__ __launch_bounds__(kUT) void union_kernel(const uint32_t* __restrict__
   const uint32_t* gb = bits + (size_t)g * kF * row_words;
   if (nr > 0) {
     if (w0 + WPT <= nw) {
-      uint32_t v[kTop][WPT];
+      // 16 rows at a time, all loads of a round issued together (rows past nr
+      // repeat the last selected one: OR is idempotent)
+      for (int r0 = 0; r0 < nr; r0 += kTop) {  // uniform
+        uint32_t v[kTop][WPT];
 #pragma unroll
-      for (int r = 0; r < kTop; ++r) Words<WPT>::load(gb + (size_t)rows[r < nr ? r : nr - 1] * row_words + w0, v[r]);
+        for (int r = 0; r < kTop; ++r)
+          Words<WPT>::load(gb + (size_t)rows[r0 + r < nr ? r0 + r : nr - 1] * row_words + w0, v[r]);
 #pragma unroll
-      for (int r = 0; r < kTop; ++r)
+        for (int r = 0; r < kTop; ++r)
 #pragma unroll
-        for (int i = 0; i < WPT; ++i) m[i] |= v[r][i];
+          for (int i = 0; i < WPT; ++i) m[i] |= v[r][i];
+      }
     } else {
       for (int r = 0; r < nr; ++r) {
         const uint32_t* src = gb + (size_t)rows[r] * row_words;
@@ -263,18 +269,18 @@ __global__ __launch_bounds__(256) void bits_kernel(const int* __restrict__ ids, 
 // union in registers; each bucket costs one block-wide popcount reduction.
 // With kAhead the next bucket's words are requested before the current
 // bucket's reduction, so the row loads overlap the decisions.
-template <int kCapT, int WPT, bool kAhead>
+template <int kCapT, int WPT, bool kAhead, int kSel>
 __global__ __launch_bounds__(kCapT) void cap_kernel(const uint32_t* __restrict__ bits, int64_t row_words,
                                                     const int* __restrict__ counts, int64_t* features, float* valid,
                                                     int* raw, int H, long long limit) {
   const int g = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  __shared__ int sel[kTop], nsel_s;
+  __shared__ int sel[kSel], nsel_s;
   __shared__ int part[2][kCapT / 64];
   if (tid == 0) {
     int n = 0;
-    for (int j = 0; j < kTop; ++j) {
-      const int64_t f = features[(size_t)g * kTop + j];
-      if (valid[(size_t)g * kTop + j] > 0.f && f >= 0 && f < kF) sel[n++] = (int)f;
+    for (int j = 0; j < kSel; ++j) {
+      const int64_t f = features[(size_t)g * kSel + j];
+      if (valid[(size_t)g * kSel + j] > 0.f && f >= 0 && f < kF) sel[n++] = (int)f;
     }
     nsel_s = n;
   }
@@ -298,7 +304,7 @@ __global__ __launch_bounds__(kCapT) void cap_kernel(const uint32_t* __restrict__
   if (kAhead && n > 0) load_row(0, cur);
   long long total = 0;
   int raw_sum = 0;
-  unsigned accepted = 0;
+  unsigned long long accepted = 0;
   for (int j = 0; j < n; ++j) {
     if (kAhead) {
       if (j + 1 < n) load_row(j + 1, nxt);
@@ -320,7 +326,7 @@ __global__ __launch_bounds__(kCapT) void cap_kernel(const uint32_t* __restrict__
       for (int u = 0; u < WPT; ++u) chosen[u] |= cur[u];
       total += add;
       raw_sum += counts[(size_t)g * kFP + sel[j]];
-      accepted |= 1u << j;
+      accepted |= 1ull << j;
     }
     if (kAhead) {
 #pragma unroll
@@ -330,10 +336,10 @@ __global__ __launch_bounds__(kCapT) void cap_kernel(const uint32_t* __restrict__
   if (tid == 0) {
     int at = 0;
     for (int j = 0; j < n; ++j)
-      if (accepted >> j & 1u) features[(size_t)g * kTop + at++] = sel[j];
-    for (int j = 0; j < kTop; ++j) {
-      if (j >= at) features[(size_t)g * kTop + j] = 0;
-      valid[(size_t)g * kTop + j] = j < at ? 1.f : 0.f;
+      if (accepted >> j & 1ull) features[(size_t)g * kSel + at++] = sel[j];
+    for (int j = 0; j < kSel; ++j) {
+      if (j >= at) features[(size_t)g * kSel + j] = 0;
+      valid[(size_t)g * kSel + j] = j < at ? 1.f : 0.f;
     }
     raw[g] = raw_sum;
   }
@@ -345,20 +351,21 @@ __global__ __launch_bounds__(kCapT) void cap_kernel(const uint32_t* __restrict__
 constexpr int kCapBigT = 1024;
 constexpr int kCapMaxWords = 32768;
 
+template <int kSel>
 __global__ __launch_bounds__(kCapBigT) void cap_big_kernel(const uint32_t* __restrict__ bits, int64_t row_words,
                                                            const int* __restrict__ counts, int64_t* features,
                                                            float* valid, int* raw, int H, long long limit) {
   const int g = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  __shared__ int sel[kTop], nsel_s;
+  __shared__ int sel[kSel], nsel_s;
   __shared__ int part[2][kCapBigT / 64];
   __shared__ uint32_t chosen[kCapMaxWords];
   const int nw = (H + 31) >> 5;
   for (int i = tid; i < nw; i += kCapBigT) chosen[i] = 0u;
   if (tid == 0) {
     int n = 0;
-    for (int j = 0; j < kTop; ++j) {
-      const int64_t f = features[(size_t)g * kTop + j];
-      if (valid[(size_t)g * kTop + j] > 0.f && f >= 0 && f < kF) sel[n++] = (int)f;
+    for (int j = 0; j < kSel; ++j) {
+      const int64_t f = features[(size_t)g * kSel + j];
+      if (valid[(size_t)g * kSel + j] > 0.f && f >= 0 && f < kF) sel[n++] = (int)f;
     }
     nsel_s = n;
   }
@@ -368,7 +375,7 @@ __global__ __launch_bounds__(kCapBigT) void cap_big_kernel(const uint32_t* __res
   const uint32_t* bg = bits + (size_t)g * kF * row_words;
   long long total = 0;
   int raw_sum = 0;
-  unsigned accepted = 0;
+  unsigned long long accepted = 0;
   for (int j = 0; j < n; ++j) {
     const uint32_t* row = bg + (size_t)sel[j] * row_words;
     int c = 0;
@@ -387,16 +394,16 @@ __global__ __launch_bounds__(kCapBigT) void cap_big_kernel(const uint32_t* __res
       for (int i = tid; i < nw; i += kCapBigT) chosen[i] |= i == nw - 1 ? (row[i] & tail_mask) : row[i];
       total += add;
       raw_sum += counts[(size_t)g * kFP + sel[j]];
-      accepted |= 1u << j;
+      accepted |= 1ull << j;
     }
   }
   if (tid == 0) {
     int at = 0;
     for (int j = 0; j < n; ++j)
-      if (accepted >> j & 1u) features[(size_t)g * kTop + at++] = sel[j];
-    for (int j = 0; j < kTop; ++j) {
-      if (j >= at) features[(size_t)g * kTop + j] = 0;
-      valid[(size_t)g * kTop + j] = j < at ? 1.f : 0.f;
+      if (accepted >> j & 1ull) features[(size_t)g * kSel + at++] = sel[j];
+    for (int j = 0; j < kSel; ++j) {
+      if (j >= at) features[(size_t)g * kSel + j] = 0;
+      valid[(size_t)g * kSel + j] = j < at ? 1.f : 0.f;
     }
     raw[g] = raw_sum;
   }
@@ -418,26 +425,48 @@ static int union_wpt(int H, int64_t row_words) {
 
 extern "C" {
 
-int prismkv_select_cap(uint64_t bits, uint64_t counts, uint64_t features, uint64_t valid, uint64_t raw, int groups,
-                       int H, int64_t limit, int64_t row_words, uint64_t stream) {
-  if (groups < 1 || groups > 65535 || H < 1 || H > (1 << 20) || limit < 0) return kBadSize;
-  if (row_words < (H + 31) / 32) return kBadSize;
-  if (!bits || !counts || !features || !valid || !raw) return kBadSize;
+}  // extern "C"
+
+template <int kSel>
+static void launch_cap(const uint32_t* b, int64_t row_words, const int* c, int64_t* f, float* v, int* r, int groups,
+                       int H, long long lim, hipStream_t s) {
   const int nw = (H + 31) / 32;
+  if (nw <= 2 * 1024)
+    hipLaunchKernelGGL((cap_kernel<1024, 2, true, kSel>), dim3(groups), dim3(1024), 0, s, b, row_words, c, f, v, r, H,
+                       lim);
+  else if (nw <= 8 * 1024)
+    hipLaunchKernelGGL((cap_kernel<1024, 8, true, kSel>), dim3(groups), dim3(1024), 0, s, b, row_words, c, f, v, r, H,
+                       lim);
+  else  // up to 2^20 tokens
+    hipLaunchKernelGGL(cap_big_kernel<kSel>, dim3(groups), dim3(kCapBigT), 0, s, b, row_words, c, f, v, r, H, lim);
+}
+
+static int select_cap(uint64_t bits, uint64_t counts, uint64_t features, uint64_t valid, uint64_t raw, int groups,
+                      int H, int64_t limit, int64_t row_words, int width, uint64_t stream) {
+  if (groups < 1 || groups > 65535 || H < 1 || H > (1 << 20) || limit < 0) return kBadSize;
+  if (row_words < (H + 31) / 32 || (width != kTop && width != 64)) return kBadSize;
+  if (!bits || !counts || !features || !valid || !raw) return kBadSize;
   const uint32_t* b = reinterpret_cast<const uint32_t*>(bits);
   const int* c = reinterpret_cast<const int*>(counts);
   int64_t* f = reinterpret_cast<int64_t*>(features);
   float* v = reinterpret_cast<float*>(valid);
   int* r = reinterpret_cast<int*>(raw);
   hipStream_t s = (hipStream_t)stream;
-  const long long lim = (long long)limit;
-  if (nw <= 2 * 1024)
-    hipLaunchKernelGGL((cap_kernel<1024, 2, true>), dim3(groups), dim3(1024), 0, s, b, row_words, c, f, v, r, H, lim);
-  else if (nw <= 8 * 1024)
-    hipLaunchKernelGGL((cap_kernel<1024, 8, true>), dim3(groups), dim3(1024), 0, s, b, row_words, c, f, v, r, H, lim);
-  else  // up to 2^20 tokens
-    hipLaunchKernelGGL(cap_big_kernel, dim3(groups), dim3(kCapBigT), 0, s, b, row_words, c, f, v, r, H, lim);
+  if (width == kTop) launch_cap<kTop>(b, row_words, c, f, v, r, groups, H, (long long)limit, s);
+  else launch_cap<64>(b, row_words, c, f, v, r, groups, H, (long long)limit, s);
   return (int)hipGetLastError();
+}
+
+extern "C" {
+
+int prismkv_select_cap(uint64_t bits, uint64_t counts, uint64_t features, uint64_t valid, uint64_t raw, int groups,
+                       int H, int64_t limit, int64_t row_words, uint64_t stream) {
+  return select_cap(bits, counts, features, valid, raw, groups, H, limit, row_words, kTop, stream);
+}
+
+int prismkv_select_cap_n(uint64_t bits, uint64_t counts, uint64_t features, uint64_t valid, uint64_t raw, int groups,
+                         int H, int64_t limit, int64_t row_words, int width, uint64_t stream) {
+  return select_cap(bits, counts, features, valid, raw, groups, H, limit, row_words, width, stream);
 }
 
 size_t prismkv_union_work_bytes(int groups, int H) {
@@ -446,30 +475,53 @@ size_t prismkv_union_work_bytes(int groups, int H) {
   return ((size_t)groups * tiles + groups + 1) * sizeof(unsigned);
 }
 
-int prismkv_union(uint64_t bits, uint64_t features, uint64_t valid, uint64_t work, uint64_t ids, uint64_t count,
-                  int groups, int H, int64_t row_words, int64_t ids_stride, uint64_t stream) {
+}  // extern "C"
+
+template <int kSel>
+static void launch_union(const uint32_t* b, int64_t row_words, const int64_t* f, const float* v, int32_t* o,
+                         int64_t ids_stride, int32_t* c, UnionWork uw, int H, int wpt, dim3 grid, hipStream_t s) {
+  const int tiles = (int)grid.x;
+  const dim3 block(kUT);
+  if (wpt == 4)
+    hipLaunchKernelGGL((union_kernel<4, kSel>), grid, block, 0, s, b, row_words, f, v, o, ids_stride, c, uw, H, tiles);
+  else if (wpt == 2)
+    hipLaunchKernelGGL((union_kernel<2, kSel>), grid, block, 0, s, b, row_words, f, v, o, ids_stride, c, uw, H, tiles);
+  else
+    hipLaunchKernelGGL((union_kernel<1, kSel>), grid, block, 0, s, b, row_words, f, v, o, ids_stride, c, uw, H, tiles);
+}
+
+static int union_impl(uint64_t bits, uint64_t features, uint64_t valid, uint64_t work, uint64_t ids, uint64_t count,
+                      int groups, int H, int64_t row_words, int64_t ids_stride, int width, uint64_t stream) {
   if (groups < 1 || groups > 65535 || H < 1 || H > (1 << 29)) return kBadSize;
-  if (row_words < (H + 31) / 32 || ids_stride < H) return kBadSize;
+  if (row_words < (H + 31) / 32 || ids_stride < H || (width != kTop && width != 64)) return kBadSize;
   if (!bits || !features || !valid || !work || !ids || !count) return kBadSize;
   const int wpt = union_wpt(H, row_words);
   const int tiles = union_tiles(H, wpt);
   // fixed layout for any H: err word, done[groups], then status[groups][tiles]
   unsigned* w = reinterpret_cast<unsigned*>(work);
   UnionWork uw{w + 1 + groups, w + 1, w};
-  const dim3 grid(tiles, groups), block(kUT);
+  const dim3 grid(tiles, groups);
   const uint32_t* b = reinterpret_cast<const uint32_t*>(bits);
   const int64_t* f = reinterpret_cast<const int64_t*>(features);
   const float* v = reinterpret_cast<const float*>(valid);
   int32_t* o = reinterpret_cast<int32_t*>(ids);
   int32_t* c = reinterpret_cast<int32_t*>(count);
   hipStream_t s = (hipStream_t)stream;
-  if (wpt == 4)
-    hipLaunchKernelGGL(union_kernel<4>, grid, block, 0, s, b, row_words, f, v, o, ids_stride, c, uw, H, tiles);
-  else if (wpt == 2)
-    hipLaunchKernelGGL(union_kernel<2>, grid, block, 0, s, b, row_words, f, v, o, ids_stride, c, uw, H, tiles);
-  else
-    hipLaunchKernelGGL(union_kernel<1>, grid, block, 0, s, b, row_words, f, v, o, ids_stride, c, uw, H, tiles);
+  if (width == kTop) launch_union<kTop>(b, row_words, f, v, o, ids_stride, c, uw, H, wpt, grid, s);
+  else launch_union<64>(b, row_words, f, v, o, ids_stride, c, uw, H, wpt, grid, s);
   return (int)hipGetLastError();
+}
+
+extern "C" {
+
+int prismkv_union(uint64_t bits, uint64_t features, uint64_t valid, uint64_t work, uint64_t ids, uint64_t count,
+                  int groups, int H, int64_t row_words, int64_t ids_stride, uint64_t stream) {
+  return union_impl(bits, features, valid, work, ids, count, groups, H, row_words, ids_stride, kTop, stream);
+}
+
+int prismkv_union_n(uint64_t bits, uint64_t features, uint64_t valid, uint64_t work, uint64_t ids, uint64_t count,
+                    int groups, int H, int64_t row_words, int64_t ids_stride, int width, uint64_t stream) {
+  return union_impl(bits, features, valid, work, ids, count, groups, H, row_words, ids_stride, width, stream);
 }
 
 int prismkv_build_bits(uint64_t ids, uint64_t offsets, uint64_t bits, int groups, int64_t cap, int64_t row_words,

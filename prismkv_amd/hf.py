@@ -13,7 +13,8 @@ densely, exactly as in the reference.
 
 Native specialisation (rejected with NotImplementedError otherwise): Qwen3
 attention with 8 KV heads x 4 query heads, head_dim 128, bf16 activations,
-router "moments" with 16 selected buckets.  `unique_cap` maps to
+16 selected buckets (per query for router "q_activation", which routes,
+unions up to 64 buckets and attends in three launches per layer).  `unique_cap` maps to
 `Native8B.unique_cap`; mode "all_read" (the dense control) runs the model's
 own attention over the whole cache.
 
@@ -60,8 +61,8 @@ class HFNative:
             raise ValueError("unique cap must be a fraction")
         if update_interval <= 0:
             raise ValueError("positive update interval required")
-        if mode == "sparse" and (router != "moments" or selected_buckets != 16):
-            raise NotImplementedError("the native path routes by moments with 16 selected buckets")
+        if mode == "sparse" and selected_buckets != 16:
+            raise NotImplementedError("the native path selects 16 buckets (per query for q_activation)")
         if not 1 <= update_interval <= MAX_BLOCK:
             raise NotImplementedError(f"the native update indexes blocks of at most {MAX_BLOCK} keys")
         self.model, self.encoders = model, encoders
@@ -164,6 +165,9 @@ class HFNative:
             W, b, scale, key_mean = self._tables[layer]
             op = Native8B.from_keys(K, h, W, b, scale, key_mean, self.library,
                                     capacity=self._capacity(total), unique_cap=self.unique_cap)
+            if self.router == "q_activation":  # the same SAEs encode the queries (hf_reference.py:213-215)
+                op.set_query_encoders(W, b, [float(self.encoders[(layer, g)].query_scale) for g in range(GROUPS)])
+                op.router = "q_activation"
             self.ops[layer] = op
         if total > op.capacity:
             op.grow(self._capacity(total))

@@ -265,6 +265,7 @@ class Native8B:
             GROUPS, DIM).contiguous()
         # encoder tables and block workspace of `append`, set by set_encoders
         self.W_enc = self.b_enc = self.key_scale = self.update_work = None
+        self.W_query = self.b_query = self.query_scale = self.qact_work = None
         self.key_mean = 0
         self.update_block = 0
 
@@ -288,17 +289,59 @@ class Native8B:
         if q.device != self.out.device:
             raise ValueError("Q must live on the index device")
         s = self._stream()
-        self.lib.call("prismkv_route", q.data_ptr(), self.moments.data_ptr(), self.n.data_ptr(),
-                      self.route_work.data_ptr(), self.features.data_ptr(), self.valid.data_ptr(),
-                      self.raw.data_ptr(), GROUPS, stream=s)
+        if self.router == "q_activation":
+            self.lib.call("prismkv_route_qact", q.data_ptr(), self.W_query.data_ptr(), self.b_query.data_ptr(),
+                          self.query_scale.data_ptr(), self.n.data_ptr(), self.qact_work.data_ptr(),
+                          self.features.data_ptr(), self.valid.data_ptr(), self.raw.data_ptr(), 0, GROUPS, stream=s)
+        else:
+            self.lib.call("prismkv_route", q.data_ptr(), self.moments.data_ptr(), self.n.data_ptr(),
+                          self.route_work.data_ptr(), self.features.data_ptr(), self.valid.data_ptr(),
+                          self.raw.data_ptr(), GROUPS, stream=s)
+        width = self.features.shape[1]
         if self.unique_cap is not None:
             limit = math.floor(self.history * self.unique_cap)
-            self.lib.call("prismkv_select_cap", self.bits.data_ptr(), self.n.data_ptr(), self.features.data_ptr(),
+            self.lib.call("prismkv_select_cap_n", self.bits.data_ptr(), self.n.data_ptr(), self.features.data_ptr(),
                           self.valid.data_ptr(), self.raw.data_ptr(), GROUPS, self.history, limit, self.row_words,
-                          stream=s)
-        self.lib.call("prismkv_union", self.bits.data_ptr(), self.features.data_ptr(), self.valid.data_ptr(),
+                          width, stream=s)
+        self.lib.call("prismkv_union_n", self.bits.data_ptr(), self.features.data_ptr(), self.valid.data_ptr(),
                       self.union_work.data_ptr(), self.ids.data_ptr(), self.count.data_ptr(), GROUPS, self.history,
-                      self.row_words, self.capacity, stream=s)
+                      self.row_words, self.capacity, width, stream=s)
+
+    @property
+    def router(self):
+        return self.__dict__.get("_router", "moments")
+
+    @router.setter
+    def router(self, router):
+        """"moments" (the native path, one launch per layer) or "q_activation"
+        (src/prismkv/core.py:131-139: route + union of up to 64 buckets, then
+        attention; needs set_query_encoders).  features / valid are [8,16]
+        for moments and [8,64] for q_activation."""
+        if router not in ("moments", "q_activation"):
+            raise ValueError("unsupported router/bucket count")
+        if router == "q_activation" and getattr(self, "W_query", None) is None:
+            raise ValueError("q_activation requires SAE and saved positive query scale")
+        width = TOPK if router == "moments" else 4 * TOPK
+        if self.features.shape[1] != width:
+            device = self.out.device
+            self.features = torch.zeros(GROUPS, width, dtype=torch.int64, device=device)
+            self.valid = torch.zeros(GROUPS, width, device=device)
+        self.__dict__["_router"] = router
+
+    def set_query_encoders(self, W, b, query_scale):
+        """Encoders of the queries for router "q_activation": W [8,3000,128],
+        b [8,3000] (the groups' SAEs) and query_scale [8] > 0."""
+        device = self.out.device
+        W = torch.as_tensor(W).to(device=device, dtype=torch.float32).contiguous()
+        b = torch.as_tensor(b).to(device=device, dtype=torch.float32).contiguous()
+        scale = torch.as_tensor(query_scale, dtype=torch.float32).reshape(-1).to(device)
+        if tuple(W.shape) != (GROUPS, FEATURES, DIM) or tuple(b.shape) != (GROUPS, FEATURES):
+            raise ValueError("W_enc [8,3000,128] and b_enc [8,3000] required")
+        if scale.numel() != GROUPS or not bool((scale > 0).all()):
+            raise ValueError("q_activation requires SAE and saved positive query scale")
+        self.W_query, self.b_query, self.query_scale = W, b, scale.contiguous()
+        self.qact_work = torch.zeros(self.lib.query("prismkv_route_qact_work_bytes", GROUPS), dtype=torch.uint8,
+                                     device=device)
 
     def _check_kv(self, q, k, v, splits, schedule):
         if not 1 <= splits <= 128 or schedule not in (0, 1, 2):
@@ -333,9 +376,10 @@ class Native8B:
         decode path: one launch, identical results, every output buffer
         (features, valid, raw, ids, count, out) written as by the two calls."""
         self._check_kv(q, k, v, kwargs.get("splits", 64), kwargs.get("schedule", 0))
-        if self.unique_cap is not None or self.history > FUSED_MAX_HISTORY:
+        if self.unique_cap is not None or self.history > FUSED_MAX_HISTORY or self.router != "moments":
             # the budgeted walk runs between selection and union; very long histories
-            # exceed one launch's group size
+            # exceed one launch's group size; the q_activation router selects up to 64
+            # buckets
             self.route(q)
             return self.attention(q, k, v, **kwargs)
         self.lib.call("prismkv_decode", q.data_ptr(), self.moments.data_ptr(), self.n.data_ptr(), self.bits.data_ptr(),

@@ -66,8 +66,8 @@ def test_session_plumbing_on_host():
     model = tiny_qwen3()
     with pytest.raises(ValueError, match="missing"):
         HFNative(model, {})
-    with pytest.raises(NotImplementedError, match="moments"):
-        HFNative(model, encoders(1), router="q_activation")
+    with pytest.raises(NotImplementedError, match="16 buckets"):
+        HFNative(model, encoders(1), selected_buckets=8)
     with pytest.raises(ValueError, match="unique cap"):
         HFNative(model, encoders(1), unique_cap=1.5)
     ids = torch.randint(0, 128, (1, 12))

@@ -205,3 +205,61 @@ def test_native_witness_unique_counts(oracle_lib):
         case = cases.native_case(H, tail, kind)
         for e in expect.expected(case):
             assert len(e["ids"]) == want
+
+
+# ---------------------------------------------------------------- q_activation router
+
+def _unit_sae(F=3000, d=128):
+    """W with row f = e_(f mod d) for f < d, zero rows beyond: a[h][f] = relu(x[h][f]) for f < d, else relu(b)."""
+    W = np.zeros((F, d), np.float32)
+    W[np.arange(d), np.arange(d)] = 1.0
+    return W, np.zeros(F, np.float32)
+
+
+def test_qact_scores_properties():
+    rng = np.random.default_rng(11)
+    W = (rng.standard_normal((3000, 128)) / np.sqrt(128)).astype(np.float32)
+    b = (rng.standard_normal(3000) * 0.1).astype(np.float32)
+    q = rng.standard_normal((4, 128)).astype(np.float32)
+    counts = rng.integers(0, 3, 3000).astype(np.int64)
+    score, order, margin = oracle.qact_scores(q, W, b, 1.5, counts)
+    # every head's weights sum to 1/4 (core.py:137-138), so the scores sum to 1
+    assert abs(float(score.astype(np.float64).sum()) - 1.0) < 1e-5
+    # the order: exactly the live positive-score buckets, score descending then id ascending
+    live = np.flatnonzero((score > 0) & (counts > 0))
+    want = live[np.lexsort((live, -score[live].astype(np.float64)))]
+    assert np.array_equal(order, want)
+    # independent recomputation in float64 with argsort (a different route to the same numbers)
+    x = q.astype(np.float64) / np.float32(1.5)
+    a = np.maximum(x @ W.astype(np.float64).T + b, 0)
+    ids = np.argsort(-a, axis=1, kind="stable")[:, :16]
+    val = np.take_along_axis(a, ids, 1)
+    val = val / np.maximum(val.sum(1, keepdims=True), 1e-20)
+    ref = np.zeros(3000)
+    np.add.at(ref, ids.ravel(), (val / 4).ravel())
+    assert np.allclose(score, ref, rtol=1e-5, atol=1e-8)
+    if margin > 1e-4:
+        live2 = np.flatnonzero((ref > 0) & (counts > 0))
+        assert np.array_equal(order, live2[np.argsort(-ref[live2], kind="stable")])
+
+
+def test_qact_scores_ties_duplicates_and_empty():
+    W, b = _unit_sae()
+    counts = np.ones(3000, np.int64)
+    # 20 equal activations in every head: the stable argsort keeps ids 0..15,
+    # each weight (1/16)/4, and all four heads pick the same buckets: 4/64 each
+    q = np.zeros((4, 128), np.float32)
+    q[:, :20] = 2.0
+    score, order, _ = oracle.qact_scores(q, W, b, 1.0, counts)
+    assert np.array_equal(order, np.arange(16))
+    assert np.allclose(score[:16], 1 / 16) and not score[16:].any()
+    # fewer than 16 positive activations: the zero-valued picks weigh nothing
+    q = np.zeros((4, 128), np.float32)
+    q[0, 5], q[1, 7] = 3.0, 1.0
+    counts[7] = 0  # an empty bucket keeps its score but leaves the order
+    score, order, _ = oracle.qact_scores(q, W, b, 1.0, counts)
+    assert np.array_equal(order, [5])
+    assert np.isclose(score[5], 0.25) and np.isclose(score[7], 0.25)
+    # no positive activation at all: the clamped sum gives zero scores, an empty order
+    score, order, _ = oracle.qact_scores(np.zeros((4, 128), np.float32), W, b, 1.0, counts)
+    assert len(order) == 0 and not score.any()
