@@ -14,7 +14,7 @@ densely, exactly as in the reference.
 Native specialisation (rejected with NotImplementedError otherwise): Qwen3
 attention with 8 KV heads x 4 query heads, head_dim 128, bf16 activations,
 16 selected buckets (per query for router "q_activation", which routes,
-unions up to 64 buckets and attends in three launches per layer).  `unique_cap` maps to
+unions up to 64 buckets and attends in four launches per layer).  `unique_cap` maps to
 `Native8B.unique_cap`; mode "all_read" (the dense control) runs the model's
 own attention over the whole cache.
 
