@@ -178,37 +178,57 @@ __device__ __forceinline__ void publish_sliced(MfmaLds<kDT / 64>& lds, float* st
 // (out = sum_k e^(m_k - M) acc_k / sum_k e^(m_k - M) den_k, 0 if the
 // denominator is 0), writes out[g][h][32c .. 32c + 32) and clears the words.
 // Thread = (dim tid & 31, split group tid >> 5): splits k = group + 16 i.
+template <int KW>
 __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int g, int h, int c, DecodeLds& lds) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, d = tid & 31, sg = tid >> 5;
   const int S = a.S;
   constexpr int kGroups = kDT / 32;  // 16
   const size_t stride = (size_t)kHq * kSlices * kSliceW;  // floats per split
   float* base = a.state + (size_t)g * S * stride + (h * kSlices + c) * kSliceW;
-  // every load of the merge is issued together and repeated until it has landed
-  unsigned long long rmz = 0;
-  unsigned racc[kMaxSplits / kGroups];
+  // Polled with two generations of loads in flight: a word that lands just
+  // after one generation was issued is seen by the next, half a round trip
+  // later.  Every load is unconditional (published words keep their value
+  // until this merge clears them), so the waits between generations stay exact.
+  constexpr int kPer = 2 * KW;  // S <= 32 KW splits: thread (d, sg) reads splits sg + 16 i, i < kPer
+  const unsigned long long* mzp =
+      reinterpret_cast<const unsigned long long*>(base + (size_t)min(tid, S - 1) * stride);
+  const unsigned* accp[kPer];
 #pragma unroll
-  for (int i = 0; i < kMaxSplits / kGroups; ++i) racc[i] = 0u;
-  for (int spins = 0;; ++spins) {
+  for (int i = 0; i < kPer; ++i)
+    accp[i] = reinterpret_cast<const unsigned*>(base + (size_t)min(sg + kGroups * i, S - 1) * stride + 2 + d);
+  unsigned long long rmz = 0, gmz[2];
+  unsigned racc[kPer], gacc[2][kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) racc[i] = 0u;
+  auto issue = [&](int gen) {
+    gmz[gen] = ld_dev(mzp);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) gacc[gen][i] = ld_dev(accp[i]);
+  };
+  auto take = [&](int gen) {  // keep the first nonzero value of every word; true when all landed
     bool ok = true;
     if (tid < S) {
-      if (rmz == 0) rmz = ld_dev(reinterpret_cast<const unsigned long long*>(base + (size_t)tid * stride));
+      rmz = rmz ? rmz : gmz[gen];
       ok = rmz != 0;
     }
 #pragma unroll
-    for (int i = 0; i < kMaxSplits / kGroups; ++i) {
-      const int k = sg + kGroups * i;
-      if (k < S) {
-        if (racc[i] == 0u) racc[i] = ld_dev(reinterpret_cast<const unsigned*>(base + (size_t)k * stride + 2 + d));
+    for (int i = 0; i < kPer; ++i)
+      if (sg + kGroups * i < S) {
+        racc[i] = racc[i] ? racc[i] : gacc[gen][i];
         ok = ok && racc[i] != 0u;
       }
-    }
-    if (__syncthreads_and(ok)) break;
+    return ok;
+  };
+  issue(0);
+  for (int spins = 0;; spins += 2) {
+    issue(1);
+    if (__syncthreads_and(take(0))) break;
+    issue(0);
+    if (__syncthreads_and(take(1))) break;
     if (spins >= kSpinLimit) {
       if (tid == 0) atomicOr(a.err, 1u);
       break;
     }
-    __builtin_amdgcn_s_sleep(1);
   }
   // M = max over splits, den = sum of weighted denominators (fixed order)
   float2 mz = make_float2(-INFINITY, 0.f);
@@ -230,7 +250,7 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int g, int h, i
   // weighted accumulators of this thread's splits
   float v = 0.f;
 #pragma unroll
-  for (int i = 0; i < kMaxSplits / kGroups; ++i) {
+  for (int i = 0; i < kPer; ++i) {
     const int k = sg + kGroups * i;
     if (k < S) {
       const float mk = lds.fin.mz[k].x;
@@ -520,7 +540,7 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   // also clears the group's statistics, candidates and tile counts (every
   // workgroup has published its state, so none reads them any more)
   if (p >= kMergers) return;
-  merge_slice(a, g, p >> 2, p & 3, lds);
+  merge_slice<KW>(a, g, p >> 2, p & 3, lds);
   if (p == 0) {
     for (int i = tid; i < kChunks * kHq; i += kDT) st_dev(&a.stats[(size_t)g * kChunks * kHq + i], 0ull);
     for (int i = tid; i < a.S * kTop; i += kDT) st_dev(&a.cand[(size_t)g * a.S * kTop + i], 0ull);
