@@ -325,16 +325,17 @@ __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p,
   // ---- 1. score the own tiles: half 0 takes tile 0, half 1 tile 1, then
   // both halves tile 2 (half h its part h).  Loads go out in one batch with
   // no branch: q first (so staging it waits for nothing else), then the
-  // tiles (a missing tile repeats a valid one), then the bucket sizes.
+  // bucket sizes, then the tiles in the order they are used (a missing tile
+  // repeats a valid one), so each round waits only for its own tile.
   {
     const int half = tid >> 8, t = tid & 255;
     unsigned qv = load_query512(a.q, g, tid);
     const int c0 = min(tile(half), kChunks - 1), c2 = min(tile(2), kChunks - 1);
+    const int* cg = a.counts + (size_t)g * kFP + (t & 31);
+    const int n0 = __builtin_nontemporal_load(cg + c0 * kChunk), n2 = __builtin_nontemporal_load(cg + c2 * kChunk);
     float4 m4[8], m2[4];
     load_tile(a.moments, g, c0, t, m4);
     load_half_tile(a.moments, g, c2, half, t, m2);
-    const int* cg = a.counts + (size_t)g * kFP + (t & 31);
-    const int n0 = cg[c0 * kChunk], n2 = cg[c2 * kChunk];
     // every load above is issued before q is first used (the asm takes q as
     // an operand, so even its conversion cannot move up between the loads)
     asm volatile("" : "+v"(qv) :: "memory");
