@@ -384,20 +384,23 @@ __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p,
     }
   }
   __syncthreads();
-  // ---- 3. this workgroup's 16 best keys
-  if (tid < 2 * 64) {
-    const int j = tid >> 5, b = tid & 31;
+  // ---- 3. this workgroup's 16 best keys: wave j < own ranks tile j's 32
+  // keys (row sorts, then rows 0 and 1 merged), wave 0 merges the tiles'
+  // lists (row j = tile j, empty rows zero)
+  if (w < own) {  // uniform
+    const int b = lane & 31;
     uint64_t key = 0;
-    if (j < own) {
-      const float lv[kHq] = {lds.tl[j][0][b], lds.tl[j][1][b], lds.tl[j][2][b], lds.tl[j][3][b]};
-      key = bucket_key(lv, lds.gmax, lds.grz, tile(j) * kChunk + b);
+    if (lane < kChunk) {
+      const float lv[kHq] = {lds.tl[w][0][b], lds.tl[w][1][b], lds.tl[w][2][b], lds.tl[w][3][b]};
+      key = bucket_key(lv, lds.gmax, lds.grz, tile(w) * kChunk + b);
     }
-    lds.sel.own[tid] = key;
+    unsigned long long v = row_sort_desc(key);
+    v = merge_top16(v, xor_rows_u64<16>(v));  // rows 0, 1: the tile's top 16
+    if (lane < kTop) lds.sel.own[kTop * w + lane] = v;
   }
   __syncthreads();
   if (w == 0) {
-    unsigned long long v[2] = {lds.sel.own[lane], lds.sel.own[64 + lane]};
-    const unsigned long long best = bitonic_top16<2>(v);  // lane j < 16: rank j
+    const unsigned long long best = rows_top16(lane < kTop * own ? lds.sel.own[lane] : 0ull);  // lane j < 16: rank j
     if (lane < kTop) st_dev(&a.cand[((size_t)g * S + p) * kTop + lane], ~best);
   }
   // ---- 4. the group's Top-16 from its S x 16 candidates, as they land
