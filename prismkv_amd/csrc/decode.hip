@@ -278,8 +278,12 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int g, int h, i
 
 // Phase 4 for KW sets of 64 candidates per wave: wave w polls the published
 // keys [64 KW w, 64 KW (w + 1)) straight into registers (each 16-lane row is
-// one workgroup's list, already in rank order), keeps their top 16; wave 0
-// then merges the 8 waves' lists into the group's Top-16.
+// one workgroup's list, already in rank order) and keeps their top 16.  The
+// group's Top-16 lies within these 8 lists (a key with fewer than 16 greater
+// keys overall has fewer than 16 in its own wave), so the rank of a listed
+// key among all candidates, when below 16, is its rank among the 128 listed
+// ones: thread t < 128 counts, for its key, the greater keys of each sorted
+// list by binary search and writes the key to win[rank].
 template <int KW>
 __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, DecodeLds& lds) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -298,22 +302,35 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, DecodeLd
   }
   const unsigned long long best = sorted_rows_top16<KW>(v);
   if (lane < kTop) lds.sel.best[kTop * w + lane] = best;
+  if (threadIdx.x < kTop) lds.win[threadIdx.x] = 0ull;  // ranks no key fills stay empty
   __syncthreads();
-  if (w == 0) {
-    unsigned long long u[2] = {lds.sel.best[lane], lds.sel.best[64 + lane]};
-    const unsigned long long win = sorted_rows_top16<2>(u);
-    const int need = __popcll(__ballot(lane < kTop && win != 0));
-    if (lane < kTop) {
-      lds.win[lane] = win;
-      lds.sel_rows[lane] = lane < need ? key_bucket(win) : 0;  // the union reads rows < need only
+  constexpr int kListed = kDT / 64 * kTop;  // 128
+  if (threadIdx.x < kListed) {
+    const unsigned long long x = lds.sel.best[threadIdx.x];
+    if (x != 0ull) {  // nonzero keys are unique, so their ranks are
+      int rank = 0;
+#pragma unroll
+      for (int L = 0; L < kDT / 64; ++L) {
+        const unsigned long long* lst = lds.sel.best + kTop * L;  // descending
+        int pos = 0;
+#pragma unroll
+        for (int step = kTop / 2; step > 0; step >>= 1) pos += lst[pos + step - 1] > x ? step : 0;
+        rank += pos + (lst[pos] > x ? 1 : 0);  // pos <= 15 here; 16 when the whole list is greater
+      }
+      if (rank < kTop) lds.win[rank] = x;
     }
-    if (lane == 0) lds.need = need;
   }
   __syncthreads();
+  if (w == 0) {
+    const unsigned long long win = lane < kTop ? lds.win[lane] : 0ull;
+    const int need = __popcll(__ballot(win != 0ull));
+    if (lane < kTop) lds.sel_rows[lane] = lane < need ? key_bucket(win) : 0;  // the union reads rows < need only
+    if (lane == 0) lds.need = need;
+  }
 }
 
-// Phases 1-4: the group's Top-16 (rank order) into lds.win / lds.sel_rows /
-// lds.need.
+// Phases 1-4: the group's Top-16 (rank order) into lds.win (every wave) and
+// lds.sel_rows / lds.need (written and read by wave 0 only).
 template <int KW>
 __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p, DecodeLds& lds) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
@@ -421,9 +438,10 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
                     a.valid + (size_t)g * kTop, a.raw + g);
 
   // ---- 5. union tile: OR the selected rows over words [64p, 64p + 64), compact
+  // (wave 0 wrote need and sel_rows itself in phase 4)
   const int nw = (a.H + 31) / 32;
-  const int nr = lds.need;
   if (w == 0) {
+    const int nr = lds.need;
     const int wd = p * kTileWords + lane;
     uint32_t m = 0;
     if (nr > 0 && wd < nw) {
