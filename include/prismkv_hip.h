@@ -116,6 +116,17 @@ int prismkv_decode(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits,
                    uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
                    uint64_t out, int groups, int H, int T, int capacity, int64_t row_words, int64_t ks, int64_t vs,
                    int64_t ids_stride, uint64_t stream);
+/* prismkv_decode with the tail length read from device memory at launch
+ * (`tail`: one int32, 4-byte aligned), clamped to [0, max_tail]; the K/V
+ * extents are checked for max_tail.  For a decode step captured once in a
+ * HIP graph and replayed as the tail grows (the caller advances the word on
+ * the stream between or inside replays): the reference binding has no
+ * counterpart (its Native8B.__call__, src/prismkv/native8b.py:104-106,
+ * takes the length from K's shape on the host). */
+int prismkv_decode_tail(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
+                        uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
+                        uint64_t out, uint64_t tail, int groups, int H, int max_tail, int capacity, int64_t row_words,
+                        int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream);
 
 /* ---- stage 4: incremental index update ---------------------------------
  * append_index (src/prismkv/core.py:186-201) for all groups at once, on the

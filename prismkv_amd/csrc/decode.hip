@@ -75,7 +75,8 @@ struct DecodeArgs {
   const uint16_t* k;
   const uint16_t* v;
   int64_t ks, vs;
-  int H, T, S, tail_per;
+  int H, T, S;          // T: the tail length, or its upper bound when tail_dev is set
+  const int* tail_dev;  // optional: the tail length in device memory (read at launch; graph replays)
   unsigned long long* stats;  // [G][kChunks][4] published (max, sum-exp) per chunk and head
   unsigned long long* cand;   // [G][S][16] published best keys of each workgroup
   unsigned* status;           // [G][S] kReady | tile count
@@ -430,6 +431,11 @@ template <int KW>
 __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   const int p = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   __shared__ DecodeLds lds;
+  // the tail length: the host's T, or the device word clamped to it (the
+  // host checked the K/V extents for T).  The word is requested now, with
+  // no branch (without a device word the load reads the error word and is
+  // ignored), so it has long landed when the attention first uses it.
+  const int tail_word = ld_dev(a.tail_dev ? a.tail_dev : reinterpret_cast<const int*>(a.err));
 
   // ---- 1-4. the group's Top-16
   decode_select<KW>(a, g, p, lds);
@@ -478,11 +484,13 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   // in 16-row blocks, four blocks per round with every K/V load of the round
   // issued up front
   const int n_sel = lds.nsel;
-  const int t_lo = min(a.T, p * a.tail_per), t_hi = min(a.T, t_lo + a.tail_per);
+  const int T = a.tail_dev ? min(max(tail_word, 0), a.T) : a.T;
+  const int tail_per = (T + a.S - 1) / a.S;
+  const int t_lo = min(T, p * tail_per), t_hi = min(T, t_lo + tail_per);
   const int n_rows = n_sel + (t_hi - t_lo);
   {
     const int j = lane & 15, qd = lane >> 4;
-    const int last_row = a.H + a.T - 1;
+    const int last_row = a.H + T - 1;
     const uint16_t* kg = a.k + (size_t)g * a.ks;
     const uint16_t* vg = a.v + (size_t)g * a.vs;
     const int per = (n_rows + kDT / 64 - 1) / (kDT / 64);
@@ -619,17 +627,10 @@ static int resident_workgroups() {
   return cached[dev];
 }
 
-extern "C" {
-
-size_t prismkv_decode_work_bytes(int groups, int capacity) {
-  if (groups < 1 || capacity < 1) return 0;
-  return DecodeWorkLayout(groups, decode_splits(capacity)).total;
-}
-
-int prismkv_decode(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
-                   uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
-                   uint64_t out, int groups, int H, int T, int capacity, int64_t row_words, int64_t ks, int64_t vs,
-                   int64_t ids_stride, uint64_t stream) {
+static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
+                       uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
+                       uint64_t out, const int* tail_dev, int groups, int H, int T, int capacity, int64_t row_words,
+                       int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream) {
   if (groups < 1 || groups > 65535 || H < 1 || H > kFusedMaxHistory || T < 0 || capacity < H) return kBadSize;
   if (row_words < (H + 31) / 32 || ids_stride < H) return kBadSize;
   if (ks < (int64_t)(H + T) * kD || vs < (int64_t)(H + T) * kD) return kBadSize;
@@ -653,7 +654,7 @@ int prismkv_decode(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits,
   a.H = H;
   a.T = T;
   a.S = S;
-  a.tail_per = (T + S - 1) / S;
+  a.tail_dev = tail_dev;
   a.stats = reinterpret_cast<unsigned long long*>(w + L.stats);
   a.cand = reinterpret_cast<unsigned long long*>(w + L.cand);
   a.status = reinterpret_cast<unsigned*>(w + L.status);
@@ -673,6 +674,31 @@ int prismkv_decode(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits,
   else if (S <= 128) hipLaunchKernelGGL(decode_kernel<4>, grid, block, 0, s, a);
   else hipLaunchKernelGGL(decode_kernel<8>, grid, block, 0, s, a);
   return (int)hipGetLastError();
+}
+
+extern "C" {
+
+size_t prismkv_decode_work_bytes(int groups, int capacity) {
+  if (groups < 1 || capacity < 1) return 0;
+  return DecodeWorkLayout(groups, decode_splits(capacity)).total;
+}
+
+int prismkv_decode(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
+                   uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
+                   uint64_t out, int groups, int H, int T, int capacity, int64_t row_words, int64_t ks, int64_t vs,
+                   int64_t ids_stride, uint64_t stream) {
+  return decode_impl(q, moments, counts, bits, k, v, work, features, valid, raw, ids, count, out, nullptr, groups, H,
+                     T, capacity, row_words, ks, vs, ids_stride, stream);
+}
+
+int prismkv_decode_tail(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
+                        uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
+                        uint64_t out, uint64_t tail, int groups, int H, int max_tail, int capacity, int64_t row_words,
+                        int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream) {
+  if (!tail || tail % 4) return kBadSize;
+  return decode_impl(q, moments, counts, bits, k, v, work, features, valid, raw, ids, count, out,
+                     reinterpret_cast<const int*>(tail), groups, H, max_tail, capacity, row_words, ks, vs, ids_stride,
+                     stream);
 }
 
 }  // extern "C"

@@ -22,6 +22,14 @@ The per-(layer, group) records of the reference (history, unique, raw,
 buckets, tail, routing_policy) are kept as device tensors and read back
 when `records` is first accessed after a step, so decoding does not
 synchronise.
+
+`DecodeGraph` (no reference counterpart; the role of the SM90 runner's
+captured step, kernels/cuda_sm90/single.py:211-233) decodes from a
+transformers `StaticCache`: the model's whole one-token forward, with every
+layer's single-launch decode reading its tail length from the device, is
+captured once in a HIP graph and replayed token after token; the lazy
+builds and the update policy run eagerly between replays, and the step is
+recaptured whenever a layer's history moves.
 """
 from __future__ import annotations
 
@@ -106,6 +114,7 @@ class HFNative:
         for cfg, old in self.configs.values():
             cfg._attn_implementation = BACKEND_EAGER if old == "eager" else BACKEND
         self._tables = {}  # layer -> encoder tables on the model's device
+        self._static = None  # the DecodeGraph driving a static cache, if any
         self.begin_request()
 
     # ------------------------------------------------------------ lifecycle
@@ -174,6 +183,8 @@ class HFNative:
         return op
 
     def _capacity(self, total):
+        if self._static is not None:  # a static cache never outgrows its buffers
+            return self._static.max_length
         step = max(self.capacity_step, self.update_interval)
         return (total // step + 1) * step
 
@@ -191,6 +202,8 @@ class HFNative:
         if kwargs.get("dropout", 0) != 0:
             raise ValueError("inference only: disable dropout")
         layer, total, steps = module.layer_idx, k.shape[-2], q.shape[-2]
+        if self._static is not None:
+            return self._forward_static(module, q, k, v, attention_mask, **kwargs)
         if attention_mask is not None:
             if attention_mask.ndim != 4:
                 raise NotImplementedError("padding/arbitrary attention masks are unsupported")
@@ -229,3 +242,134 @@ class HFNative:
         self._pending.append((layer, op.history, total, op.count.clone(), op.raw.clone(),
                               (op.valid > 0).sum(1), prefix))
         return out.reshape(1, 1, queries, d), None
+
+    def _forward_static(self, module, q, k, v, attention_mask, **kwargs):
+        """forward() over a StaticCache: K/V are the whole preallocated buffers
+        and the positions come from `position_ids`.  Prefill (eager) runs the
+        model's own attention under an explicit causal mask; a decode step
+        launches the layer's single-launch decode with the tail length
+        computed on the device, so it can be captured and replayed."""
+        layer, steps, d = module.layer_idx, q.shape[-2], q.shape[-1]
+        pos = kwargs.get("position_ids")
+        if pos is None:
+            raise ValueError("a static-cache forward passes position_ids")
+        pos = pos.reshape(-1)
+        if self.force_prefill or layer not in self.prefix_lengths or steps > 1:
+            if q.is_cuda and torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("prefill cannot be captured")
+            self.prefix_lengths[layer] = int(pos[-1]) + 1
+            self.ops.pop(layer, None)
+            if attention_mask is None:  # key j is visible to the query at position p iff j <= p
+                visible = torch.arange(k.shape[-2], device=q.device)[None] <= pos.to(q.device)[:, None]
+                attention_mask = torch.zeros((1, 1, steps, k.shape[-2]), device=q.device, dtype=q.dtype)
+                attention_mask.masked_fill_(~visible[None, None], -torch.inf)
+            return self.original[layer](module, q, k, v, attention_mask, **kwargs)
+        if steps != 1:
+            raise NotImplementedError("decode reference is one token per forward")
+        groups, queries = k.shape[1], q.shape[1]
+        if groups != GROUPS or queries != GROUPS * HEADS or d != DIM or q.dtype != torch.bfloat16:
+            raise NotImplementedError("the native path decodes 8 KV groups x 4 query heads, d=128, in bf16")
+        op = self.ops.get(layer)
+        if op is None:
+            raise RuntimeError("static-cache decode steps run through DecodeGraph")
+        tail = (pos[-1:] + 1 - op.history).to(torch.int32)
+        out = op(q[0, :, 0].reshape(GROUPS, HEADS, DIM).contiguous(), k[0], v[0], tail=tail)
+        return out.reshape(1, 1, queries, d), None
+
+
+class DecodeGraph:
+    """One-token decode steps of `session.model` from a transformers
+    StaticCache, captured in a HIP graph and replayed.  Create it before
+    the prefill (the session then runs every forward over the static
+    buffers), prefill the prompt through the model with position_ids, then
+    call it once per generated token.
+
+    Each call takes the next token id ([1, 1] int64 on the model's device)
+    and returns the last-position logits (a static buffer, overwritten by
+    the next step).  Before a step, on the host: every layer without an
+    index is built from its prefix (hf_reference.py:196-198) and every
+    index absorbs the complete old tail blocks (the update loop of
+    :205-211); if any history moved, the step is captured again.  The
+    capture covers the model's forward with the cache write, RoPE and every
+    layer's single-launch decode (tail length = position + 1 - history,
+    computed on the device).  With graph=False every step runs eagerly
+    through the same code.  Sparse mode, the moments router and no unique cap
+    only (the single-launch decode); records are not kept."""
+
+    def __init__(self, session, cache, *, graph=True):
+        if session.mode != "sparse" or session.router != "moments" or session.unique_cap is not None:
+            raise NotImplementedError("DecodeGraph drives the single-launch decode: sparse mode, moments router, "
+                                      "no unique cap")
+        if session._static is not None:
+            raise ValueError("the session already drives a static cache")
+        device = next(session.model.parameters()).device
+        self.session, self.cache, self.position = session, cache, None
+        self.max_length = int(cache.max_cache_len)
+        self.use_graph = bool(graph)
+        self.ids = torch.zeros((1, 1), dtype=torch.long, device=device)
+        self.pos = torch.zeros((1, 1), dtype=torch.long, device=device)
+        self.graph, self.logits, self.stale = None, None, True
+        self.eager_steps = 0
+        session._static = self
+
+    def close(self):
+        if self.session._static is self:
+            self.session._static = None
+        self.graph = self.logits = None
+
+    def _layer_keys(self, layer):
+        keys = self.cache.layers[layer].keys
+        return keys[0]
+
+    def _prepare(self, total):
+        """Lazy builds and updates for a step that ends with `total` tokens;
+        True when any layer's history moved (the captured step is stale)."""
+        s, moved = self.session, False
+        for layer in s.modules:
+            K = self._layer_keys(layer)
+            if layer not in s.ops:
+                s._op(layer, K, total)
+                moved = True
+            op = s.ops[layer]
+            if op.catch_up(K, total, s.update_interval):
+                moved = True
+        return moved
+
+    def _forward(self):
+        out = self.session.model(self.ids, position_ids=self.pos, attention_mask={"full_attention": None},
+                                 past_key_values=self.cache, use_cache=True, logits_to_keep=1)
+        return out.logits
+
+    @torch.no_grad()
+    def __call__(self, ids):
+        if self.position is None:  # the first step follows the prefill
+            lengths = set(self.session.prefix_lengths.get(layer) for layer in self.session.modules)
+            if len(lengths) != 1 or None in lengths:
+                raise RuntimeError("prefill every layer through the model before decoding")
+            self.position = lengths.pop()
+        if self.position >= self.max_length:
+            raise ValueError("the static cache is full")
+        if self._prepare(self.position + 1):
+            self.stale = True
+        self.ids.copy_(ids.reshape(1, 1))
+        self.pos.fill_(self.position)
+        if not self.use_graph or self.eager_steps == 0:
+            # eager: always without a graph, and once before the first capture
+            # (library handles and workspaces are created outside the capture)
+            logits = self._forward()
+            self.eager_steps += 1
+        else:
+            if self.stale:
+                # the replaced graph stays alive until the new one is captured
+                # into its memory pool
+                old = self.graph
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph, pool=old.pool() if old is not None else None):
+                    self.logits = self._forward()
+                self.graph, self.stale = graph, False
+                del old
+            self.graph.replay()
+            logits = self.logits
+        self.position += 1
+        return logits
+

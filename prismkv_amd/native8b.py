@@ -371,11 +371,33 @@ class Native8B:
                       stream=self._stream())
         return self.out
 
-    def __call__(self, q, k, v, **kwargs):
+    def __call__(self, q, k, v, *, tail=None, **kwargs):
         """route + attention (src/prismkv/native8b.py:104-106) through the fused
         decode path: one launch, identical results, every output buffer
-        (features, valid, raw, ids, count, out) written as by the two calls."""
+        (features, valid, raw, ids, count, out) written as by the two calls.
+
+        `tail` (no reference counterpart): an int32 CUDA tensor of one element
+        holding the tail length T, read by the kernel at launch instead of
+        taking T = K rows - history from K's shape; K/V then only need rows
+        for T up to their length (a static KV buffer).  A launch captured in a
+        HIP graph is replayed with whatever the tensor holds, clamped to
+        [0, K rows - history].  Fused path only (no unique cap, history up to
+        FUSED_MAX_HISTORY, moments router)."""
         self._check_kv(q, k, v, kwargs.get("splits", 64), kwargs.get("schedule", 0))
+        if tail is not None:
+            if self.unique_cap is not None or self.history > FUSED_MAX_HISTORY or self.router != "moments":
+                raise NotImplementedError("a device tail length needs the single-launch decode (no unique cap, "
+                                          "history <= FUSED_MAX_HISTORY, moments router)")
+            if (not isinstance(tail, torch.Tensor) or tail.dtype != torch.int32 or tail.numel() != 1
+                    or tail.device != self.out.device):
+                raise ValueError("tail must be a one-element int32 tensor on the index device")
+            self.lib.call("prismkv_decode_tail", q.data_ptr(), self.moments.data_ptr(), self.n.data_ptr(),
+                          self.bits.data_ptr(), k.data_ptr(), v.data_ptr(), self.decode_work.data_ptr(),
+                          self.features.data_ptr(), self.valid.data_ptr(), self.raw.data_ptr(), self.ids.data_ptr(),
+                          self.count.data_ptr(), self.out.data_ptr(), tail.data_ptr(), GROUPS, self.history,
+                          k.shape[1] - self.history, self.capacity, self.row_words, k.stride(0), v.stride(0),
+                          self.capacity, stream=self._stream())
+            return self.out
         if self.unique_cap is not None or self.history > FUSED_MAX_HISTORY or self.router != "moments":
             # the budgeted walk runs between selection and union; very long histories
             # exceed one launch's group size; the q_activation router selects up to 64

@@ -109,6 +109,12 @@ def test_native_error_codes(lib):
     assert call_raw(lib, "prismkv_build", *[16] * 9, 8, 8, 100, 8, 2, good, 4) == -2  # unknown flag
     assert call_raw(lib, "prismkv_build", *[0] * 9, 8, 8, 100, 8, 0, good, 4) == -1   # null pointers
     assert call_raw(lib, "prismkv_build", *[18] + [16] * 8, 8, 8, 100, 8, 0, good, 4) == -1  # misaligned K
+    # prismkv_decode_tail(13 buffers, tail, groups, H, max_tail, capacity, row_words, ks, vs, ids_stride)
+    ok = (100 + 8) * 128
+    assert call_raw(lib, "prismkv_decode_tail", *[16] * 13, 0, 8, 100, 8, 100, 4, ok, ok, 100) == -1   # no word
+    assert call_raw(lib, "prismkv_decode_tail", *[16] * 13, 18, 8, 100, 8, 100, 4, ok, ok, 100) == -1  # misaligned
+    assert call_raw(lib, "prismkv_decode_tail", *[16] * 14, 8, 100, -1, 100, 4, ok, ok, 100) == -1  # negative bound
+    assert call_raw(lib, "prismkv_decode_tail", *[16] * 14, 8, 100, 9, 100, 4, ok, ok, 100) == -1  # K < H + bound
 
 
 def test_native8b_host_validation_without_gpu():

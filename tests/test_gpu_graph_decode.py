@@ -1,0 +1,131 @@
+"""Decode steps replayed from a HIP graph while the tail grows.
+
+  * `Native8B.__call__(..., tail=t)` (`prismkv_decode_tail`: the tail length
+    read from device memory at launch) gives bit-identical features, ids,
+    counts and output to the host-length launch over the same rows;
+  * one captured launch replayed with different device tail lengths equals
+    the eager launch for each;
+  * `hf.DecodeGraph`: a small random-init Qwen3 with the 8B attention
+    geometry decodes from a transformers StaticCache; the eager steps match
+    the oracle's route + attention (src/prismkv/core.py:106-183) over the
+    index the device holds, the update policy (hf_reference.py:205-211)
+    moves the history across the run, and the graph-replayed steps give
+    bit-identical logits to the eager ones.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import cases
+from tests.gpu_util import bf16_bits, log, operator, route_outputs
+from tests.test_gpu_hf import Capture, check_call, encoders, tiny_qwen3
+
+pytestmark = pytest.mark.gpu
+
+
+def _snapshot(op):
+    return [bf16_bits(op.out).copy(), *[x.copy() for x in route_outputs(op)]]
+
+
+def _same(a, b):
+    return all(np.array_equal(x, y) for x, y in zip(a, b))
+
+
+def test_device_tail_matches_host_tail():
+    case = cases.native_case(4096, 64, "random", seed=4)
+    op, q, k, v = operator(case)
+    H = op.history
+    t = torch.zeros(1, dtype=torch.int32, device="cuda")
+    for T in (0, 1, 37, 64):
+        op(q, k[:, :H + T], v[:, :H + T])
+        torch.cuda.synchronize()
+        host = _snapshot(op)
+        op.out.zero_()
+        op.ids.zero_()
+        t.fill_(T)
+        op(q, k, v, tail=t)
+        torch.cuda.synchronize()
+        assert _same(host, _snapshot(op)), T
+    # a word beyond K's rows is clamped to them
+    t.fill_(1000)
+    op(q, k, v, tail=t)
+    torch.cuda.synchronize()
+    assert _same(host, _snapshot(op))
+    assert op.decode_errors() == 0
+
+
+def test_captured_launch_follows_the_tail_word():
+    case = cases.native_case(8192, 256, "random", seed=6)
+    op, q, k, v = operator(case)
+    H = op.history
+    want = {}
+    for T in (256, 1, 100, 0, 255):
+        op(q, k[:, :H + T], v[:, :H + T])
+        torch.cuda.synchronize()
+        want[T] = _snapshot(op)
+    t = torch.zeros(1, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        op(q, k, v, tail=t)
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        op(q, k, v, tail=t)
+    for T in (256, 1, 100, 0, 255):
+        op.out.zero_()
+        t.fill_(T)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert _same(want[T], _snapshot(op)), T
+    assert op.decode_errors() == 0
+
+
+def _prefill(session, model, cache, ids, P, chunk=1024):
+    with torch.no_grad(), session.prefill():
+        for lo in range(0, P, chunk):
+            hi = min(P, lo + chunk)
+            model(ids[:, lo:hi], position_ids=torch.arange(lo, hi, device="cuda")[None], past_key_values=cache,
+                  use_cache=True, logits_to_keep=1)
+
+
+def test_static_cache_decode_graph():
+    from transformers import StaticCache
+    from prismkv_amd.hf import DecodeGraph, HFNative
+    layers, P, N, interval = 2, 2048, 80, 64
+    model = tiny_qwen3(layers)
+    session = HFNative(model, encoders(layers), update_interval=interval)
+    ids = torch.randint(0, 256, (1, P + N), generator=torch.Generator().manual_seed(9)).cuda()
+    logits = {}
+    checks = {0, 64, N - 1}
+    for use_graph in (False, True):
+        session.begin_request()
+        cache = StaticCache(config=model.config, max_cache_len=P + N + 16)
+        step = DecodeGraph(session, cache, graph=use_graph)
+        _prefill(session, model, cache, ids, P)
+        cap = Capture(session) if not use_graph else None
+        out = []
+        for s in range(N):
+            n_calls = len(cap.calls) if cap else 0
+            out.append(step(ids[:, P + s:P + s + 1]).clone())
+            if cap and s in checks:
+                torch.cuda.synchronize()
+                for layer, q, K, V, o in cap.calls[n_calls:]:
+                    total = P + s + 1
+                    err = check_call(session.ops[layer], layer, q, K[:, :total], V[:, :total], o)
+                    log(f"  eager step {s} layer {layer}: history={session.ops[layer].history} {err}")
+            if cap:
+                cap.calls = []
+        torch.cuda.synchronize()
+        if cap:
+            session.forward = cap._forward
+        for layer, op in session.ops.items():
+            assert op.history == P + interval, (use_graph, layer, op.history)
+            assert op.decode_errors() == 0
+        step.close()
+        logits[use_graph] = torch.stack(out)
+        log(f"graph={use_graph}: {N} steps, histories {[op.history for op in session.ops.values()]}")
+    assert torch.isfinite(logits[False]).all()
+    assert torch.equal(logits[False], logits[True])
+    session.close()

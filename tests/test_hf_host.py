@@ -83,3 +83,32 @@ def test_session_plumbing_on_host():
         HFNative(model, encoders(1))
     session.close()
     assert model.config._attn_implementation == "sdpa"
+
+
+def test_static_cache_session_on_host():
+    from transformers import StaticCache
+    from prismkv_amd.hf import DecodeGraph, HFNative
+    model = tiny_qwen3()
+    ids = torch.randint(0, 128, (1, 12))
+    with torch.no_grad():
+        dense = model(ids).logits[:, -1]
+    session = HFNative(model, encoders(1), router="q_activation")
+    with pytest.raises(NotImplementedError, match="moments router"):
+        DecodeGraph(session, StaticCache(config=model.config, max_cache_len=32))
+    session.close()
+    session = HFNative(model, encoders(1))
+    cache = StaticCache(config=model.config, max_cache_len=32)
+    step = DecodeGraph(session, cache)
+    with pytest.raises(ValueError, match="already drives"):
+        DecodeGraph(session, cache)
+    with pytest.raises(RuntimeError, match="prefill every layer"):
+        step(ids[:, :1])
+    # the prefill over the static buffers (explicit causal mask from the
+    # positions) gives the dense model's logits
+    with torch.no_grad(), session.prefill():
+        static = model(ids, position_ids=torch.arange(12)[None], past_key_values=cache, use_cache=True).logits[:, -1]
+    assert torch.allclose(static, dense, atol=1e-5, rtol=1e-5)
+    assert session.prefix_lengths == {0: 12} and session._capacity(13) == 32
+    step.close()
+    assert session._static is None
+    session.close()
