@@ -129,3 +129,44 @@ def test_static_cache_decode_graph():
     assert torch.isfinite(logits[False]).all()
     assert torch.equal(logits[False], logits[True])
     session.close()
+
+
+def test_36_layer_step_graph():
+    # the 36 attention layers of the 8B geometry (32 query / 8 KV heads,
+    # d = 128; hidden 1024 keeps the random weights small): the whole
+    # one-token forward captured once and replayed, bit-identical to eager
+    import time
+    from transformers import Qwen3Config, Qwen3ForCausalLM, StaticCache
+    from prismkv_amd.hf import DecodeGraph, HFNative
+    L, P, N = 36, 8192, 8
+    cfg = Qwen3Config(vocab_size=1000, hidden_size=1024, intermediate_size=2048, num_hidden_layers=L,
+                      num_attention_heads=32, num_key_value_heads=8, head_dim=128, max_position_embeddings=16384)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(5)
+    model = Qwen3ForCausalLM(cfg).to(device="cuda", dtype=torch.bfloat16).eval()
+    session = HFNative(model, encoders(L))
+    ids = torch.randint(0, 1000, (1, P + N), generator=torch.Generator().manual_seed(12)).cuda()
+    logits, ms = {}, {}
+    for use_graph in (False, True):
+        session.begin_request()
+        cache = StaticCache(config=cfg, max_cache_len=P + N + 8)
+        step = DecodeGraph(session, cache, graph=use_graph)
+        _prefill(session, model, cache, ids, P, chunk=2048)
+        out, times = [], []
+        for s in range(N):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out.append(step(ids[:, P + s:P + s + 1]).clone())
+            torch.cuda.synchronize()
+            times.append(time.perf_counter() - t0)
+        assert all(op.decode_errors() == 0 and op.history == P for op in session.ops.values())
+        if use_graph:
+            unique = [float(session.ops[layer].count.float().mean()) for layer in sorted(session.ops)]
+            log("  unique ids per group by layer (last step): " + " ".join(f"{u:.0f}" for u in unique))
+        step.close()
+        logits[use_graph] = torch.stack(out)
+        ms[use_graph] = 1e3 * float(np.median(times[2:]))
+    log(f"36-layer one-token step, H={P}: eager {ms[False]:.2f} ms, graph replay {ms[True]:.2f} ms")
+    assert torch.isfinite(logits[False]).all()
+    assert torch.equal(logits[False], logits[True])
+    session.close()
