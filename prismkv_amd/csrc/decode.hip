@@ -12,8 +12,9 @@
 // Grid (S, G) x 512, S = clamp(ceil(ceil(H/32) / 64), 32, 256).  Workgroup p
 // of group g owns the contiguous moment tiles kp .. kp + k - 1 of the 94
 // (k = ceil(94 / S) <= 3: one 96 KB stream per workgroup),
-// bitmap words [64p, 64p + 64) (tokens [2048p, 2048p + 2048)) and tail rows
-// [p * ceil(T/S), ...).  Phases:
+// bitmap words [tw p, tw (p + 1)), tw = ceil(ceil(H/32) / S) <= 64 (tokens
+// [32 tw p, 32 tw (p + 1)), so every workgroup gathers its share of the
+// selected rows at any history) and tail rows [p * ceil(T/S), ...).  Phases:
 //   1. score its tiles (two 256-thread scorers side by side, every tile load
 //      issued up front) into LDS logits; publish each tile's per-head
 //      (max, sum-exp) statistics;
@@ -25,7 +26,7 @@
 //   4. read the group's S x 16 candidates as they land and rank them: the
 //      group's Top-16 is among them, and every workgroup computes the same
 //      winners; workgroup 0 writes features / valid / raw;
-//   5. union tile: one wave ORs the selected rows over its 64 words and
+//   5. union tile: one wave ORs the selected rows over its tw words and
 //      compacts the set bits into an LDS token list, publishing the tile's
 //      count (and requesting the lower tiles' counts);
 //   6. attention over the tile's tokens plus its tail share: wave w takes a
@@ -56,7 +57,7 @@ namespace prismkv {
 namespace {
 
 constexpr int kDT = kAT;           // 512 threads, 8 waves
-constexpr int kTileWords = 64;     // bitmap words per workgroup
+constexpr int kTileWords = 64;     // most bitmap words per workgroup (ceil(words / S) in a launch)
 constexpr int kTileTokens = 32 * kTileWords;
 constexpr int kMinSplits = 32;     // at least one workgroup per CU for the scoring
 constexpr int kMaxSplits = 256;    // one group's workgroups must fit on the GPU at once
@@ -76,6 +77,7 @@ struct DecodeArgs {
   const uint16_t* v;
   int64_t ks, vs;
   int H, T, S;          // T: the tail length, or its upper bound when tail_dev is set
+  int tw;               // bitmap words per workgroup, ceil(ceil(H / 32) / S) <= 64
   const int* tail_dev;  // optional: the tail length in device memory (read at launch; graph replays)
   unsigned long long* stats;  // [G][kChunks][4] published (max, sum-exp) per chunk and head
   unsigned long long* cand;   // [G][S][16] published best keys of each workgroup
@@ -443,14 +445,14 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     write_selection(lds.win, lds.need, a.counts + (size_t)g * kFP, a.features + (size_t)g * kTop,
                     a.valid + (size_t)g * kTop, a.raw + g);
 
-  // ---- 5. union tile: OR the selected rows over words [64p, 64p + 64), compact
+  // ---- 5. union tile: OR the selected rows over words [tw p, tw (p + 1)), compact
   // (wave 0 wrote need and sel_rows itself in phase 4)
   const int nw = (a.H + 31) / 32;
   if (w == 0) {
     const int nr = lds.need;
-    const int wd = p * kTileWords + lane;
+    const int wd = p * a.tw + lane;
     uint32_t m = 0;
-    if (nr > 0 && wd < nw) {
+    if (nr > 0 && lane < a.tw && wd < nw) {
       const uint32_t* gb = a.bits + (size_t)g * kF * a.row_words + wd;
       uint32_t v[kTop];
 #pragma unroll
@@ -654,6 +656,7 @@ static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t b
   a.H = H;
   a.T = T;
   a.S = S;
+  a.tw = ((H + 31) / 32 + S - 1) / S;
   a.tail_dev = tail_dev;
   a.stats = reinterpret_cast<unsigned long long*>(w + L.stats);
   a.cand = reinterpret_cast<unsigned long long*>(w + L.cand);
