@@ -99,6 +99,7 @@ struct DecodeLds {
   alignas(16) unsigned long long win[kTop];
   int sel_rows[kTop];
   int need, nsel, base;
+  unsigned cover[kDT / 64];  // per wave: the winners' ranks whose rows it prefetched
   float gmax[kHq], grz[kHq];
   union alignas(16) {
     struct {
@@ -109,6 +110,7 @@ struct DecodeLds {
     struct {
       alignas(16) unsigned long long own[2 * 64];  // this workgroup's keys (<= 96 used)
       alignas(16) unsigned long long best[kDT / 64 * kTop];
+      unsigned ors[kDT / 64][kTileWords];  // per wave: OR of its prefetched winning rows over the tile's words
     } sel;
     MfmaLds<kDT / 64> mf;
     struct {
@@ -287,8 +289,16 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int g, int h, i
 // key among all candidates, when below 16, is its rank among the 128 listed
 // ones: thread t < 128 counts, for its key, the greater keys of each sorted
 // list by binary search and writes the key to win[rank].
+//
+// The union's bitmap words are requested early: as soon as it has its list,
+// each wave loads words [tw p, tw (p + 1)) of the rows of its kPrefetch best
+// keys, which land while the ranks are counted; the group's winners are
+// usually among them.  Once the ranks are known, each wave ORs the rows of its
+// prefetched keys that won into lds.sel.ors[w] and marks their ranks in
+// lds.cover[w]; the union loads only the winners no wave prefetched.
+constexpr int kPrefetch = 6;
 template <int KW>
-__device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, DecodeLds& lds) {
+__device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, DecodeLds& lds) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int nk = a.S * kTop;
   const unsigned long long* cg = a.cand + (size_t)g * a.S * kTop;
@@ -306,6 +316,17 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, DecodeLd
   const unsigned long long best = sorted_rows_top16<KW>(v);
   if (lane < kTop) lds.sel.best[kTop * w + lane] = best;
   if (threadIdx.x < kTop) lds.win[threadIdx.x] = 0ull;  // ranks no key fills stay empty
+  const int nw = (a.H + 31) / 32;
+  const int wd = p * a.tw + lane;
+  const bool word = lane < a.tw && wd < nw;
+  const uint32_t* gb = a.bits + (size_t)g * kF * a.row_words + min(wd, nw - 1);
+  unsigned long long pk[kPrefetch];
+  uint32_t pw[kPrefetch];
+#pragma unroll
+  for (int r = 0; r < kPrefetch; ++r) {
+    pk[r] = readlane_u64(best, r);  // rank r of this wave's list (uniform)
+    pw[r] = pk[r] ? __builtin_nontemporal_load(gb + (size_t)key_bucket(pk[r]) * a.row_words) : 0u;
+  }
   __syncthreads();
   constexpr int kListed = kDT / 64 * kTop;  // 128
   if (threadIdx.x < kListed) {
@@ -324,12 +345,26 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, DecodeLd
     }
   }
   __syncthreads();
+  // the winners are exactly the candidates >= the last winner's key (nonzero
+  // keys are unique); a prefetched winner's rank = the winners above it
+  const unsigned long long win = lane < kTop ? lds.win[lane] : 0ull;
+  const int need = __popcll(__ballot(win != 0ull));
+  const unsigned long long last = need ? readlane_u64(win, need - 1) : ~0ull;
+  uint32_t part = 0u;
+  unsigned covered = 0u;
+#pragma unroll
+  for (int r = 0; r < kPrefetch; ++r)
+    if (pk[r] != 0ull && pk[r] >= last) {  // uniform
+      part |= pw[r];
+      covered |= 1u << __popcll(__ballot(lane < need && win > pk[r]));
+    }
+  lds.sel.ors[w][lane] = word ? part : 0u;
+  if (lane == 0) lds.cover[w] = covered;
   if (w == 0) {
-    const unsigned long long win = lane < kTop ? lds.win[lane] : 0ull;
-    const int need = __popcll(__ballot(win != 0ull));
     if (lane < kTop) lds.sel_rows[lane] = lane < need ? key_bucket(win) : 0;  // the union reads rows < need only
     if (lane == 0) lds.need = need;
   }
+  __syncthreads();
 }
 
 // Phases 1-4: the group's Top-16 (rank order) into lds.win (every wave) and
@@ -424,7 +459,7 @@ __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p,
     if (lane < kTop) st_dev(&a.cand[((size_t)g * S + p) * kTop + lane], ~best);
   }
   // ---- 4. the group's Top-16 from its S x 16 candidates, as they land
-  final_top16<KW>(a, g, lds);
+  final_top16<KW>(a, g, p, lds);
 }
 
 // KW = 64-key candidate sets per wave, ceil(S / 32): one instantiation per
@@ -452,15 +487,26 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     const int nr = lds.need;
     const int wd = p * a.tw + lane;
     uint32_t m = 0;
-    if (nr > 0 && lane < a.tw && wd < nw) {
+    unsigned covered = 0u;
+#pragma unroll
+    for (int k = 0; k < kDT / 64; ++k) {
+      m |= lds.sel.ors[k][lane];
+      covered |= lds.cover[k];
+    }
+    const unsigned missing = ((1u << nr) - 1u) & ~covered;  // winners' ranks no wave prefetched (uniform)
+    if (missing && lane < a.tw && wd < nw) {
+      // one round of loads: every rank loads (a covered one repeats the first
+      // missing row) and only the missing ones are kept
       const uint32_t* gb = a.bits + (size_t)g * kF * a.row_words + wd;
+      const int first = __builtin_ctz(missing);
       uint32_t v[kTop];
 #pragma unroll
-      for (int r = 0; r < kTop; ++r) v[r] = __builtin_nontemporal_load(gb + (size_t)lds.sel_rows[r < nr ? r : nr - 1] * a.row_words);
+      for (int r = 0; r < kTop; ++r)
+        v[r] = __builtin_nontemporal_load(gb + (size_t)lds.sel_rows[(missing >> r) & 1u ? r : first] * a.row_words);
 #pragma unroll
-      for (int r = 0; r < kTop; ++r) m |= v[r];
-      if (wd == nw - 1 && (a.H & 31)) m &= (1u << (a.H & 31)) - 1u;
+      for (int r = 0; r < kTop; ++r) m |= (missing >> r) & 1u ? v[r] : 0u;
     }
+    if (wd == nw - 1 && (a.H & 31)) m &= (1u << (a.H & 31)) - 1u;
     const int n = __popc(m);
     const int incl = wave_scan_i(n);
     int at = incl - n;

@@ -98,6 +98,12 @@ __device__ __forceinline__ unsigned long long dpp_u64(unsigned long long v) {
   const int hi = __builtin_amdgcn_mov_dpp((int)(unsigned)(v >> 32), kCtrl, 0xF, 0xF, false);
   return ((unsigned long long)(unsigned)hi << 32) | (unsigned long long)(unsigned)lo;
 }
+// The key held by lane `src` (uniform), in every lane.
+__device__ __forceinline__ unsigned long long readlane_u64(unsigned long long v, int src) {
+  const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(v >> 32), src);
+  const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)(unsigned)v, src);
+  return ((unsigned long long)hi << 32) | (unsigned long long)lo;
+}
 // The key of lane (lane ^ M) for M = 16 or 32 (permlane swaps, no LDS).
 template <int M>
 __device__ __forceinline__ unsigned long long xor_rows_u64(unsigned long long v) {
