@@ -9,10 +9,11 @@
 // padding rules of kernels/ppu_8b/route_parallel.cu:12,23,29 and the ascending
 // emission of kernels/ppu_8b/union.cu:26.
 //
-// Grid (S, G) x 512, S = clamp(ceil(ceil(H/32) / 64), 32, 256).  Workgroup p
+// Grid (S, G) x 512, S = clamp(256 / G, 32, 256) (32 for 8 groups: the whole
+// launch is resident at once, one workgroup per CU, at any history).  Workgroup p
 // of group g owns the contiguous moment tiles kp .. kp + k - 1 of the 94
 // (k = ceil(94 / S) <= 3: one 96 KB stream per workgroup),
-// bitmap words [tw p, tw (p + 1)), tw = ceil(ceil(H/32) / S) <= 64 (tokens
+// bitmap words [tw p, tw (p + 1)), tw = ceil(ceil(H/32) / S) <= 512 (tokens
 // [32 tw p, 32 tw (p + 1)), so every workgroup gathers its share of the
 // selected rows at any history) and tail rows [p * ceil(T/S), ...).  Phases:
 //   1. score its tiles (two 256-thread scorers side by side, every tile load
@@ -26,7 +27,7 @@
 //   4. read the group's S x 16 candidates as they land and rank them: the
 //      group's Top-16 is among them, and every workgroup computes the same
 //      winners; workgroup 0 writes features / valid / raw;
-//   5. union tile: one wave ORs the selected rows over its tw words and
+//   5. union tile: one wave per 64 of its tw words ORs the selected rows and
 //      compacts the set bits into an LDS token list, publishing the tile's
 //      count (and requesting the lower tiles' counts);
 //   6. attention over the tile's tokens plus its tail share: wave w takes a
@@ -57,8 +58,9 @@ namespace prismkv {
 namespace {
 
 constexpr int kDT = kAT;           // 512 threads, 8 waves
-constexpr int kTileWords = 64;     // most bitmap words per workgroup (ceil(words / S) in a launch)
-constexpr int kTileTokens = 32 * kTileWords;
+constexpr int kTileWords = 64;     // bitmap words per union chunk (one wave, one word per lane)
+constexpr int kMaxTileWords = 512; // bitmap words per workgroup at most (8 chunks, one per wave)
+constexpr int kTileTokens = 32 * kMaxTileWords;
 constexpr int kMinSplits = 32;     // at least one workgroup per CU for the scoring
 constexpr int kMaxSplits = 256;    // one group's workgroups must fit on the GPU at once
 constexpr int kMaxOwn = (kChunks + kMinSplits - 1) / kMinSplits;  // moment tiles per workgroup (3)
@@ -77,7 +79,7 @@ struct DecodeArgs {
   const uint16_t* v;
   int64_t ks, vs;
   int H, T, S;          // T: the tail length, or its upper bound when tail_dev is set
-  int tw;               // bitmap words per workgroup, ceil(ceil(H / 32) / S) <= 64
+  int tw;               // bitmap words per workgroup, ceil(ceil(H / 32) / S) <= 512
   const int* tail_dev;  // optional: the tail length in device memory (read at launch; graph replays)
   unsigned long long* stats;  // [G][kChunks][4] published (max, sum-exp) per chunk and head
   unsigned long long* cand;   // [G][S][16] published best keys of each workgroup
@@ -93,13 +95,16 @@ struct DecodeArgs {
   uint16_t* out;
 };
 
+// The tile's selected tokens live in dynamic LDS after this struct, sized
+// per launch (32 tw ints): a launch allocates only what its history needs
+// (8 KB at 64K), since a larger LDS allocation slows every launch.
 struct DecodeLds {
-  int rows[kTileTokens];  // the tile's selected tokens, ascending
   float tl[kMaxOwn][kHq][kChunk];  // logits of this workgroup's moment tiles
   alignas(16) unsigned long long win[kTop];
   int sel_rows[kTop];
   int need, nsel, base;
   unsigned cover[kDT / 64];  // per wave: the winners' ranks whose rows it prefetched
+  int chunk_rows[kDT / 64];  // per union chunk: its selected tokens
   float gmax[kHq], grz[kHq];
   union alignas(16) {
     struct {
@@ -468,6 +473,7 @@ template <int KW>
 __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   const int p = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   __shared__ DecodeLds lds;
+  extern __shared__ int rows[];  // the tile's selected tokens, ascending (32 tw of them)
   // the tail length: the host's T, or the device word clamped to it (the
   // host checked the K/V extents for T).  The word is requested now, with
   // no branch (without a device word the load reads the error word and is
@@ -480,44 +486,85 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     write_selection(lds.win, lds.need, a.counts + (size_t)g * kFP, a.features + (size_t)g * kTop,
                     a.valid + (size_t)g * kTop, a.raw + g);
 
-  // ---- 5. union tile: OR the selected rows over words [tw p, tw (p + 1)), compact
-  // (wave 0 wrote need and sel_rows itself in phase 4)
+  // ---- 5. union tile: OR the selected rows over words [tw p, tw (p + 1)), compact.
+  // One 64-word chunk (histories up to 64K at 8 groups): wave 0 ORs the rows
+  // the waves prefetched in phase 4 and loads any winner none prefetched.
+  // More chunks: wave w < ceil(tw / 64) loads chunk w of every selected row;
+  // the chunks' counts give each its offset.  (Phase 4's final barrier
+  // publishes need and sel_rows.)
   const int nw = (a.H + 31) / 32;
-  if (w == 0) {
+  if (a.tw <= kTileWords) {
+    if (w == 0) {
+      const int nr = lds.need;
+      const int wd = p * a.tw + lane;
+      uint32_t m = 0;
+      unsigned covered = 0u;
+#pragma unroll
+      for (int k = 0; k < kDT / 64; ++k) {
+        m |= lds.sel.ors[k][lane];
+        covered |= lds.cover[k];
+      }
+      const unsigned missing = ((1u << nr) - 1u) & ~covered;  // winners' ranks no wave prefetched (uniform)
+      if (missing && lane < a.tw && wd < nw) {
+        // one round of loads: every rank loads (a covered one repeats the first
+        // missing row) and only the missing ones are kept
+        const uint32_t* gb = a.bits + (size_t)g * kF * a.row_words + wd;
+        const int first = __builtin_ctz(missing);
+        uint32_t v[kTop];
+#pragma unroll
+        for (int r = 0; r < kTop; ++r)
+          v[r] = __builtin_nontemporal_load(gb + (size_t)lds.sel_rows[(missing >> r) & 1u ? r : first] * a.row_words);
+#pragma unroll
+        for (int r = 0; r < kTop; ++r) m |= (missing >> r) & 1u ? v[r] : 0u;
+      }
+      if (wd == nw - 1 && (a.H & 31)) m &= (1u << (a.H & 31)) - 1u;
+      const int n = __popc(m);
+      const int incl = wave_scan_i(n);
+      int at = incl - n;
+      while (m) {
+        rows[at++] = wd * 32 + (int)__builtin_ctz(m);
+        m &= m - 1u;
+      }
+      const int total = __shfl(incl, 63);
+      if (lane == 0) {
+        lds.nsel = total;
+        st_dev(&a.status[(size_t)g * a.S + p], kReady | (unsigned)total);
+      }
+    }
+  } else {
+    const int chunks = (a.tw + kTileWords - 1) / kTileWords;  // <= 8
+    const int cw = w * kTileWords + lane, wd = p * a.tw + cw;
     const int nr = lds.need;
-    const int wd = p * a.tw + lane;
-    uint32_t m = 0;
-    unsigned covered = 0u;
+    uint32_t m = 0u;
+    int n = 0, incl = 0;
+    if (w < chunks) {
+      if (nr > 0 && cw < a.tw && wd < nw) {
+        const uint32_t* gb = a.bits + (size_t)g * kF * a.row_words + wd;
+        uint32_t v[kTop];
 #pragma unroll
-    for (int k = 0; k < kDT / 64; ++k) {
-      m |= lds.sel.ors[k][lane];
-      covered |= lds.cover[k];
-    }
-    const unsigned missing = ((1u << nr) - 1u) & ~covered;  // winners' ranks no wave prefetched (uniform)
-    if (missing && lane < a.tw && wd < nw) {
-      // one round of loads: every rank loads (a covered one repeats the first
-      // missing row) and only the missing ones are kept
-      const uint32_t* gb = a.bits + (size_t)g * kF * a.row_words + wd;
-      const int first = __builtin_ctz(missing);
-      uint32_t v[kTop];
+        for (int r = 0; r < kTop; ++r)
+          v[r] = __builtin_nontemporal_load(gb + (size_t)lds.sel_rows[r < nr ? r : nr - 1] * a.row_words);
 #pragma unroll
-      for (int r = 0; r < kTop; ++r)
-        v[r] = __builtin_nontemporal_load(gb + (size_t)lds.sel_rows[(missing >> r) & 1u ? r : first] * a.row_words);
-#pragma unroll
-      for (int r = 0; r < kTop; ++r) m |= (missing >> r) & 1u ? v[r] : 0u;
+        for (int r = 0; r < kTop; ++r) m |= v[r];
+      }
+      if (wd == nw - 1 && (a.H & 31)) m &= (1u << (a.H & 31)) - 1u;
+      n = __popc(m);
+      incl = wave_scan_i(n);
+      if (lane == 63) lds.chunk_rows[w] = incl;
     }
-    if (wd == nw - 1 && (a.H & 31)) m &= (1u << (a.H & 31)) - 1u;
-    const int n = __popc(m);
-    const int incl = wave_scan_i(n);
-    int at = incl - n;
-    while (m) {
-      lds.rows[at++] = wd * 32 + (int)__builtin_ctz(m);
-      m &= m - 1u;
-    }
-    const int total = __shfl(incl, 63);
-    if (lane == 0) {
-      lds.nsel = total;
-      st_dev(&a.status[(size_t)g * a.S + p], kReady | (unsigned)total);
+    __syncthreads();  // every chunk's count, for the offsets
+    if (w < chunks) {
+      int off = 0;
+      for (int k = 0; k < w; ++k) off += lds.chunk_rows[k];
+      int at = off + incl - n;
+      while (m) {
+        rows[at++] = wd * 32 + (int)__builtin_ctz(m);
+        m &= m - 1u;
+      }
+      if (w == chunks - 1 && lane == 63) {
+        lds.nsel = off + incl;
+        st_dev(&a.status[(size_t)g * a.S + p], kReady | (unsigned)(off + incl));
+      }
     }
   }
   __syncthreads();
@@ -547,7 +594,7 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     // repeat the range's first row (masked, same lines)
     auto row_pos = [&](int r) {
       r = r < r1 ? r : r0;
-      int pos = r < n_sel ? lds.rows[r] : a.H + t_lo + (r - n_sel);
+      int pos = r < n_sel ? rows[r] : a.H + t_lo + (r - n_sel);
       return pos < 0 ? 0 : (pos > last_row ? last_row : pos);
     };
     MfmaAttn st;
@@ -604,13 +651,13 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     // ---- 8. the split state (after the look-back: its publication tells
     // workgroup 0 that this workgroup no longer reads any published word);
     // its barriers also publish lds.base to every wave
-    __syncthreads();  // the LDS union is free (rows[] and base stay)
+    __syncthreads();  // the LDS union is free (the rows and base stay)
     mfma_stash(st, lds.mf, w);
     publish_sliced(lds.mf, a.state + (size_t)(g * a.S + p) * kHq * kSlices * kSliceW);
   }
   {
     int32_t* dst = a.ids + (size_t)g * a.ids_stride + lds.base;
-    for (int i = tid; i < n_sel; i += kDT) dst[i] = lds.rows[i];
+    for (int i = tid; i < n_sel; i += kDT) dst[i] = rows[i];
   }
 
   // ---- 9. workgroups 0..15 each merge one (head, 32-dim slice) of the S
@@ -631,12 +678,13 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
 
 using namespace prismkv;
 
-static int decode_splits(int H) {
-  return std::min(kMaxSplits, std::max(kMinSplits, ((H + 31) / 32 + kTileWords - 1) / kTileWords));
-}
-static constexpr int kFusedMaxHistory = kMaxSplits * kTileTokens;  // 524288
+// Workgroups per group: 256 / groups (32 for 8 groups), so the whole launch is
+// resident at once, one workgroup per CU, at any history; the union tile
+// grows with H instead (tw <= 512 words up to kFusedMaxHistory).
+static int decode_splits(int groups) { return std::min(kMaxSplits, std::max(kMinSplits, 256 / std::max(groups, 1))); }
+static constexpr int kFusedMaxHistory = kMinSplits * kTileTokens;  // 524288
 
-// Work layout (bytes), sized for the largest split count the buffer serves:
+// Work layout (bytes) for the split count of `groups` groups:
 // err | stats | candidates | status | state
 struct DecodeWorkLayout {
   size_t err, stats, cand, status, state, total;
@@ -653,7 +701,8 @@ struct DecodeWorkLayout {
 };
 
 // Workgroups of decode_kernel resident on device `dev` at once (CUs x blocks
-// per CU), queried once per device.
+// per CU) with the largest row list (64 KB of dynamic LDS), queried once per
+// device; the instantiations are allowed that much dynamic LDS here.
 static int resident_workgroups() {
   static int cached[64] = {0};
   int dev = 0;
@@ -666,7 +715,11 @@ static int resident_workgroups() {
     const void* fns[] = {reinterpret_cast<const void*>(decode_kernel<1>), reinterpret_cast<const void*>(decode_kernel<2>),
                          reinterpret_cast<const void*>(decode_kernel<4>), reinterpret_cast<const void*>(decode_kernel<8>)};
     for (const void* fn : fns) {
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kDT, 0) != hipSuccess) return 0;
+      if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kTileTokens * (int)sizeof(int)) !=
+          hipSuccess)
+        return 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kDT, kTileTokens * sizeof(int)) != hipSuccess)
+        return 0;
       least = std::min(least, per_cu);
     }
     per_cu = least;
@@ -685,9 +738,9 @@ static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t b
   if (!q || !moments || !counts || !bits || !k || !v || !work || !features || !valid || !raw || !ids || !count ||
       !out)
     return kBadSize;
-  const int S = decode_splits(H);
+  const int S = decode_splits(groups);
   if (S > resident_workgroups()) return kBadSize;  // a group's workgroups must be resident together
-  const DecodeWorkLayout L(groups, decode_splits(capacity));
+  const DecodeWorkLayout L(groups, S);
   char* w = reinterpret_cast<char*>(work);
   DecodeArgs a;
   a.q = reinterpret_cast<const uint16_t*>(q);
@@ -718,10 +771,11 @@ static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t b
   a.out = reinterpret_cast<uint16_t*>(out);
   const dim3 grid(S, groups), block(kDT);
   hipStream_t s = (hipStream_t)stream;
-  if (S <= 32) hipLaunchKernelGGL(decode_kernel<1>, grid, block, 0, s, a);
-  else if (S <= 64) hipLaunchKernelGGL(decode_kernel<2>, grid, block, 0, s, a);
-  else if (S <= 128) hipLaunchKernelGGL(decode_kernel<4>, grid, block, 0, s, a);
-  else hipLaunchKernelGGL(decode_kernel<8>, grid, block, 0, s, a);
+  const size_t rows_bytes = (size_t)32 * a.tw * sizeof(int);  // the tile's row list (dynamic LDS)
+  if (S <= 32) hipLaunchKernelGGL(decode_kernel<1>, grid, block, rows_bytes, s, a);
+  else if (S <= 64) hipLaunchKernelGGL(decode_kernel<2>, grid, block, rows_bytes, s, a);
+  else if (S <= 128) hipLaunchKernelGGL(decode_kernel<4>, grid, block, rows_bytes, s, a);
+  else hipLaunchKernelGGL(decode_kernel<8>, grid, block, rows_bytes, s, a);
   return (int)hipGetLastError();
 }
 
@@ -729,7 +783,7 @@ extern "C" {
 
 size_t prismkv_decode_work_bytes(int groups, int capacity) {
   if (groups < 1 || capacity < 1) return 0;
-  return DecodeWorkLayout(groups, decode_splits(capacity)).total;
+  return DecodeWorkLayout(groups, decode_splits(groups)).total;
 }
 
 int prismkv_decode(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,

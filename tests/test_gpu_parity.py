@@ -145,8 +145,8 @@ def test_graph_replay_matches_eager():
 
 
 def test_no_tail_and_uneven_split_count():
-    # T = 0 (the step right after an index update) and H = 81920: 40 workgroups
-    # per group, 3 moment tiles each, 640 candidates per group
+    # T = 0 (the step right after an index update) and H = 81920: 80-word union
+    # tiles, two 64-word chunks per workgroup
     check_case(cases.native_case(4096, 0, "random", seed=7), splits_list=(32,), schedules=(0,))
     check_case(cases.native_case(81920, 9, "random", seed=8), splits_list=(64,), schedules=(0,))
 
@@ -159,9 +159,8 @@ def test_long_history_uses_split_path(monkeypatch):
     check_case(cases.native_case(1025, 3, "random"), splits_list=(32,), schedules=(0,))
 
 
-def test_fused_decode_beyond_128_splits():
-    # H = 300000: 147 workgroups per group, 8 candidate sets of 64 per wave in
-    # the single-launch selection
+def test_fused_decode_long_tiles():
+    # H = 300000: 293-word union tiles (5 chunks, 9376 tokens per workgroup)
     check_case(cases.native_case(300000, 3, "random", seed=9), splits_list=(128,), schedules=(0,))
 
 
@@ -213,3 +212,38 @@ def test_strict_unique_cap(H, tail, kind, cap):
     out = op(q, k, v)  # __call__ with a cap: same kernels, same bits
     torch.cuda.synchronize()
     assert np.array_equal(bf16_bits(out), first)
+
+
+@pytest.mark.parametrize("groups", [1, 2, 4])
+def test_fused_decode_fewer_groups(groups):
+    # prismkv_decode on the first `groups` groups runs 256 / groups workgroups
+    # per group (64 / 128 / 256 splits: 2, 4 or 8 candidate sets per wave in
+    # the selection); it selects exactly what the 8-group launch selects for
+    # those groups, and its attention is within tolerance of the oracle's
+    case = cases.native_case(16384, 40, "random", seed=13)
+    op, q, k, v = operator(case)
+    op(q, k, v)
+    torch.cuda.synchronize()
+    ref = route_outputs(op)
+    groups_want = expect.expected(case)
+    want = expect.expected_attention(case, groups_want)
+    work = torch.zeros(op.lib.query("prismkv_decode_work_bytes", groups, op.capacity), dtype=torch.uint8,
+                       device="cuda")
+    feats, valid, raw = torch.zeros_like(op.features), torch.zeros_like(op.valid), torch.zeros_like(op.raw)
+    ids, count, out = torch.zeros_like(op.ids), torch.zeros_like(op.count), torch.zeros_like(op.out)
+    op.lib.call("prismkv_decode", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(), op.bits.data_ptr(),
+                k.data_ptr(), v.data_ptr(), work.data_ptr(), feats.data_ptr(), valid.data_ptr(), raw.data_ptr(),
+                ids.data_ptr(), count.data_ptr(), out.data_ptr(), groups, op.history, k.shape[1] - op.history,
+                op.capacity, op.row_words, k.stride(0), v.stride(0), op.capacity,
+                stream=torch.cuda.current_stream().cuda_stream)
+    torch.cuda.synchronize()
+    assert int(work[:4].view(torch.int32)[0]) == 0  # no bounded wait gave up
+    got = (feats.cpu().numpy(), valid.cpu().numpy(), raw.cpu().numpy(), ids.cpu().numpy(), count.cpu().numpy())
+    for g in range(groups):
+        assert np.array_equal(got[0][g], ref[0][g]) and np.array_equal(got[1][g], ref[1][g]), g
+        assert got[2][g] == ref[2][g] and got[4][g] == ref[4][g], g
+        assert np.array_equal(got[3][g][:got[4][g]], ref[3][g][:ref[4][g]]), g
+    err = expect.attention_errors(bf16_bits(out)[:groups], want[:groups])
+    log(f"  groups={groups}: {err}")
+    assert err["rel_l2"] <= AV_TOL and err["max_abs"] < 0.05, err
+
