@@ -159,7 +159,22 @@ def stage_bytes(ops, H, T):
 
 
 @torch.no_grad()
-def update_timing(lib_path, H, blocks, steps, warmup, seed, device):
+def update_cpu_baseline(h0, center, counts, mean, var, keys, W, b, budget_s):
+    """C oracle append_index (src/prismkv/core.py:186-201) of one group's block,
+    one thread: (median us, repetitions)."""
+    import oracle
+    oracle.build()
+    index = oracle.Index(h0, center, counts, mean, var, [np.zeros(0, np.int64)] * F)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or not times:
+        t0 = time.perf_counter()
+        oracle.append_index(index, keys, W, b, 1.0, 8)
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)) * 1e6, len(times)
+
+
+def update_timing(lib_path, H, blocks, steps, warmup, seed, device, cpu_budget_s=0.0):
     """Amortised index update: one prismkv_update launch sequence per replay
     (encode, BatchTopK threshold, bitmap append, moment merge for 8 groups),
     indexing a block of N keys at history H - N of a dedicated table (so the
@@ -196,6 +211,16 @@ def update_timing(lib_path, H, blocks, steps, warmup, seed, device):
         out[str(N)] = dict(us_per_block=round(us, 2), us_per_token_per_layer=round(us / N, 4),
                            encode_gflop=round(flops / 1e9, 2), encode_tflops_if_alone=round(flops / (us * 1e-6) / 1e12, 2))
         log(f"update N={N}: {us:.1f} us per block ({us / N:.3f} us per token per layer, amortised)")
+        if cpu_budget_s > 0 and N == min(blocks):
+            c_us, reps = update_cpu_baseline(h0, op.center[0].cpu().numpy(), counts[0].cpu().numpy(),
+                                             mean[0].cpu().numpy(), var[0].cpu().numpy(),
+                                             k[0, h0:H].float().cpu().numpy(), W[0].cpu().numpy(),
+                                             b[0].cpu().numpy(), cpu_budget_s)
+            out[str(N)]["cpu_baseline"] = dict(
+                value=round(c_us * G, 1), unit="us/block (8 groups)", cores=1, kind="port",
+                sample=f"C oracle append_index of group 0's {N}-key block (encode, BatchTopK, summaries, Chan "
+                       f"merge), one thread, median of {reps}; x8 for the 8 groups")
+            log(f"update N={N}: CPU oracle {c_us:.0f} us for one group ({reps} repetitions)")
         del op
     del k, W, b
     torch.cuda.empty_cache()
@@ -360,7 +385,8 @@ def main():
     update = None
     if "update" in stages:
         blocks = [int(x) for x in a.update_blocks.split(",") if x]
-        update = update_timing(lib_path, H, blocks, a.steps, a.warmup, a.seed, device)
+        update = update_timing(lib_path, H, blocks, a.steps, a.warmup, a.seed, device,
+                               cpu_budget_s=0.0 if a.no_cpu_baseline else 3.0)
     build = build_timing(lib_path, H, a.steps, a.warmup, a.seed, device) if "build" in stages else None
     fused = [n for n in ("decode",) if n in stage_report]
     dominant = max(fused or stage_report, key=lambda n: stage_report[n]["us_per_launch"]) if stage_report else None
