@@ -507,11 +507,22 @@ __global__ __launch_bounds__(kUT) void moments_kernel(UpdateArgs a) {
   const int na = a.counts[(size_t)g * kFP + f], nbn = nb[col];
   const float fa = (float)na, fb = (float)nbn;
   const float total = fa + fb, den = total < 1.f ? 1.f : total;
-  for (int k = tid >> 5; k < kD; k += kUT / kChunk) {
-    const float ma = tile[k * kChunk + col], va = tile[(kD + k) * kChunk + col];
+  // every old mean and variance of the thread's 16 dims is requested before
+  // the first merge, so the tile costs one memory round trip
+  constexpr int kRowsPerThread = kD / (kUT / kChunk);  // 16
+  float ma[kRowsPerThread], va[kRowsPerThread];
+#pragma unroll
+  for (int i = 0; i < kRowsPerThread; ++i) {
+    const int k = (tid >> 5) + (kUT / kChunk) * i;
+    ma[i] = tile[k * kChunk + col];
+    va[i] = tile[(kD + k) * kChunk + col];
+  }
+#pragma unroll
+  for (int i = 0; i < kRowsPerThread; ++i) {
+    const int k = (tid >> 5) + (kUT / kChunk) * i;
     const float mb = nm[col][k], vb = nv[col][k];
-    tile[k * kChunk + col] = merge_mean(fa, fb, den, ma, mb);
-    tile[(kD + k) * kChunk + col] = merge_var(fa, fb, den, ma, mb, va, vb);
+    tile[k * kChunk + col] = merge_mean(fa, fb, den, ma[i], mb);
+    tile[(kD + k) * kChunk + col] = merge_var(fa, fb, den, ma[i], mb, va[i], vb);
   }
   if (tid < kChunk) a.counts[(size_t)g * kFP + f] = na + nbn;
 }
