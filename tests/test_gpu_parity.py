@@ -10,7 +10,7 @@ import torch
 
 import oracle
 from oracle import cases, expect
-from tests.gpu_util import bf16_bits, log, operator, route_outputs
+from tests.gpu_util import bf16_bits, device_layer, log, operator, route_outputs
 
 pytestmark = pytest.mark.gpu
 
@@ -162,6 +162,35 @@ def test_long_history_uses_split_path(monkeypatch):
 def test_fused_decode_long_tiles():
     # H = 300000: 293-word union tiles (5 chunks, 9376 tokens per workgroup)
     check_case(cases.native_case(300000, 3, "random", seed=9), splits_list=(128,), schedules=(0,))
+
+
+def test_fused_decode_one_word_second_chunk():
+    # H = 65537: 65-word union tiles, the second chunk of each one word long
+    check_case(cases.native_case(65537, 5, "ties", seed=21), splits_list=(64,), schedules=(0,))
+
+
+def test_fused_decode_largest_history_matches_split_path():
+    # H = 524288, the single launch's limit: 512-word tiles (8 chunks, 16384
+    # tokens and 64 KB of row list per workgroup).  The oracle's case
+    # generator is too slow at this size, so the layer is built on the device
+    # and the single launch must select exactly what the separate route +
+    # union select (oracle-checked up to H = 300000) and attend within the
+    # same tolerance
+    op, q, k, v = device_layer(524288, 7, seed=3)
+    fused = bf16_bits(op(q, k, v).clone())
+    f1 = route_outputs(op)
+    op.route(q)
+    split = bf16_bits(op.attention(q, k, v).clone())
+    f2 = route_outputs(op)
+    for a, b in zip(f1[:3], f2[:3]):
+        assert np.array_equal(a, b)
+    assert np.array_equal(f1[4], f2[4])
+    for g in range(8):
+        assert np.array_equal(f1[3][g][:f1[4][g]], f2[3][g][:f2[4][g]]), g
+    rel = np.linalg.norm(oracle.bf16_to_f32(fused).astype(np.float64) - oracle.bf16_to_f32(split)) / \
+        np.linalg.norm(oracle.bf16_to_f32(split).astype(np.float64))
+    log(f"  H=524288: unique ids per group {f1[4].tolist()}, fused vs split relL2 {rel:.2e}")
+    assert rel <= AV_TOL and op.decode_errors() == 0
 
 
 def test_union_262k_history():
