@@ -110,7 +110,8 @@ int prismkv_attend(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t co
  * zero-filled once before first use; its first 32-bit word is the error word
  * (nonzero if a bounded inter-workgroup wait gave up).  The workgroups of one
  * group wait on each other: it returns -1 if one group's
- * max(32, ceil(H/2048)) workgroups cannot be resident on the device at once. */
+ * min(256, max(32, 256 / groups)) workgroups cannot be resident on the device
+ * at once. */
 size_t prismkv_decode_work_bytes(int groups, int capacity);
 int prismkv_decode(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
                    uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
