@@ -325,10 +325,10 @@ def main():
         for op, q, k, v in layers:
             op(q, k, v)
 
-    def route_only():  # moment scoring + Top-16 (Native8B.route also runs the union)
+    def route_only():  # moment scoring + Top-16, one launch (Native8B.route also runs the union)
         for op, q, k, v in layers:
-            op.lib.call("prismkv_route", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(),
-                        op.route_work.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(),
+            op.lib.call("prismkv_route_single", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(),
+                        op.decode_work.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(),
                         op.raw.data_ptr(), G, stream=stream())
 
     def union_only():

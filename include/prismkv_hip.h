@@ -72,6 +72,14 @@ int attention_tuned(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t c
 size_t prismkv_route_work_bytes(int groups);
 int prismkv_route(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
                   uint64_t valid, uint64_t raw, int groups, uint64_t stream);
+/* Stage 1 in ONE launch (the same replacement and semantics as prismkv_route,
+ * identical features / valid / raw): the selection phases of prismkv_decode
+ * alone.  `work` is prismkv_decode's workspace (prismkv_decode_work_bytes,
+ * zero-filled once; the launch leaves it zero) and its first 32-bit word the
+ * same error word; -1 when one group's workgroups cannot be resident at once,
+ * as for prismkv_decode. */
+int prismkv_route_single(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
+                         uint64_t valid, uint64_t raw, int groups, uint64_t stream);
 
 /* Stage 2 (replaces launch_union_warp, src/prismkv/native8b.py:88-89;
  * semantics kernels/ppu_8b/union.cu:14-27): one launch, any H up to 2^29. */

@@ -301,8 +301,9 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int g, int h, i
 // usually among them.  Once the ranks are known, each wave ORs the rows of its
 // prefetched keys that won into lds.sel.ors[w] and marks their ranks in
 // lds.cover[w]; the union loads only the winners no wave prefetched.
+// Without kUnion (the route-only launch) nothing is prefetched.
 constexpr int kPrefetch = 6;
-template <int KW>
+template <int KW, bool kUnion = true>
 __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, DecodeLds& lds) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int nk = a.S * kTop;
@@ -330,7 +331,7 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, D
 #pragma unroll
   for (int r = 0; r < kPrefetch; ++r) {
     pk[r] = readlane_u64(best, r);  // rank r of this wave's list (uniform)
-    pw[r] = pk[r] ? __builtin_nontemporal_load(gb + (size_t)key_bucket(pk[r]) * a.row_words) : 0u;
+    pw[r] = (kUnion && pk[r]) ? __builtin_nontemporal_load(gb + (size_t)key_bucket(pk[r]) * a.row_words) : 0u;
   }
   __syncthreads();
   constexpr int kListed = kDT / 64 * kTop;  // 128
@@ -373,8 +374,9 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, D
 }
 
 // Phases 1-4: the group's Top-16 (rank order) into lds.win (every wave) and
-// lds.sel_rows / lds.need (written and read by wave 0 only).
-template <int KW>
+// lds.sel_rows / lds.need (written and read by wave 0 only).  Without kUnion
+// only workgroup 0 runs phase 4.
+template <int KW, bool kUnion = true>
 __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p, DecodeLds& lds) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int S = a.S;
@@ -464,7 +466,10 @@ __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p,
     if (lane < kTop) st_dev(&a.cand[((size_t)g * S + p) * kTop + lane], ~best);
   }
   // ---- 4. the group's Top-16 from its S x 16 candidates, as they land
-  final_top16<KW>(a, g, p, lds);
+  if constexpr (!kUnion) {
+    if (p != 0) return;
+  }
+  final_top16<KW, kUnion>(a, g, p, lds);
 }
 
 // KW = 64-key candidate sets per wave, ceil(S / 32): one instantiation per
@@ -673,6 +678,25 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   }
 }
 
+// Stage 1 alone in one launch (the separate route of the capped and
+// compatibility paths): phases 1-4 as in decode_kernel, except that only
+// workgroup 0 ranks the group's candidates.  It writes features / valid /
+// raw and clears the group's statistics and candidates: every workgroup read
+// the statistics before publishing its candidates, and no other reads those,
+// so the workspace is all zero again when the launch ends.
+template <int KW>
+__global__ __launch_bounds__(kDT) void route_kernel(DecodeArgs a) {
+  const int p = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, w = tid >> 6;
+  __shared__ DecodeLds lds;
+  decode_select<KW, false>(a, g, p, lds);
+  if (p != 0) return;
+  if (w == 0)
+    write_selection(lds.win, lds.need, a.counts + (size_t)g * kFP, a.features + (size_t)g * kTop,
+                    a.valid + (size_t)g * kTop, a.raw + g);
+  for (int i = tid; i < kChunks * kHq; i += kDT) st_dev(&a.stats[(size_t)g * kChunks * kHq + i], 0ull);
+  for (int i = tid; i < a.S * kTop; i += kDT) st_dev(&a.cand[(size_t)g * a.S * kTop + i], 0ull);
+}
+
 }  // namespace
 }  // namespace prismkv
 
@@ -702,7 +726,9 @@ struct DecodeWorkLayout {
 
 // Workgroups of decode_kernel resident on device `dev` at once (CUs x blocks
 // per CU) with the largest row list (64 KB of dynamic LDS), queried once per
-// device; the instantiations are allowed that much dynamic LDS here.
+// device; the instantiations are allowed that much dynamic LDS here.  The
+// route-only kernels (no dynamic LDS) are counted at the same size, which
+// can only understate them.
 static int resident_workgroups() {
   static int cached[64] = {0};
   int dev = 0;
@@ -713,7 +739,9 @@ static int resident_workgroups() {
     // the instantiations differ only in the selection code; take the least resident
     int least = 1 << 30;
     const void* fns[] = {reinterpret_cast<const void*>(decode_kernel<1>), reinterpret_cast<const void*>(decode_kernel<2>),
-                         reinterpret_cast<const void*>(decode_kernel<4>), reinterpret_cast<const void*>(decode_kernel<8>)};
+                         reinterpret_cast<const void*>(decode_kernel<4>), reinterpret_cast<const void*>(decode_kernel<8>),
+                         reinterpret_cast<const void*>(route_kernel<1>),  reinterpret_cast<const void*>(route_kernel<2>),
+                         reinterpret_cast<const void*>(route_kernel<4>),  reinterpret_cast<const void*>(route_kernel<8>)};
     for (const void* fn : fns) {
       if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kTileTokens * (int)sizeof(int)) !=
           hipSuccess)
@@ -792,6 +820,37 @@ int prismkv_decode(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits,
                    int64_t ids_stride, uint64_t stream) {
   return decode_impl(q, moments, counts, bits, k, v, work, features, valid, raw, ids, count, out, nullptr, groups, H,
                      T, capacity, row_words, ks, vs, ids_stride, stream);
+}
+
+int prismkv_route_single(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
+                         uint64_t valid, uint64_t raw, int groups, uint64_t stream) {
+  if (groups < 1 || groups > 65535) return kBadSize;
+  if (!q || !moments || !counts || !work || !features || !valid || !raw) return kBadSize;
+  const int S = decode_splits(groups);
+  if (S > resident_workgroups()) return kBadSize;  // a group's workgroups must be resident together
+  const DecodeWorkLayout L(groups, S);
+  char* w = reinterpret_cast<char*>(work);
+  DecodeArgs a{};  // no bitmap, K/V, ids or split states: phases 1-4 only
+  a.q = reinterpret_cast<const uint16_t*>(q);
+  a.moments = reinterpret_cast<const float*>(moments);
+  a.counts = reinterpret_cast<const int*>(counts);
+  a.H = 1;
+  a.S = S;
+  a.stats = reinterpret_cast<unsigned long long*>(w + L.stats);
+  a.cand = reinterpret_cast<unsigned long long*>(w + L.cand);
+  a.status = reinterpret_cast<unsigned*>(w + L.status);
+  a.err = reinterpret_cast<unsigned*>(w + L.err);
+  a.state = reinterpret_cast<float*>(w + L.state);
+  a.features = reinterpret_cast<int64_t*>(features);
+  a.valid = reinterpret_cast<float*>(valid);
+  a.raw = reinterpret_cast<int*>(raw);
+  const dim3 grid(S, groups), block(kDT);
+  hipStream_t s = (hipStream_t)stream;
+  if (S <= 32) hipLaunchKernelGGL(route_kernel<1>, grid, block, 0, s, a);
+  else if (S <= 64) hipLaunchKernelGGL(route_kernel<2>, grid, block, 0, s, a);
+  else if (S <= 128) hipLaunchKernelGGL(route_kernel<4>, grid, block, 0, s, a);
+  else hipLaunchKernelGGL(route_kernel<8>, grid, block, 0, s, a);
+  return (int)hipGetLastError();
 }
 
 int prismkv_decode_tail(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,

@@ -252,8 +252,6 @@ class Native8B:
         self.count = torch.zeros(GROUPS, dtype=torch.int32, device=device)
         self.row_words = bitmap_row_words(self.capacity)
         self.bits = torch.zeros(GROUPS, FEATURES, self.row_words, dtype=torch.int32, device=device)
-        self.route_work = torch.zeros(self.lib.query("prismkv_route_work_bytes", GROUPS), dtype=torch.uint8,
-                                      device=device)
         self.union_work = torch.zeros(self.lib.query("prismkv_union_work_bytes", GROUPS, self.capacity),
                                       dtype=torch.uint8, device=device)
         self.state = torch.zeros(self.lib.query("prismkv_attend_work_bytes", GROUPS, ATTEND_SPLITS),
@@ -294,8 +292,9 @@ class Native8B:
                           self.query_scale.data_ptr(), self.n.data_ptr(), self.qact_work.data_ptr(),
                           self.features.data_ptr(), self.valid.data_ptr(), self.raw.data_ptr(), 0, GROUPS, stream=s)
         else:
-            self.lib.call("prismkv_route", q.data_ptr(), self.moments.data_ptr(), self.n.data_ptr(),
-                          self.route_work.data_ptr(), self.features.data_ptr(), self.valid.data_ptr(),
+            # one launch: the selection phases of the decode, on its workspace
+            self.lib.call("prismkv_route_single", q.data_ptr(), self.moments.data_ptr(), self.n.data_ptr(),
+                          self.decode_work.data_ptr(), self.features.data_ptr(), self.valid.data_ptr(),
                           self.raw.data_ptr(), GROUPS, stream=s)
         width = self.features.shape[1]
         if self.unique_cap is not None:

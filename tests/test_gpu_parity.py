@@ -193,6 +193,47 @@ def test_fused_decode_largest_history_matches_split_path():
     assert rel <= AV_TOL and op.decode_errors() == 0
 
 
+@pytest.mark.parametrize("H", [4096, 65536])
+def test_single_launch_route_matches_three_launch_route(H):
+    # prismkv_route_single (one launch, the decode's selection phases, on the
+    # decode workspace) against prismkv_route (scoring, parts, final): the same
+    # features, valid and raw bits, on repeated calls and after a decode on
+    # the same workspace (each launch leaves the workspace zero)
+    op, q, k, v = device_layer(H, 16, seed=11)
+    lib, s = op.lib, torch.cuda.current_stream().cuda_stream
+    work = torch.zeros(lib.query("prismkv_route_work_bytes", 8), dtype=torch.uint8, device="cuda")
+
+    def three():
+        lib.call("prismkv_route", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(), work.data_ptr(),
+                 op.features.data_ptr(), op.valid.data_ptr(), op.raw.data_ptr(), 8, stream=s)
+
+    def one():
+        lib.call("prismkv_route_single", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(),
+                 op.decode_work.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(), op.raw.data_ptr(), 8,
+                 stream=s)
+
+    def selection():
+        torch.cuda.synchronize()
+        out = [x.cpu().numpy().copy() for x in (op.features, op.valid, op.raw)]
+        for x in (op.features, op.valid, op.raw):
+            x.zero_()
+        return out
+
+    three()
+    want = selection()
+    for step in range(3):
+        one()
+        got = selection()
+        for a, b in zip(want, got):
+            assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), step
+        if step == 1:
+            op(q, k, v)
+            torch.cuda.synchronize()
+    assert int(op.decode_work.view(torch.int32)[0]) == 0
+    log(f"  H={H}: single-launch route equals the three-launch route over 3 calls; "
+        f"buckets of group 0: {want[0][0].tolist()}")
+
+
 def test_union_262k_history():
     # H beyond the reference union limit (131072): 8 groups x 262144 tokens
     check_case(cases.native_case(262144, 64, "random", seed=5), splits_list=(128,), schedules=(0,))
