@@ -136,6 +136,18 @@ int prismkv_decode_tail(uint64_t q, uint64_t moments, uint64_t counts, uint64_t 
                         uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
                         uint64_t out, uint64_t tail, int groups, int H, int max_tail, int capacity, int64_t row_words,
                         int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream);
+/* Stages 2-3 fused from a given selection (replaces launch_union_warp +
+ * attention_tuned, src/prismkv/native8b.py:88-89 and :100-101): ONE launch
+ * for the union and the sparse attention of prismkv_decode, over the
+ * selection in features / valid read as prismkv_union reads it (the valid
+ * entries with in-range bucket ids, in order; up to 16 per group), e.g. as
+ * prismkv_select_cap left it.  Writes the same ids / count as prismkv_union
+ * and the same out as prismkv_attend; features / valid / raw are not
+ * touched.  `work` is prismkv_decode's workspace; the limits and the -1 for
+ * a group that cannot be resident are prismkv_decode's. */
+int prismkv_union_attend(uint64_t q, uint64_t bits, uint64_t k, uint64_t v, uint64_t work, uint64_t features,
+                         uint64_t valid, uint64_t ids, uint64_t count, uint64_t out, int groups, int H, int T,
+                         int capacity, int64_t row_words, int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream);
 
 /* ---- stage 4: incremental index update ---------------------------------
  * append_index (src/prismkv/core.py:186-201) for all groups at once, on the

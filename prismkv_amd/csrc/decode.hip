@@ -473,8 +473,10 @@ __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p,
 }
 
 // KW = 64-key candidate sets per wave, ceil(S / 32): one instantiation per
-// range of S, so a launch carries only the selection code it runs.
-template <int KW>
+// range of S, so a launch carries only the selection code it runs.  With
+// kGiven the selection is not computed but read from features / valid (as
+// a strict unique cap leaves them) and phases 5-9 run on it.
+template <int KW, bool kGiven = false>
 __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   const int p = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   __shared__ DecodeLds lds;
@@ -485,11 +487,32 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   // ignored), so it has long landed when the attention first uses it.
   const int tail_word = ld_dev(a.tail_dev ? a.tail_dev : reinterpret_cast<const int*>(a.err));
 
-  // ---- 1-4. the group's Top-16
-  decode_select<KW>(a, g, p, lds);
-  if (p == 0 && w == 0)
-    write_selection(lds.win, lds.need, a.counts + (size_t)g * kFP, a.features + (size_t)g * kTop,
-                    a.valid + (size_t)g * kTop, a.raw + g);
+  if constexpr (kGiven) {
+    // ---- 1-4. the given selection: the valid, in-range buckets in order (an
+    // out-of-range id selects nothing, as in union_kernel); no row is
+    // prefetched, so the union loads every selected row
+    if (w == 0) {
+      bool ok = false;
+      int f = 0;
+      if (lane < kTop && a.valid[(size_t)g * kTop + lane] > 0.f) {
+        const int64_t fe = a.features[(size_t)g * kTop + lane];
+        ok = fe >= 0 && fe < kF;
+        f = (int)fe;
+      }
+      const unsigned long long m = __ballot(ok);
+      if (ok) lds.sel_rows[__popcll(m & ((1ull << lane) - 1ull))] = f;
+      if (lane == 0) lds.need = __popcll(m);
+    }
+    lds.sel.ors[w][lane] = 0u;
+    if (lane == 0) lds.cover[w] = 0u;
+    __syncthreads();
+  } else {
+    // ---- 1-4. the group's Top-16
+    decode_select<KW>(a, g, p, lds);
+    if (p == 0 && w == 0)
+      write_selection(lds.win, lds.need, a.counts + (size_t)g * kFP, a.features + (size_t)g * kTop,
+                      a.valid + (size_t)g * kTop, a.raw + g);
+  }
 
   // ---- 5. union tile: OR the selected rows over words [tw p, tw (p + 1)), compact.
   // One 64-word chunk (histories up to 64K at 8 groups): wave 0 ORs the rows
@@ -741,7 +764,11 @@ static int resident_workgroups() {
     const void* fns[] = {reinterpret_cast<const void*>(decode_kernel<1>), reinterpret_cast<const void*>(decode_kernel<2>),
                          reinterpret_cast<const void*>(decode_kernel<4>), reinterpret_cast<const void*>(decode_kernel<8>),
                          reinterpret_cast<const void*>(route_kernel<1>),  reinterpret_cast<const void*>(route_kernel<2>),
-                         reinterpret_cast<const void*>(route_kernel<4>),  reinterpret_cast<const void*>(route_kernel<8>)};
+                         reinterpret_cast<const void*>(route_kernel<4>),  reinterpret_cast<const void*>(route_kernel<8>),
+                         reinterpret_cast<const void*>(decode_kernel<1, true>),
+                         reinterpret_cast<const void*>(decode_kernel<2, true>),
+                         reinterpret_cast<const void*>(decode_kernel<4, true>),
+                         reinterpret_cast<const void*>(decode_kernel<8, true>)};
     for (const void* fn : fns) {
       if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kTileTokens * (int)sizeof(int)) !=
           hipSuccess)
@@ -758,13 +785,14 @@ static int resident_workgroups() {
 
 static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
                        uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
-                       uint64_t out, const int* tail_dev, int groups, int H, int T, int capacity, int64_t row_words,
-                       int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream) {
+                       uint64_t out, const int* tail_dev, bool given, int groups, int H, int T, int capacity,
+                       int64_t row_words, int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream) {
   if (groups < 1 || groups > 65535 || H < 1 || H > kFusedMaxHistory || T < 0 || capacity < H) return kBadSize;
   if (row_words < (H + 31) / 32 || ids_stride < H) return kBadSize;
   if (ks < (int64_t)(H + T) * kD || vs < (int64_t)(H + T) * kD) return kBadSize;
-  if (!q || !moments || !counts || !bits || !k || !v || !work || !features || !valid || !raw || !ids || !count ||
-      !out)
+  // a given selection needs neither the moment tables nor raw
+  if (!q || (!given && (!moments || !counts || !raw)) || !bits || !k || !v || !work || !features || !valid || !ids ||
+      !count || !out)
     return kBadSize;
   const int S = decode_splits(groups);
   if (S > resident_workgroups()) return kBadSize;  // a group's workgroups must be resident together
@@ -800,10 +828,17 @@ static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t b
   const dim3 grid(S, groups), block(kDT);
   hipStream_t s = (hipStream_t)stream;
   const size_t rows_bytes = (size_t)32 * a.tw * sizeof(int);  // the tile's row list (dynamic LDS)
-  if (S <= 32) hipLaunchKernelGGL(decode_kernel<1>, grid, block, rows_bytes, s, a);
-  else if (S <= 64) hipLaunchKernelGGL(decode_kernel<2>, grid, block, rows_bytes, s, a);
-  else if (S <= 128) hipLaunchKernelGGL(decode_kernel<4>, grid, block, rows_bytes, s, a);
-  else hipLaunchKernelGGL(decode_kernel<8>, grid, block, rows_bytes, s, a);
+  if (given) {
+    if (S <= 32) hipLaunchKernelGGL((decode_kernel<1, true>), grid, block, rows_bytes, s, a);
+    else if (S <= 64) hipLaunchKernelGGL((decode_kernel<2, true>), grid, block, rows_bytes, s, a);
+    else if (S <= 128) hipLaunchKernelGGL((decode_kernel<4, true>), grid, block, rows_bytes, s, a);
+    else hipLaunchKernelGGL((decode_kernel<8, true>), grid, block, rows_bytes, s, a);
+  } else {
+    if (S <= 32) hipLaunchKernelGGL(decode_kernel<1>, grid, block, rows_bytes, s, a);
+    else if (S <= 64) hipLaunchKernelGGL(decode_kernel<2>, grid, block, rows_bytes, s, a);
+    else if (S <= 128) hipLaunchKernelGGL(decode_kernel<4>, grid, block, rows_bytes, s, a);
+    else hipLaunchKernelGGL(decode_kernel<8>, grid, block, rows_bytes, s, a);
+  }
   return (int)hipGetLastError();
 }
 
@@ -818,8 +853,15 @@ int prismkv_decode(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits,
                    uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
                    uint64_t out, int groups, int H, int T, int capacity, int64_t row_words, int64_t ks, int64_t vs,
                    int64_t ids_stride, uint64_t stream) {
-  return decode_impl(q, moments, counts, bits, k, v, work, features, valid, raw, ids, count, out, nullptr, groups, H,
-                     T, capacity, row_words, ks, vs, ids_stride, stream);
+  return decode_impl(q, moments, counts, bits, k, v, work, features, valid, raw, ids, count, out, nullptr, false, groups,
+                     H, T, capacity, row_words, ks, vs, ids_stride, stream);
+}
+
+int prismkv_union_attend(uint64_t q, uint64_t bits, uint64_t k, uint64_t v, uint64_t work, uint64_t features,
+                         uint64_t valid, uint64_t ids, uint64_t count, uint64_t out, int groups, int H, int T,
+                         int capacity, int64_t row_words, int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream) {
+  return decode_impl(q, 0, 0, bits, k, v, work, features, valid, 0, ids, count, out, nullptr, true, groups, H, T,
+                     capacity, row_words, ks, vs, ids_stride, stream);
 }
 
 int prismkv_route_single(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
@@ -859,8 +901,8 @@ int prismkv_decode_tail(uint64_t q, uint64_t moments, uint64_t counts, uint64_t 
                         int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream) {
   if (!tail || tail % 4) return kBadSize;
   return decode_impl(q, moments, counts, bits, k, v, work, features, valid, raw, ids, count, out,
-                     reinterpret_cast<const int*>(tail), groups, H, max_tail, capacity, row_words, ks, vs, ids_stride,
-                     stream);
+                     reinterpret_cast<const int*>(tail), false, groups, H, max_tail, capacity, row_words, ks, vs,
+                     ids_stride, stream);
 }
 
 }  // extern "C"

@@ -282,6 +282,14 @@ class Native8B:
         self.__dict__["_unique_cap"] = cap
 
     def route(self, q):
+        width = self._select(q)
+        self.lib.call("prismkv_union_n", self.bits.data_ptr(), self.features.data_ptr(), self.valid.data_ptr(),
+                      self.union_work.data_ptr(), self.ids.data_ptr(), self.count.data_ptr(), GROUPS, self.history,
+                      self.row_words, self.capacity, width, stream=self._stream())
+
+    def _select(self, q):
+        """Stage 1 and the optional strict unique cap: features / valid / raw.
+        Returns the selection width (16, or 64 for the q_activation router)."""
         if tuple(q.shape) != (GROUPS, HEADS, DIM) or q.dtype != torch.bfloat16 or not q.is_contiguous():
             raise ValueError("contiguous BF16 Q[8,4,128] required")
         if q.device != self.out.device:
@@ -302,9 +310,7 @@ class Native8B:
             self.lib.call("prismkv_select_cap_n", self.bits.data_ptr(), self.n.data_ptr(), self.features.data_ptr(),
                           self.valid.data_ptr(), self.raw.data_ptr(), GROUPS, self.history, limit, self.row_words,
                           width, stream=s)
-        self.lib.call("prismkv_union_n", self.bits.data_ptr(), self.features.data_ptr(), self.valid.data_ptr(),
-                      self.union_work.data_ptr(), self.ids.data_ptr(), self.count.data_ptr(), GROUPS, self.history,
-                      self.row_words, self.capacity, width, stream=s)
+        return width
 
     @property
     def router(self):
@@ -374,6 +380,8 @@ class Native8B:
         """route + attention (src/prismkv/native8b.py:104-106) through the fused
         decode path: one launch, identical results, every output buffer
         (features, valid, raw, ids, count, out) written as by the two calls.
+        With a unique cap: the route and the budgeted walk, then the union and
+        the attention in one launch over the walked selection.
 
         `tail` (no reference counterpart): an int32 CUDA tensor of one element
         holding the tail length T, read by the kernel at launch instead of
@@ -397,12 +405,21 @@ class Native8B:
                           k.shape[1] - self.history, self.capacity, self.row_words, k.stride(0), v.stride(0),
                           self.capacity, stream=self._stream())
             return self.out
-        if self.unique_cap is not None or self.history > FUSED_MAX_HISTORY or self.router != "moments":
-            # the budgeted walk runs between selection and union; very long histories
-            # exceed one launch's group size; the q_activation router selects up to 64
-            # buckets
+        if self.history > FUSED_MAX_HISTORY or self.router != "moments":
+            # very long histories exceed one launch's group size; the q_activation
+            # router selects up to 64 buckets
             self.route(q)
             return self.attention(q, k, v, **kwargs)
+        if self.unique_cap is not None:
+            # the budgeted walk runs between selection and union: route and walk,
+            # then union + attention in one launch on the walked selection
+            self._select(q)
+            self.lib.call("prismkv_union_attend", q.data_ptr(), self.bits.data_ptr(), k.data_ptr(), v.data_ptr(),
+                          self.decode_work.data_ptr(), self.features.data_ptr(), self.valid.data_ptr(),
+                          self.ids.data_ptr(), self.count.data_ptr(), self.out.data_ptr(), GROUPS, self.history,
+                          k.shape[1] - self.history, self.capacity, self.row_words, k.stride(0), v.stride(0),
+                          self.capacity, stream=self._stream())
+            return self.out
         self.lib.call("prismkv_decode", q.data_ptr(), self.moments.data_ptr(), self.n.data_ptr(), self.bits.data_ptr(),
                       k.data_ptr(), v.data_ptr(), self.decode_work.data_ptr(), self.features.data_ptr(),
                       self.valid.data_ptr(), self.raw.data_ptr(), self.ids.data_ptr(), self.count.data_ptr(),

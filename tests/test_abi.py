@@ -87,6 +87,9 @@ def test_native_error_codes(lib):
     assert call_raw(lib, "prismkv_route", *[1] * 7, 0) == -1          # no groups
     assert call_raw(lib, "prismkv_route_single", *[0] * 7, 8) == -1   # null pointers
     assert call_raw(lib, "prismkv_route_single", *[1] * 7, 0) == -1   # no groups
+    assert call_raw(lib, "prismkv_union_attend", *[0] * 10, 8, 100, 4, 100, 4, 104 * 128, 104 * 128, 100) == -1
+    assert call_raw(lib, "prismkv_union_attend", *[1] * 10, 8, 0, 4, 100, 4, 104 * 128, 104 * 128, 100) == -1
+    assert call_raw(lib, "prismkv_union_attend", *[1] * 10, 8, 100, 4, 100, 4, 103 * 128, 104 * 128, 100) == -1
     assert call_raw(lib, "prismkv_union", *[1] * 6, 8, 0, 1, 1) == -1  # H < 1
     assert call_raw(lib, "prismkv_union", *[1] * 6, 8, 100, 3, 100) == -1  # row_words too small
     assert call_raw(lib, "prismkv_union", *[1] * 6, 8, 100, 4, 99) == -1   # ids stride too small

@@ -279,9 +279,22 @@ def test_strict_unique_cap(H, tail, kind, cap):
     first = bf16_bits(out).copy()
     err = expect.attention_errors(first, expected)
     assert err["rel_l2"] <= AV_TOL and err["max_abs"] < 0.05, err
-    out = op(q, k, v)  # __call__ with a cap: same kernels, same bits
+    # __call__ with a cap: route and walk, then union + attention in one
+    # launch (prismkv_union_attend) over the walked selection: the same
+    # selection, ids and count, and the attention within the same bound
+    op.ids.zero_()
+    op.count.zero_()
+    out = op(q, k, v)
     torch.cuda.synchronize()
-    assert np.array_equal(bf16_bits(out), first)
+    f3, v3, r3, i3, c3 = route_outputs(op)
+    for a, b in ((f2, f3), (v2, v3), (r2, r3), (c2, c3)):
+        assert np.array_equal(a, b)
+    for g in range(8):
+        assert np.array_equal(i3[g][:c3[g]], i2[g][:c2[g]]), ("ids, one launch", g)
+    err = expect.attention_errors(bf16_bits(out), expected)
+    log(f"  capped call, union + attention in one launch: {err}")
+    assert err["rel_l2"] <= AV_TOL and err["max_abs"] < 0.05, err
+    assert op.decode_errors() == 0
 
 
 @pytest.mark.parametrize("groups", [1, 2, 4])
