@@ -378,8 +378,9 @@ class Native8B:
 
     def __call__(self, q, k, v, *, tail=None, **kwargs):
         """route + attention (src/prismkv/native8b.py:104-106) through the fused
-        decode path: one launch, identical results, every output buffer
-        (features, valid, raw, ids, count, out) written as by the two calls.
+        decode path: one launch, every output buffer (features, valid, raw,
+        ids, count, out) written as by the two calls -- the selection and ids
+        bit-identical, out within rounding of the separate attention kernel.
         With a unique cap: the route and the budgeted walk, then the union and
         the attention in one launch over the walked selection.
 
