@@ -267,53 +267,69 @@ __global__ __launch_bounds__(256) void bits_kernel(const int* __restrict__ ids, 
 // One workgroup of kCapT threads per group.  Thread tid owns bitmap words
 // tid + kCapT u (u < WPT) of every row and keeps its slice of the running
 // union in registers; each bucket costs one block-wide popcount reduction.
-// With kAhead the next bucket's words are requested before the current
-// bucket's reduction, so the row loads overlap the decisions.
-template <int kCapT, int WPT, bool kAhead, int kSel>
+// The walk's loop issues no load whose value it waits for at once: wave 0
+// compacts the selection and stages the buckets' sizes in LDS first; every
+// row load is unconditional (clamped address, the word mask applied where
+// the word is used), kAhead rows ahead, into kAhead + 1 register sets that
+// rotate by name (a copy would wait for the load), so each decision waits
+// only for its own row, requested kAhead decisions earlier: one workgroup
+// streams its group's rows, so rows in flight set its pace.
+template <int kCapT, int WPT, int kSel>
 __global__ __launch_bounds__(kCapT) void cap_kernel(const uint32_t* __restrict__ bits, int64_t row_words,
                                                     const int* __restrict__ counts, int64_t* features, float* valid,
                                                     int* raw, int H, long long limit) {
   const int g = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  __shared__ int sel[kSel], nsel_s;
+  __shared__ int sel[kSel], size[kSel], nsel_s;
   __shared__ int part[2][kCapT / 64];
-  if (tid == 0) {
-    int n = 0;
-    for (int j = 0; j < kSel; ++j) {
-      const int64_t f = features[(size_t)g * kSel + j];
-      if (valid[(size_t)g * kSel + j] > 0.f && f >= 0 && f < kF) sel[n++] = (int)f;
+  if (w == 0) {
+    // the valid, in-range selections in rank order (an out-of-range id selects nothing)
+    const int j = lane < kSel ? lane : kSel - 1;
+    const int64_t fe = features[(size_t)g * kSel + j];
+    const float va = valid[(size_t)g * kSel + j];
+    const bool ok = lane < kSel && va > 0.f && fe >= 0 && fe < kF;
+    const int f = ok ? (int)fe : 0;
+    const int cnt = counts[(size_t)g * kFP + f];
+    const unsigned long long m = __ballot(ok);
+    if (ok) {
+      const int at = __popcll(m & ((1ull << lane) - 1ull));
+      sel[at] = f;
+      size[at] = cnt;
     }
-    nsel_s = n;
+    if (lane == 0) nsel_s = __popcll(m);
   }
   __syncthreads();
   const int n = nsel_s;
   const int nw = (H + 31) >> 5;
   const uint32_t tail_mask = (H & 31) ? (1u << (H & 31)) - 1u : ~0u;
   const uint32_t* bg = bits + (size_t)g * kF * row_words;
-  auto load_row = [&](int j, uint32_t (&r)[WPT]) {
-    const uint32_t* row = bg + (size_t)sel[j] * row_words;
+  uint32_t wmask[WPT];
+  unsigned wcol[WPT];  // unsigned: scalar base + 32-bit offset addressing
 #pragma unroll
-    for (int u = 0; u < WPT; ++u) {
-      const int wd = tid + u * kCapT;
-      const uint32_t m = wd < nw ? row[wd] : 0u;
-      r[u] = wd == nw - 1 ? (m & tail_mask) : m;
-    }
+  for (int u = 0; u < WPT; ++u) {
+    const int wd = tid + u * kCapT;
+    wmask[u] = wd < nw ? (wd == nw - 1 ? tail_mask : ~0u) : 0u;
+    wcol[u] = (unsigned)(wd < nw ? wd : nw - 1);
+  }
+  auto load_row = [&](int j, uint32_t (&r)[WPT]) {  // row j (clamped to the last bucket), words unmasked
+    // the bucket is uniform: a scalar row base, so each load needs only its word offset
+    const int b = __builtin_amdgcn_readfirstlane(sel[j < n ? j : n - 1]);
+    const uint32_t* row = bg + (size_t)b * row_words;
+#pragma unroll
+    for (int u = 0; u < WPT; ++u) r[u] = __builtin_nontemporal_load(row + wcol[u]);
   };
-  uint32_t chosen[WPT], cur[WPT], nxt[WPT];
+  constexpr int kAhead = WPT >= 8 ? 3 : 7;  // as many rows as the registers hold without spilling
+  uint32_t chosen[WPT], rs[kAhead + 1][WPT];
 #pragma unroll
-  for (int u = 0; u < WPT; ++u) chosen[u] = cur[u] = nxt[u] = 0u;
-  if (kAhead && n > 0) load_row(0, cur);
+  for (int u = 0; u < WPT; ++u) chosen[u] = 0u;
   long long total = 0;
   int raw_sum = 0;
   unsigned long long accepted = 0;
-  for (int j = 0; j < n; ++j) {
-    if (kAhead) {
-      if (j + 1 < n) load_row(j + 1, nxt);
-    } else {
-      load_row(j, cur);
-    }
+  // decision j on row `cur` (none for j >= n), requesting row j + kAhead into `fill`
+  auto step = [&](int j, uint32_t (&cur)[WPT], uint32_t (&fill)[WPT]) {
+    load_row(j + kAhead, fill);
     int c = 0;
 #pragma unroll
-    for (int u = 0; u < WPT; ++u) c += __popc(cur[u] & ~chosen[u]);
+    for (int u = 0; u < WPT; ++u) c += __popc(cur[u] & wmask[u] & ~chosen[u]);
     c = wave_sum_i(c);
     if (lane == 0) part[j & 1][w] = c;
     __syncthreads();
@@ -321,16 +337,23 @@ __global__ __launch_bounds__(kCapT) void cap_kernel(const uint32_t* __restrict__
     long long add = 0;
 #pragma unroll
     for (int i = 0; i < kCapT / 64; ++i) add += part[j & 1][i];
-    if (total + add <= limit) {  // uniform: every thread holds the same sums
+    if (j < n && total + add <= limit) {  // uniform: every thread holds the same sums
 #pragma unroll
-      for (int u = 0; u < WPT; ++u) chosen[u] |= cur[u];
+      for (int u = 0; u < WPT; ++u) chosen[u] |= cur[u] & wmask[u];
       total += add;
-      raw_sum += counts[(size_t)g * kFP + sel[j]];
+      raw_sum += size[j];
       accepted |= 1ull << j;
     }
-    if (kAhead) {
+  };
+  if (n > 0) {
 #pragma unroll
-      for (int u = 0; u < WPT; ++u) cur[u] = nxt[u];
+    for (int i = 0; i < kAhead; ++i) load_row(i, rs[i]);
+    // all kAhead + 1 steps of a round run (n is uniform; steps past n decide
+    // nothing and their rows repeat the last one), so no row load is left
+    // pending where branches join; size[] is read only for j < n
+    for (int j = 0; j < n; j += kAhead + 1) {
+#pragma unroll
+      for (int i = 0; i <= kAhead; ++i) step(j + i, rs[i], rs[(i + kAhead) % (kAhead + 1)]);
     }
   }
   if (tid == 0) {
@@ -432,10 +455,10 @@ static void launch_cap(const uint32_t* b, int64_t row_words, const int* c, int64
                        int H, long long lim, hipStream_t s) {
   const int nw = (H + 31) / 32;
   if (nw <= 2 * 1024)
-    hipLaunchKernelGGL((cap_kernel<1024, 2, true, kSel>), dim3(groups), dim3(1024), 0, s, b, row_words, c, f, v, r, H,
+    hipLaunchKernelGGL((cap_kernel<1024, 2, kSel>), dim3(groups), dim3(1024), 0, s, b, row_words, c, f, v, r, H,
                        lim);
   else if (nw <= 8 * 1024)
-    hipLaunchKernelGGL((cap_kernel<1024, 8, true, kSel>), dim3(groups), dim3(1024), 0, s, b, row_words, c, f, v, r, H,
+    hipLaunchKernelGGL((cap_kernel<1024, 8, kSel>), dim3(groups), dim3(1024), 0, s, b, row_words, c, f, v, r, H,
                        lim);
   else  // up to 2^20 tokens
     hipLaunchKernelGGL(cap_big_kernel<kSel>, dim3(groups), dim3(kCapBigT), 0, s, b, row_words, c, f, v, r, H, lim);
