@@ -264,11 +264,26 @@ __global__ __launch_bounds__(256) void bits_kernel(const int* __restrict__ ids, 
 // features / valid / raw with the accepted buckets compacted to the front in
 // rank order (unused slots id 0, valid 0), which the union then consumes.
 //
+// Sum of v over the 64 lanes of a wave through DPP moves (no LDS round
+// trips): pairs, quads (quad_perm), 8 (row_half_mirror), 16 (row_mirror),
+// then row 0 into row 1 and row 2 into row 3 (row_bcast:15), rows 0-1 into
+// rows 2-3 (row_bcast:31); lane 63 holds the total.
+__device__ __forceinline__ int wave_sum_dpp(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+  v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+  v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);  // row_mirror
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2, 3
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
 // One workgroup of kCapT threads per group.  Thread tid owns bitmap words
 // tid + kCapT u (u < WPT) of every row and keeps its slice of the running
 // union in registers; each bucket costs one block-wide popcount reduction.
 // The walk's loop issues no load whose value it waits for at once: wave 0
-// compacts the selection and stages the buckets' sizes in LDS first; every
+// compacts the selection into LDS first (each lane keeps its bucket's size,
+// requested then and summed for raw after the walk); every
 // row load is unconditional (clamped address, the word mask applied where
 // the word is used), kAhead rows ahead, into kAhead + 1 register sets that
 // rotate by name (a copy would wait for the load), so each decision waits
@@ -279,22 +294,22 @@ __global__ __launch_bounds__(kCapT) void cap_kernel(const uint32_t* __restrict__
                                                     const int* __restrict__ counts, int64_t* features, float* valid,
                                                     int* raw, int H, long long limit) {
   const int g = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  __shared__ int sel[kSel], size[kSel], nsel_s;
+  __shared__ int sel[kSel], nsel_s;
   __shared__ int part[2][kCapT / 64];
+  // wave 0, lane j < kSel: ranked entry j, its rank among the valid ones and its size
+  bool ok = false;
+  int at = 0, cnt = 0;
   if (w == 0) {
     // the valid, in-range selections in rank order (an out-of-range id selects nothing)
     const int j = lane < kSel ? lane : kSel - 1;
     const int64_t fe = features[(size_t)g * kSel + j];
     const float va = valid[(size_t)g * kSel + j];
-    const bool ok = lane < kSel && va > 0.f && fe >= 0 && fe < kF;
+    ok = lane < kSel && va > 0.f && fe >= 0 && fe < kF;
     const int f = ok ? (int)fe : 0;
-    const int cnt = counts[(size_t)g * kFP + f];
+    cnt = counts[(size_t)g * kFP + f];  // used after the walk
     const unsigned long long m = __ballot(ok);
-    if (ok) {
-      const int at = __popcll(m & ((1ull << lane) - 1ull));
-      sel[at] = f;
-      size[at] = cnt;
-    }
+    at = __popcll(m & ((1ull << lane) - 1ull));
+    if (ok) sel[at] = f;
     if (lane == 0) nsel_s = __popcll(m);
   }
   __syncthreads();
@@ -322,7 +337,6 @@ __global__ __launch_bounds__(kCapT) void cap_kernel(const uint32_t* __restrict__
 #pragma unroll
   for (int u = 0; u < WPT; ++u) chosen[u] = 0u;
   long long total = 0;
-  int raw_sum = 0;
   unsigned long long accepted = 0;
   // decision j on row `cur` (none for j >= n), requesting row j + kAhead into `fill`
   auto step = [&](int j, uint32_t (&cur)[WPT], uint32_t (&fill)[WPT]) {
@@ -330,7 +344,7 @@ __global__ __launch_bounds__(kCapT) void cap_kernel(const uint32_t* __restrict__
     int c = 0;
 #pragma unroll
     for (int u = 0; u < WPT; ++u) c += __popc(cur[u] & wmask[u] & ~chosen[u]);
-    c = wave_sum_i(c);
+    c = wave_sum_dpp(c);
     if (lane == 0) part[j & 1][w] = c;
     __syncthreads();
     // part[j & 1] is rewritten two buckets later, after the next barrier
@@ -341,7 +355,6 @@ __global__ __launch_bounds__(kCapT) void cap_kernel(const uint32_t* __restrict__
 #pragma unroll
       for (int u = 0; u < WPT; ++u) chosen[u] |= cur[u] & wmask[u];
       total += add;
-      raw_sum += size[j];
       accepted |= 1ull << j;
     }
   };
@@ -350,21 +363,24 @@ __global__ __launch_bounds__(kCapT) void cap_kernel(const uint32_t* __restrict__
     for (int i = 0; i < kAhead; ++i) load_row(i, rs[i]);
     // all kAhead + 1 steps of a round run (n is uniform; steps past n decide
     // nothing and their rows repeat the last one), so no row load is left
-    // pending where branches join; size[] is read only for j < n
+    // pending where branches join
     for (int j = 0; j < n; j += kAhead + 1) {
 #pragma unroll
       for (int i = 0; i <= kAhead; ++i) step(j + i, rs[i], rs[(i + kAhead) % (kAhead + 1)]);
     }
   }
-  if (tid == 0) {
-    int at = 0;
-    for (int j = 0; j < n; ++j)
-      if (accepted >> j & 1ull) features[(size_t)g * kSel + at++] = sel[j];
-    for (int j = 0; j < kSel; ++j) {
-      if (j >= at) features[(size_t)g * kSel + j] = 0;
-      valid[(size_t)g * kSel + j] = j < at ? 1.f : 0.f;
+  if (w == 0) {
+    const int raw_sum = wave_sum_dpp(ok && (accepted >> at & 1ull) ? cnt : 0);
+    if (lane == 0) {
+      int kept = 0;
+      for (int j = 0; j < n; ++j)
+        if (accepted >> j & 1ull) features[(size_t)g * kSel + kept++] = sel[j];
+      for (int j = 0; j < kSel; ++j) {
+        if (j >= kept) features[(size_t)g * kSel + j] = 0;
+        valid[(size_t)g * kSel + j] = j < kept ? 1.f : 0.f;
+      }
+      raw[g] = raw_sum;
     }
-    raw[g] = raw_sum;
   }
 }
 
