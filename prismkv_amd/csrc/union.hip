@@ -332,7 +332,7 @@ __global__ __launch_bounds__(kCapT) void cap_kernel(const uint32_t* __restrict__
 #pragma unroll
     for (int u = 0; u < WPT; ++u) r[u] = __builtin_nontemporal_load(row + wcol[u]);
   };
-  constexpr int kAhead = WPT >= 8 ? 3 : 7;  // as many rows as the registers hold without spilling
+  constexpr int kAhead = WPT >= 16 ? 3 : 7;  // as many rows as the registers hold without spilling
   uint32_t chosen[WPT], rs[kAhead + 1][WPT];
 #pragma unroll
   for (int u = 0; u < WPT; ++u) chosen[u] = 0u;
@@ -470,12 +470,12 @@ template <int kSel>
 static void launch_cap(const uint32_t* b, int64_t row_words, const int* c, int64_t* f, float* v, int* r, int groups,
                        int H, long long lim, hipStream_t s) {
   const int nw = (H + 31) / 32;
-  if (nw <= 2 * 1024)
-    hipLaunchKernelGGL((cap_kernel<1024, 2, kSel>), dim3(groups), dim3(1024), 0, s, b, row_words, c, f, v, r, H,
-                       lim);
-  else if (nw <= 8 * 1024)
-    hipLaunchKernelGGL((cap_kernel<1024, 8, kSel>), dim3(groups), dim3(1024), 0, s, b, row_words, c, f, v, r, H,
-                       lim);
+  // 512 threads: half the waves to synchronise per decision, and the
+  // registers for 16 words per thread
+  if (nw <= 4 * 512)
+    hipLaunchKernelGGL((cap_kernel<512, 4, kSel>), dim3(groups), dim3(512), 0, s, b, row_words, c, f, v, r, H, lim);
+  else if (nw <= 16 * 512)
+    hipLaunchKernelGGL((cap_kernel<512, 16, kSel>), dim3(groups), dim3(512), 0, s, b, row_words, c, f, v, r, H, lim);
   else  // up to 2^20 tokens
     hipLaunchKernelGGL(cap_big_kernel<kSel>, dim3(groups), dim3(kCapBigT), 0, s, b, row_words, c, f, v, r, H, lim);
 }
