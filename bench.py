@@ -16,9 +16,10 @@ in a HIP graph and replayed.  The headline value is the replay time per
 layer in microseconds (lower is better); since every layer is one launch of
 the decode kernel, it is also that kernel's average launch time, which the
 roofline object divides the algorithmic bytes by.  The separate
-route/union/attend entry points are timed in isolated-stage graphs too.  The
-CPU baseline times the C oracle (single thread) on a bounded sample of the
-same layer workload.
+route (one launch) / union / attend entry points are timed in isolated-stage
+graphs too.  The CPU baseline times the C oracle on a bounded sample of the
+same layer workload: one KV group per host thread (8 threads), and on one
+thread beside it.
 """
 from __future__ import annotations
 
