@@ -9,6 +9,11 @@
 // padding rules of kernels/ppu_8b/route_parallel.cu:12,23,29 and the ascending
 // emission of kernels/ppu_8b/union.cu:26.
 //
+// Two more launches share these phases: route_kernel runs phases 1-4 alone
+// (prismkv_route_single), and decode_kernel<KW, true> runs phases 5-9 on a
+// selection read from features / valid (prismkv_union_attend, after a strict
+// unique cap has walked it).
+//
 // Grid (S, G) x 512, S = clamp(256 / G, 32, 256) (32 for 8 groups: the whole
 // launch is resident at once, one workgroup per CU, at any history).  Workgroup p
 // of group g owns the contiguous moment tiles kp .. kp + k - 1 of the 94
