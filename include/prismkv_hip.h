@@ -116,7 +116,8 @@ int prismkv_attend(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t co
  * prismkv_attend.  H <= 524288.  `work` is sized for the largest history the
  * caller will use (`capacity` >= H) by prismkv_decode_work_bytes and is
  * zero-filled once before first use; its first 32-bit word is the error word
- * (nonzero if a bounded inter-workgroup wait gave up).  The workgroups of one
+ * (nonzero if a bounded inter-workgroup wait gave up; see the bounded-wait
+ * section below).  The workgroups of one
  * group wait on each other: it returns -1 if one group's
  * min(256, max(32, 256 / groups)) workgroups cannot be resident on the device
  * at once. */
@@ -148,6 +149,26 @@ int prismkv_decode_tail(uint64_t q, uint64_t moments, uint64_t counts, uint64_t 
 int prismkv_union_attend(uint64_t q, uint64_t bits, uint64_t k, uint64_t v, uint64_t work, uint64_t features,
                          uint64_t valid, uint64_t ids, uint64_t count, uint64_t out, int groups, int H, int T,
                          int capacity, int64_t row_words, int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream);
+
+/* ---- bounded waits and their error words (no reference counterpart: the
+ * reference kernels never wait across workgroups) --------------------------
+ * Every inter-workgroup wait of prismkv_decode, prismkv_decode_tail,
+ * prismkv_union_attend, prismkv_route_single and prismkv_union gives up after
+ * a process-wide number of sleeps (64 clocks each; default 2^20, tens of
+ * milliseconds), writes 1 to its workspace's first 32-bit word (the sticky
+ * error word, cleared only by the caller) and lets the launch run to its end
+ * with every access in range; the results of such a launch are invalid and
+ * the workspace must be zero-filled again before the next launch.  If the
+ * workspace's 8-byte slot at byte offset 8 holds a nonzero device address (of
+ * a host-mapped 32-bit word, see prismkv_mapped_pointer), the wait also writes
+ * 1 there, so a host binding can notice it without synchronising.
+ * prismkv_set_spin_limit sets the bound for launches enqueued afterwards and
+ * returns the previous one (-1 for a negative limit). */
+int prismkv_set_spin_limit(int limit);
+int prismkv_get_spin_limit(void);
+/* The device address of a host pointer from hipHostMalloc (e.g. a pinned
+ * torch tensor), 0 if it is not device-accessible. */
+uint64_t prismkv_mapped_pointer(uint64_t host);
 
 /* ---- stage 4: incremental index update ---------------------------------
  * append_index (src/prismkv/core.py:186-201) for all groups at once, on the

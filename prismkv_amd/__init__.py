@@ -6,9 +6,9 @@ declared in `include/prismkv_hip.h`.  `prismkv_amd.weights` reads and writes
 the reference's encoder bundles; `prismkv_amd.hf.HFNative` is the Hugging
 Face decode backend over `Native8B` (imports transformers when used).
 """
-from .native8b import FeatureIndex, Native8B, compile_hip, tile_moments, untile_moments
+from .native8b import FeatureIndex, Native8B, compile_hip, set_spin_limit, tile_moments, untile_moments
 from ._lib import load as load_library
 from .weights import Encoder, SharedSAE, load_encoders, save_encoders
 
 __all__ = ["Encoder", "FeatureIndex", "Native8B", "SharedSAE", "compile_hip", "load_encoders", "load_library",
-           "save_encoders", "tile_moments", "untile_moments"]
+           "save_encoders", "set_spin_limit", "tile_moments", "untile_moments"]

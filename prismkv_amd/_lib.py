@@ -49,6 +49,10 @@ SIGNATURES = {
     "prismkv_route_qact": ([_U64] * 10 + [_I32], True, _I32),
     "prismkv_union_n": ([_U64] * 6 + [_I32, _I32, _I64, _I64, _I32], True, _I32),
     "prismkv_select_cap_n": ([_U64] * 5 + [_I32, _I32, _I64, _I64, _I32], True, _I32),
+    # error handling of the bounded inter-workgroup waits
+    "prismkv_set_spin_limit": ([_I32], False, _I32),
+    "prismkv_get_spin_limit": ([], False, _I32),
+    "prismkv_mapped_pointer": ([_U64], False, _U64),
 }
 
 _loaded: dict[str, "Library"] = {}

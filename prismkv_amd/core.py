@@ -382,6 +382,9 @@ def select_buckets(q, index, *, unique_cap=None, **kwargs):
     lib.call("prismkv_union_n", t.bits.data_ptr(), features.data_ptr(), valid.data_ptr(), work.data_ptr(),
              ids.data_ptr(), count.data_ptr(), 1, H, t.row_words, ids.shape[1], width, stream=_stream())
     n = int(count.item())
+    if int(work[:4].view(torch.int32).item()):  # a bounded wait of the union gave up
+        work.zero_()
+        raise RuntimeError("prismkv_union_n: a bounded inter-workgroup wait gave up; the workspace was reset")
     kept = features[0][valid[0] > 0].tolist()
     assert n <= limit
     return ids[0, :n].long(), dict(features=kept, raw=int(raw.item()), unique=n, limit=limit,

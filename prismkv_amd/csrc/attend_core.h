@@ -127,10 +127,7 @@ __device__ __forceinline__ void attend_step(const float (&qf)[kHq][8], const uin
 
 // Merges the 32 slot states of the workgroup in LDS and stores the result as
 // split state `stp` ((max, den, acc[128]) per head; head h at stp + h * hstride).
-// With `published`, every word holds the complement of the value's bits, so
-// a reader polling the words sees 0 until the store has landed.
-__device__ void store_wg_state(const SlotState& s, AttendLds& lds, float* stp, size_t hstride,
-                               bool published = false) {
+__device__ void store_wg_state(const SlotState& s, AttendLds& lds, float* stp, size_t hstride) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, q16 = lane & 15, slot = lane >> 4;
   __syncthreads();  // LDS shared with the caller's earlier phases is free again
   // gather the slot's per-head max / denominator into every lane
@@ -178,64 +175,27 @@ __device__ void store_wg_state(const SlotState& s, AttendLds& lds, float* stp, s
       v = fmaf(wgt, lds.red.sacc[k][h][d], v);
     }
     float* sh = stp + (size_t)h * hstride;
-    if (published) {
-      if (d == 0)
-        st_dev(reinterpret_cast<unsigned long long*>(sh),
-               ~(((unsigned long long)__float_as_uint(den) << 32) | (unsigned long long)__float_as_uint(M)));
-      st_dev(reinterpret_cast<unsigned*>(sh + 2 + d), ~__float_as_uint(v));
-    } else {
-      if (d == 0) st_dev2(sh, M, den);
-      st_dev(sh + 2 + d, v);
-    }
+    if (d == 0) st_dev2(sh, M, den);
+    st_dev(sh + 2 + d, v);
   }
 }
 
 // Merges the S split states of group g into out[g] (thread = head tid >> 7,
 // dim tid & 127).  Splits go in batches of 32: each thread issues its 32
 // accumulator loads and each wave its 32 (max, den) loads before any is
-// used, so S <= 32 costs one memory round trip.  With `err`, the states are
-// published words (complemented bits, 0 = not yet): loads are repeated until
-// every word has landed, a bounded wait that reports through *err.
-__device__ void merge_group(const float* state, int S, int g, uint16_t* out, float (&wts)[kAT / 64][64],
-                            unsigned* err = nullptr) {
+// used, so S <= 32 costs one memory round trip.  The caller has seen every
+// split's arrival (the states are complete when this runs).
+__device__ void merge_group(const float* state, int S, int g, uint16_t* out, float (&wts)[kAT / 64][64]) {
   const int tid = threadIdx.x, h = tid >> 7, d = tid & (kD - 1), w = tid >> 6, lane = tid & 63;
   const float* st = state + (size_t)(g * kHq + h) * S * kStateW;
   float M = -INFINITY, den = 0.f, v = 0.f;
   for (int p0 = 0; p0 < S; p0 += 32) {
     const int n = min(32, S - p0);
     const float* mzp = st + (size_t)(p0 + min(lane & 31, n - 1)) * kStateW;
-    float2 mz;
+    const float2 mz = ld_dev2(mzp);
     float av[32];
-    if (err) {
-      unsigned long long r = 0;
-      unsigned ra[32];
 #pragma unroll
-      for (int i = 0; i < 32; ++i) ra[i] = 0u;
-      for (int spins = 0;; ++spins) {
-        bool ok = true;
-        if (r == 0) r = ld_dev(reinterpret_cast<const unsigned long long*>(mzp));
-        ok = ok && r != 0;
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-          if (ra[i] == 0u) ra[i] = ld_dev(reinterpret_cast<const unsigned*>(st + (size_t)(p0 + min(i, n - 1)) * kStateW + 2 + d));
-          ok = ok && ra[i] != 0u;
-        }
-        if (__ballot(!ok) == 0) break;
-        if (spins >= kSpinLimit) {
-          if (lane == 0) atomicOr(err, 1u);
-          break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-      }
-      r = ~r;
-      mz = make_float2(__uint_as_float((unsigned)r), __uint_as_float((unsigned)(r >> 32)));
-#pragma unroll
-      for (int i = 0; i < 32; ++i) av[i] = __uint_as_float(~ra[i]);
-    } else {
-      mz = ld_dev2(mzp);
-#pragma unroll
-      for (int i = 0; i < 32; ++i) av[i] = ld_dev(st + (size_t)(p0 + min(i, n - 1)) * kStateW + 2 + d);
-    }
+    for (int i = 0; i < 32; ++i) av[i] = ld_dev(st + (size_t)(p0 + min(i, n - 1)) * kStateW + 2 + d);
     // online merge across batches: rescale what is accumulated when the max grows
     const bool mine = lane < n;  // lanes 32..63 duplicate lanes 0..31 and stay out
     const float bm = wave_max(mine ? mz.x : -INFINITY);

@@ -174,9 +174,30 @@ __device__ __forceinline__ unsigned block_incl_scan(unsigned v, unsigned* wsum) 
   return v + add;
 }
 
-// Bounded spin used by every inter-workgroup wait: about 2^20 sleeps of 64
-// clocks (tens of milliseconds) before the waiter gives up and reports.
+// Bounded spin used by every inter-workgroup wait: by default about 2^20
+// sleeps of 64 clocks (tens of milliseconds) before the waiter gives up and
+// reports.  The limit is process-wide and host-settable
+// (prismkv_set_spin_limit); every launch passes the current value to its
+// kernel as an argument.
 constexpr int kSpinLimit = 1 << 20;
+int spin_limit();  // the current process-wide limit (defined in decode.hip)
+
+// Error words.  A workspace's first 32-bit word is its sticky error word; its
+// 8-byte slot at byte offset 8 optionally holds the device address of a
+// host-mapped 32-bit word (0 = none), so a host binding can notice a wait that
+// gave up without copying or synchronising.  A wait that gives up writes 1 to
+// both (system scope: the host word lives in host memory).
+__device__ __forceinline__ void report_error(unsigned* err, unsigned* const* host_slot) {
+  __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  if (host_slot) {
+    unsigned* host = __hip_atomic_load(host_slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (host) __hip_atomic_store(host, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+}
+// The host-pointer slot of a workspace whose error word is `err`.
+__host__ __device__ inline unsigned* const* error_host_slot(unsigned* err) {
+  return reinterpret_cast<unsigned* const*>(reinterpret_cast<char*>(err) + 8);
+}
 
 // Cross-workgroup communication.  Data one workgroup hands to another is
 // written through to the device coherence point and read back from it with

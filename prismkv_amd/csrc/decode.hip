@@ -89,7 +89,9 @@ struct DecodeArgs {
   unsigned long long* stats;  // [G][kChunks][4] published (max, sum-exp) per chunk and head
   unsigned long long* cand;   // [G][S][16] published best keys of each workgroup
   unsigned* status;           // [G][S] kReady | tile count
-  unsigned* err;
+  unsigned* err;                  // sticky error word (a wait gave up)
+  unsigned* const* err_host;      // optional slot holding a host-mapped error word's address
+  int spin;                       // bound of every wait (sleeps), prismkv_set_spin_limit
   float* state;  // [G][S][4 heads][4 slices][34] published split states
   int64_t* features;
   float* valid;
@@ -132,18 +134,25 @@ struct DecodeLds {
 };
 
 // Bounded spin until `pred` holds for every lane of the calling wave; sets
-// the error word and gives up instead of hanging.
-template <typename Pred>
-__device__ __forceinline__ void wait_all(Pred pred, unsigned* err) {
+// the error words and gives up instead of hanging.  A wait that gives up
+// leaves the unlanded words at zero; every reader maps a zero word to an
+// in-range value (bucket 0, count 0, NaN state), so the launch still ends
+// normally, with the error reported.
+template <typename Pred, typename Args>
+__device__ __forceinline__ void wait_all(Pred pred, const Args& a) {
   for (int spins = 0;; ++spins) {
     if (__ballot(!pred()) == 0) return;
-    if (spins >= kSpinLimit) {
-      if ((threadIdx.x & 63) == 0) atomicOr(err, 1u);
+    if (spins >= a.spin) {
+      if ((threadIdx.x & 63) == 0) report_error(a.err, a.err_host);
       return;
     }
     __builtin_amdgcn_s_sleep(1);
   }
 }
+
+// Bitmap row of a candidate key.  Landed keys always name a bucket below
+// 3000; the clamp keeps a key read after a wait gave up in range too.
+__device__ __forceinline__ int row_of(unsigned long long key) { return min(key_bucket(key), kF - 1); }
 
 // Published words: the complement of the value's bits, so 0 = not yet.
 __device__ __forceinline__ void pub(float* p, float v) { st_dev(reinterpret_cast<unsigned*>(p), ~__float_as_uint(v)); }
@@ -240,8 +249,8 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int g, int h, i
     if (__syncthreads_and(take(0))) break;
     issue(0);
     if (__syncthreads_and(take(1))) break;
-    if (spins >= kSpinLimit) {
-      if (tid == 0) atomicOr(a.err, 1u);
+    if (spins >= a.spin) {
+      if (tid == 0) report_error(a.err, a.err_host);
       break;
     }
   }
@@ -321,7 +330,7 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, D
     wait_all([&] {
       if (i < nk && r == 0) r = ld_dev(cg + i);
       return i >= nk || r != 0;
-    }, a.err);
+    }, a);
     v[k] = i < nk ? ~r : 0ull;
   }
   const unsigned long long best = sorted_rows_top16<KW>(v);
@@ -336,7 +345,7 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, D
 #pragma unroll
   for (int r = 0; r < kPrefetch; ++r) {
     pk[r] = readlane_u64(best, r);  // rank r of this wave's list (uniform)
-    pw[r] = (kUnion && pk[r]) ? __builtin_nontemporal_load(gb + (size_t)key_bucket(pk[r]) * a.row_words) : 0u;
+    pw[r] = (kUnion && pk[r]) ? __builtin_nontemporal_load(gb + (size_t)row_of(pk[r]) * a.row_words) : 0u;
   }
   __syncthreads();
   constexpr int kListed = kDT / 64 * kTop;  // 128
@@ -372,7 +381,7 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, D
   lds.sel.ors[w][lane] = word ? part : 0u;
   if (lane == 0) lds.cover[w] = covered;
   if (w == 0) {
-    if (lane < kTop) lds.sel_rows[lane] = lane < need ? key_bucket(win) : 0;  // the union reads rows < need only
+    if (lane < kTop) lds.sel_rows[lane] = lane < need ? row_of(win) : 0;  // the union reads rows < need only
     if (lane == 0) lds.need = need;
   }
   __syncthreads();
@@ -443,7 +452,7 @@ __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p,
       if (lane < kChunks && r0 == 0) r0 = ld_dev(st + lane * kHq);
       if (lane + 64 < kChunks && r1 == 0) r1 = ld_dev(st + (lane + 64) * kHq);
       return (lane >= kChunks || r0 != 0) && (lane + 64 >= kChunks || r1 != 0);
-    }, a.err);
+    }, a);
     const float2 mz = merge_chunk_stats([&](int ch) { return unpub2(ch == lane ? r0 : r1); });
     if (lane == 0) {
       lds.gmax[h] = mz.x;
@@ -488,9 +497,9 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   extern __shared__ int rows[];  // the tile's selected tokens, ascending (32 tw of them)
   // the tail length: the host's T, or the device word clamped to it (the
   // host checked the K/V extents for T).  The word is requested now, with
-  // no branch (without a device word the load reads the error word and is
-  // ignored), so it has long landed when the attention first uses it.
-  const int tail_word = ld_dev(a.tail_dev ? a.tail_dev : reinterpret_cast<const int*>(a.err));
+  // no branch (without a device word the load reads q and is ignored), so
+  // it has long landed when the attention first uses it.
+  const int tail_word = ld_dev(a.tail_dev ? a.tail_dev : reinterpret_cast<const int*>(a.q));
 
   if constexpr (kGiven) {
     // ---- 1-4. the given selection: the valid, in-range buckets in order (an
@@ -672,7 +681,7 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
         wait_all([&] {
           if (qq < p && !(v & kReady)) v = ld_dev(tiles + qq);
           return (v & kReady) != 0u;
-        }, a.err);
+        }, a);
         prefix += (unsigned)wave_sum_i(qq < p ? (int)(v & ~kReady) : 0);
       }
       if (lane == 0) {
@@ -736,8 +745,14 @@ using namespace prismkv;
 static int decode_splits(int groups) { return std::min(kMaxSplits, std::max(kMinSplits, 256 / std::max(groups, 1))); }
 static constexpr int kFusedMaxHistory = kMinSplits * kTileTokens;  // 524288
 
+// The process-wide bound of every inter-workgroup wait, passed to each launch.
+static int g_spin_limit = kSpinLimit;
+namespace prismkv {
+int spin_limit() { return __atomic_load_n(&g_spin_limit, __ATOMIC_RELAXED); }
+}  // namespace prismkv
+
 // Work layout (bytes) for the split count of `groups` groups:
-// err | stats | candidates | status | state
+// err (the error word, then the host-word slot at byte 8) | stats | candidates | status | state
 struct DecodeWorkLayout {
   size_t err, stats, cand, status, state, total;
   DecodeWorkLayout(int groups, int S) {
@@ -791,7 +806,8 @@ static int resident_workgroups() {
 static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
                        uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
                        uint64_t out, const int* tail_dev, bool given, int groups, int H, int T, int capacity,
-                       int64_t row_words, int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream) {
+                       int64_t row_words, int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream,
+                       unsigned* err = nullptr) {
   if (groups < 1 || groups > 65535 || H < 1 || H > kFusedMaxHistory || T < 0 || capacity < H) return kBadSize;
   if (row_words < (H + 31) / 32 || ids_stride < H) return kBadSize;
   if (ks < (int64_t)(H + T) * kD || vs < (int64_t)(H + T) * kD) return kBadSize;
@@ -821,7 +837,10 @@ static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t b
   a.stats = reinterpret_cast<unsigned long long*>(w + L.stats);
   a.cand = reinterpret_cast<unsigned long long*>(w + L.cand);
   a.status = reinterpret_cast<unsigned*>(w + L.status);
-  a.err = reinterpret_cast<unsigned*>(w + L.err);
+  // the workspace's own error word and host-word slot, or the caller's word
+  a.err = err ? err : reinterpret_cast<unsigned*>(w + L.err);
+  a.err_host = err ? nullptr : error_host_slot(a.err);
+  a.spin = spin_limit();
   a.state = reinterpret_cast<float*>(w + L.state);
   a.features = reinterpret_cast<int64_t*>(features);
   a.valid = reinterpret_cast<float*>(valid);
@@ -848,6 +867,19 @@ static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t b
 }
 
 extern "C" {
+
+int prismkv_set_spin_limit(int limit) {
+  if (limit < 0) return kBadSize;
+  return __atomic_exchange_n(&g_spin_limit, limit, __ATOMIC_RELAXED);
+}
+
+int prismkv_get_spin_limit(void) { return spin_limit(); }
+
+uint64_t prismkv_mapped_pointer(uint64_t host) {
+  void* dev = nullptr;
+  if (!host || hipHostGetDevicePointer(&dev, reinterpret_cast<void*>(host), 0) != hipSuccess) return 0;
+  return reinterpret_cast<uint64_t>(dev);
+}
 
 size_t prismkv_decode_work_bytes(int groups, int capacity) {
   if (groups < 1 || capacity < 1) return 0;
@@ -887,6 +919,8 @@ int prismkv_route_single(uint64_t q, uint64_t moments, uint64_t counts, uint64_t
   a.cand = reinterpret_cast<unsigned long long*>(w + L.cand);
   a.status = reinterpret_cast<unsigned*>(w + L.status);
   a.err = reinterpret_cast<unsigned*>(w + L.err);
+  a.err_host = error_host_slot(a.err);
+  a.spin = spin_limit();
   a.state = reinterpret_cast<float*>(w + L.state);
   a.features = reinterpret_cast<int64_t*>(features);
   a.valid = reinterpret_cast<float*>(valid);

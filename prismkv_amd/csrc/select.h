@@ -221,7 +221,7 @@ __device__ void write_selection(const unsigned long long* sel, int need, const C
   const int tid = threadIdx.x;
   if (tid < 64) {
     const bool hit = tid < need;
-    const int b = hit ? key_bucket(sel[tid]) : 0;
+    const int b = hit ? min(key_bucket(sel[tid]), kF - 1) : 0;  // in range even for a key read after a give-up
     if (tid < kTop) {
       features[tid] = b;
       valid[tid] = hit ? 1.0f : 0.0f;

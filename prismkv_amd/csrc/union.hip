@@ -29,7 +29,8 @@ constexpr unsigned kValMask = (1u << 30) - 1;
 struct UnionWork {
   unsigned* status;  // [groups][tiles]
   unsigned* done;    // [groups]
-  unsigned* err;     // [1]
+  unsigned* err;     // [1] sticky error word; its host-word slot at byte 8
+  int spin;          // bound of every wait (sleeps)
 };
 
 __host__ __device__ inline int union_tiles(int H, int wpt) {
@@ -63,7 +64,7 @@ struct Words<4> {
 
 // Exclusive prefix of tile t of a group by decoupled look-back (run by wave 0).
 // Returns the prefix; publishes the inclusive status of tile t.
-__device__ unsigned look_back(unsigned* st, int t, unsigned total, unsigned* err) {
+__device__ unsigned look_back(unsigned* st, int t, unsigned total, const UnionWork& work) {
   const int lane = threadIdx.x & 63;
   if (t == 0) {
     if (lane == 0) st_dev(&st[0], kFlagInc | total);
@@ -77,8 +78,8 @@ __device__ unsigned look_back(unsigned* st, int t, unsigned total, unsigned* err
     unsigned s = p >= 0 ? ld_dev(&st[p]) : (kFlagInc | 0u);
     for (int spins = 0;; ++spins) {
       if (!__ballot((s >> 30) == 0)) break;
-      if (spins >= kSpinLimit) {  // a predecessor never published: report, do not hang
-        if (lane == 0) atomicOr(err, 1u);
+      if (spins >= work.spin) {  // a predecessor never published: report, do not hang
+        if (lane == 0) report_error(work.err, error_host_slot(work.err));
         s = kFlagInc | 0u;
         break;
       }
@@ -170,7 +171,7 @@ __global__ __launch_bounds__(kUT) void union_kernel(const uint32_t* __restrict__
   unsigned* st = work.status + (size_t)g * tiles;
   if (tid < 64) {
     const unsigned total = wsum[0] + wsum[1] + wsum[2] + wsum[3];
-    const unsigned prefix = look_back(st, t, total, work.err);
+    const unsigned prefix = look_back(st, t, total, work);
     if (tid == 0) {
       base = prefix;
       if (t == tiles - 1) count[g] = (int32_t)(prefix + total);
@@ -511,7 +512,7 @@ int prismkv_select_cap_n(uint64_t bits, uint64_t counts, uint64_t features, uint
 size_t prismkv_union_work_bytes(int groups, int H) {
   if (groups < 1 || H < 1) return 0;
   const int tiles = union_tiles(H, 1);  // the largest tile count of any variant
-  return ((size_t)groups * tiles + groups + 1) * sizeof(unsigned);
+  return ((size_t)groups * tiles + groups + 4) * sizeof(unsigned);
 }
 
 }  // extern "C"
@@ -536,9 +537,11 @@ static int union_impl(uint64_t bits, uint64_t features, uint64_t valid, uint64_t
   if (!bits || !features || !valid || !work || !ids || !count) return kBadSize;
   const int wpt = union_wpt(H, row_words);
   const int tiles = union_tiles(H, wpt);
-  // fixed layout for any H: err word, done[groups], then status[groups][tiles]
+  // fixed layout for any H: err word, its host-word slot (bytes 8-15),
+  // done[groups], then status[groups][tiles]
+  if (work % 8) return kBadSize;
   unsigned* w = reinterpret_cast<unsigned*>(work);
-  UnionWork uw{w + 1 + groups, w + 1, w};
+  UnionWork uw{w + 4 + groups, w + 4, w, spin_limit()};
   const dim3 grid(tiles, groups);
   const uint32_t* b = reinterpret_cast<const uint32_t*>(bits);
   const int64_t* f = reinterpret_cast<const int64_t*>(features);

@@ -152,6 +152,8 @@ class HFNative:
     def records(self):
         """Per-(layer, group) decode records in the reference's fields."""
         if self._pending:
+            torch.cuda.synchronize()
+            self.check_errors()
             for layer, history, total, count, raw, buckets, prefix in self._pending:
                 count, raw, buckets = count.tolist(), raw.tolist(), buckets.tolist()
                 for g in range(GROUPS):
@@ -162,6 +164,12 @@ class HFNative:
                     self._records.append(rec)
             self._pending = []
         return self._records
+
+    def check_errors(self):
+        """RuntimeError if a bounded wait of any layer's launches gave up
+        (reads host-mapped words; no synchronisation)."""
+        for op in self.ops.values():
+            op.check_errors()
 
     # ------------------------------------------------------------ forward
 
@@ -349,6 +357,7 @@ class DecodeGraph:
             self.position = lengths.pop()
         if self.position >= self.max_length:
             raise ValueError("the static cache is full")
+        self.session.check_errors()  # a give-up of an earlier replay surfaces here
         if self._prepare(self.position + 1):
             self.stale = True
         self.ids.copy_(ids.reshape(1, 1))

@@ -26,6 +26,11 @@ shapes as the reference binding:
 
 All validation happens on the host before anything is enqueued (ValueError
 for shapes/dtypes/devices/strides, RuntimeError for a nonzero launch code).
+Every inter-workgroup wait of the kernels is bounded: a wait that gives up
+marks a host-mapped error word of the instance, which the next route /
+attention / call (and `check_errors`, `decode_errors`) reads without
+synchronising and turns into a RuntimeError after resetting the
+workspaces.
 route/attention allocate nothing and never synchronise, so they can be
 captured into a HIP graph.  Instance buffers are shared state: use one
 instance per stream.  There is no CPU fallback: without the HIP library the
@@ -78,6 +83,16 @@ class FeatureIndex:
     @property
     def memberships(self):
         return sum(len(x) for x in self.lists)
+
+
+def set_spin_limit(limit: int, library=None) -> int:
+    """Process-wide bound (in sleeps of 64 clocks) of every inter-workgroup
+    wait of the kernels; returns the previous bound.  The default, 2^20, is
+    tens of milliseconds; a smaller bound makes a wait give up (and report)
+    sooner.  Launches read it when they are enqueued."""
+    if int(limit) < 0:
+        raise ValueError("the spin limit must be >= 0")
+    return _lib.load(library).query("prismkv_set_spin_limit", int(limit))
 
 
 def tile_moments(mean: torch.Tensor, variance: torch.Tensor) -> torch.Tensor:
@@ -258,6 +273,12 @@ class Native8B:
                                  dtype=torch.uint8, device=device)
         self.decode_work = torch.zeros(self.lib.query("prismkv_decode_work_bytes", GROUPS, self.capacity),
                                        dtype=torch.uint8, device=device)
+        # host-mapped error word the kernels mark when a bounded wait gives up
+        self._err_host = torch.zeros(4, dtype=torch.int32, pin_memory=True)
+        self._err_device_address = self.lib.query("prismkv_mapped_pointer", self._err_host.data_ptr())
+        if not self._err_device_address:
+            raise RuntimeError("prismkv_mapped_pointer: the pinned error word is not device-accessible")
+        self._attach_error_word()
         self.out = torch.zeros(GROUPS, HEADS, DIM, dtype=torch.bfloat16, device=device)
         self.center = None if center is None else center.to(device=device, dtype=torch.float32).reshape(
             GROUPS, DIM).contiguous()
@@ -269,6 +290,35 @@ class Native8B:
 
     def _stream(self):
         return torch.cuda.current_stream().cuda_stream
+
+    def _attach_error_word(self):
+        """Writes the host-mapped error word's device address into the
+        host-word slot (bytes 8-15) of the workspaces whose kernels wait."""
+        for work in (self.decode_work, self.union_work):
+            work[8:16].view(torch.int64).fill_(self._err_device_address)
+
+    def check_errors(self):
+        """Raise RuntimeError if a bounded inter-workgroup wait of an earlier
+        launch gave up (its results are invalid).  Reads the host-mapped error
+        word, so it neither synchronises nor sees launches that have not run
+        yet; on an error the device is synchronised, every workspace is
+        zeroed (a late workgroup may have left published words behind) and the
+        error words are cleared before raising."""
+        if int(self._err_host[0]) == 0:
+            return
+        self.reset_workspaces()
+        raise RuntimeError("prismkv decode: a bounded inter-workgroup wait gave up; the results of the launches "
+                           "since the last check are invalid (the workspaces have been reset)")
+
+    def reset_workspaces(self):
+        """Zero the decode, union and attention workspaces and the error
+        words (after synchronising the device)."""
+        torch.cuda.synchronize(self.out.device)
+        for work in (self.decode_work, self.union_work, self.state):
+            work.zero_()
+        self._err_host.zero_()
+        self._attach_error_word()
+        torch.cuda.synchronize(self.out.device)
 
     @property
     def unique_cap(self):
@@ -282,6 +332,7 @@ class Native8B:
         self.__dict__["_unique_cap"] = cap
 
     def route(self, q):
+        self.check_errors()
         width = self._select(q)
         self.lib.call("prismkv_union_n", self.bits.data_ptr(), self.features.data_ptr(), self.valid.data_ptr(),
                       self.union_work.data_ptr(), self.ids.data_ptr(), self.count.data_ptr(), GROUPS, self.history,
@@ -370,6 +421,7 @@ class Native8B:
         not change the result, and the kernel always uses ATTEND_SPLITS
         workgroups per group with rows dealt evenly to their waves."""
         self._check_kv(q, k, v, splits, schedule)
+        self.check_errors()
         self.lib.call("prismkv_attend", q.data_ptr(), k.data_ptr(), v.data_ptr(), self.ids.data_ptr(),
                       self.count.data_ptr(), self.state.data_ptr(), self.out.data_ptr(), GROUPS, self.history,
                       k.shape[1] - self.history, k.stride(0), v.stride(0), self.capacity, ATTEND_SPLITS,
@@ -392,6 +444,7 @@ class Native8B:
         [0, K rows - history].  Fused path only (no unique cap, history up to
         FUSED_MAX_HISTORY, moments router)."""
         self._check_kv(q, k, v, kwargs.get("splits", 64), kwargs.get("schedule", 0))
+        self.check_errors()
         if tail is not None:
             if self.unique_cap is not None or self.history > FUSED_MAX_HISTORY or self.router != "moments":
                 raise NotImplementedError("a device tail length needs the single-launch decode (no unique cap, "
@@ -521,6 +574,7 @@ class Native8B:
                                       dtype=torch.uint8, device=device)
         self.decode_work = torch.zeros(self.lib.query("prismkv_decode_work_bytes", GROUPS, capacity),
                                        dtype=torch.uint8, device=device)
+        self._attach_error_word()
 
     def export_indices(self):
         """The device tables as 8 FeatureIndex objects (counts i64, mean and
@@ -542,9 +596,12 @@ class Native8B:
         return out
 
     def decode_errors(self):
-        """Error word of the single-launch decode (nonzero if a bounded
-        inter-workgroup wait gave up); synchronises."""
-        return int(self.decode_work[:4].view(torch.int32).item())
+        """Nonzero if a bounded inter-workgroup wait of any launch since the
+        last reset gave up (the decode and union workspaces' sticky error
+        words and the host-mapped word); synchronises, raises nothing."""
+        torch.cuda.synchronize(self.out.device)
+        return (int(self.decode_work[:4].view(torch.int32).item()) | int(self.union_work[:4].view(torch.int32).item())
+                | int(self._err_host[0]))
 
     def buffer_bytes(self):
         """Live tensors owned here; excludes model/KV, caller indices and build temporaries."""

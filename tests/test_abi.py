@@ -22,7 +22,7 @@ def lib():
 
 def declared_symbols():
     text = HEADER.read_text()
-    return re.findall(r"^\s*(?:int|size_t)\s+(\w+)\s*\(", text, flags=re.M)
+    return re.findall(r"^\s*(?:int|size_t|uint64_t)\s+(\w+)\s*\(", text, flags=re.M)
 
 
 def test_header_declares_reference_symbols():
@@ -131,3 +131,22 @@ def test_native8b_host_validation_without_gpu():
         Native8B([idx] * 7)
     with pytest.raises(ValueError, match="device tensor"):
         Native8B([idx] * 8)
+
+
+def test_spin_limit_is_host_settable(lib):
+    from prismkv_amd import set_spin_limit
+    default = lib.query("prismkv_get_spin_limit")
+    assert default == 1 << 20
+    assert set_spin_limit(12345) == default
+    try:
+        assert lib.query("prismkv_get_spin_limit") == 12345
+        assert lib.query("prismkv_set_spin_limit", -1) == -1  # rejected, unchanged
+        assert lib.query("prismkv_get_spin_limit") == 12345
+    finally:
+        assert set_spin_limit(default) == 12345
+    with pytest.raises(ValueError):
+        set_spin_limit(-1)
+
+
+def test_mapped_pointer_rejects_null(lib):
+    assert lib.query("prismkv_mapped_pointer", 0) == 0

@@ -79,10 +79,11 @@ def test_build_and_summarize():
     assert (np.abs(c - exact) <= np.spacing(np.abs(exact).astype(np.float32))).all()
     ref = oracle.build_index(kf, enc.W_enc.detach().numpy(), enc.b_enc.detach().numpy(), 1.25, 8, center=c)
     act = oracle.sae_dense((kf - c) / np.float32(1.25), enc.W_enc.detach().numpy(), enc.b_enc.detach().numpy())
-    same = all(np.array_equal(a.cpu().numpy(), b) for a, b in zip(idx.lists, ref.lists))
-    margin = oracle.topk_margin(act, 8 * H)
-    log(f"  build: {idx.memberships} memberships, lists identical={same}, margin={margin:.2e}")
-    assert same or margin < 1e-5
+    x = (kf - c) / np.float32(1.25)
+    moved = expect.check_memberships(ref.lists, [l.cpu().numpy() for l in idx.lists], act, 8 * H,
+                                     expect.encode_error_bound(x, enc.W_enc.detach().numpy(),
+                                                               enc.b_enc.detach().numpy()), "build")
+    log(f"  build: {idx.memberships} memberships, {moved} differing from the oracle (within rounding of tau)")
     assert idx.history == H and idx.counts.dtype == torch.long
     # summarize over the device lists, with and without a center
     c2, m2, v2 = oracle.summarize(kf, [l.cpu().numpy() for l in idx.lists])
@@ -110,8 +111,12 @@ def test_append_index():
     o1, act = oracle.append_index(o0, kf[H:H + N], enc.W_enc.detach().numpy(), enc.b_enc.detach().numpy(), 1.5, 8,
                                   return_act=True)
     same = all(np.array_equal(a.cpu().numpy(), b) for a, b in zip(nxt.lists, o1.lists))
-    log(f"  append: lists identical={same}")
-    assert same or oracle.topk_margin(act, 8 * N) < 1e-5
+    from tests.test_gpu_build import block_lists
+    x = (kf[H:H + N] - idx.center.cpu().numpy()) / np.float32(1.5)
+    moved = expect.check_memberships(block_lists(o1.lists, H, N), block_lists([l.cpu() for l in nxt.lists], H, N),
+                                     act, 8 * N, expect.encode_error_bound(x, enc.W_enc.detach().numpy(),
+                                                                           enc.b_enc.detach().numpy()), "append")
+    log(f"  append: lists identical={same}, block memberships differing (within rounding of tau): {moved}")
     if same:
         assert np.array_equal(nxt.counts.cpu().numpy(), o1.counts)
         assert np.allclose(nxt.mean.cpu().numpy(), o1.mean, rtol=1e-5, atol=1e-6)
@@ -135,7 +140,7 @@ def test_scores_selection_and_attention(cap):
                                                           idx.variance.cpu().numpy())
     o = order.cpu().numpy()
     log(f"  order identical={np.array_equal(o, w_order)} margin={margin:.2e}")
-    assert np.array_equal(o, w_order) or margin < 1e-6
+    assert np.array_equal(o, w_order), (o.tolist(), w_order.tolist(), margin)
     assert np.allclose(score.cpu().numpy(), w_score, rtol=1e-5, atol=1e-9)
     ids, meta = core.select_buckets(q, idx, unique_cap=cap)
     w_ids, w_meta = oracle.select_buckets(o, lists, H, cap)

@@ -23,7 +23,7 @@ pytestmark = pytest.mark.gpu
 def check_order(got, want, margin, tag):
     same = np.array_equal(got, want)
     log(f"  {tag}: {len(got)} buckets, order identical={same}, margin={margin:.2e}")
-    assert same or margin < 1e-5, tag
+    assert same, (tag, np.asarray(got).tolist(), np.asarray(want).tolist(), margin)
     return same
 
 
@@ -86,9 +86,8 @@ def test_native8b_q_activation(cap):
         else:
             order = w_order  # the device's pre-cap order is not kept; the walk runs over the oracle's
         w_ids, w_meta = oracle.select_buckets(order, lists, H, cap)
-        if cap is None or margin >= 1e-5:
-            assert feats[g][:nf].tolist() == w_meta["features"] and int(raw[g]) == w_meta["raw"], g
-            assert np.array_equal(ids[g][:count[g]].astype(np.int64), w_ids), g
+        assert feats[g][:nf].tolist() == w_meta["features"] and int(raw[g]) == w_meta["raw"], (g, margin)
+        assert np.array_equal(ids[g][:count[g]].astype(np.int64), w_ids), g
         want.append(dict(ids=ids[g][:count[g]].astype(np.int64)))
     idx = [oracle.Index(H, i.center.cpu().numpy(), i.counts.cpu().numpy(), i.mean.cpu().numpy(),
                         i.variance.cpu().numpy(), [l.numpy() for l in i.lists]) for i in got]
