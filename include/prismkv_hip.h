@@ -150,6 +150,24 @@ int prismkv_union_attend(uint64_t q, uint64_t bits, uint64_t k, uint64_t v, uint
                          uint64_t valid, uint64_t ids, uint64_t count, uint64_t out, int groups, int H, int T,
                          int capacity, int64_t row_words, int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream);
 
+/* The allocation-free decode.  No counterpart in the reference: for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Same launch and outputs as
+ * prismkv_decode, but the workspace is the library's own file-scope device
+ * array of prismkv_scratch_bytes() = 1 MiB (one copy per GPU, held until the
+ * process ends), which holds the workspace of up to 13 groups; -1 for more
+ * groups or a null / misaligned `err`.  `err` (one int32, device or
+ * host-mapped memory) receives 1 if a bounded wait gave up; it is not
+ * cleared by the call.  Each call first clears the array with a small kernel
+ * (no memset node, so the call can be captured), then decodes; it calls no
+ * hipMalloc, hipFree or allocating library routine.  Calls on one GPU share
+ * the array: calls that overlap on one GPU (other streams) race. */
+size_t prismkv_scratch_bytes(void);
+int prismkv_decode_noalloc(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
+                           uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
+                           uint64_t out, uint64_t err, int groups, int H, int T, int capacity, int64_t row_words,
+                           int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream);
+
 /* ---- bounded waits and their error words (no reference counterpart: the
  * reference kernels never wait across workgroups) --------------------------
  * Every inter-workgroup wait of prismkv_decode, prismkv_decode_tail,

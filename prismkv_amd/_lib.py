@@ -53,6 +53,9 @@ SIGNATURES = {
     "prismkv_set_spin_limit": ([_I32], False, _I32),
     "prismkv_get_spin_limit": ([], False, _I32),
     "prismkv_mapped_pointer": ([_U64], False, _U64),
+    # the allocation-free decode (workspace in the library's own device array)
+    "prismkv_scratch_bytes": ([], False, _SZ),
+    "prismkv_decode_noalloc": ([_U64] * 13 + [_I32] * 4 + [_I64] * 4, True, _I32),
 }
 
 _loaded: dict[str, "Library"] = {}

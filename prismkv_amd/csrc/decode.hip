@@ -55,6 +55,7 @@
 // through write-through (agent-scope) stores and loads, never through
 // device-scope fences.
 #include <algorithm>
+#include <mutex>
 
 #include "attend_mfma.h"
 #include "score.h"
@@ -866,7 +867,60 @@ static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t b
   return (int)hipGetLastError();
 }
 
+// ---- the allocation-free decode ----------------------------------------
+// Callers that cannot allocate (code under graph capture, tight serving
+// loops) get the decode workspace from this file-scope array instead of a
+// caller-owned buffer: 1 MiB, which holds the workspace of up to 13 groups.
+// Every GPU the library runs on holds its own copy until the process ends;
+// its device address is looked up once per device (hipGetSymbolAddress, with
+// that device current) and only that address is handed to kernels.
+constexpr size_t kScratchBytes = 1u << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+// The address of this device's scratch array, or nullptr if the lookup fails.
+static char* scratch_address() {
+  static std::mutex mu;
+  static char* address[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return nullptr;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!address[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return nullptr;
+    address[dev] = static_cast<char*>(p);
+  }
+  return address[dev];
+}
+
+// Zero-fills n16 16-byte words (a kernel rather than a memset, so the call
+// stays capturable into a graph).
+__global__ __launch_bounds__(256) void clear_words(uint4* p, size_t n16) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += (size_t)gridDim.x * 256)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
 extern "C" {
+
+size_t prismkv_scratch_bytes(void) { return kScratchBytes; }
+
+int prismkv_decode_noalloc(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
+                           uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
+                           uint64_t out, uint64_t err, int groups, int H, int T, int capacity, int64_t row_words,
+                           int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream) {
+  if (groups < 1 || groups > 65535 || !err || err % 4) return kBadSize;
+  const DecodeWorkLayout L(groups, decode_splits(groups));
+  if (L.total > kScratchBytes) return kBadSize;  // the workspace of more than 13 groups does not fit
+  char* work = scratch_address();
+  if (!work) return (int)hipErrorInvalidSymbol;
+  // a call that gave up may have left published words behind: start from zero
+  hipLaunchKernelGGL(clear_words, dim3((unsigned)std::min<size_t>(1024, (L.total / 16 + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, reinterpret_cast<uint4*>(work), L.total / 16);
+  const int rc = (int)hipGetLastError();
+  if (rc) return rc;
+  return decode_impl(q, moments, counts, bits, k, v, reinterpret_cast<uint64_t>(work), features, valid, raw, ids,
+                     count, out, nullptr, false, groups, H, T, capacity, row_words, ks, vs, ids_stride, stream,
+                     reinterpret_cast<unsigned*>(err));
+}
 
 int prismkv_set_spin_limit(int limit) {
   if (limit < 0) return kBadSize;
