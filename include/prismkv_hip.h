@@ -149,6 +149,16 @@ int prismkv_decode_tail(uint64_t q, uint64_t moments, uint64_t counts, uint64_t 
 int prismkv_union_attend(uint64_t q, uint64_t bits, uint64_t k, uint64_t v, uint64_t work, uint64_t features,
                          uint64_t valid, uint64_t ids, uint64_t count, uint64_t out, int groups, int H, int T,
                          int capacity, int64_t row_words, int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream);
+/* prismkv_union_attend with the tail length read from device memory at
+ * launch (`tail`: one int32, 4-byte aligned), clamped to [0, max_tail], as
+ * prismkv_decode_tail: the capped step (route, budgeted walk, union +
+ * attention) of a decode captured once in a HIP graph and replayed as the
+ * tail grows.  No reference counterpart (the reference takes the tail length
+ * from K's shape on the host). */
+int prismkv_union_attend_tail(uint64_t q, uint64_t bits, uint64_t k, uint64_t v, uint64_t work, uint64_t features,
+                              uint64_t valid, uint64_t ids, uint64_t count, uint64_t out, uint64_t tail, int groups, int H,
+                              int max_tail, int capacity, int64_t row_words, int64_t ks, int64_t vs, int64_t ids_stride,
+                              uint64_t stream);
 
 /* The allocation-free decode.  No counterpart in the reference: for callers
  * that cannot allocate device memory (code under HIP graph capture, tight

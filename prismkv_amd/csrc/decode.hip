@@ -955,6 +955,15 @@ int prismkv_union_attend(uint64_t q, uint64_t bits, uint64_t k, uint64_t v, uint
                      capacity, row_words, ks, vs, ids_stride, stream);
 }
 
+int prismkv_union_attend_tail(uint64_t q, uint64_t bits, uint64_t k, uint64_t v, uint64_t work, uint64_t features,
+                              uint64_t valid, uint64_t ids, uint64_t count, uint64_t out, uint64_t tail, int groups, int H,
+                              int max_tail, int capacity, int64_t row_words, int64_t ks, int64_t vs, int64_t ids_stride,
+                              uint64_t stream) {
+  if (!tail || tail % 4) return kBadSize;
+  return decode_impl(q, 0, 0, bits, k, v, work, features, valid, 0, ids, count, out, reinterpret_cast<const int*>(tail),
+                     true, groups, H, max_tail, capacity, row_words, ks, vs, ids_stride, stream);
+}
+
 int prismkv_route_single(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
                          uint64_t valid, uint64_t raw, int groups, uint64_t stream) {
   if (groups < 1 || groups > 65535) return kBadSize;

@@ -441,17 +441,26 @@ class Native8B:
         taking T = K rows - history from K's shape; K/V then only need rows
         for T up to their length (a static KV buffer).  A launch captured in a
         HIP graph is replayed with whatever the tensor holds, clamped to
-        [0, K rows - history].  Fused path only (no unique cap, history up to
-        FUSED_MAX_HISTORY, moments router)."""
+        [0, K rows - history].  The moments router with histories up to
+        FUSED_MAX_HISTORY: the single launch, or with a unique cap the route,
+        the walk and the union + attention launch."""
         self._check_kv(q, k, v, kwargs.get("splits", 64), kwargs.get("schedule", 0))
         self.check_errors()
         if tail is not None:
-            if self.unique_cap is not None or self.history > FUSED_MAX_HISTORY or self.router != "moments":
-                raise NotImplementedError("a device tail length needs the single-launch decode (no unique cap, "
-                                          "history <= FUSED_MAX_HISTORY, moments router)")
+            if self.history > FUSED_MAX_HISTORY or self.router != "moments":
+                raise NotImplementedError("a device tail length needs the fused decode (history <= "
+                                          "FUSED_MAX_HISTORY, moments router)")
             if (not isinstance(tail, torch.Tensor) or tail.dtype != torch.int32 or tail.numel() != 1
                     or tail.device != self.out.device):
                 raise ValueError("tail must be a one-element int32 tensor on the index device")
+            if self.unique_cap is not None:
+                self._select(q)
+                self.lib.call("prismkv_union_attend_tail", q.data_ptr(), self.bits.data_ptr(), k.data_ptr(),
+                              v.data_ptr(), self.decode_work.data_ptr(), self.features.data_ptr(),
+                              self.valid.data_ptr(), self.ids.data_ptr(), self.count.data_ptr(), self.out.data_ptr(),
+                              tail.data_ptr(), GROUPS, self.history, k.shape[1] - self.history, self.capacity,
+                              self.row_words, k.stride(0), v.stride(0), self.capacity, stream=self._stream())
+                return self.out
             self.lib.call("prismkv_decode_tail", q.data_ptr(), self.moments.data_ptr(), self.n.data_ptr(),
                           self.bits.data_ptr(), k.data_ptr(), v.data_ptr(), self.decode_work.data_ptr(),
                           self.features.data_ptr(), self.valid.data_ptr(), self.raw.data_ptr(), self.ids.data_ptr(),

@@ -1,0 +1,113 @@
+"""The stress configuration end to end: 36 layers x 8 KV groups, H = 262144
+keys per group drawn from a 64-component Gaussian mixture (centers ~ N(0, I),
+sigma 0.3), indexed on the device, strict unique cap floor(H / 16).
+
+The whole step -- for every layer the route, the budgeted walk and the union
++ attention launch, the tail length read from device memory -- is captured in
+ONE HIP graph and replayed; every replay must be bit-identical to the eager
+step (the role of kernels/cuda_sm90/single.py:211-232, which checks the
+captured step against eager at atol 0).  Two sampled layers are checked
+against the oracle: the device's ranked order (src/prismkv/core.py:106-130),
+the budgeted walk over it (:149-163) and the attention (:170-183).
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import cases, expect
+from tests.gpu_util import bf16_bits, log, route_outputs
+
+pytestmark = pytest.mark.gpu
+
+L, H, T, CAP = 36, 262144, 16, 1 / 16
+
+
+def mixture_layer(layer, sae):
+    from prismkv_amd import Native8B
+    gen = torch.Generator(device="cuda").manual_seed(1000 + layer)
+    centers = torch.randn(8, 64, 128, generator=gen, device="cuda")
+    comp = torch.randint(0, 64, (8, H + T), generator=gen, device="cuda")
+    k = torch.randn(8, H + T, 128, generator=gen, device="cuda").mul_(0.3)
+    k.add_(torch.gather(centers, 1, comp[..., None].expand(-1, -1, 128)))
+    k = k.to(torch.bfloat16)
+    v = torch.randn(8, H + T, 128, generator=gen, device="cuda").to(torch.bfloat16)
+    q = torch.randn(8, 4, 128, generator=gen, device="cuda").to(torch.bfloat16)
+    W, b, scale = (torch.from_numpy(sae[x]) for x in ("W", "b", "scale"))
+    op = Native8B.from_keys(k, H, W, b, scale, 8, capacity=H + T, unique_cap=CAP)
+    return op, q, k, v
+
+
+def snapshot(op):
+    limit = int(H * CAP)
+    return [op.features.clone(), op.valid.clone(), op.raw.clone(), op.count.clone(), op.ids[:, :limit].clone(),
+            op.out.clone()]
+
+
+def test_capped_step_graph_36_layers():
+    sae = cases.build_case("random", H=1, T=0, seed=152)  # per-group SAE tables and scales
+    layers = [mixture_layer(i, sae) for i in range(L)]
+    torch.cuda.synchronize()
+    tail = torch.full((1,), T, dtype=torch.int32, device="cuda")
+
+    def step():
+        for op, q, k, v in layers:
+            op(q, k, v, tail=tail)
+
+    step()
+    torch.cuda.synchronize()
+    eager = [snapshot(l[0]) for l in layers]
+    assert all(l[0].decode_errors() == 0 for l in layers)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for replay in range(3):
+        for l in layers:
+            l[0].out.zero_()
+            l[0].ids.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, l in enumerate(layers):
+            got = snapshot(l[0])
+            same = all(torch.equal(a.view(torch.int16) if a.dtype == torch.bfloat16 else a,
+                                   b.view(torch.int16) if b.dtype == torch.bfloat16 else b)
+                       for a, b in zip(eager[i], got))
+            assert same, (replay, i)
+    assert all(l[0].decode_errors() == 0 for l in layers)
+    kept = [int((e[1] > 0).sum()) for e in eager]
+    log(f"  36-layer capped step: replays bit-identical to eager; kept buckets per layer {kept[:6]}...; "
+        f"unique ids (layer 0) {eager[0][3].tolist()}")
+    # sampled layers against the oracle: ranked order, budgeted walk, attention
+    for i in (0, L - 1):
+        op, q, k, v = layers[i]
+        got = op.export_indices()
+        idx = [oracle.Index(H, x.center.cpu().numpy(), x.counts.cpu().numpy(), x.mean.cpu().numpy(),
+                            x.variance.cpu().numpy(), [l.numpy() for l in x.lists]) for x in got]
+        case = dict(H=H, T=T, q=bf16_bits(q), k=bf16_bits(k), v=bf16_bits(v), indices=idx, kind="mixture")
+        groups = expect.expected(case)
+        op.lib.call("prismkv_route_single", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(),
+                    op.decode_work.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(), op.raw.data_ptr(), 8,
+                    stream=torch.cuda.current_stream().cuda_stream)
+        features, valid, raw, _, _ = route_outputs(op)
+        for g in range(8):  # the ranked order, before the walk, is the oracle's
+            n = len(groups[g]["order"])
+            assert np.array_equal(features[g][:n], groups[g]["order"]) and (valid[g] > 0).sum() == n, (i, g)
+        want = []
+        f_e, v_e, r_e, c_e, ids_e, out_e = (x.cpu() for x in eager[i])
+        for g in range(8):
+            w_ids, meta = oracle.select_buckets(groups[g]["order"], idx[g].lists, H, CAP)
+            nf = len(meta["features"])
+            assert meta["limit"] == int(H * CAP)
+            assert f_e[g][:nf].tolist() == meta["features"] and int((v_e[g] > 0).sum()) == nf, (i, g)
+            assert int(r_e[g]) == meta["raw"] and int(c_e[g]) == len(w_ids), (i, g)
+            assert np.array_equal(ids_e[g][:len(w_ids)].numpy().astype(np.int64), w_ids), (i, g)
+            want.append(dict(ids=w_ids))
+        err = expect.attention_errors(bf16_bits(out_e), expect.expected_attention(case, want))
+        log(f"  layer {i}: ranked order, walk and ids equal the oracle's; attention {err}")
+        assert err["rel_l2"] <= 2e-3 and err["max_abs"] < 0.05, err

@@ -16,6 +16,7 @@ import numpy as np
 import pytest
 import torch
 
+import oracle
 from oracle import cases
 from tests.gpu_util import bf16_bits, log, operator, route_outputs
 from tests.test_gpu_hf import Capture, check_call, encoders, tiny_qwen3
@@ -167,6 +168,50 @@ def test_36_layer_step_graph():
         logits[use_graph] = torch.stack(out)
         ms[use_graph] = 1e3 * float(np.median(times[2:]))
     log(f"36-layer one-token step, H={P}: eager {ms[False]:.2f} ms, graph replay {ms[True]:.2f} ms")
+    assert torch.isfinite(logits[False]).all()
+    assert torch.equal(logits[False], logits[True])
+    session.close()
+
+
+def test_static_cache_decode_graph_with_cap():
+    # DecodeGraph over the capped step (route, budgeted walk, union + attention
+    # with the device tail length): replays bit-identical to the eager steps,
+    # and the eager steps match the oracle's walk over the device's index
+    from transformers import StaticCache
+    from prismkv_amd.hf import DecodeGraph, HFNative
+    layers, P, N, interval, cap = 2, 2048, 40, 32, 0.05
+    model = tiny_qwen3(layers)
+    session = HFNative(model, encoders(layers, seed=31), update_interval=interval, unique_cap=cap)
+    ids = torch.randint(0, 256, (1, P + N), generator=torch.Generator().manual_seed(19)).cuda()
+    logits = {}
+    for use_graph in (False, True):
+        session.begin_request()
+        cache = StaticCache(config=model.config, max_cache_len=P + N + 16)
+        step = DecodeGraph(session, cache, graph=use_graph)
+        _prefill(session, model, cache, ids, P)
+        out = []
+        for s in range(N):
+            out.append(step(ids[:, P + s:P + s + 1]).clone())
+            if not use_graph and s in (0, N - 1):
+                torch.cuda.synchronize()
+                for layer, op in session.ops.items():
+                    got = op.export_indices()
+                    feats, valid = op.features.cpu().numpy(), op.valid.cpu().numpy()
+                    count = op.count.cpu().numpy()
+                    for g in range(8):
+                        kept = [int(f) for f, ok in zip(feats[g], valid[g]) if ok > 0]
+                        lists = [l.numpy() for l in got[g].lists]
+                        w_ids, meta = oracle.select_buckets(np.array(kept, np.int64), lists, op.history, None)
+                        assert len(w_ids) <= int(op.history * cap)
+                        assert np.array_equal(op.ids[g, :count[g]].cpu().numpy().astype(np.int64), w_ids)
+                        assert int(op.raw[g]) == meta["raw"]
+        torch.cuda.synchronize()
+        for op in session.ops.values():
+            assert op.decode_errors() == 0
+        step.close()
+        logits[use_graph] = torch.stack(out)
+        log(f"capped graph={use_graph}: {N} steps, histories {[op.history for op in session.ops.values()]}, "
+            f"unique {[int(op.count.max()) for op in session.ops.values()]}")
     assert torch.isfinite(logits[False]).all()
     assert torch.equal(logits[False], logits[True])
     session.close()

@@ -142,3 +142,42 @@ def test_all_read_is_the_dense_model():
     for a, b in zip(dense, control):
         assert torch.equal(a, b)
     assert all(r["unique"] == 190 for r in session.records)
+
+
+def test_detailed_records_match_the_oracle():
+    # detailed_records=True adds initial_history, old_unique, old_raw and the
+    # generated_indexed_* fields (src/prismkv/hf_reference.py:216-231); after
+    # update blocks some selected ids lie beyond the prefix, so the generated
+    # fields are nonzero.  Checked against the oracle's walk over the device's
+    # kept buckets on the index the device holds.
+    from prismkv_amd.hf import HFNative
+    from transformers import DynamicCache
+    layers, P, steps, interval = 1, 600, 70, 32
+    model = tiny_qwen3(layers)
+    session = HFNative(model, encoders(layers, seed=21), update_interval=interval, detailed_records=True)
+    ids = torch.randint(0, 256, (1, P + steps), generator=torch.Generator().manual_seed(5)).cuda()
+    cache = DynamicCache(config=model.config)
+    generated = 0
+    with torch.no_grad():
+        model(ids[:, :P], past_key_values=cache, use_cache=True)
+        for s in range(steps):
+            model(ids[:, P + s:P + s + 1], past_key_values=cache, use_cache=True)
+            if s in (0, steps - 1):
+                op = session.ops[0]
+                recs = session.records[-8:]
+                got = op.export_indices()
+                feats, valid = op.features.cpu().numpy(), op.valid.cpu().numpy()
+                for g, rec in enumerate(recs):
+                    kept = [int(f) for f, ok in zip(feats[g], valid[g]) if ok > 0]
+                    lists = [l.numpy() for l in got[g].lists]
+                    w_ids, meta = oracle.select_buckets(np.array(kept, np.int64), lists, op.history, None)
+                    old_unique = int((w_ids < P).sum())
+                    old_raw = sum(int((lists[b] < P).sum()) for b in kept)
+                    assert rec["initial_history"] == P and rec["unique"] == len(w_ids) and rec["raw"] == meta["raw"]
+                    assert rec["old_unique"] == old_unique and rec["old_raw"] == old_raw, (s, g, rec)
+                    assert rec["generated_indexed_unique"] == len(w_ids) - old_unique
+                    assert rec["generated_indexed_raw"] == meta["raw"] - old_raw
+                    generated += rec["generated_indexed_unique"]
+                log(f"  step {s}: history={op.history}, generated ids selected {[r['generated_indexed_unique'] for r in recs]}")
+    assert session.ops[0].history > P and generated > 0
+    session.close()

@@ -4,9 +4,15 @@ layers, 32 query / 8 KV heads, head_dim 128, hidden 4096, MLP 12288 (vocab
 reduced to 32000), 32768 prefilled synthetic tokens, then 512 generated
 tokens decoded one by one (each layer's index is built on the device at the
 first decode step; the 512-token tail is attended densely).  At the last
-step every layer's sparse output is checked against the oracle's route +
-attention (src/prismkv/core.py:106-183) over the index the device holds,
-for three layers in full, and every layer reports no device error.
+step:
+  * every third layer (and the last) is checked in full against the oracle's
+    route + attention (src/prismkv/core.py:106-183) over the index the device
+    holds, and every layer reports no device error;
+  * every layer's Top-16 sparse output is compared with the all-read dense
+    attention over the same 33280 rows (exact fp32 softmax on the device):
+    the per-layer deviation of sparse from dense that the configuration
+    names, logged for all 36 layers (a measure of the routing's
+    approximation on this random-weight model, not a parity bar).
 """
 import numpy as np
 import pytest
@@ -16,6 +22,17 @@ from tests.gpu_util import log
 from tests.test_gpu_hf import Capture, check_call
 
 pytestmark = pytest.mark.gpu
+
+
+def dense_deviation(q, K, V, out):
+    """Relative L2 of the sparse output from the exact all-read attention of
+    the same 4 heads per group over every row (fp32 on the device)."""
+    qf = q.float()                                   # [8, 4, 128]
+    kt = K.float().transpose(1, 2).contiguous()      # [8, 128, rows]
+    p = torch.softmax((qf @ kt) / 128 ** 0.5, dim=-1)
+    dense = p @ V.float()                            # [8, 4, 128]
+    sparse = out.float()
+    return float((sparse - dense).norm() / dense.norm())
 
 
 def test_qwen3_8b_geometry_36_layer_step():
@@ -59,11 +76,19 @@ def test_qwen3_8b_geometry_36_layer_step():
     assert len(cap.calls) == L
     for layer, op in session.ops.items():
         assert op.history == P and op.decode_errors() == 0, layer
+    checked = set(range(0, L, 3)) | {L - 1}
+    deviation = {}
     for layer, q, K, V, out in cap.calls:
         assert K.shape[1] == P + T
-        if layer in (0, 17, 35):
+        if layer in checked:
             err = check_call(session.ops[layer], layer, q, K, V, out)
             log(f"  layer {layer}: history={P} tail={T} {err}")
+        deviation[layer] = dense_deviation(q, K, V, out)
+    log("  sparse vs all-read dense attention, relative L2 per layer: " +
+        " ".join(f"{layer}:{deviation[layer]:.3f}" for layer in sorted(deviation)))
+    dev = np.array([deviation[layer] for layer in sorted(deviation)])
+    log(f"  deviation over the 36 layers: mean {dev.mean():.3f}, min {dev.min():.3f}, max {dev.max():.3f}")
+    assert len(dev) == L and np.isfinite(dev).all()
     recs = session.records[-L * 8:]
     assert all(r["tail"] == T and r["buckets"] == 16 for r in recs)
     log(f"  unique ids per group, last step: mean {np.mean([r['unique'] for r in recs]):.0f}")

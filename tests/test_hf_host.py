@@ -112,3 +112,39 @@ def test_static_cache_session_on_host():
     step.close()
     assert session._static is None
     session.close()
+
+
+def test_detailed_record_fields_from_bitmaps():
+    # the detailed record fields (src/prismkv/hf_reference.py:216-231) computed
+    # from the device layout -- ascending ids with a count, bitmap rows of the
+    # kept buckets -- equal a direct count over the bucket lists
+    from types import SimpleNamespace
+    from prismkv_amd.hf import _old_unique_raw, _popcount32
+    words = torch.tensor([0, 1, -1, 0x7FFFFFFF, -2147483648, 0x55555555], dtype=torch.int32)
+    assert _popcount32(words).tolist() == [0, 1, 32, 31, 1, 16]
+    gen = torch.Generator().manual_seed(9)
+    H, width, row_words = 300, 16, 12
+    lists = [[torch.unique(torch.randint(0, H, (int(torch.randint(0, 40, (1,), generator=gen)),), generator=gen))
+              for _ in range(3000)] for _ in range(8)]
+    bits = torch.zeros(8, 3000, row_words, dtype=torch.int64)
+    for g in range(8):
+        for f in range(3000):
+            for t in lists[g][f].tolist():
+                bits[g, f, t // 32] |= 1 << (t % 32)
+    bits = torch.where(bits >= 2 ** 31, bits - 2 ** 32, bits).to(torch.int32)
+    features = torch.randint(0, 3000, (8, width), generator=gen)
+    valid = (torch.rand(8, width, generator=gen) > 0.3).float()
+    ids = torch.zeros(8, H, dtype=torch.int32)
+    count = torch.zeros(8, dtype=torch.int32)
+    for g in range(8):
+        u = torch.unique(torch.cat([lists[g][int(f)] for f, ok in zip(features[g], valid[g]) if ok > 0] +
+                                   [torch.zeros(0, dtype=torch.long)]))
+        ids[g, :len(u)] = u.int()
+        count[g] = len(u)
+    op = SimpleNamespace(ids=ids, count=count, bits=bits, features=features, valid=valid)
+    for prefix in (0, 1, 31, 32, 33, 100, 299, 300):
+        old_unique, old_raw = _old_unique_raw(op, prefix)
+        for g in range(8):
+            kept = [int(f) for f, ok in zip(features[g], valid[g]) if ok > 0]
+            assert int(old_unique[g]) == int((ids[g, :count[g]] < prefix).sum())
+            assert int(old_raw[g]) == sum(int((lists[g][f] < prefix).sum()) for f in kept), (prefix, g)
