@@ -78,6 +78,8 @@ def parse():
     p.add_argument("--update-blocks", default="1024,4096",
                    help="block sizes of the amortised index-update timing (tokens per append)")
     p.add_argument("--stages", default=DEFAULT_STAGES, help="comma list of timed regions (for profiling runs)")
+    p.add_argument("--library", default=None,
+                   help="a libprismkv_hip.so other than the in-tree one (A/B builds of prismkv_amd.build)")
     return p.parse_args()
 
 
@@ -545,7 +547,7 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(2)
     from prismkv_amd import _lib
-    lib_path = _lib.DEFAULT_LIBRARY
+    lib_path = a.library or _lib.DEFAULT_LIBRARY
     _lib.load(lib_path)
     device = torch.device("cuda", 0)
     torch.cuda.set_device(device)

@@ -39,13 +39,14 @@ def _sources(source_root: Path):
     return [source_root / s for s in SOURCES if (source_root / s).exists()]
 
 
-def _compile(hipcc, sources, output: Path, include_dirs, log):
+def _compile(hipcc, sources, output: Path, include_dirs, log, defines=()):
     """Compile each source to an object in parallel, then link the shared library."""
     with tempfile.TemporaryDirectory(prefix="prismkv_build_") as tmp:
         objects, commands = [], []
         for src in sources:
             obj = Path(tmp) / (src.stem + ".o")
-            cmd = [hipcc, *HIP_FLAGS, *[f"-I{d}" for d in include_dirs], "-c", str(src), "-o", str(obj)]
+            cmd = [hipcc, *HIP_FLAGS, *[f"-D{d}" for d in defines], *[f"-I{d}" for d in include_dirs], "-c", str(src),
+                   "-o", str(obj)]
             objects.append(obj)
             commands.append(cmd)
         with ThreadPoolExecutor(max_workers=min(len(commands), os.cpu_count() or 4)) as pool:
@@ -65,8 +66,10 @@ def _compile(hipcc, sources, output: Path, include_dirs, log):
         return rc, commands
 
 
-def compile_hip(source_root=CSRC, output_dir=None, rocm_root="/opt/rocm"):
-    """Build libprismkv_hip.so into a NEW directory; returns the library path."""
+def compile_hip(source_root=CSRC, output_dir=None, rocm_root="/opt/rocm", defines=()):
+    """Build libprismkv_hip.so into a NEW directory; returns the library path.
+    `defines` are NAME=VALUE preprocessor definitions (e.g.
+    PRISMKV_VALU_ATTENTION=1, the decode's VALU-attention A/B build)."""
     source_root = Path(source_root)
     if output_dir is None:
         raise ValueError("output_dir is required")
@@ -76,7 +79,7 @@ def compile_hip(source_root=CSRC, output_dir=None, rocm_root="/opt/rocm"):
     log: list[str] = []
     start = time.perf_counter()
     rc, commands = _compile(_hipcc(rocm_root), sources, output_dir / LIBRARY_NAME,
-                            [source_root, INCLUDE], log)
+                            [source_root, INCLUDE], log, defines)
     (output_dir / "build.log").write_text("\n".join(log), encoding="utf8")
     (output_dir / "build.json").write_text(json.dumps(dict(
         command=commands, seconds=time.perf_counter() - start, returncode=rc,
@@ -97,4 +100,12 @@ def build_inplace(rocm_root="/opt/rocm") -> Path:
 
 
 if __name__ == "__main__":
-    print(build_inplace())
+    import argparse
+    ap = argparse.ArgumentParser(description="build libprismkv_hip.so (in-tree by default)")
+    ap.add_argument("--output-dir", help="build into this new directory instead of in-tree")
+    ap.add_argument("--define", action="append", default=[], help="NAME=VALUE preprocessor definition")
+    args = ap.parse_args()
+    if args.output_dir:
+        print(compile_hip(CSRC, args.output_dir, defines=args.define))
+    else:
+        print(build_inplace())

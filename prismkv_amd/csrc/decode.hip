@@ -60,6 +60,15 @@
 #include "attend_mfma.h"
 #include "score.h"
 
+// The attention phase runs on the matrix cores (v_mfma_f32_16x16x32_bf16 for
+// QK, 16x16x16 for PV).  Building with -DPRISMKV_VALU_ATTENTION=1 swaps in the
+// fp32 VALU attention of attend_core.h (same loads, online softmax, state
+// layout and merge) for the A/B that chose the matrix cores: 26.9 against
+// 30.3 us per layer at H = 65536 on MI355X.
+#ifndef PRISMKV_VALU_ATTENTION
+#define PRISMKV_VALU_ATTENTION 0
+#endif
+
 namespace prismkv {
 namespace {
 
@@ -640,8 +649,29 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
       int pos = r < n_sel ? rows[r] : a.H + t_lo + (r - n_sel);
       return pos < 0 ? 0 : (pos > last_row ? last_row : pos);
     };
+#if PRISMKV_VALU_ATTENTION
+    // VALU attention (the A/B alternative, built with -DPRISMKV_VALU_ATTENTION=1):
+    // lane (q16, slot) holds dims 8 q16 .. 8 q16 + 8 of the rows of its slot
+    // (4 slots of 16 lanes, 4 rows each per 16-row block); P stays fp32
+    const int q16 = j, slot = qd;
+    float qf[kHq][8];
+#pragma unroll
+    for (int h = 0; h < kHq; ++h) {
+      unpack8(*reinterpret_cast<const uint4*>(a.q + ((size_t)g * kHq + h) * kD + 8 * q16), qf[h]);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qf[h][i] *= kLog2eScale;
+    }
+    SlotState st;
+    st.m = -INFINITY;
+    st.z = 0.f;
+#pragma unroll
+    for (int h = 0; h < kHq; ++h)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) st.acc[h][i] = 0.f;
+#else
     MfmaAttn st;
     mfma_init(st, a.q + (size_t)g * kHq * kD);
+#endif
     constexpr int kPerRound = 4;
     for (int b0 = r0; b0 < r1; b0 += kPerRound * 16) {
       uint4 kr[kPerRound][4], vr[kPerRound][4];
@@ -649,11 +679,20 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
       for (int i = 0; i < kPerRound; ++i) {
         const int base = b0 + 16 * i;
         if (base < r1) {  // uniform per wave
+#if PRISMKV_VALU_ATTENTION
+#pragma unroll
+          for (int b = 0; b < 4; ++b) {
+            const size_t at = (size_t)row_pos(base + 4 * slot + b) * kD + 8 * q16;
+            kr[i][b] = load_nt16(kg + at);
+            vr[i][b] = load_nt16(vg + at);
+          }
+#else
           const uint16_t* kp = kg + (size_t)row_pos(base + j) * kD + 8 * qd;
 #pragma unroll
           for (int c = 0; c < 4; ++c) kr[i][c] = load_nt16(kp + 32 * c);
 #pragma unroll
           for (int t = 0; t < 4; ++t) vr[i][t] = load_nt16(vg + (size_t)row_pos(base + 4 * qd + t) * kD + 8 * j);
+#endif
         }
       }
       asm volatile("" ::: "memory");  // every load of the round is in flight before any is used
@@ -667,7 +706,11 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
 #pragma unroll
       for (int i = 0; i < kPerRound; ++i) {
         const int base = b0 + 16 * i;
+#if PRISMKV_VALU_ATTENTION
+        if (base < r1) attend_step(qf, kr[i], vr[i], max(0, min(4, r1 - base - 4 * slot)), st);
+#else
         if (base < r1) mfma_block16(st, kr[i], vr[i], min(16, r1 - base));
+#endif
       }
     }
 
@@ -695,7 +738,40 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     // workgroup 0 that this workgroup no longer reads any published word);
     // its barriers also publish lds.base to every wave
     __syncthreads();  // the LDS union is free (the rows and base stay)
+#if PRISMKV_VALU_ATTENTION
+    {
+      // merge the wave's 4 slot states (lane bits 4, 5) into the stash layout
+      const int h = q16 & 3;
+      float M = fmaxf(st.m, xor16(st.m));
+      M = fmaxf(M, xor32(M));  // head h's max over the slots (lanes with q16 & 3 == h)
+      const float wgt = st.m == -INFINITY ? 0.f : exp2f(st.m - M);
+      float z = wgt * st.z;
+      z += xor16(z);
+      z += xor32(z);
+      if (slot == 0 && q16 < kHq) {
+        lds.mf.sm[w][h] = M;
+        lds.mf.sz[w][h] = z;
+      }
+#pragma unroll
+      for (int hh = 0; hh < kHq; ++hh) {
+        const float wh = __shfl(wgt, slot * 16 + hh);  // weight of head hh in this lane's slot
+        float acc[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          acc[i] = wh * st.acc[hh][i];
+          acc[i] += xor16(acc[i]);
+          acc[i] += xor32(acc[i]);
+        }
+        if (slot == 0) {
+          float4* dst = reinterpret_cast<float4*>(&lds.mf.sacc[w][hh][8 * q16]);
+          dst[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+          dst[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+        }
+      }
+    }
+#else
     mfma_stash(st, lds.mf, w);
+#endif
     publish_sliced(lds.mf, a.state + (size_t)(g * a.S + p) * kHq * kSlices * kSliceW);
   }
   {
