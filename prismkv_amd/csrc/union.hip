@@ -279,24 +279,82 @@ __device__ __forceinline__ int wave_sum_dpp(int v) {
   return __builtin_amdgcn_readlane(v, 63);
 }
 
-// One workgroup of kCapT threads per group.  Thread tid owns bitmap words
-// tid + kCapT u (u < WPT) of every row and keeps its slice of the running
-// union in registers; each bucket costs one block-wide popcount reduction.
-// The walk's loop issues no load whose value it waits for at once: wave 0
-// compacts the selection into LDS first (each lane keeps its bucket's size,
-// requested then and summed for raw after the walk); every
-// row load is unconditional (clamped address, the word mask applied where
-// the word is used), kAhead rows ahead, into kAhead + 1 register sets that
-// rotate by name (a copy would wait for the load), so each decision waits
-// only for its own row, requested kAhead decisions earlier: one workgroup
-// streams its group's rows, so rows in flight set its pace.
-template <int kCapT, int WPT, int kSel>
+// Raw buffer loads (gfx9 resource word 3: 32-bit data format) with the
+// non-temporal hint.
+constexpr int kRawBufferWord3 = 0x00020000;
+constexpr int kLoadNonTemporal = 2;
+template <int V>
+__device__ __forceinline__ void load_run(__amdgpu_buffer_rsrc_t r, unsigned byte_offset, uint32_t* m);
+template <>
+__device__ __forceinline__ void load_run<1>(__amdgpu_buffer_rsrc_t r, unsigned byte_offset, uint32_t* m) {
+  m[0] = __builtin_amdgcn_raw_buffer_load_b32(r, byte_offset, 0, kLoadNonTemporal);
+}
+template <>
+__device__ __forceinline__ void load_run<4>(__amdgpu_buffer_rsrc_t r, unsigned byte_offset, uint32_t* m) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, kLoadNonTemporal);
+  m[0] = v.x; m[1] = v.y; m[2] = v.z; m[3] = v.w;
+}
+
+// Row register sets of the walk: an even number of rows, as many as the load
+// counter (63 loads in flight) and about 128 registers hold, at most 16.
+constexpr int cap_row_sets(int loads_per_row, int words_per_row) {
+  int sets = 63 / loads_per_row;
+  if (128 / words_per_row < sets) sets = 128 / words_per_row;
+  return (sets < 16 ? sets : 16) & ~1;
+}
+
+// Workgroups past the groups' walkers pull the selected rows into L2 so
+// that the walker's loads hit there: workgroup b >= groups serves group
+// b % groups (with groups a multiple of 8, the walker's XCD under the
+// round-robin dispatch) and touches one word per 64 bytes of its part of
+// every selected row.  It reads the selection the walker rewrites at its
+// end; a helper that starts that late only touches other rows.
+template <int kSel>
+__device__ void touch_rows(const uint32_t* bits, int64_t row_words, const int64_t* features, const float* valid,
+                           int g, int part, int parts, int nw) {
+  const int lines = (nw + 15) >> 4, per = (lines + parts - 1) / parts;
+  const int lo = part * per, hi = lo + per < lines ? lo + per : lines;
+  const uint32_t* bg = bits + (size_t)g * kF * row_words;
+  unsigned acc = 0;
+  for (int j = 0; j < kSel; ++j) {
+    const int64_t f = features[(size_t)g * kSel + j];
+    if (!(valid[(size_t)g * kSel + j] > 0.f && f >= 0 && f < kF)) continue;
+    const uint32_t* row = bg + (size_t)f * row_words;
+    for (int l = lo + (int)threadIdx.x; l < hi; l += blockDim.x) acc ^= row[16 * l];
+  }
+  asm volatile("" ::"v"(acc));  // keeps the loads
+}
+
+// The budgeted walk, one workgroup of kCapT threads per group (workgroups
+// past `groups` are row-touching helpers).  Thread tid owns runs of V
+// consecutive words, V (tid + kCapT u) .. + V - 1 for u < R, of every row
+// (V = 4: one 16-byte load per run), and keeps its slice of the running
+// union U in registers.  Decisions go in pairs, one block-wide reduction per
+// pair: for ranked rows a, b with x = a \ U and y = b \ U the block sums
+// |x|, |y \ x| and |y ∩ x|; a is kept when total + |x| fits the limit, and b
+// when its size over the union as it then stands, |y \ x| if a was kept and
+// |y \ x| + |y ∩ x| if not, fits what is left -- the decisions of the
+// one-bucket-at-a-time walk.
+// Loads: every wave holds the selection in a register (lane j: ranked
+// bucket j), so a row's address is one lane read.  Each pair step requests
+// the rows kSets - 2 ranks ahead into register sets that rotate by name (a
+// copy would wait for the load), through a buffer resource whose range is
+// empty past the selection (such loads return 0 without a memory request).
+// kSets R loads in flight stay within the 63 that a wave's load counter
+// tracks, so the wait for a pair's rows is exact.
+template <int kCapT, int V, int R, int kSel>
 __global__ __launch_bounds__(kCapT) void cap_kernel(const uint32_t* __restrict__ bits, int64_t row_words,
                                                     const int* __restrict__ counts, int64_t* features, float* valid,
-                                                    int* raw, int H, long long limit) {
+                                                    int* raw, int H, long long limit, int groups) {
+  constexpr int WPT = V * R;
+  if ((int)blockIdx.x >= groups) {
+    touch_rows<kSel>(bits, row_words, features, valid, blockIdx.x % groups, blockIdx.x / groups - 1,
+                     gridDim.x / groups - 1, (H + 31) >> 5);
+    return;
+  }
   const int g = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   __shared__ int sel[kSel], nsel_s;
-  __shared__ int part[2][kCapT / 64];
+  __shared__ u32x4 part[2][kCapT / 64];  // per wave and pair: |x|, |y \ x|, |y ∩ x|
   // wave 0, lane j < kSel: ranked entry j, its rank among the valid ones and its size
   bool ok = false;
   int at = 0, cnt = 0;
@@ -314,74 +372,117 @@ __global__ __launch_bounds__(kCapT) void cap_kernel(const uint32_t* __restrict__
     if (lane == 0) nsel_s = __popcll(m);
   }
   __syncthreads();
-  const int n = nsel_s;
+  const int n = __builtin_amdgcn_readfirstlane(nsel_s);  // uniform: the row resources live in scalars
+  const int selv = sel[lane < kSel ? lane : kSel - 1];   // lane j < n: ranked bucket j
+  const int lim = limit < H ? (int)limit : H;            // a union never exceeds H
   const int nw = (H + 31) >> 5;
+  const int last_run = (nw - 1) / V;  // the last run that holds a word below nw
   const uint32_t tail_mask = (H & 31) ? (1u << (H & 31)) - 1u : ~0u;
   const uint32_t* bg = bits + (size_t)g * kF * row_words;
   uint32_t wmask[WPT];
-  unsigned wcol[WPT];  // unsigned: scalar base + 32-bit offset addressing
+  unsigned rcol[R];
 #pragma unroll
-  for (int u = 0; u < WPT; ++u) {
-    const int wd = tid + u * kCapT;
-    wmask[u] = wd < nw ? (wd == nw - 1 ? tail_mask : ~0u) : 0u;
-    wcol[u] = (unsigned)(wd < nw ? wd : nw - 1);
+  for (int u = 0; u < R; ++u) {
+    const int run = tid + u * kCapT;
+    rcol[u] = (unsigned)(V * (run <= last_run ? run : last_run));
+#pragma unroll
+    for (int e = 0; e < V; ++e) {
+      const int wd = V * run + e;
+      wmask[V * u + e] = run <= last_run && wd < nw ? (wd == nw - 1 ? tail_mask : ~0u) : 0u;
+    }
   }
-  auto load_row = [&](int j, uint32_t (&r)[WPT]) {  // row j (clamped to the last bucket), words unmasked
-    // the bucket is uniform: a scalar row base, so each load needs only its word offset
-    const int b = __builtin_amdgcn_readfirstlane(sel[j < n ? j : n - 1]);
-    const uint32_t* row = bg + (size_t)b * row_words;
+  const int row_bytes = (int)(4 * row_words);
+  auto load_row = [&](int j, uint32_t (&r)[WPT]) {  // j uniform
+    const int b = __builtin_amdgcn_readlane(selv, j < n ? j : n - 1);
+    const uint64_t a = reinterpret_cast<uint64_t>(bg + (size_t)b * row_words);
+    const uint64_t base = (uint64_t)__builtin_amdgcn_readfirstlane((unsigned)(a >> 32)) << 32 |
+                          (unsigned)__builtin_amdgcn_readfirstlane((unsigned)a);
+    const __amdgpu_buffer_rsrc_t rows = __builtin_amdgcn_make_buffer_rsrc(
+        reinterpret_cast<void*>(base), (short)0, __builtin_amdgcn_readfirstlane(j < n ? row_bytes : 0),
+        kRawBufferWord3);
 #pragma unroll
-    for (int u = 0; u < WPT; ++u) r[u] = __builtin_nontemporal_load(row + wcol[u]);
+    for (int u = 0; u < R; ++u) load_run<V>(rows, 4 * rcol[u], r + V * u);
   };
-  constexpr int kAhead = WPT >= 16 ? 3 : 7;  // as many rows as the registers hold without spilling
-  uint32_t chosen[WPT], rs[kAhead + 1][WPT];
+  constexpr int kSets = cap_row_sets(R, WPT), kAhead = kSets - 2;
+  static_assert(kSets >= 4 && kSets * R <= 63, "rows in flight exceed the load counter");
+  uint32_t chosen[WPT], rs[kSets][WPT];
 #pragma unroll
   for (int u = 0; u < WPT; ++u) chosen[u] = 0u;
-  long long total = 0;
+  int total = 0;
   unsigned long long accepted = 0;
-  // decision j on row `cur` (none for j >= n), requesting row j + kAhead into `fill`
-  auto step = [&](int j, uint32_t (&cur)[WPT], uint32_t (&fill)[WPT]) {
-    load_row(j + kAhead, fill);
-    int c = 0;
+  // decisions j and j + 1 (j < n) on rows ra, rb, requesting rows j + kAhead, j + kAhead + 1
+  auto pair = [&](int j, uint32_t (&ra)[WPT], uint32_t (&rb)[WPT], uint32_t (&fa)[WPT], uint32_t (&fb)[WPT]) {
+    load_row(j + kAhead, fa);
+    load_row(j + kAhead + 1, fb);
+    __builtin_amdgcn_sched_barrier(0);  // the requests go out before this pair waits
+    int cx = 0, cy = 0, cxy = 0;
 #pragma unroll
-    for (int u = 0; u < WPT; ++u) c += __popc(cur[u] & wmask[u] & ~chosen[u]);
-    c = wave_sum_dpp(c);
-    if (lane == 0) part[j & 1][w] = c;
+    for (int u = 0; u < WPT; ++u) {
+      const uint32_t x = ra[u] & wmask[u] & ~chosen[u], y = rb[u] & wmask[u] & ~chosen[u];
+      cx += __popc(x);
+      cy += __popc(y & ~x);
+      cxy += __popc(y & x);
+    }
+    cx = wave_sum_dpp(cx);
+    cy = wave_sum_dpp(cy);
+    cxy = wave_sum_dpp(cxy);
+    u32x4* slot = part[(j >> 1) & 1];
+    if (lane == 0) slot[w] = u32x4{(unsigned)cx, (unsigned)cy, (unsigned)cxy, 0u};
     __syncthreads();
-    // part[j & 1] is rewritten two buckets later, after the next barrier
-    long long add = 0;
+    // part[(j >> 1) & 1] is rewritten two pairs later, after the next barrier
+    int sx = 0, sy = 0, sxy = 0;
 #pragma unroll
-    for (int i = 0; i < kCapT / 64; ++i) add += part[j & 1][i];
-    if (j < n && total + add <= limit) {  // uniform: every thread holds the same sums
+    for (int i = 0; i < kCapT / 64; ++i) {
+      const u32x4 p = slot[i];
+      sx += (int)p.x;
+      sy += (int)p.y;
+      sxy += (int)p.z;
+    }
+    // uniform: every thread holds the same sums
+    const bool take_a = total + sx <= lim;
+    const int base = take_a ? total + sx : total, size_b = take_a ? sy : sy + sxy;
+    const bool take_b = j + 1 < n && base + size_b <= lim;
+    total = take_b ? base + size_b : base;
+    if (take_a) {
 #pragma unroll
-      for (int u = 0; u < WPT; ++u) chosen[u] |= cur[u] & wmask[u];
-      total += add;
+      for (int u = 0; u < WPT; ++u) chosen[u] |= ra[u] & wmask[u];
       accepted |= 1ull << j;
+    }
+    if (take_b) {
+#pragma unroll
+      for (int u = 0; u < WPT; ++u) chosen[u] |= rb[u] & wmask[u];
+      accepted |= 1ull << (j + 1);
     }
   };
   if (n > 0) {
+    // rows requested in rank order, as the loop requests them: the counter
+    // wait for a pair then covers exactly the rows before it
 #pragma unroll
-    for (int i = 0; i < kAhead; ++i) load_row(i, rs[i]);
-    // all kAhead + 1 steps of a round run (n is uniform; steps past n decide
-    // nothing and their rows repeat the last one), so no row load is left
-    // pending where branches join
-    for (int j = 0; j < n; j += kAhead + 1) {
+    for (int i = 0; i < kAhead; ++i) {
+      load_row(i, rs[i]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    // the walk leaves after its last decision (n is uniform); the loads
+    // still pending then are of empty ranges
+    for (int j = 0; j < n; j += kSets) {
 #pragma unroll
-      for (int i = 0; i <= kAhead; ++i) step(j + i, rs[i], rs[(i + kAhead) % (kAhead + 1)]);
+      for (int i = 0; i < kSets; i += 2) {
+        if (j + i >= n) break;
+        pair(j + i, rs[i], rs[i + 1], rs[(i + kAhead) % kSets], rs[(i + kAhead + 1) % kSets]);
+      }
     }
   }
+  // wave 0 writes the kept buckets in rank order, lane j its own
   if (w == 0) {
     const int raw_sum = wave_sum_dpp(ok && (accepted >> at & 1ull) ? cnt : 0);
-    if (lane == 0) {
-      int kept = 0;
-      for (int j = 0; j < n; ++j)
-        if (accepted >> j & 1ull) features[(size_t)g * kSel + kept++] = sel[j];
-      for (int j = 0; j < kSel; ++j) {
-        if (j >= kept) features[(size_t)g * kSel + j] = 0;
-        valid[(size_t)g * kSel + j] = j < kept ? 1.f : 0.f;
-      }
-      raw[g] = raw_sum;
+    const int kept = __popcll(accepted);
+    if (lane < kSel) {
+      int64_t* fg = features + (size_t)g * kSel;
+      if (lane < n && (accepted >> lane & 1ull)) fg[__popcll(accepted & ((1ull << lane) - 1ull))] = selv;
+      if (lane >= kept) fg[lane] = 0;
+      valid[(size_t)g * kSel + lane] = lane < kept ? 1.f : 0.f;
     }
+    if (lane == 0) raw[g] = raw_sum;
   }
 }
 
@@ -471,14 +572,23 @@ template <int kSel>
 static void launch_cap(const uint32_t* b, int64_t row_words, const int* c, int64_t* f, float* v, int* r, int groups,
                        int H, long long lim, hipStream_t s) {
   const int nw = (H + 31) / 32;
-  // 512 threads: half the waves to synchronise per decision, and the
-  // registers for 16 words per thread
-  if (nw <= 4 * 512)
-    hipLaunchKernelGGL((cap_kernel<512, 4, kSel>), dim3(groups), dim3(512), 0, s, b, row_words, c, f, v, r, H, lim);
-  else if (nw <= 16 * 512)
-    hipLaunchKernelGGL((cap_kernel<512, 16, kSel>), dim3(groups), dim3(512), 0, s, b, row_words, c, f, v, r, H, lim);
-  else  // up to 2^20 tokens
+  // 16-byte runs where every row starts 16-byte aligned
+  const bool quads = (row_words & 3) == 0 && (reinterpret_cast<uintptr_t>(b) & 15) == 0;
+  // 512 threads: half the waves to synchronise per decision of 1024, and the
+  // registers for 16 words per thread; above 2048 words a row, one
+  // row-touching workgroup per group for every 1024 words
+  const int parts = nw > 2048 ? (nw + 1023) / 1024 : 0;
+  const dim3 grid(groups * (1 + parts)), block(512);
+  if (nw > 16 * 512 || (!quads && nw > 4 * 512))  // up to 2^20 tokens
     hipLaunchKernelGGL(cap_big_kernel<kSel>, dim3(groups), dim3(kCapBigT), 0, s, b, row_words, c, f, v, r, H, lim);
+  else if (!quads)
+    hipLaunchKernelGGL((cap_kernel<512, 1, 4, kSel>), grid, block, 0, s, b, row_words, c, f, v, r, H, lim, groups);
+  else if (nw <= 4 * 512)
+    hipLaunchKernelGGL((cap_kernel<512, 4, 1, kSel>), grid, block, 0, s, b, row_words, c, f, v, r, H, lim, groups);
+  else if (nw <= 8 * 512)
+    hipLaunchKernelGGL((cap_kernel<512, 4, 2, kSel>), grid, block, 0, s, b, row_words, c, f, v, r, H, lim, groups);
+  else
+    hipLaunchKernelGGL((cap_kernel<512, 4, 4, kSel>), grid, block, 0, s, b, row_words, c, f, v, r, H, lim, groups);
 }
 
 static int select_cap(uint64_t bits, uint64_t counts, uint64_t features, uint64_t valid, uint64_t raw, int groups,

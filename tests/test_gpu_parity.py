@@ -297,6 +297,66 @@ def test_strict_unique_cap(H, tail, kind, cap):
     assert op.decode_errors() == 0
 
 
+@pytest.mark.parametrize("H,pad", [(1000, 0), (65536, 0), (65536, 1), (100000, 0), (262144, 0), (200000, 1),
+                                   (300000, 0)])
+def test_cap_walk_layouts(H, pad):
+    # prismkv_select_cap straight on bitmaps (src/prismkv/core.py:149-163):
+    # 16-byte runs at up to 2048 / 4096 / 8192 words a row (the latter two
+    # with row-touching workgroups), single words where a row is not 16-byte
+    # aligned (pad = 1 makes row_words odd), the LDS-union walk above 8192
+    # words or for an odd layout above 2048.  Rows of densities 1/2 .. 1/64,
+    # a selection with gaps and an out-of-range id, limits that keep from
+    # none to most of the ranked buckets; features / valid / raw must equal
+    # the oracle's walk over the valid ranked buckets.
+    from prismkv_amd import _lib
+    lib = _lib.load()
+    G, F = 8, 3000
+    nw = (H + 31) // 32
+    row_words = nw + pad
+    rng = np.random.default_rng(H + pad)
+    bits = torch.zeros(G, F, row_words, dtype=torch.int32, device="cuda")
+    counts = torch.zeros(G, 3008, dtype=torch.int32, device="cuda")
+    sel = np.stack([rng.permutation(F)[:16] for _ in range(G)]).astype(np.int64)
+    valid = np.ones((G, 16), np.float32)
+    valid[:, 5] = 0.0       # a gap in the ranked list
+    sel[3, 9] = F + 7       # an out-of-range id selects nothing
+    lists = [dict() for _ in range(G)]
+    for g in range(G):
+        for j in range(16):
+            b = int(sel[g, j])
+            if b >= F:
+                continue
+            dens = 2.0 ** -rng.integers(1, 7)
+            member = np.flatnonzero(rng.random(H) < dens)
+            lists[g][b] = member
+            words = np.zeros(row_words, np.uint32)
+            np.bitwise_or.at(words, member >> 5, (np.uint32(1) << (member & 31).astype(np.uint32)))
+            bits[g, b] = torch.from_numpy(words.view(np.int32)).cuda()
+            counts[g, b] = len(member)
+    stream = torch.cuda.current_stream().cuda_stream
+    for cap in (1 / 64, 1 / 16, 1 / 5, 1.0):
+        f = torch.from_numpy(sel).cuda()
+        v = torch.from_numpy(valid).cuda()
+        raw = torch.zeros(G, dtype=torch.int32, device="cuda")
+        limit = int(np.floor(H * cap))
+        lib.call("prismkv_select_cap", bits.data_ptr(), counts.data_ptr(), f.data_ptr(), v.data_ptr(), raw.data_ptr(),
+                 G, H, limit, row_words, stream=stream)
+        torch.cuda.synchronize()
+        f, v, raw = f.cpu().numpy(), v.cpu().numpy(), raw.cpu().numpy()
+        kept = []
+        for g in range(G):
+            order = [int(b) for b, ok in zip(sel[g], valid[g]) if ok > 0 and b < F]
+            table = [lists[g].get(b, np.zeros(0, np.int64)) for b in range(F)]
+            _, meta = oracle.select_buckets(np.array(order, np.int64), table, H, cap)
+            nf = len(meta["features"])
+            assert meta["limit"] == limit
+            assert f[g][:nf].tolist() == meta["features"] and not f[g][nf:].any(), (cap, g)
+            assert v[g].tolist() == [1.0] * nf + [0.0] * (16 - nf), (cap, g)
+            assert int(raw[g]) == meta["raw"], (cap, g)
+            kept.append(nf)
+        log(f"  walk H={H} row_words={row_words} cap={cap:.4f}: kept {kept}")
+
+
 @pytest.mark.parametrize("groups", [1, 2, 4])
 def test_fused_decode_fewer_groups(groups):
     # prismkv_decode on the first `groups` groups runs 256 / groups workgroups
