@@ -351,11 +351,13 @@ def long_history(lib_path, steps, warmup, seed, device, layers_total, replicas=1
 
 @torch.no_grad()
 def capped(lib_path, steps, warmup, seed, device, layers_total, replicas=12, H=262144, T=256, cap=1 / 16):
-    """Configuration 5: the capped step at H=262144 over mixture keys, three
-    launches per layer (prismkv_route_single, prismkv_select_cap_n,
-    prismkv_union_attend), 12 distinct layers chained to `layers_total`, in
-    one graph; per-stage graphs of each launch; the uncapped single launch
-    at the same history."""
+    """Configuration 5: the capped step at H=262144 over mixture keys, one
+    launch per layer (prismkv_decode_capped: route, the budgeted walk spread
+    over the group's workgroups, union + attention), 12 distinct layers
+    chained to `layers_total`, in one graph; for comparison the same step as
+    three launches (prismkv_route_single, prismkv_select_cap_n,
+    prismkv_union_attend) and per-stage graphs of each; the uncapped single
+    launch at the same history."""
     log(f"capped: building {replicas} mixture-key layers H={H} T={T} on the device ...")
     t0 = time.perf_counter()
     layers = [make_mixture_layer(lib_path, 200 + i, H, T, seed, device, cap) for i in range(replicas)]
@@ -381,6 +383,9 @@ def capped(lib_path, steps, warmup, seed, device, layers_total, replicas=12, H=2
     b_cap = float(np.mean([(r * nw * 4).sum() + G * TOPK * 12 for r in ranked]))
     b_ua = float(np.mean([(kp * nw * 4 + u * 4 + 4 + (u + T) * 2 * D * 2).sum() + 2 * G * HQ * D * 2
                           for kp, u in zip(kept, uniq)]))
+    # the one launch reads each ranked row once (the walk's words are the union's)
+    b_one = b_route + float(np.mean([(r * nw * 4).sum() for r in ranked])) + float(np.mean(
+        [(u * 4 + 4 + (u + T) * 2 * D * 2).sum() + 2 * G * HQ * D * 2 for u in uniq]))
 
     def step():
         for i in range(layers_total):
@@ -419,6 +424,8 @@ def capped(lib_path, steps, warmup, seed, device, layers_total, replicas=12, H=2
     for op, q, k, v in layers:
         op(q, k, v)  # the capped selection in features / valid again
     us_ua = stage(union_attend_only)
+    us_three = stage(lambda op, q, k, v: (route_only(op, q, k, v), walk_only(op, q, k, v),
+                                          union_attend_only(op, q, k, v)))
     # the uncapped single launch at the same history
     for op, _, _, _ in layers:
         op.unique_cap = None
@@ -430,16 +437,17 @@ def capped(lib_path, steps, warmup, seed, device, layers_total, replicas=12, H=2
     r, u, a, uniq_u = stage_bytes([l[0] for l in layers], H, T)
     out = dict(history=H, tail=T, unique_cap=cap, limit=limit, layers=layers_total, distinct_layers=replicas,
                keys="64-component Gaussian mixture, sigma 0.3, device-built index (global budget 8H)",
-               us_per_layer=round(us, 3), ms_per_step=round(ms, 4),
-               launches_per_layer=3, mean_ranked_buckets=round(float(np.mean(ranked)), 2),
+               us_per_layer=round(us, 3), ms_per_step=round(ms, 4), launches_per_layer=1,
+               decode_capped=rate(b_one, us), mean_ranked_buckets=round(float(np.mean(ranked)), 2),
                mean_kept_buckets=round(float(np.mean(kept)), 2),
                mean_unique_ids_per_group=round(float(np.mean(uniq)), 1), wait_errors=errors,
-               stages={"route_kernel": rate(b_route, us_route), "cap_walk": rate(b_cap, us_walk),
-                       "union_attend": rate(b_ua, us_ua)},
+               three_launches=dict(us_per_layer=round(us_three, 3),
+                                   stages={"route_kernel": rate(b_route, us_route), "cap_walk": rate(b_cap, us_walk),
+                                           "union_attend": rate(b_ua, us_ua)}),
                uncapped_single_launch=dict(rate(r + u + a, us_uncapped),
                                            mean_unique_ids_per_group=round(uniq_u, 1)))
-    log(f"capped: {us:.2f} us/layer (route {us_route:.2f} + walk {us_walk:.2f} + union/attend {us_ua:.2f}); "
-        f"uncapped single launch {us_uncapped:.2f}")
+    log(f"capped: {us:.2f} us/layer in one launch; three launches {us_three:.2f} (route {us_route:.2f} + walk "
+        f"{us_walk:.2f} + union/attend {us_ua:.2f}); uncapped single launch {us_uncapped:.2f}")
     del layers, run
     torch.cuda.empty_cache()
     return out

@@ -159,6 +159,29 @@ int prismkv_union_attend_tail(uint64_t q, uint64_t bits, uint64_t k, uint64_t v,
                               uint64_t valid, uint64_t ids, uint64_t count, uint64_t out, uint64_t tail, int groups, int H,
                               int max_tail, int capacity, int64_t row_words, int64_t ks, int64_t vs, int64_t ids_stride,
                               uint64_t stream);
+/* The capped step in ONE launch (replaces the strict unique cap branch of
+ * select_buckets, src/prismkv/core.py:149-163, between route and union,
+ * src/prismkv/native8b.py:104-106 with a cap): prismkv_decode with the
+ * budgeted walk between the selection and the union.  The group's Top-16 in
+ * rank order is walked with limit `limit` (>= 0; floor(H * unique_cap) in
+ * the reference): a bucket is kept when the union of the kept buckets,
+ * itself included, stays within the limit.  Writes features / valid / raw
+ * for the kept buckets (compacted in rank order, as prismkv_select_cap
+ * leaves them), their union's ids / count and the attention over it, the
+ * same results as prismkv_route_single + prismkv_select_cap +
+ * prismkv_union_attend.  The limits, workspace and -1 are prismkv_decode's. */
+int prismkv_decode_capped(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
+                          uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
+                          uint64_t out, int groups, int H, int T, int capacity, int64_t limit, int64_t row_words,
+                          int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream);
+/* prismkv_decode_capped with the tail length read from device memory at
+ * launch, as prismkv_decode_tail (no reference counterpart: a captured capped
+ * step replayed as the tail grows). */
+int prismkv_decode_capped_tail(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
+                               uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids,
+                               uint64_t count, uint64_t out, uint64_t tail, int groups, int H, int max_tail,
+                               int capacity, int64_t limit, int64_t row_words, int64_t ks, int64_t vs,
+                               int64_t ids_stride, uint64_t stream);
 
 /* The allocation-free decode.  No counterpart in the reference: for callers
  * that cannot allocate device memory (code under HIP graph capture, tight
@@ -181,7 +204,8 @@ int prismkv_decode_noalloc(uint64_t q, uint64_t moments, uint64_t counts, uint64
 /* ---- bounded waits and their error words (no reference counterpart: the
  * reference kernels never wait across workgroups) --------------------------
  * Every inter-workgroup wait of prismkv_decode, prismkv_decode_tail,
- * prismkv_union_attend, prismkv_route_single and prismkv_union gives up after
+ * prismkv_decode_capped(_tail), prismkv_union_attend, prismkv_route_single
+ * and prismkv_union gives up after
  * a process-wide number of sleeps (64 clocks each; default 2^20, tens of
  * milliseconds), writes 1 to its workspace's first 32-bit word (the sticky
  * error word, cleared only by the caller) and lets the launch run to its end

@@ -36,6 +36,9 @@ SIGNATURES = {
     "prismkv_union_attend": ([_U64] * 10 + [_I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64], True, _I32),
     "prismkv_decode_tail": ([_U64] * 14 + [_I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64], True, _I32),
     "prismkv_union_attend_tail": ([_U64] * 11 + [_I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64], True, _I32),
+    "prismkv_decode_capped": ([_U64] * 13 + [_I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64, _I64], True, _I32),
+    "prismkv_decode_capped_tail": ([_U64] * 14 + [_I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64, _I64], True,
+                                   _I32),
     "prismkv_select_cap": ([_U64] * 5 + [_I32, _I32, _I64, _I64], True, _I32),
     "prismkv_update_work_bytes": ([_I32, _I32], False, _SZ),
     "prismkv_update": ([_U64] * 9 + [_I32] * 4 + [_I64, _I64], True, _I32),

@@ -148,6 +148,20 @@ __device__ __forceinline__ int wave_sum_i(int v) {
   return v;
 }
 
+// Sum of v over the 64 lanes of a wave through DPP moves (no LDS round
+// trips): pairs, quads (quad_perm), 8 (row_half_mirror), 16 (row_mirror),
+// then row 0 into row 1 and row 2 into row 3 (row_bcast:15), rows 0-1 into
+// rows 2-3 (row_bcast:31); lane 63 holds the total.
+__device__ __forceinline__ int wave_sum_dpp(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+  v += __builtin_amdgcn_update_dpp(0, v, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+  v += __builtin_amdgcn_update_dpp(0, v, 0x141, 0xF, 0xF, false);  // row_half_mirror
+  v += __builtin_amdgcn_update_dpp(0, v, 0x140, 0xF, 0xF, false);  // row_mirror
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1, 3
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2, 3
+  return __builtin_amdgcn_readlane(v, 63);
+}
+
 // Inclusive prefix sum over the lanes of a wave64.
 __device__ __forceinline__ unsigned wave_incl_scan(unsigned v) {
   const int lane = threadIdx.x & 63;

@@ -103,6 +103,8 @@ struct DecodeArgs {
   unsigned* const* err_host;      // optional slot holding a host-mapped error word's address
   int spin;                       // bound of every wait (sleeps), prismkv_set_spin_limit
   float* state;  // [G][S][4 heads][4 slices][34] published split states
+  unsigned* walk;  // [G][4 windows][S][8] published pattern counts (capped launch)
+  int limit;       // the strict unique cap's limit (capped launch)
   int64_t* features;
   float* valid;
   int* raw;
@@ -123,6 +125,8 @@ struct DecodeLds {
   unsigned cover[kDT / 64];  // per wave: the winners' ranks whose rows it prefetched
   int chunk_rows[kDT / 64];  // per union chunk: its selected tokens
   float gmax[kHq], grz[kHq];
+  int walk_part[kDT / 64][8];  // capped launch: per wave, its packed pattern counts
+  unsigned walk_keep;          // capped launch: the window's kept rows
   union alignas(16) {
     struct {
       float4 qq[kRow];
@@ -325,9 +329,10 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int g, int h, i
 // usually among them.  Once the ranks are known, each wave ORs the rows of its
 // prefetched keys that won into lds.sel.ors[w] and marks their ranks in
 // lds.cover[w]; the union loads only the winners no wave prefetched.
-// Without kUnion (the route-only launch) nothing is prefetched.
+// Without kPrefetchRows (the route-only and the capped launch) nothing is
+// prefetched.
 constexpr int kPrefetch = 6;
-template <int KW, bool kUnion = true>
+template <int KW, bool kPrefetchRows = true>
 __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, DecodeLds& lds) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int nk = a.S * kTop;
@@ -355,7 +360,7 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, D
 #pragma unroll
   for (int r = 0; r < kPrefetch; ++r) {
     pk[r] = readlane_u64(best, r);  // rank r of this wave's list (uniform)
-    pw[r] = (kUnion && pk[r]) ? __builtin_nontemporal_load(gb + (size_t)row_of(pk[r]) * a.row_words) : 0u;
+    pw[r] = (kPrefetchRows && pk[r]) ? __builtin_nontemporal_load(gb + (size_t)row_of(pk[r]) * a.row_words) : 0u;
   }
   __syncthreads();
   constexpr int kListed = kDT / 64 * kTop;  // 128
@@ -398,9 +403,9 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, D
 }
 
 // Phases 1-4: the group's Top-16 (rank order) into lds.win (every wave) and
-// lds.sel_rows / lds.need (written and read by wave 0 only).  Without kUnion
-// only workgroup 0 runs phase 4.
-template <int KW, bool kUnion = true>
+// lds.sel_rows / lds.need.  Without kUnion only workgroup 0 runs phase 4;
+// kPrefetchRows requests the union's bitmap words in phase 4.
+template <int KW, bool kUnion = true, bool kPrefetchRows = kUnion>
 __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p, DecodeLds& lds) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int S = a.S;
@@ -493,14 +498,145 @@ __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p,
   if constexpr (!kUnion) {
     if (p != 0) return;
   }
-  final_top16<KW, kUnion>(a, g, p, lds);
+  final_top16<KW, kUnion && kPrefetchRows>(a, g, p, lds);
+}
+
+// ---- 4b. (capped launch) the strict unique cap's budgeted walk over the
+// group's ranked buckets (src/prismkv/core.py:149-163), spread over the
+// group's workgroups: workgroup p owns words [tw p, tw (p + 1)) of every
+// ranked row, thread t word tw p + t, and keeps its word of the union U of
+// the kept rows.  The ranks go in windows of 4.  For the window's rows,
+// x_i = row_i \ U, each workgroup counts its tokens of every membership
+// pattern m = 1..15 (the tokens in exactly the rows of m among the 4),
+// publishes the 15 counts and reads every workgroup's: row i then adds the
+// tokens whose pattern holds i and no row kept before it in the window,
+// which decides the window's rows in rank order exactly as the
+// one-bucket-at-a-time walk does, and every workgroup decides the same from
+// the same sums.  Returns this thread's word of U (0 past the tile) and the
+// kept ranks in *keep.
+constexpr int kWindow = 4;
+constexpr int kWindows = kTop / kWindow;
+constexpr int kPacked = 8;  // 15 pattern counts, two 16-bit counts per word
+
+__device__ __forceinline__ uint32_t capped_walk(const DecodeArgs& a, int g, int p, DecodeLds& lds, unsigned* keep) {
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int nr = lds.need;
+  const int nw = (a.H + 31) / 32, wd = p * a.tw + tid;
+  const bool col = tid < a.tw && wd < nw;
+  const uint32_t wmask = !col ? 0u : (wd == nw - 1 && (a.H & 31)) ? (1u << (a.H & 31)) - 1u : ~0u;
+  // every ranked row's word, all requested at once
+  uint32_t v[kTop];
+  {
+    const uint32_t* gb = a.bits + (size_t)g * kF * a.row_words + (col ? wd : 0);
+#pragma unroll
+    for (int r = 0; r < kTop; ++r)
+      v[r] = nr > 0 ? __builtin_nontemporal_load(gb + (size_t)lds.sel_rows[r < nr ? r : nr - 1] * a.row_words) : 0u;
+#pragma unroll
+    for (int r = 0; r < kTop; ++r) v[r] &= r < nr ? wmask : 0u;
+  }
+  const int lim = a.limit < a.H ? a.limit : a.H;  // a union never exceeds H
+  unsigned* rec = a.walk + (size_t)g * kWindows * a.S * kPacked;
+  uint32_t U = 0u;
+  int total = 0;
+  unsigned kept = 0u;
+#pragma unroll
+  for (int k = 0; k < kWindows; ++k) {
+    if (kWindow * k >= nr) break;  // uniform
+    uint32_t x[kWindow];
+#pragma unroll
+    for (int i = 0; i < kWindow; ++i) x[i] = v[kWindow * k + i] & ~U;
+    // pattern m = (rows 0, 1: m & 3) x (rows 2, 3: m >> 2)
+    const uint32_t lo[4] = {~x[0] & ~x[1], x[0] & ~x[1], ~x[0] & x[1], x[0] & x[1]};
+    const uint32_t hi[4] = {~x[2] & ~x[3], x[2] & ~x[3], ~x[2] & x[3], x[2] & x[3]};
+    int packed[kPacked];  // per wave: <= 2048 per count, so two fit a word
+#pragma unroll
+    for (int j = 0; j < kPacked; ++j) {
+      const int m0 = 2 * j + 1, m1 = 2 * j + 2;
+      const int c0 = __popc(lo[m0 & 3] & hi[m0 >> 2]);
+      const int c1 = m1 < 16 ? __popc(lo[m1 & 3] & hi[(m1 >> 2) & 3]) : 0;
+      packed[j] = wave_sum_dpp(c0 | c1 << 16);
+    }
+    if (lane == 0) {
+#pragma unroll
+      for (int j = 0; j < kPacked; ++j) lds.walk_part[w][j] = packed[j];
+    }
+    __syncthreads();
+    if (w == 0) {
+      // the workgroup's counts (<= 16384 each: no carry between the halves),
+      // published complemented; then every workgroup's, lane l summing word
+      // l & 7 of workgroups (l >> 3) + 8 i
+      if (lane < kPacked) {
+        unsigned sum = 0u;
+#pragma unroll
+        for (int ww = 0; ww < kDT / 64; ++ww) sum += (unsigned)lds.walk_part[ww][lane];
+        st_dev(&rec[((size_t)k * a.S + p) * kPacked + lane], ~sum);
+      }
+      const int j = lane & 7;
+      int s0 = 0, s1 = 0;
+      for (int q0 = lane >> 3; q0 < a.S; q0 += 32) {
+        unsigned r[4] = {0u, 0u, 0u, 0u};
+        wait_all([&] {
+          bool done = true;
+#pragma unroll
+          for (int t = 0; t < 4; ++t) {
+            const int q = q0 + 8 * t;
+            if (q < a.S && r[t] == 0u) r[t] = ld_dev(&rec[((size_t)k * a.S + q) * kPacked + j]);
+            done = done && (q >= a.S || r[t] != 0u);
+          }
+          return done;
+        }, a);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          if (q0 + 8 * t < a.S) {
+            const unsigned c = ~r[t];
+            s0 += (int)(c & 0xFFFFu);
+            s1 += (int)(c >> 16);
+          }
+      }
+#pragma unroll
+      for (int o = 8; o < 64; o <<= 1) {
+        s0 += __shfl_xor(s0, o);
+        s1 += __shfl_xor(s1, o);
+      }
+      // lane j < 8: the group's counts of patterns 2j + 1 (s0) and 2j + 2 (s1)
+      int cnt[16];
+      cnt[0] = 0;
+#pragma unroll
+      for (int jj = 0; jj < kPacked; ++jj) {
+        cnt[2 * jj + 1] = __builtin_amdgcn_readlane(s0, jj);
+        if (2 * jj + 2 < 16) cnt[2 * jj + 2] = __builtin_amdgcn_readlane(s1, jj);
+      }
+      unsigned kw = 0u;  // the window's kept rows so far
+#pragma unroll
+      for (int i = 0; i < kWindow; ++i) {
+        if (kWindow * k + i >= nr) break;
+        int add = 0;
+#pragma unroll
+        for (int m = 1; m < 16; ++m) add += ((m >> i) & 1) && !(m & kw) ? cnt[m] : 0;
+        if (total + add <= lim) {
+          kw |= 1u << i;
+          total += add;
+        }
+      }
+      if (lane == 0) lds.walk_keep = kw;
+    }
+    __syncthreads();
+    const unsigned kw = lds.walk_keep;
+#pragma unroll
+    for (int i = 0; i < kWindow; ++i) U |= (kw >> i) & 1u ? x[i] : 0u;
+    kept |= kw << (kWindow * k);
+  }
+  *keep = kept;
+  return U;
 }
 
 // KW = 64-key candidate sets per wave, ceil(S / 32): one instantiation per
 // range of S, so a launch carries only the selection code it runs.  With
 // kGiven the selection is not computed but read from features / valid (as
-// a strict unique cap leaves them) and phases 5-9 run on it.
-template <int KW, bool kGiven = false>
+// a strict unique cap leaves them) and phases 5-9 run on it.  With kCap the
+// strict unique cap's walk (phase 4b) runs between the selection and the
+// union, on the same launch.
+template <int KW, bool kGiven = false, bool kCap = false>
 __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   const int p = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   __shared__ DecodeLds lds;
@@ -530,12 +666,34 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     lds.sel.ors[w][lane] = 0u;
     if (lane == 0) lds.cover[w] = 0u;
     __syncthreads();
-  } else {
+  } else if constexpr (!kCap) {
     // ---- 1-4. the group's Top-16
     decode_select<KW>(a, g, p, lds);
     if (p == 0 && w == 0)
       write_selection(lds.win, lds.need, a.counts + (size_t)g * kFP, a.features + (size_t)g * kTop,
                       a.valid + (size_t)g * kTop, a.raw + g);
+  }
+  // ---- 1-4b. the group's Top-16, then the budgeted walk over it: this
+  // thread's word of the kept rows' union, and the kept buckets (in rank
+  // order, compacted) into features / valid / raw
+  uint32_t walked = 0u;
+  if constexpr (kCap) {
+    decode_select<KW, true, false>(a, g, p, lds);
+    unsigned keep = 0u;
+    walked = capped_walk(a, g, p, lds, &keep);
+    if (p == 0 && w == 0) {
+      const int nkept = __popc(keep);
+      const bool kept = lane < kTop && ((keep >> lane) & 1u);
+      const int b = lane < kTop ? lds.sel_rows[lane] : 0;
+      if (lane < kTop) {
+        int64_t* fg = a.features + (size_t)g * kTop;
+        if (kept) fg[__popc(keep & ((1u << lane) - 1u))] = b;
+        if (lane >= nkept) fg[lane] = 0;
+        a.valid[(size_t)g * kTop + lane] = lane < nkept ? 1.f : 0.f;
+      }
+      const int n = wave_sum_i(kept ? a.counts[(size_t)g * kFP + b] : 0);
+      if (lane == 0) a.raw[g] = n;
+    }
   }
 
   // ---- 5. union tile: OR the selected rows over words [tw p, tw (p + 1)), compact.
@@ -549,14 +707,16 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     if (w == 0) {
       const int nr = lds.need;
       const int wd = p * a.tw + lane;
-      uint32_t m = 0;
+      uint32_t m = walked;  // the capped launch's union word (lane = tile word)
       unsigned covered = 0u;
+      if constexpr (!kCap) {
 #pragma unroll
-      for (int k = 0; k < kDT / 64; ++k) {
-        m |= lds.sel.ors[k][lane];
-        covered |= lds.cover[k];
+        for (int k = 0; k < kDT / 64; ++k) {
+          m |= lds.sel.ors[k][lane];
+          covered |= lds.cover[k];
+        }
       }
-      const unsigned missing = ((1u << nr) - 1u) & ~covered;  // winners' ranks no wave prefetched (uniform)
+      const unsigned missing = kCap ? 0u : ((1u << nr) - 1u) & ~covered;  // winners' ranks no wave prefetched (uniform)
       if (missing && lane < a.tw && wd < nw) {
         // one round of loads: every rank loads (a covered one repeats the first
         // missing row) and only the missing ones are kept
@@ -587,10 +747,10 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     const int chunks = (a.tw + kTileWords - 1) / kTileWords;  // <= 8
     const int cw = w * kTileWords + lane, wd = p * a.tw + cw;
     const int nr = lds.need;
-    uint32_t m = 0u;
+    uint32_t m = walked;  // the capped launch's union word (thread = tile word)
     int n = 0, incl = 0;
     if (w < chunks) {
-      if (nr > 0 && cw < a.tw && wd < nw) {
+      if (!kCap && nr > 0 && cw < a.tw && wd < nw) {
         const uint32_t* gb = a.bits + (size_t)g * kF * a.row_words + wd;
         uint32_t v[kTop];
 #pragma unroll
@@ -789,6 +949,8 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     for (int i = tid; i < kChunks * kHq; i += kDT) st_dev(&a.stats[(size_t)g * kChunks * kHq + i], 0ull);
     for (int i = tid; i < a.S * kTop; i += kDT) st_dev(&a.cand[(size_t)g * a.S * kTop + i], 0ull);
     for (int i = tid; i < a.S; i += kDT) st_dev(&a.status[(size_t)g * a.S + i], 0u);
+    if constexpr (kCap)
+      for (int i = tid; i < kWindows * a.S * kPacked; i += kDT) st_dev(&a.walk[(size_t)g * kWindows * a.S * kPacked + i], 0u);
   }
 }
 
@@ -829,9 +991,11 @@ int spin_limit() { return __atomic_load_n(&g_spin_limit, __ATOMIC_RELAXED); }
 }  // namespace prismkv
 
 // Work layout (bytes) for the split count of `groups` groups:
-// err (the error word, then the host-word slot at byte 8) | stats | candidates | status | state
+// err (the error word, then the host-word slot at byte 8) | stats | candidates | status | state | walk.
+// The walk's records come last: only the capped launch uses them, so the
+// other launches touch the first `walk` bytes only.
 struct DecodeWorkLayout {
-  size_t err, stats, cand, status, state, total;
+  size_t err, stats, cand, status, state, walk, total;
   DecodeWorkLayout(int groups, int S) {
     size_t o = 0;
     auto take = [&](size_t n) { const size_t at = o; o += (n + 255) & ~(size_t)255; return at; };
@@ -840,6 +1004,7 @@ struct DecodeWorkLayout {
     cand = take((size_t)groups * S * kTop * sizeof(unsigned long long));
     status = take((size_t)groups * S * sizeof(unsigned));
     state = take((size_t)groups * S * kHq * kSlices * kSliceW * sizeof(float));
+    walk = take((size_t)groups * kWindows * S * kPacked * sizeof(unsigned));
     total = o;
   }
 };
@@ -865,7 +1030,11 @@ static int resident_workgroups() {
                          reinterpret_cast<const void*>(decode_kernel<1, true>),
                          reinterpret_cast<const void*>(decode_kernel<2, true>),
                          reinterpret_cast<const void*>(decode_kernel<4, true>),
-                         reinterpret_cast<const void*>(decode_kernel<8, true>)};
+                         reinterpret_cast<const void*>(decode_kernel<8, true>),
+                         reinterpret_cast<const void*>(decode_kernel<1, false, true>),
+                         reinterpret_cast<const void*>(decode_kernel<2, false, true>),
+                         reinterpret_cast<const void*>(decode_kernel<4, false, true>),
+                         reinterpret_cast<const void*>(decode_kernel<8, false, true>)};
     for (const void* fn : fns) {
       if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kTileTokens * (int)sizeof(int)) !=
           hipSuccess)
@@ -884,8 +1053,10 @@ static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t b
                        uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
                        uint64_t out, const int* tail_dev, bool given, int groups, int H, int T, int capacity,
                        int64_t row_words, int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream,
-                       unsigned* err = nullptr) {
+                       unsigned* err = nullptr, int64_t limit = -1) {
+  // limit >= 0: the capped launch (route, the strict unique cap's walk, union + attention)
   if (groups < 1 || groups > 65535 || H < 1 || H > kFusedMaxHistory || T < 0 || capacity < H) return kBadSize;
+  if (given && limit >= 0) return kBadSize;
   if (row_words < (H + 31) / 32 || ids_stride < H) return kBadSize;
   if (ks < (int64_t)(H + T) * kD || vs < (int64_t)(H + T) * kD) return kBadSize;
   // a given selection needs neither the moment tables nor raw
@@ -919,6 +1090,8 @@ static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t b
   a.err_host = err ? nullptr : error_host_slot(a.err);
   a.spin = spin_limit();
   a.state = reinterpret_cast<float*>(w + L.state);
+  a.walk = reinterpret_cast<unsigned*>(w + L.walk);
+  a.limit = (int)std::min<int64_t>(limit, H);
   a.features = reinterpret_cast<int64_t*>(features);
   a.valid = reinterpret_cast<float*>(valid);
   a.raw = reinterpret_cast<int*>(raw);
@@ -929,7 +1102,12 @@ static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t b
   const dim3 grid(S, groups), block(kDT);
   hipStream_t s = (hipStream_t)stream;
   const size_t rows_bytes = (size_t)32 * a.tw * sizeof(int);  // the tile's row list (dynamic LDS)
-  if (given) {
+  if (limit >= 0) {
+    if (S <= 32) hipLaunchKernelGGL((decode_kernel<1, false, true>), grid, block, rows_bytes, s, a);
+    else if (S <= 64) hipLaunchKernelGGL((decode_kernel<2, false, true>), grid, block, rows_bytes, s, a);
+    else if (S <= 128) hipLaunchKernelGGL((decode_kernel<4, false, true>), grid, block, rows_bytes, s, a);
+    else hipLaunchKernelGGL((decode_kernel<8, false, true>), grid, block, rows_bytes, s, a);
+  } else if (given) {
     if (S <= 32) hipLaunchKernelGGL((decode_kernel<1, true>), grid, block, rows_bytes, s, a);
     else if (S <= 64) hipLaunchKernelGGL((decode_kernel<2, true>), grid, block, rows_bytes, s, a);
     else if (S <= 128) hipLaunchKernelGGL((decode_kernel<4, true>), grid, block, rows_bytes, s, a);
@@ -984,13 +1162,14 @@ int prismkv_decode_noalloc(uint64_t q, uint64_t moments, uint64_t counts, uint64
                            uint64_t out, uint64_t err, int groups, int H, int T, int capacity, int64_t row_words,
                            int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream) {
   if (groups < 1 || groups > 65535 || !err || err % 4) return kBadSize;
+  // the uncapped launch touches the layout's first L.walk bytes only
   const DecodeWorkLayout L(groups, decode_splits(groups));
-  if (L.total > kScratchBytes) return kBadSize;  // the workspace of more than 13 groups does not fit
+  if (L.walk > kScratchBytes) return kBadSize;  // the workspace of more than 13 groups does not fit
   char* work = scratch_address();
   if (!work) return (int)hipErrorInvalidSymbol;
   // a call that gave up may have left published words behind: start from zero
-  hipLaunchKernelGGL(clear_words, dim3((unsigned)std::min<size_t>(1024, (L.total / 16 + 255) / 256)), dim3(256), 0,
-                     (hipStream_t)stream, reinterpret_cast<uint4*>(work), L.total / 16);
+  hipLaunchKernelGGL(clear_words, dim3((unsigned)std::min<size_t>(1024, (L.walk / 16 + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, reinterpret_cast<uint4*>(work), L.walk / 16);
   const int rc = (int)hipGetLastError();
   if (rc) return rc;
   return decode_impl(q, moments, counts, bits, k, v, reinterpret_cast<uint64_t>(work), features, valid, raw, ids,
@@ -1081,6 +1260,26 @@ int prismkv_decode_tail(uint64_t q, uint64_t moments, uint64_t counts, uint64_t 
   return decode_impl(q, moments, counts, bits, k, v, work, features, valid, raw, ids, count, out,
                      reinterpret_cast<const int*>(tail), false, groups, H, max_tail, capacity, row_words, ks, vs,
                      ids_stride, stream);
+}
+
+int prismkv_decode_capped(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
+                          uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
+                          uint64_t out, int groups, int H, int T, int capacity, int64_t limit, int64_t row_words,
+                          int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream) {
+  if (limit < 0) return kBadSize;
+  return decode_impl(q, moments, counts, bits, k, v, work, features, valid, raw, ids, count, out, nullptr, false, groups,
+                     H, T, capacity, row_words, ks, vs, ids_stride, stream, nullptr, limit);
+}
+
+int prismkv_decode_capped_tail(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
+                               uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids,
+                               uint64_t count, uint64_t out, uint64_t tail, int groups, int H, int max_tail,
+                               int capacity, int64_t limit, int64_t row_words, int64_t ks, int64_t vs,
+                               int64_t ids_stride, uint64_t stream) {
+  if (!tail || tail % 4 || limit < 0) return kBadSize;
+  return decode_impl(q, moments, counts, bits, k, v, work, features, valid, raw, ids, count, out,
+                     reinterpret_cast<const int*>(tail), false, groups, H, max_tail, capacity, row_words, ks, vs,
+                     ids_stride, stream, nullptr, limit);
 }
 
 }  // extern "C"

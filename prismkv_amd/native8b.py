@@ -357,11 +357,15 @@ class Native8B:
                           self.raw.data_ptr(), GROUPS, stream=s)
         width = self.features.shape[1]
         if self.unique_cap is not None:
-            limit = math.floor(self.history * self.unique_cap)
             self.lib.call("prismkv_select_cap_n", self.bits.data_ptr(), self.n.data_ptr(), self.features.data_ptr(),
-                          self.valid.data_ptr(), self.raw.data_ptr(), GROUPS, self.history, limit, self.row_words,
-                          width, stream=s)
+                          self.valid.data_ptr(), self.raw.data_ptr(), GROUPS, self.history, self._cap_limit(),
+                          self.row_words, width, stream=s)
         return width
+
+    def _cap_limit(self):
+        """The strict unique cap's limit, floor(history * unique_cap)
+        (src/prismkv/core.py:155)."""
+        return math.floor(self.history * self.unique_cap)
 
     @property
     def router(self):
@@ -433,8 +437,9 @@ class Native8B:
         decode path: one launch, every output buffer (features, valid, raw,
         ids, count, out) written as by the two calls -- the selection and ids
         bit-identical, out within rounding of the separate attention kernel.
-        With a unique cap: the route and the budgeted walk, then the union and
-        the attention in one launch over the walked selection.
+        With a unique cap the same launch runs the budgeted walk between the
+        selection and the union (features / valid / raw then hold the kept
+        buckets, compacted in rank order, as route() leaves them).
 
         `tail` (no reference counterpart): an int32 CUDA tensor of one element
         holding the tail length T, read by the kernel at launch instead of
@@ -442,8 +447,7 @@ class Native8B:
         for T up to their length (a static KV buffer).  A launch captured in a
         HIP graph is replayed with whatever the tensor holds, clamped to
         [0, K rows - history].  The moments router with histories up to
-        FUSED_MAX_HISTORY: the single launch, or with a unique cap the route,
-        the walk and the union + attention launch."""
+        FUSED_MAX_HISTORY (the single launch, with or without a cap)."""
         self._check_kv(q, k, v, kwargs.get("splits", 64), kwargs.get("schedule", 0))
         self.check_errors()
         if tail is not None:
@@ -454,12 +458,13 @@ class Native8B:
                     or tail.device != self.out.device):
                 raise ValueError("tail must be a one-element int32 tensor on the index device")
             if self.unique_cap is not None:
-                self._select(q)
-                self.lib.call("prismkv_union_attend_tail", q.data_ptr(), self.bits.data_ptr(), k.data_ptr(),
-                              v.data_ptr(), self.decode_work.data_ptr(), self.features.data_ptr(),
-                              self.valid.data_ptr(), self.ids.data_ptr(), self.count.data_ptr(), self.out.data_ptr(),
+                self.lib.call("prismkv_decode_capped_tail", q.data_ptr(), self.moments.data_ptr(),
+                              self.n.data_ptr(), self.bits.data_ptr(), k.data_ptr(), v.data_ptr(),
+                              self.decode_work.data_ptr(), self.features.data_ptr(), self.valid.data_ptr(),
+                              self.raw.data_ptr(), self.ids.data_ptr(), self.count.data_ptr(), self.out.data_ptr(),
                               tail.data_ptr(), GROUPS, self.history, k.shape[1] - self.history, self.capacity,
-                              self.row_words, k.stride(0), v.stride(0), self.capacity, stream=self._stream())
+                              self._cap_limit(), self.row_words, k.stride(0), v.stride(0), self.capacity,
+                              stream=self._stream())
                 return self.out
             self.lib.call("prismkv_decode_tail", q.data_ptr(), self.moments.data_ptr(), self.n.data_ptr(),
                           self.bits.data_ptr(), k.data_ptr(), v.data_ptr(), self.decode_work.data_ptr(),
@@ -474,14 +479,13 @@ class Native8B:
             self.route(q)
             return self.attention(q, k, v, **kwargs)
         if self.unique_cap is not None:
-            # the budgeted walk runs between selection and union: route and walk,
-            # then union + attention in one launch on the walked selection
-            self._select(q)
-            self.lib.call("prismkv_union_attend", q.data_ptr(), self.bits.data_ptr(), k.data_ptr(), v.data_ptr(),
-                          self.decode_work.data_ptr(), self.features.data_ptr(), self.valid.data_ptr(),
-                          self.ids.data_ptr(), self.count.data_ptr(), self.out.data_ptr(), GROUPS, self.history,
-                          k.shape[1] - self.history, self.capacity, self.row_words, k.stride(0), v.stride(0),
-                          self.capacity, stream=self._stream())
+            # the budgeted walk runs between selection and union, on the same launch
+            self.lib.call("prismkv_decode_capped", q.data_ptr(), self.moments.data_ptr(), self.n.data_ptr(),
+                          self.bits.data_ptr(), k.data_ptr(), v.data_ptr(), self.decode_work.data_ptr(),
+                          self.features.data_ptr(), self.valid.data_ptr(), self.raw.data_ptr(), self.ids.data_ptr(),
+                          self.count.data_ptr(), self.out.data_ptr(), GROUPS, self.history,
+                          k.shape[1] - self.history, self.capacity, self._cap_limit(), self.row_words, k.stride(0),
+                          v.stride(0), self.capacity, stream=self._stream())
             return self.out
         self.lib.call("prismkv_decode", q.data_ptr(), self.moments.data_ptr(), self.n.data_ptr(), self.bits.data_ptr(),
                       k.data_ptr(), v.data_ptr(), self.decode_work.data_ptr(), self.features.data_ptr(),

@@ -279,9 +279,9 @@ def test_strict_unique_cap(H, tail, kind, cap):
     first = bf16_bits(out).copy()
     err = expect.attention_errors(first, expected)
     assert err["rel_l2"] <= AV_TOL and err["max_abs"] < 0.05, err
-    # __call__ with a cap: route and walk, then union + attention in one
-    # launch (prismkv_union_attend) over the walked selection: the same
-    # selection, ids and count, and the attention within the same bound
+    # __call__ with a cap: route, the walk spread over the group's
+    # workgroups, union and attention in one launch (prismkv_decode_capped):
+    # the same selection, ids and count, and the attention within the bound
     op.ids.zero_()
     op.count.zero_()
     out = op(q, k, v)
@@ -292,9 +292,32 @@ def test_strict_unique_cap(H, tail, kind, cap):
     for g in range(8):
         assert np.array_equal(i3[g][:c3[g]], i2[g][:c2[g]]), ("ids, one launch", g)
     err = expect.attention_errors(bf16_bits(out), expected)
-    log(f"  capped call, union + attention in one launch: {err}")
+    log(f"  capped call, one launch: {err}")
     assert err["rel_l2"] <= AV_TOL and err["max_abs"] < 0.05, err
+    # ... and bit for bit the three launches (route, prismkv_select_cap,
+    # prismkv_union_attend over the walked selection)
+    fused = bf16_bits(out).copy()
+    three = three_launch_capped(op, q, k, v)
+    assert np.array_equal(fused, three), "capped: one launch vs three"
     assert op.decode_errors() == 0
+
+
+def three_launch_capped(op, q, k, v, groups=8, work=None):
+    """The capped step as three launches into op's buffers: the route
+    (prismkv_route_single), the walk (prismkv_select_cap) and union +
+    attention over the walked selection (prismkv_union_attend); out bits."""
+    s = torch.cuda.current_stream().cuda_stream
+    work = op.decode_work if work is None else work
+    op.lib.call("prismkv_route_single", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(), work.data_ptr(),
+                op.features.data_ptr(), op.valid.data_ptr(), op.raw.data_ptr(), groups, stream=s)
+    op.lib.call("prismkv_select_cap", op.bits.data_ptr(), op.n.data_ptr(), op.features.data_ptr(),
+                op.valid.data_ptr(), op.raw.data_ptr(), groups, op.history, op._cap_limit(), op.row_words, stream=s)
+    op.lib.call("prismkv_union_attend", q.data_ptr(), op.bits.data_ptr(), k.data_ptr(), v.data_ptr(),
+                work.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(), op.ids.data_ptr(),
+                op.count.data_ptr(), op.out.data_ptr(), groups, op.history, k.shape[1] - op.history, op.capacity,
+                op.row_words, k.stride(0), v.stride(0), op.capacity, stream=s)
+    torch.cuda.synchronize()
+    return bf16_bits(op.out).copy()
 
 
 @pytest.mark.parametrize("H,pad", [(1000, 0), (65536, 0), (65536, 1), (100000, 0), (262144, 0), (200000, 1),
@@ -355,6 +378,42 @@ def test_cap_walk_layouts(H, pad):
             assert int(raw[g]) == meta["raw"], (cap, g)
             kept.append(nf)
         log(f"  walk H={H} row_words={row_words} cap={cap:.4f}: kept {kept}")
+
+
+@pytest.mark.parametrize("groups", [1, 2, 4, 8])
+def test_capped_decode_groups(groups):
+    # prismkv_decode_capped on the first `groups` groups (32 .. 256 workgroups
+    # per group, so 32 .. 256 records per walk window): features / valid /
+    # raw / ids / count and out bit for bit as the three launches on the same
+    # groups, at caps that keep from none to all of the ranked buckets
+    case = cases.native_case(32768, 40, "random", seed=17)
+    op, q, k, v = operator(case)
+    s = torch.cuda.current_stream().cuda_stream
+    work = torch.zeros(op.lib.query("prismkv_decode_work_bytes", groups, op.capacity), dtype=torch.uint8,
+                       device="cuda")
+    kept = []
+    for cap in (0.0, 0.01, 0.05, 0.2, 1.0):
+        op.unique_cap = cap
+        three = three_launch_capped(op, q, k, v, groups, work)
+        ref = [x.clone() for x in (op.features, op.valid, op.raw, op.ids, op.count)]
+        for x in (op.features, op.valid, op.raw, op.ids, op.count, op.out):
+            x.zero_()
+        op.lib.call("prismkv_decode_capped", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(),
+                    op.bits.data_ptr(), k.data_ptr(), v.data_ptr(), work.data_ptr(), op.features.data_ptr(),
+                    op.valid.data_ptr(), op.raw.data_ptr(), op.ids.data_ptr(), op.count.data_ptr(),
+                    op.out.data_ptr(), groups, op.history, k.shape[1] - op.history, op.capacity, op._cap_limit(),
+                    op.row_words, k.stride(0), v.stride(0), op.capacity, stream=s)
+        torch.cuda.synchronize()
+        assert int(work[:4].view(torch.int32)[0]) == 0  # no bounded wait gave up
+        got = (op.features, op.valid, op.raw, op.ids, op.count)
+        for g in range(groups):
+            for a, b in zip(got[:3], ref[:3]):
+                assert torch.equal(a[g], b[g]), (cap, g)
+            n = int(ref[4][g])
+            assert int(got[4][g]) == n and torch.equal(got[3][g][:n], ref[3][g][:n]), (cap, g)
+        assert np.array_equal(bf16_bits(op.out)[:groups], three[:groups]), cap
+        kept.append([int((op.valid[g] > 0).sum()) for g in range(groups)])
+    log(f"  groups={groups}: kept buckets per cap {kept}")
 
 
 @pytest.mark.parametrize("groups", [1, 2, 4])
