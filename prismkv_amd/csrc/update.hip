@@ -95,22 +95,29 @@ __device__ __forceinline__ unsigned* hist_of(const UpdateArgs& a, int g, int lev
 }
 
 // ---------------------------------------------------------------------------
-// encode: grid (kFTiles, Y, G) x 256.  Workgroup (ft, y) keeps W of buckets
-// [64 ft, 64 ft + 64) in LDS (fp32 [bucket][dim]); each wave walks its own
-// 16-token tiles 4 y + w, 4 y + w + 4 Y, ... with no workgroup barrier, so
-// the histogram is flushed once per workgroup.  Products run on fp32 MFMA
-// (v_mfma_f32_16x16x4f32: lane l feeds A[i = l % 16][k], B[k][j = l % 16]
-// and holds D[4 (l / 16) + r][l % 16]).  Lane (i, q) = (l % 16, l / 16)
-// supplies the dims 16 kb + 4 q + t of dim block kb to step t: its A values
-// are x = (k - center) / scale of token row i at those 32 dims, loaded from
-// K straight into registers (the next tile's while the current one is
-// multiplied), and its B values one 16-byte LDS read per bucket tile and
-// block.  A and B always pair the same dim, so the steps only reorder the
-// sum over the 128 dims.
+// encode: grid (ceil(N / 128), P, G) x 512.  Workgroup (y, part) takes the
+// tokens [128 y, 128 y + 128), wave w the 16 rows 128 y + 16 w + i, and the
+// bucket tiles part, part + P, ... (64 buckets each).  The wave's
+// x = (k - center) / scale is computed once, into registers, and each bucket
+// tile's W streams through LDS, double-buffered: the next tile's W is
+// requested into registers while the current tile is multiplied, then
+// stored to the other buffer.  Products run on fp32 MFMA
+// (v_mfma_f32_16x16x4f32: lane l feeds A[i = l % 16][k], B[k][j = l % 16] and
+// holds D[4 (l / 16) + r][l % 16]).  Lane (i, q) = (l % 16, l / 16) supplies
+// the dims 16 kb + 4 q + t of dim block kb to step t: its A values are x of
+// token row i at those 32 dims, its B values one 16-byte LDS read per
+// 16-bucket column and block.  A and B always pair the same dim, so the
+// steps only reorder the sum over the 128 dims (the same order for every
+// token and bucket).  P is the smallest count that gives the launch
+// kEncMinWgs workgroups (two per CU), so the x of a token is computed P times
+// in all rather than once per bucket tile.
 // ---------------------------------------------------------------------------
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-constexpr int kEncodeTileWgs = 128;  // token-tile workgroups per (bucket tile, group) at most
-constexpr int kRowTile = 16;         // tokens per wave tile
+constexpr int kET = 512;                          // encode workgroup
+constexpr int kRowTile = 16;                      // tokens per wave
+constexpr int kEncTokens = kET / 64 * kRowTile;   // tokens per workgroup (128)
+constexpr int kEncMinWgs = 512;                   // workgroups the bucket-tile parts aim for
+constexpr int kWLoads = kFT * kD / 4 / kET;       // float4 of a W tile per thread (4)
 
 // K chunk kb (4 bf16 dims 16 kb + 4 q ..) of token row t0 + i for lane (i, q).
 __device__ __forceinline__ uint2 key_chunk(const UpdateArgs& a, int g, int t0, int kb) {
@@ -119,53 +126,70 @@ __device__ __forceinline__ uint2 key_chunk(const UpdateArgs& a, int g, int t0, i
   return *reinterpret_cast<const uint2*>(a.k + (size_t)g * a.ks + (size_t)(a.H + row) * kD + 16 * kb + 4 * lq);
 }
 
-__global__ __launch_bounds__(kUT) void encode_kernel(UpdateArgs a) {
-  const int ft = blockIdx.x, g = blockIdx.z, tid = threadIdx.x;
+__global__ __launch_bounds__(kET) void encode_kernel(UpdateArgs a) {
+  const int y = blockIdx.x, part = blockIdx.y, parts = gridDim.y, g = blockIdx.z, tid = threadIdx.x;
   const int w = tid >> 6, lane = tid & 63, li = lane & 15, lq = lane >> 4;
-  __shared__ __align__(16) float ws[kFT][kD + 4];  // [bucket][dim], padded against bank conflicts
-  __shared__ __align__(16) float cs[kD];           // center
+  __shared__ __align__(16) float ws[2][kFT][kD + 4];  // [buffer][bucket][dim], padded against bank conflicts
+  __shared__ __align__(16) float cs[kD];              // center
   __shared__ unsigned hist[kBins];
-  const int f0 = ft * kFT;
-  const int tiles = (a.N + kRowTile - 1) / kRowTile;
-  const int first = blockIdx.y * (kUT / 64) + w, stride = gridDim.y * (kUT / 64);
+  const int t0 = y * kEncTokens + w * kRowTile;  // the wave's first token
   uint2 kr[kD / 16];
-  if (first < tiles)
 #pragma unroll
-    for (int kb = 0; kb < kD / 16; ++kb) kr[kb] = key_chunk(a, g, first * kRowTile, kb);
-  for (int i = tid; i < kBins; i += kUT) hist[i] = 0;
-  if (tid < kD) cs[tid] = a.center[(size_t)g * kD + tid];
-  {
-    const float* wg = a.W + (size_t)g * kF * kD;
-    for (int i = tid; i < kFT * kD / 4; i += kUT) {
-      const int f = i / (kD / 4), d0 = (i % (kD / 4)) * 4;
-      float4 wv = make_float4(0.f, 0.f, 0.f, 0.f);
-      if (f0 + f < kF) wv = *reinterpret_cast<const float4*>(wg + (size_t)(f0 + f) * kD + d0);
-      *reinterpret_cast<float4*>(&ws[f][d0]) = wv;
+  for (int kb = 0; kb < kD / 16; ++kb) kr[kb] = key_chunk(a, g, t0, kb);
+  const float* wg = a.W + (size_t)g * kF * kD;
+  // thread tid moves float4 tid + kET u of a 64 x 128 W tile (bucket i / 32, dims 4 (i % 32) ..)
+  auto load_w = [&](int ft, float4 (&r)[kWLoads]) {
+#pragma unroll
+    for (int u = 0; u < kWLoads; ++u) {
+      const int i = tid + kET * u, f = ft * kFT + i / (kD / 4);
+      r[u] = f < kF ? *reinterpret_cast<const float4*>(wg + (size_t)f * kD + 4 * (i % (kD / 4)))
+                    : make_float4(0.f, 0.f, 0.f, 0.f);
     }
-  }
+  };
+  auto store_w = [&](int buf, const float4 (&r)[kWLoads]) {
+#pragma unroll
+    for (int u = 0; u < kWLoads; ++u) {
+      const int i = tid + kET * u;
+      *reinterpret_cast<float4*>(&ws[buf][i / (kD / 4)][4 * (i % (kD / 4))]) = r[u];
+    }
+  };
+  float4 wr[kWLoads];
+  load_w(part, wr);
+  for (int i = tid; i < kBins; i += kET) hist[i] = 0;
+  if (tid < kD) cs[tid] = a.center[(size_t)g * kD + tid];
+  __syncthreads();
+  // x = (k - center) / key_scale in fp32 (core.py:98) for this lane's row and 32 dims
   const float sc = a.scale[g];
+  float4 xs[kD / 16];
+#pragma unroll
+  for (int kb = 0; kb < kD / 16; ++kb) {
+    const uint2 r = kr[kb];
+    const float4 c = *reinterpret_cast<const float4*>(&cs[16 * kb + 4 * lq]);
+    xs[kb] = make_float4((bf16_lo(r.x) - c.x) / sc, (bf16_hi(r.x) - c.y) / sc, (bf16_lo(r.y) - c.z) / sc,
+                         (bf16_hi(r.y) - c.w) / sc);
+  }
+  store_w(0, wr);
+  __syncthreads();
   const float* bg = a.b + (size_t)g * kF;
   float* ag = a.act + (size_t)g * a.N * kF;
-  float bias[kFT / 16];
+  int buf = 0;
+  for (int ft = part; ft < kFTiles; ft += parts) {  // uniform
+    const bool more = ft + parts < kFTiles;
+    if (more) load_w(ft + parts, wr);  // in flight while this tile is multiplied
+    const int f0 = ft * kFT;
+    float bias[kFT / 16];
 #pragma unroll
-  for (int j = 0; j < kFT / 16; ++j) bias[j] = f0 + 16 * j + li < kF ? bg[f0 + 16 * j + li] : 0.f;
-  __syncthreads();
-  for (int tt = first; tt < tiles; tt += stride) {  // uniform per wave
-    const bool more = tt + stride < tiles;
+    for (int j = 0; j < kFT / 16; ++j) bias[j] = f0 + 16 * j + li < kF ? bg[f0 + 16 * j + li] : 0.f;
     f32x4 acc[kFT / 16];
 #pragma unroll
     for (int j = 0; j < kFT / 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kb = 0; kb < kD / 16; ++kb) {
-      // x = (k - center) / key_scale in fp32 (core.py:98) for this lane's 4 dims
-      const uint2 r = kr[kb];
-      const float4 c = *reinterpret_cast<const float4*>(&cs[16 * kb + 4 * lq]);
-      const float4 xa = make_float4((bf16_lo(r.x) - c.x) / sc, (bf16_hi(r.x) - c.y) / sc,
-                                    (bf16_lo(r.y) - c.z) / sc, (bf16_hi(r.y) - c.w) / sc);
-      if (more) kr[kb] = key_chunk(a, g, (tt + stride) * kRowTile, kb);  // next tile, in flight meanwhile
+      const float4 xa = xs[kb];
       float4 bv[kFT / 16];
 #pragma unroll
-      for (int j = 0; j < kFT / 16; ++j) bv[j] = *reinterpret_cast<const float4*>(&ws[16 * j + li][16 * kb + 4 * lq]);
+      for (int j = 0; j < kFT / 16; ++j)
+        bv[j] = *reinterpret_cast<const float4*>(&ws[buf][16 * j + li][16 * kb + 4 * lq]);
       // the four accumulators interleaved: no MFMA waits on the one before it
 #pragma unroll
       for (int j = 0; j < kFT / 16; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.x, bv[j].x, acc[j], 0, 0, 0);
@@ -175,18 +199,16 @@ __global__ __launch_bounds__(kUT) void encode_kernel(UpdateArgs a) {
       for (int j = 0; j < kFT / 16; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.z, bv[j].z, acc[j], 0, 0, 0);
 #pragma unroll
       for (int j = 0; j < kFT / 16; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.w, bv[j].w, acc[j], 0, 0, 0);
-      // keep each block's B reads next to its MFMAs (hoisting all of them
-      // costs 128 registers and halves the waves per SIMD)
       __builtin_amdgcn_sched_barrier(0);
     }
     // bias, relu, histogram of the positive values, store: lane (i, q) holds
-    // buckets f0 + 16 j + i of tokens 16 tt + 4 q + r
+    // buckets f0 + 16 j + i of tokens t0 + 4 q + r
 #pragma unroll
     for (int j = 0; j < kFT / 16; ++j) {
       const int f = f0 + 16 * j + li;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int tok = tt * kRowTile + 4 * lq + r;
+        const int tok = t0 + 4 * lq + r;
         const float x = acc[j][r] + bias[j];
         const float v = x > 0.f ? x : 0.f;  // relu; non-positive values are never selected
         if (tok < a.N && f < kF) {
@@ -195,10 +217,15 @@ __global__ __launch_bounds__(kUT) void encode_kernel(UpdateArgs a) {
         }
       }
     }
+    if (more) {  // the other buffer was last read before the previous barrier
+      store_w(buf ^ 1, wr);
+      __syncthreads();
+      buf ^= 1;
+    }
   }
   __syncthreads();
-  unsigned* hg = hist_of(a, g, 0) + ((ft + blockIdx.y) % kRep) * kBins;
-  for (int i = tid; i < kBins; i += kUT)
+  unsigned* hg = hist_of(a, g, 0) + ((part + y) % kRep) * kBins;
+  for (int i = tid; i < kBins; i += kET)
     if (hist[i]) atomicAdd(&hg[i], hist[i]);
 }
 
@@ -914,9 +941,9 @@ static UpdateArgs make_args(uint64_t k, uint64_t W, uint64_t b, uint64_t center,
 // encode .. ties: the exact batch-wide positive Top-k of the N keys' activations
 // and their bitmap bits.
 static void launch_selection(const UpdateArgs& a, int groups, hipStream_t s) {
-  const int wave_tiles = (a.N + kRowTile - 1) / kRowTile;
-  const int wgs = std::min((wave_tiles + kUT / 64 - 1) / (kUT / 64), kEncodeTileWgs);
-  hipLaunchKernelGGL(encode_kernel, dim3(kFTiles, wgs, groups), dim3(kUT), 0, s, a);
+  const int token_tiles = (a.N + kEncTokens - 1) / kEncTokens;
+  const int parts = std::max(1, std::min(kFTiles, (kEncMinWgs + token_tiles * groups - 1) / (token_tiles * groups)));
+  hipLaunchKernelGGL(encode_kernel, dim3(token_tiles, parts, groups), dim3(kET), 0, s, a);
   hipLaunchKernelGGL(digit_kernel, dim3(groups), dim3(kUT), 0, s, a, 0);
   for (int level = 1; level < kLevels; ++level) {
     hipLaunchKernelGGL(refine_kernel, dim3(kRefineBlocks, groups), dim3(kUT), 0, s, a, level);
