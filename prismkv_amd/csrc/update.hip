@@ -462,6 +462,7 @@ __global__ __launch_bounds__(kUT) void tie_take_kernel(UpdateArgs a) {
 // merge, thread = (dim k, bucket col) pairs of mean row k and var row 128+k.
 // ---------------------------------------------------------------------------
 constexpr int kMaxBlock = 4096;  // new tokens per update (LDS member list per wave)
+constexpr int kMomBatch = 16;    // member key words requested at once
 
 __device__ __forceinline__ float merge_mean(float a, float b, float den, float ma, float mb) {
 #pragma clang fp contract(off)
@@ -478,24 +479,38 @@ __global__ __launch_bounds__(kUT) void moments_kernel(UpdateArgs a) {
   const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   __shared__ float nm[kChunk][kD], nv[kChunk][kD];
   __shared__ int nb[kChunk];
-  __shared__ int toks[kUT / 64][kMaxBlock];
+  // the wave's member list, in dynamic LDS sized by the block (N tokens per
+  // wave at most), so that several workgroups share a CU
+  extern __shared__ int toks_all[];
+  int* toks = toks_all + (size_t)w * a.N;
   const int w_lo = a.H >> 5, w_hi = (a.H + a.N - 1) >> 5;
   const uint16_t* kg = a.k + (size_t)g * a.ks;
-  for (int j = 0; j < kChunk / 4; ++j) {
-    const int col = w * (kChunk / 4) + j, f = c * kChunk + col;
+  // the first 64 bitmap words of the wave's 8 buckets, all requested at once
+  // (the whole block's words up to 2016 tokens)
+  constexpr int kCols = kChunk / 4;
+  uint32_t first[kCols];
+#pragma unroll
+  for (int j = 0; j < kCols; ++j) {
+    const int f = c * kChunk + w * kCols + j;
+    const int wd = w_lo + lane;
+    first[j] = f < kF && wd <= w_hi ? a.bits[((size_t)g * kF + f) * a.row_words + wd] : 0u;
+  }
+#pragma unroll
+  for (int j = 0; j < kCols; ++j) {
+    const int col = w * kCols + j, f = c * kChunk + col;
     int b = 0;
     if (f < kF) {
       const uint32_t* row = a.bits + ((size_t)g * kF + f) * a.row_words;
       for (int w0 = w_lo; w0 <= w_hi; w0 += 64) {
         const int wd = w0 + lane;
-        uint32_t m = wd <= w_hi ? row[wd] : 0u;
+        uint32_t m = w0 == w_lo ? first[j] : (wd <= w_hi ? row[wd] : 0u);
         if (wd == w_lo) m &= ~0u << (a.H & 31);                               // tokens before H
         if (wd == w_hi && ((a.H + a.N) & 31)) m &= (1u << ((a.H + a.N) & 31)) - 1u;  // tokens past H+N
         const int pc = __popc(m);
         const int incl = (int)wave_incl_scan((unsigned)pc);
         int at = b + incl - pc;
         while (m) {
-          toks[w][at++] = wd * 32 + (int)__builtin_ctz(m);
+          toks[at++] = wd * 32 + (int)__builtin_ctz(m);
           m &= m - 1u;
         }
         b += __shfl(incl, 63);
@@ -503,22 +518,49 @@ __global__ __launch_bounds__(kUT) void moments_kernel(UpdateArgs a) {
     }
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_s_waitcnt(0);
-    // two-pass moments of the ORIGINAL keys (core.py:84-88); lane owns dims 2l, 2l+1
+    // two-pass moments of the ORIGINAL keys (core.py:84-88); lane owns dims
+    // 2l, 2l+1.  Members are summed in ascending order; their key words are
+    // requested kMomBatch at a time, and a bucket of at most kMomBatch members
+    // keeps them in registers for the second pass.
+    auto key_word = [&](int i) { return *reinterpret_cast<const uint32_t*>(kg + (size_t)toks[i] * kD + 2 * lane); };
     float s0 = 0.f, s1 = 0.f;
-#pragma unroll 4
-    for (int i = 0; i < b; ++i) {
-      const uint32_t r = *reinterpret_cast<const uint32_t*>(kg + (size_t)toks[w][i] * kD + 2 * lane);
-      s0 += bf16_lo(r);
-      s1 += bf16_hi(r);
+    uint32_t kept[kMomBatch];
+    for (int i0 = 0; i0 < b; i0 += kMomBatch) {  // uniform
+      uint32_t r[kMomBatch];
+#pragma unroll
+      for (int u = 0; u < kMomBatch; ++u) r[u] = key_word(min(i0 + u, b - 1));  // unconditional: one round trip
+#pragma unroll
+      for (int u = 0; u < kMomBatch; ++u) {
+        if (i0 + u < b) {
+          s0 += bf16_lo(r[u]);
+          s1 += bf16_hi(r[u]);
+        }
+        kept[u] = r[u];
+      }
     }
     const float m0 = b ? s0 / (float)b : 0.f, m1 = b ? s1 / (float)b : 0.f;
     float q0 = 0.f, q1 = 0.f;
-#pragma unroll 4
-    for (int i = 0; i < b; ++i) {
-      const uint32_t r = *reinterpret_cast<const uint32_t*>(kg + (size_t)toks[w][i] * kD + 2 * lane);
-      const float d0 = bf16_lo(r) - m0, d1 = bf16_hi(r) - m1;
-      q0 += d0 * d0;
-      q1 += d1 * d1;
+    if (b <= kMomBatch) {
+#pragma unroll
+      for (int u = 0; u < kMomBatch; ++u)
+        if (u < b) {
+          const float d0 = bf16_lo(kept[u]) - m0, d1 = bf16_hi(kept[u]) - m1;
+          q0 += d0 * d0;
+          q1 += d1 * d1;
+        }
+    } else {
+      for (int i0 = 0; i0 < b; i0 += kMomBatch) {
+        uint32_t r[kMomBatch];
+#pragma unroll
+        for (int u = 0; u < kMomBatch; ++u) r[u] = key_word(min(i0 + u, b - 1));
+#pragma unroll
+        for (int u = 0; u < kMomBatch; ++u)
+          if (i0 + u < b) {
+            const float d0 = bf16_lo(r[u]) - m0, d1 = bf16_hi(r[u]) - m1;
+            q0 += d0 * d0;
+            q1 += d1 * d1;
+          }
+      }
     }
     nm[col][2 * lane] = m0;
     nm[col][2 * lane + 1] = m1;
@@ -977,7 +1019,12 @@ int prismkv_update(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t
                                  row_words, L);
   hipStream_t s = (hipStream_t)stream;
   launch_selection(a, groups, s);
-  hipLaunchKernelGGL(moments_kernel, dim3(kChunks, groups), dim3(kUT), 0, s, a);
+  // member lists: N ints per wave of dynamic LDS (up to 64 KB, allowed once)
+  static const hipError_t lds_ok = hipFuncSetAttribute(reinterpret_cast<const void*>(moments_kernel),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       (int)(kUT / 64 * kMaxBlock * sizeof(int)));
+  if (lds_ok != hipSuccess) return (int)lds_ok;
+  hipLaunchKernelGGL(moments_kernel, dim3(kChunks, groups), dim3(kUT), (size_t)(kUT / 64) * N * sizeof(int), s, a);
   return (int)hipGetLastError();
 }
 
