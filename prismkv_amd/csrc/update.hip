@@ -62,11 +62,12 @@ constexpr int kMaxTieBlocks = 4096;  // contiguous ranges of a per group for the
 constexpr int kTieMinLen = 65536;    // values per range at least (multiple of 4 * kUT)
 constexpr int kTieGrid = 256;        // workgroups per group of the tie kernels
 constexpr int kCenterParts = 64;     // row ranges of the center sum
+constexpr int kListCap = 1 << 17;    // candidates per group of the compact list (see refine)
 constexpr int kMaxBuild = 1 << 20;   // keys per group of a build (N * F < 2^32 flat indices)
 constexpr int kBuildCenter = 1;      // prismkv_build flag: compute the center (else it is an input)
 
 // ctl words per group
-enum { kMode = 0, kPrefix, kRem, kTau, kNeed, kTies, kOrdered, kCount, kCtl = 16 };
+enum { kMode = 0, kPrefix, kRem, kTau, kNeed, kTies, kOrdered, kCount, kListed, kListLen, kCtl = 16 };
 enum { kModeTopK = 0, kModeAllPositive = 1 };
 
 struct UpdateArgs {
@@ -84,6 +85,7 @@ struct UpdateArgs {
   unsigned* hist;  // [G][kLevels][kRep][kBins]
   unsigned* ctl;   // [G][kCtl]
   unsigned* tcount;  // [G][tie_blocks] ties per contiguous range of a
+  uint2* list;       // [G][kListCap] (flat index, value bits) of the values at or above tau's first digit
   int H, N;          // first key row / bitmap column, keys indexed
   long long budget;  // N * key_mean
   int tie_blocks;
@@ -275,6 +277,7 @@ __global__ __launch_bounds__(kUT) void digit_kernel(UpdateArgs a, int level) {
         ctl[kTies] = 0;
         ctl[kOrdered] = 0;
         ctl[kCount] = count;
+        ctl[kListed] = 0;
       }
       return;
     }
@@ -300,6 +303,13 @@ __global__ __launch_bounds__(kUT) void digit_kernel(UpdateArgs a, int level) {
   __syncthreads();
   if (tid == 0) {
     const unsigned prefix = (prefix_in << width) | found_digit;
+    if (level == 0) {
+      // every value the selection can take lies in the first digit's bin or
+      // above it: (count - found_rem) above, found_ties in it.  If they fit,
+      // the first refine pass collects them and the later passes read only them.
+      ctl[kListed] = (unsigned long long)(count - found_rem) + found_ties <= (unsigned long long)kListCap;
+      ctl[kListLen] = 0;
+    }
     ctl[kMode] = kModeTopK;
     ctl[kPrefix] = prefix;
     ctl[kRem] = found_rem;
@@ -317,35 +327,92 @@ __global__ __launch_bounds__(kUT) void digit_kernel(UpdateArgs a, int level) {
 }
 
 // ---------------------------------------------------------------------------
-// refine: grid (kRefineBlocks, G) x 256 over a; histogram of the next digit
-// of the positive values whose higher bits equal the prefix.
+// refine: grid (kRefineBlocks, G) x 256; histogram of the next digit of the
+// positive values whose higher bits equal the prefix.  Level 1 reads a and,
+// when the digit kernel found that they fit (ctl kListed), also collects every
+// positive value whose first digit is at or above tau's into the group's
+// compact list: a workgroup gathers its own in LDS (slots by LDS atomics) and
+// reserves its range of the list with one global atomic at its end (a wave
+// that finds the LDS buffer full reserves its own slots instead); level 2
+// and the emit then read only the list.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kUT) void refine_kernel(UpdateArgs a, int level) {
-  const int g = blockIdx.y, tid = threadIdx.x;
-  const unsigned* ctl = a.ctl + (size_t)g * kCtl;
+  const int g = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+  unsigned* ctl = a.ctl + (size_t)g * kCtl;
   if (ctl[kMode] != kModeTopK || ctl[kTau] == 0x7f800000u) return;
+  constexpr int kBuf = 1024;  // LDS list entries per workgroup
   __shared__ unsigned hist[kBins];
+  __shared__ uint2 buf[kBuf];
+  __shared__ unsigned nbuf, first_miss, base_s;
   for (int i = tid; i < kBins; i += kUT) hist[i] = 0;
+  if (tid == 0) {
+    nbuf = 0u;
+    first_miss = kBuf;
+  }
   __syncthreads();
   const unsigned prefix = ctl[kPrefix];
+  const bool listed = ctl[kListed] != 0u;
   const int shift_hi = level == 1 ? 20 : 9;  // bits above this level's digit
   const int shift = level == 1 ? 9 : 0;
   const unsigned dmask = level == 1 ? 0x7ffu : 0x1ffu;
-  const size_t n = (size_t)a.N * kF;
-  const float4* ag = reinterpret_cast<const float4*>(a.act + (size_t)g * n);
-  for (size_t i = (size_t)blockIdx.x * kUT + tid; i < n / 4; i += (size_t)gridDim.x * kUT) {
-    const float4 v4 = ag[i];
-    const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+  uint2* list = a.list + (size_t)g * kListCap;
+  if (level == 2 && listed) {
+    const unsigned len = min(ctl[kListLen], (unsigned)kListCap);
+    for (unsigned i = blockIdx.x * kUT + tid; i < len; i += gridDim.x * kUT) {
+      const unsigned u = list[i].y;
+      if ((u >> shift_hi) == prefix) atomicAdd(&hist[(u >> shift) & dmask], 1u);
+    }
+  } else {
+    const size_t n = (size_t)a.N * kF;
+    const float4* ag = reinterpret_cast<const float4*>(a.act + (size_t)g * n);
+    const bool collect = level == 1 && listed;
+    for (size_t i = (size_t)blockIdx.x * kUT + tid; i < (n / 4 + kUT - 1) / kUT * kUT;
+         i += (size_t)gridDim.x * kUT) {  // every lane of a wave iterates alike (the list's ballot)
+      const bool in = i < n / 4;
+      const float4 v4 = in ? ag[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+      const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const unsigned u = __float_as_uint(vv[j]);
-      if (vv[j] > 0.f && (u >> shift_hi) == prefix) atomicAdd(&hist[(u >> shift) & dmask], 1u);
+      for (int j = 0; j < 4; ++j) {
+        const unsigned u = __float_as_uint(vv[j]);
+        if (vv[j] > 0.f && (u >> shift_hi) == prefix) atomicAdd(&hist[(u >> shift) & dmask], 1u);
+        if (collect) {
+          const bool take = vv[j] > 0.f && (u >> 20) >= prefix;
+          const unsigned long long m = __ballot(take);
+          if (m) {  // uniform
+            const unsigned cnt = (unsigned)__popcll(m), rank = (unsigned)__popcll(m & ((1ull << lane) - 1ull));
+            unsigned at = 0u;
+            if (lane == 0) at = atomicAdd(&nbuf, cnt);
+            at = __shfl(at, 0);
+            if (at + cnt <= (unsigned)kBuf) {  // uniform
+              if (take) buf[at + rank] = make_uint2((unsigned)(4 * i + j), u);
+            } else {
+              // the buffer is full: straight to the list.  Reservations come in
+              // increasing order, so every one that fitted lies below the first
+              // that did not, and the buffer's valid entries are those below it.
+              unsigned g_at = 0u;
+              if (lane == 0) {
+                atomicMin(&first_miss, at);
+                g_at = atomicAdd(&ctl[kListLen], cnt);
+              }
+              g_at = __shfl(g_at, 0);
+              if (take && g_at + rank < (unsigned)kListCap) list[g_at + rank] = make_uint2((unsigned)(4 * i + j), u);
+            }
+          }
+        }
+      }
     }
   }
   __syncthreads();
   unsigned* hg = hist_of(a, g, level) + (blockIdx.x % kRep) * kBins;
   for (int i = tid; i < kBins; i += kUT)
     if (hist[i]) atomicAdd(&hg[i], hist[i]);
+  // the workgroup's buffered candidates
+  const unsigned nb = min(nbuf, first_miss);
+  if (nb == 0u) return;  // uniform
+  if (tid == 0) base_s = atomicAdd(&ctl[kListLen], nb);
+  __syncthreads();
+  for (unsigned i = tid; i < nb; i += kUT)
+    if (base_s + i < (unsigned)kListCap) list[base_s + i] = buf[i];
 }
 
 __device__ __forceinline__ void set_member(const UpdateArgs& a, int g, unsigned flat) {
@@ -363,6 +430,16 @@ __global__ __launch_bounds__(kUT) void emit_kernel(UpdateArgs a) {
   const unsigned mode = ctl[kMode];
   const float tau = __uint_as_float(ctl[kTau]);
   const bool take_ties = mode == kModeTopK && !ctl[kOrdered] && tau > 0.f;
+  if (mode == kModeTopK && ctl[kListed]) {  // every candidate is in the compact list
+    const uint2* list = a.list + (size_t)g * kListCap;
+    const unsigned len = min(ctl[kListLen], (unsigned)kListCap);
+    for (unsigned i = blockIdx.x * kUT + tid; i < len; i += gridDim.x * kUT) {
+      const uint2 e = list[i];
+      const float v = __uint_as_float(e.y);
+      if (v > tau || (take_ties && v == tau)) set_member(a, g, e.x);
+    }
+    return;
+  }
   const size_t n = (size_t)a.N * kF;
   const float4* ag = reinterpret_cast<const float4*>(a.act + (size_t)g * n);
   for (size_t i = (size_t)blockIdx.x * kUT + tid; i < n / 4; i += (size_t)gridDim.x * kUT) {
@@ -935,7 +1012,7 @@ __global__ __launch_bounds__(kUT) void flat_emit_kernel(UpdateArgs a, int64_t* o
 using namespace prismkv;
 
 struct UpdateLayout {
-  size_t act, hist, ctl, tcount, part, total;
+  size_t act, hist, ctl, tcount, part, list, total;
   UpdateLayout(int groups, int N) {
     size_t o = 0;
     auto take = [&](size_t n) { const size_t at = o; o += (n + 255) & ~(size_t)255; return at; };
@@ -944,6 +1021,7 @@ struct UpdateLayout {
     ctl = take((size_t)groups * kCtl * sizeof(unsigned));
     tcount = take((size_t)groups * kMaxTieBlocks * 2 * sizeof(unsigned));
     part = take((size_t)groups * kCenterParts * kD * sizeof(double));
+    list = take((size_t)groups * kListCap * sizeof(uint2));
     total = o;
   }
 };
@@ -967,6 +1045,7 @@ static UpdateArgs make_args(uint64_t k, uint64_t W, uint64_t b, uint64_t center,
   a.hist = reinterpret_cast<unsigned*>(w + L.hist);
   a.ctl = reinterpret_cast<unsigned*>(w + L.ctl);
   a.tcount = reinterpret_cast<unsigned*>(w + L.tcount);
+  a.list = reinterpret_cast<uint2*>(w + L.list);
   a.H = H;
   a.N = N;
   a.budget = (long long)N * key_mean;

@@ -37,13 +37,30 @@ def sae(seed, bias=0.0):
     return s
 
 
-@pytest.mark.parametrize("kind", ["random", "signed", "ties", "few", "empty_budget", "big_budget", "bf16"])
+@pytest.mark.parametrize("kind", ["random", "signed", "ties", "few", "empty_budget", "big_budget", "bf16",
+                                  "crowded", "wide_bin"])
 def test_positive_global_topk(kind):
     from prismkv_amd import core
     gen = torch.Generator(device="cuda").manual_seed(3)
     N = 257
     a = torch.randn(N, F, generator=gen, device="cuda")
     count = 8 * N
+    if kind == "crowded":
+        # 2048 values in [10, 11) (one first-digit bin, tau's) at flat indices
+        # [0, 1024) and [262144, 263168): the positions one refine workgroup
+        # reads, so its 1024-entry candidate buffer overflows into the list
+        a = a.abs() * 0.01
+        flat = a.view(-1)
+        big = 10.0 + torch.rand(2048, generator=gen, device="cuda")
+        flat[:1024] = big[:1024]
+        flat[262144:263168] = big[1024:]
+        count = 1500
+    elif kind == "wide_bin":
+        # 200000 positive values in tau's first-digit bin: more candidates than
+        # the compact list holds, so the later passes scan every value
+        a = 1.0 + torch.rand(N, F, generator=gen, device="cuda") * 0.0625
+        a.view(-1)[200000:] = -1.0
+        count = 5000
     if kind == "random":
         a = a.relu()
     elif kind == "ties":
