@@ -85,18 +85,18 @@ __device__ __forceinline__ float xor32(float v) { return __uint_as_float(xor32_u
 __device__ __forceinline__ float xor16(float v) { return __uint_as_float(xor16_u(__float_as_uint(v))); }
 // Transpose-reduce step across lane bit 5 (M = 32) or 4 (M = 16): lanes with
 // the bit clear return lo + lo of lane l ^ M, lanes with it set hi + hi of
-// lane l ^ M (own term first).
+// lane l ^ M.  After the swap one register holds the own term and the other
+// the partner's (which is which depends on the lane); IEEE addition is
+// commutative, so one add gives both lanes of a pair the same bits.
 template <int M>
 __device__ __forceinline__ float swap_add(float lo, float hi) {
   const unsigned a = __float_as_uint(lo), b = __float_as_uint(hi);
   if constexpr (M == 32) {
     const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
-    return (threadIdx.x & 32) ? __uint_as_float(r[1]) + __uint_as_float(r[0])
-                              : __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
   } else {
     const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
-    return (threadIdx.x & 16) ? __uint_as_float(r[1]) + __uint_as_float(r[0])
-                              : __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
   }
 }
 

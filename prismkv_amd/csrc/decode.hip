@@ -413,11 +413,11 @@ __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p,
   const int kper = (kChunks + S - 1) / S;
   const int own = max(0, min(kper, kChunks - kper * p));
   auto tile = [&](int j) { return kper * p + j; };
-  // ---- 1. score the own tiles: half 0 takes tile 0, half 1 tile 1, then
-  // both halves tile 2 (half h its part h).  Loads go out in one batch with
-  // no branch: q first (so staging it waits for nothing else), then the
-  // bucket sizes, then the tiles in the order they are used (a missing tile
-  // repeats a valid one), so each round waits only for its own tile.
+  // ---- 1. score the own tiles: half 0 takes tile 0, half 1 tile 1, and
+  // both halves tile 2 (half h its part h), in one pass.  Loads go out in one
+  // batch with no branch: q first (so staging it waits for nothing else),
+  // then the bucket sizes, then the tiles (a missing tile repeats a valid
+  // one), so the products of the first tiles run while the rest lands.
   {
     const int half = tid >> 8, t = tid & 255;
     unsigned qv = load_query512(a.q, g, tid);
@@ -432,29 +432,16 @@ __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p,
     asm volatile("" : "+v"(qv) :: "memory");
     store_query512(qv, lds.score.qq, tid);
     __syncthreads();
-    // the statistics are published after both rounds: a store issued between
-    // the second tile's loads and their use would make that wait cover the
-    // store's write-through as well (stores count in the same counter)
-    float2 st0 = make_float2(0.f, 0.f), st2 = make_float2(0.f, 0.f);
-    {
-      const bool has = half < own;
-      const float l = tile_logit(lds.score.qq, m4, t, lds.score.tile[half], n0, has);
-      if (t < kHq * kChunk && has) {
-        lds.tl[half][t >> 5][t & 31] = l;
-        st0 = chunk_stats(l);
-      }
-    }
-    if (own > 2) {  // uniform; its LDS is disjoint from the first round's
-      const float l = tile_logit_split(lds.score.qq, m2, tid, lds.score.split, n2, true);
-      if (tid < kHq * kChunk) {
-        lds.tl[2][tid >> 5][tid & 31] = l;
-        st2 = chunk_stats(l);
-      }
-    }
-    if (t < kHq * kChunk && (t & 31) == 0) {
-      const int h = t >> 5;
-      if (half < own) pub2(&a.stats[((size_t)g * kChunks + tile(half)) * kHq + h], st0.x, st0.y);
-      if (half == 0 && own > 2) pub2(&a.stats[((size_t)g * kChunks + tile(2)) * kHq + h], st2.x, st2.y);
+    // logits: tile `half` in threads t < 128 of each half, tile 2 in threads
+    // 128..255 of half 0; each head's 32 buckets fill half a wave
+    const float2 l = tile_logits3(lds.score.qq, m4, m2, tid, lds.score.tile, lds.score.split, n0, n2);
+    const bool mine = t < kHq * kChunk ? half < own : half == 0 && own > 2;  // uniform per wave
+    if (mine) {
+      const int j = t < kHq * kChunk ? half : 2, h = (t >> 5) & 3;
+      const float x = t < kHq * kChunk ? l.x : l.y;
+      lds.tl[j][h][t & 31] = x;
+      const float2 st = chunk_stats(x);
+      if ((t & 31) == 0) pub2(&a.stats[((size_t)g * kChunks + tile(j)) * kHq + h], st.x, st.y);
     }
   }
   __syncthreads();

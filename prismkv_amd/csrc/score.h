@@ -9,9 +9,12 @@
 //
 // A tile is f32 [256 rows][32 buckets] (rows k < 128: mean dim k, k >= 128:
 // variance dim k - 128).  256 threads score it: thread t = bucket quad
-// (t & 7) x row phase (t >> 3) issues 8 independent 16-byte loads; the
-// 2 parts x 4 heads x 4 buckets products are reduced across the 8 row lanes
-// of a wave with a transpose-reduce and across the 4 waves in LDS, in a fixed
+// (t & 7) x row phase (t >> 3) issues 8 independent 16-byte loads.  The
+// products run on the matrix cores as v_mfma_f32_4x4x1_16b_f32 outer
+// products (block = 4 lanes of one row: 4 buckets x 4 heads, K = 1), each a
+// chain of exact fused multiply-adds over the thread's rows, bit for bit the
+// fmaf chain; the partial sums are then reduced across the 8 row lanes of a
+// wave with a transpose-reduce and across the 4 waves in LDS, in a fixed
 // order, so results are run-to-run identical.
 #pragma once
 
@@ -83,6 +86,36 @@ __device__ __forceinline__ void load_tile(const float* moments, int g, int c, in
   }
 }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// One K = 1 step of 16 independent 4 x 4 outer products: block b = lanes
+// 4b..4b+3; D[b][i][j] += A[b][i] B[b][j] with A[b][i] = `a` of lane 4b + i
+// and B[b][j] = `b` of lane 4b + j; VGPR v of lane 4b + j holds D[b][v][j].
+// Each step is an exact fused multiply-add (a chain equals the fmaf chain).
+__device__ __forceinline__ f32x4 outer4(float a, float b, f32x4 d) {
+  return __builtin_amdgcn_mfma_f32_4x4x1f32(a, b, d, 0, 0, 0);
+}
+
+// The row products of one thread's loads as 4 x 4 blocks: load i of lane l
+// holds buckets 4 (l & 7) .. +3 of its row, so component c of the lanes of
+// block b = l >> 2 (same row, quads 4 (b & 1) + i) gives A = buckets
+// 16 (b & 1) + 4 i + c, and B = q of head l & 3 at that row (from `qq`).
+// d[c] then holds, in VGPR v of lane l, the partial over the loaded rows of
+// bucket 16 ((l >> 2) & 1) + 4 v + c, head l & 3.
+template <int N>
+__device__ __forceinline__ void row_products(const float4* qq, const float4* m, const int* rows, int lane,
+                                             f32x4 (&d)[4]) {
+  const float* qf = reinterpret_cast<const float*>(qq);
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const float qb = qf[rows[i] * 4 + (lane & 3)];
+    d[0] = outer4(m[i].x, qb, d[0]);
+    d[1] = outer4(m[i].y, qb, d[1]);
+    d[2] = outer4(m[i].z, qb, d[2]);
+    d[3] = outer4(m[i].w, qb, d[3]);
+  }
+}
+
 // Products and reductions of one tile; returns, in thread t < 128, the logit
 // of head t >> 5 for bucket 32c + (t & 31) whose size is `n` (loaded by the
 // caller with the tile, so no load waits here; -inf for a dead bucket).
@@ -91,34 +124,35 @@ __device__ __forceinline__ void load_tile(const float* moments, int g, int c, in
 __device__ __forceinline__ float tile_logit(const float4* qq, const float4 (&m4)[8], int t, TileLds& s, int n,
                                             bool has) {
   const int r = t >> 3, w = t >> 6, lane = t & 63;
-  // acc[part*16 + head*4 + j]: part 0 = mean rows, 1 = variance rows
+  // acc[part * 16 + c * 4 + v]: part 0 = mean rows r + 32 i (i < 4), 1 = variance rows
   float acc[32];
 #pragma unroll
-  for (int i = 0; i < 32; ++i) acc[i] = 0.f;
+  for (int part = 0; part < 2; ++part) {
+    f32x4 d[4];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float4 qv = qq[r + 32 * i];
-    const float* hq = reinterpret_cast<const float*>(&qv);
-    const float* mv = reinterpret_cast<const float*>(&m4[i]);
-    const int part = i >> 2;
+    for (int c = 0; c < 4; ++c) d[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int rows[4] = {r + 128 * part, r + 32 + 128 * part, r + 64 + 128 * part, r + 96 + 128 * part};
+    row_products<4>(qq, m4 + 4 * part, rows, lane, d);
 #pragma unroll
-    for (int h = 0; h < kHq; ++h)
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[part * 16 + h * 4 + j] = fmaf(hq[h], mv[j], acc[part * 16 + h * 4 + j]);
+      for (int v = 0; v < 4; ++v) acc[part * 16 + c * 4 + v] = d[c][v];
   }
-  // reduce over the 8 row lanes of the wave (lane bits 5,4,3)
+  // reduce over the 8 row lanes of the wave (lane bits 5,4,3 = row bits 2,1,0)
   treduce<16, 32>(acc);
   treduce<8, 16>(acc);
   treduce<4, 8>(acc);
-  // lane now holds part (lane>>5)&1, head (lane>>3)&3, buckets 4*quad .. +3
+  // lane now holds part (lane >> 5) & 1, c = 2 ((lane >> 4) & 1) + ((lane >> 3) & 1),
+  // head lane & 3: buckets 16 ((lane >> 2) & 1) + 4 v + c, v = 0..3
   s.red[w][lane] = make_float4(acc[0], acc[1], acc[2], acc[3]);
   __syncthreads();
   {
-    const int l = t >> 2, j = t & 3;
-    const float v = ((reinterpret_cast<const float*>(&s.red[0][l])[j] + reinterpret_cast<const float*>(&s.red[1][l])[j]) +
-                     reinterpret_cast<const float*>(&s.red[2][l])[j]) +
-                    reinterpret_cast<const float*>(&s.red[3][l])[j];
-    s.dots[(l >> 5) & 1][(l >> 3) & 3][4 * (l & 7) + j] = v;
+    const int l = t >> 2, v = t & 3;
+    const float x = ((reinterpret_cast<const float*>(&s.red[0][l])[v] + reinterpret_cast<const float*>(&s.red[1][l])[v]) +
+                     reinterpret_cast<const float*>(&s.red[2][l])[v]) +
+                    reinterpret_cast<const float*>(&s.red[3][l])[v];
+    const int c = 2 * ((l >> 4) & 1) + ((l >> 3) & 1);
+    s.dots[(l >> 5) & 1][l & 3][16 * ((l >> 2) & 1) + 4 * v + c] = x;
   }
   __syncthreads();
   float l = -INFINITY;
@@ -136,8 +170,9 @@ __device__ __forceinline__ float tile_logit(const float4* qq, const float4 (&m4)
 // One tile scored by both halves of a 512-thread workgroup: half h takes
 // part h (h = 0: mean rows 0..127, 1: variance rows 128..255) with 4 loads
 // per thread.  Every dot product is the same tree of additions as in
-// tile_logit (row lanes paired by lane bit 5, then 4, then 3; each pair sum
-// is commutative; then the 4 waves in order), so the logits are bit-identical.
+// tile_logit (the same fused chain over a thread's 4 rows, row lanes paired
+// by lane bit 5, then 4, then 3; each pair sum is commutative; then the 4
+// waves in order), so the logits are bit-identical.
 struct SplitLds {
   float2 red[2][4][64];
   float dots[2][kHq][kChunk];
@@ -154,50 +189,85 @@ __device__ __forceinline__ void load_half_tile(const float* moments, int g, int 
   }
 }
 
-// Returns the logit in threads tid < 128 (head tid >> 5, bucket 32c + (tid & 31),
-// size n); every thread of the 512 must call it (two barriers).
-__device__ __forceinline__ float tile_logit_split(const float4* qq, const float4 (&m4)[4], int tid, SplitLds& s, int n,
-                                                  bool has) {
+// Three tiles scored by a 512-thread workgroup in one pass: half h takes all
+// of tile A_h (8 loads per thread, m8) and part h of tile B (4 loads, m4),
+// so the two reductions interleave and share their 2 barriers.  The log of
+// each bucket size is taken before the products, off the chain that follows
+// the last load.  Returns (x) the logit of tile A_h in threads t < 128 of
+// half h (head t >> 5, bucket t & 31) and (y) tile B's in threads
+// 128 <= tid < 256 (head (tid - 128) >> 5, bucket tid & 31), -inf for a
+// dead bucket; na / nb are the sizes of bucket tid & 31 of A_h / B.  Every
+// dot product is the same tree of additions as in tile_logit (the same
+// fused chains over a thread's rows, row lanes paired by lane bit 5, then
+// 4, then 3, each pair sum commutative, then the 4 waves in order), so the
+// logits are bit-identical to tile_logit's.
+__device__ __forceinline__ float2 tile_logits3(const float4* qq, const float4 (&m8)[8], const float4 (&m4)[4], int tid,
+                                               TileLds (&sa)[2], SplitLds& sb, int na, int nb) {
   const int half = tid >> 8, t = tid & 255, r = t >> 3, w = t >> 6, lane = t & 63;
-  float acc[16];
+  const float lca = logf((float)na), lcb = logf((float)nb);
+  float a[32];  // a[part * 16 + c * 4 + v]
+  float b[16];  // b[c * 4 + v], part = half
 #pragma unroll
-  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+  for (int part = 0; part < 2; ++part) {
+    f32x4 d[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float4 qv = qq[r + 32 * i + 128 * half];
-    const float* hq = reinterpret_cast<const float*>(&qv);
-    const float* mv = reinterpret_cast<const float*>(&m4[i]);
+    for (int c = 0; c < 4; ++c) d[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int rows[4] = {r + 128 * part, r + 32 + 128 * part, r + 64 + 128 * part, r + 96 + 128 * part};
+    row_products<4>(qq, m8 + 4 * part, rows, lane, d);
 #pragma unroll
-    for (int h = 0; h < kHq; ++h)
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[h * 4 + j] = fmaf(hq[h], mv[j], acc[h * 4 + j]);
+      for (int v = 0; v < 4; ++v) a[part * 16 + c * 4 + v] = d[c][v];
   }
-  // lane bit 5 -> head bit 1, bit 4 -> head bit 0, bit 3 -> bucket bit 1
-  treduce<8, 32>(acc);
-  treduce<4, 16>(acc);
-  treduce<2, 8>(acc);
-  s.red[half][w][lane] = make_float2(acc[0], acc[1]);
+  {
+    f32x4 d[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) d[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int rows[4] = {r + 128 * half, r + 32 + 128 * half, r + 64 + 128 * half, r + 96 + 128 * half};
+    row_products<4>(qq, m4, rows, lane, d);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) b[c * 4 + v] = d[c][v];
+  }
+  treduce<16, 32>(a);
+  treduce<8, 32>(b);
+  treduce<8, 16>(a);
+  treduce<4, 16>(b);
+  treduce<4, 8>(a);
+  treduce<2, 8>(b);
+  sa[half].red[w][lane] = make_float4(a[0], a[1], a[2], a[3]);
+  sb.red[half][w][lane] = make_float2(b[0], b[1]);
   __syncthreads();
+  {
+    const int l = t >> 2, v = t & 3;
+    const float x = ((reinterpret_cast<const float*>(&sa[half].red[0][l])[v] +
+                      reinterpret_cast<const float*>(&sa[half].red[1][l])[v]) +
+                     reinterpret_cast<const float*>(&sa[half].red[2][l])[v]) +
+                    reinterpret_cast<const float*>(&sa[half].red[3][l])[v];
+    const int c = 2 * ((l >> 4) & 1) + ((l >> 3) & 1);
+    sa[half].dots[(l >> 5) & 1][l & 3][16 * ((l >> 2) & 1) + 4 * v + c] = x;
+  }
   if (t < kHq * kChunk) {
-    const int h = t >> 5, b = t & 31;
-    const int L = ((h >> 1) << 5) | ((h & 1) << 4) | (((b & 3) >> 1) << 3) | (b >> 2);
-    const bool hi = b & 1;
-    const float v = (((hi ? s.red[half][0][L].y : s.red[half][0][L].x) + (hi ? s.red[half][1][L].y : s.red[half][1][L].x)) +
-                     (hi ? s.red[half][2][L].y : s.red[half][2][L].x)) +
-                    (hi ? s.red[half][3][L].y : s.red[half][3][L].x);
-    s.dots[half][h][b] = v;
+    const int h = t >> 5, bk = t & 31;
+    const int qh = bk >> 4, v = (bk >> 2) & 3, c = bk & 3;
+    const int L = h | (qh << 2) | ((v >> 1) << 3) | ((c & 1) << 4) | ((c >> 1) << 5);
+    const bool hi = v & 1;
+    const float x = (((hi ? sb.red[half][0][L].y : sb.red[half][0][L].x) + (hi ? sb.red[half][1][L].y : sb.red[half][1][L].x)) +
+                     (hi ? sb.red[half][2][L].y : sb.red[half][2][L].x)) +
+                    (hi ? sb.red[half][3][L].y : sb.red[half][3][L].x);
+    sb.dots[half][h][bk] = x;
   }
   __syncthreads();
-  float l = -INFINITY;
-  if (tid < kHq * kChunk && has) {
-    const int h = tid >> 5, b = tid & 31;
-    if (n > 0) {
-      // core.py:122-127: log(count) + (q @ mean^T) / sqrt(d) + (q^2 @ var^T) / (2d)
-      const float lc = logf((float)n);
-      l = (lc + s.dots[0][h][b] / kSqrtD) + s.dots[1][h][b] / (2.0f * kD);
-    }
+  float2 out = make_float2(-INFINITY, -INFINITY);
+  const int h = (t >> 5) & 3, bk = t & 31;
+  if (t < kHq * kChunk) {
+    // core.py:122-127: log(count) + (q @ mean^T) / sqrt(d) + (q^2 @ var^T) / (2d)
+    if (na > 0) out.x = (lca + sa[half].dots[0][h][bk] / kSqrtD) + sa[half].dots[1][h][bk] / (2.0f * kD);
+  } else if (half == 0) {
+    if (nb > 0) out.y = (lcb + sb.dots[0][h][bk] / kSqrtD) + sb.dots[1][h][bk] / (2.0f * kD);
   }
-  return l;
+  return out;
 }
 
 // (max, sum of exp(l - max)) over the 32 lanes of a head (lanes 0-31 or
