@@ -1,5 +1,6 @@
-// Sparse attention of one wave on the matrix cores: 32 rows per block,
-// QK^T and PV both as v_mfma_f32_16x16x32_bf16, online softmax in fp32.
+// Sparse attention of one wave on the matrix cores in 16-row blocks: QK^T
+// as v_mfma_f32_16x16x32_bf16, PV as v_mfma_f32_16x16x16_bf16, online
+// softmax in fp32.
 //
 // Semantics: src/prismkv/core.py:170-183 (exact softmax over the selected
 // rows and the tail, scale 1/sqrt(d)): scores are fp32 sums of exact bf16
@@ -7,21 +8,20 @@
 // split into a bf16 head and a bf16 remainder (two products), so P.V carries
 // ~16 significant bits of P instead of bf16's 8; accumulation is fp32.
 //
-// Operand layout of 16x16x32 (lane l, j = l % 16, q = l / 16): A[i][k] with
-// i = j, k = 8q + t; B[k][jj] with jj = j, k = 8q + t; D[i][jj] with
-// i = 4q + r, jj = j (t = 0..7 bf16 elements, r = 0..3 fp32 results).
-//   QK:  D[row][head] = K . Q^T over 4 chunks of 32 dims.  Lane l supplies
-//        row j of each 16-row group, dims 32c + 8q .. +8 -- one 16-byte load
-//        per chunk of its own row -- and Q[head j] (zero for j >= 4).  The
-//        scores of rows 4q + r (group 0) and 16 + 4q + r (group 1) for head j
-//        land in lane l.
-//   PV:  D[head][dim] = P . V with the reduction index k = 8q + t mapped to
-//        the rows the lane already scored (t < 4: row 4q + t, t >= 4: row
-//        16 + 4q + t - 4), so P needs no lane exchange; the 8 column blocks
-//        n map dim 8j + n to column j, so lane l reads its 8 rows at dims
-//        8j .. 8j + 8 (16-byte loads; each load instruction covers 4 whole
-//        rows) and pairs them per dim with v_perm.  Lanes 0-15 end with
-//        out[head r][8j + n] in acc[n][r].
+// Operand layouts (lane l, j = l % 16, q = l / 16; r = 0..3 fp32 results,
+// D[i][jj] with i = 4q + r, jj = j for both shapes):
+//   QK (16x16x32: A[i][k] with i = j, k = 8q + t; B[k][jj] with jj = j):
+//        D[row][head] = K . Q^T over 4 chunks of 32 dims.  Lane l supplies
+//        row j of the block, dims 32c + 8q .. +8 -- one 16-byte load per
+//        chunk of its own row -- and Q[head j] (zero for j >= 4).  The scores
+//        of rows 4q + r for head j land in lane l.
+//   PV (16x16x16: A[i][k] with i = j, k = 4q + t; B[k][jj] with jj = j):
+//        D[head][dim] = P . V with the reduction index k = 4q + t exactly
+//        the rows the lane scored, so P needs no lane exchange; the 8 column
+//        blocks n map dim 8j + n to column j, so lane l reads rows 4q + t at
+//        dims 8j .. 8j + 8 (16-byte loads; each load instruction covers 4
+//        whole rows) and pairs them per dim with v_perm.  Lanes 0-15 end
+//        with out[head r][8j + n] in acc[n][r].
 #pragma once
 
 #include "attend_core.h"
@@ -31,8 +31,6 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-constexpr int kBlockRows = 32;
 
 struct MfmaAttn {
   bf16x8 qop[4];  // Q^T operand per 32-dim chunk (zero in lanes with j >= 4)
@@ -75,93 +73,39 @@ __device__ __forceinline__ unsigned dim_pair(const uint4& a, const uint4& b) {
   return __builtin_amdgcn_perm(wb, wa, (N & 1) ? 0x07060302u : 0x05040100u);
 }
 
-template <int N>
-__device__ __forceinline__ bf16x8 v_operand(const uint4 (&vr)[8]) {
-  const u32x4 u = {dim_pair<N>(vr[0], vr[1]), dim_pair<N>(vr[2], vr[3]), dim_pair<N>(vr[4], vr[5]),
-                   dim_pair<N>(vr[6], vr[7])};
-  return __builtin_bit_cast(bf16x8, u);
-}
-
-// One block of 32 rows.  kr[4g + c]: lane's row j of group g, dims 32c + 8q;
-// vr[4g + t]: row 16g + 4q + t, dims 8j .. 8j + 8.  Rows >= nvalid are
-// masked (their loads may repeat any valid row).
-__device__ __forceinline__ void mfma_block(MfmaAttn& st, const uint4 (&kr)[8], const uint4 (&vr)[8], int nvalid) {
-  const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
-  f32x4 d0 = {0.f, 0.f, 0.f, 0.f}, d1 = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    d0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kr[c]), st.qop[c], d0, 0, 0, 0);
-    d1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kr[4 + c]), st.qop[c], d1, 0, 0, 0);
-  }
-  float s[8];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    s[r] = (j < kHq && 4 * q + r < nvalid) ? d0[r] * kLog2eScale : -INFINITY;
-    s[4 + r] = (j < kHq && 16 + 4 * q + r < nvalid) ? d1[r] * kLog2eScale : -INFINITY;
-  }
-  float bm = s[0];
-#pragma unroll
-  for (int t = 1; t < 8; ++t) bm = fmaxf(bm, s[t]);
-  bm = fmaxf(bm, xor16(bm));
-  bm = fmaxf(bm, xor32(bm));
-  // lazy rescale: the running max moves only when a score exceeds it by kSlack
-  const bool grow = bm > st.m + kSlack || (st.m == -INFINITY && bm != -INFINITY);
-  if (__ballot(grow)) {
-    const float nm = grow ? bm : st.m;
-    const float alpha = grow ? exp2_or_zero(st.m - nm) : 1.0f;
-    st.m = nm;
-    st.z *= alpha;
-    float ah[kHq];
-#pragma unroll
-    for (int r = 0; r < kHq; ++r) ah[r] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(alpha), r));
-#pragma unroll
-    for (int n = 0; n < 8; ++n)
-#pragma unroll
-      for (int r = 0; r < kHq; ++r) st.acc[n][r] *= ah[r];
-  }
-  float p[8];
-  float zs = 0.f;
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    p[t] = s[t] == -INFINITY ? 0.f : exp2f(s[t] - st.m);
-    zs += p[t];
-  }
-  st.z += zs;
-  // P = head + remainder, both bf16: head = the top 16 bits, remainder rounded to nearest
-  unsigned hi[8], lo[8];
-#pragma unroll
-  for (int t = 0; t < 8; ++t) {
-    const unsigned b = __float_as_uint(p[t]);
-    hi[t] = b >> 16;
-    lo[t] = f32_to_bf16(p[t] - __uint_as_float(b & 0xffff0000u));
-  }
-  const u32x4 uh = {hi[0] | hi[1] << 16, hi[2] | hi[3] << 16, hi[4] | hi[5] << 16, hi[6] | hi[7] << 16};
-  const u32x4 ul = {lo[0] | lo[1] << 16, lo[2] | lo[3] << 16, lo[4] | lo[5] << 16, lo[6] | lo[7] << 16};
-  const bf16x8 ph = __builtin_bit_cast(bf16x8, uh), pl = __builtin_bit_cast(bf16x8, ul);
-#define PRISMKV_PV(N)                                                              \
-  {                                                                                \
-    const bf16x8 vb = v_operand<N>(vr);                                            \
-    st.acc[N] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph, vb, st.acc[N], 0, 0, 0); \
-    st.acc[N] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pl, vb, st.acc[N], 0, 0, 0); \
-  }
-  PRISMKV_PV(0) PRISMKV_PV(1) PRISMKV_PV(2) PRISMKV_PV(3) PRISMKV_PV(4) PRISMKV_PV(5) PRISMKV_PV(6) PRISMKV_PV(7)
-#undef PRISMKV_PV
-}
-
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 
-// One block of 16 rows: QK as above (one group), PV as 16x16x16 products
-// whose reduction index k = 4q + t is exactly the lane's scored rows 4q + t.
-// kr[c]: lane's row j, dims 32c + 8q; vr[t]: row 4q + t, dims 8j .. 8j + 8.
-__device__ __forceinline__ void mfma_block16(MfmaAttn& st, const uint4 (&kr)[4], const uint4 (&vr)[4], int nvalid) {
+// Up to NB blocks of 16 rows as ONE step of the online softmax: the QK
+// products of every block first (independent MFMA chains), then one
+// running-max update for all of them (lazy: the max moves only when a score
+// exceeds it by kSlack), then the PV products, so the blocks of a round
+// share one max reduction and one rescale instead of waiting on each
+// other's.  kr[i][c]: lane's row j of block i, dims 32c + 8q; vr[i][t]: row
+// 4q + t, dims 8j .. 8j + 8.  Block i has nvalid[i] live rows (0: no block
+// i; uniform per wave); rows >= nvalid[i] are masked (their loads may repeat
+// any row), and its loads must be valid whenever nvalid[i] > 0.
+template <int NB>
+__device__ __forceinline__ void mfma_blocks16(MfmaAttn& st, const uint4 (&kr)[NB][4], const uint4 (&vr)[NB][4],
+                                              const int (&nvalid)[NB]) {
   const int lane = threadIdx.x & 63, j = lane & 15, q = lane >> 4;
-  f32x4 d = {0.f, 0.f, 0.f, 0.f};
+  f32x4 d[NB];
 #pragma unroll
-  for (int c = 0; c < 4; ++c) d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kr[c]), st.qop[c], d, 0, 0, 0);
-  float s[4];
+  for (int i = 0; i < NB; ++i) {
+    d[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (nvalid[i] > 0) {
 #pragma unroll
-  for (int r = 0; r < 4; ++r) s[r] = (j < kHq && 4 * q + r < nvalid) ? d[r] * kLog2eScale : -INFINITY;
-  float bm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+      for (int c = 0; c < 4; ++c) d[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kr[i][c]), st.qop[c], d[i], 0, 0, 0);
+    }
+  }
+  float s[NB][4];
+  float bm = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      s[i][r] = (j < kHq && 4 * q + r < nvalid[i]) ? d[i][r] * kLog2eScale : -INFINITY;
+      bm = fmaxf(bm, s[i][r]);
+    }
   bm = fmaxf(bm, xor16(bm));
   bm = fmaxf(bm, xor32(bm));
   const bool grow = bm > st.m + kSlack || (st.m == -INFINITY && bm != -INFINITY);
@@ -178,31 +122,36 @@ __device__ __forceinline__ void mfma_block16(MfmaAttn& st, const uint4 (&kr)[4],
 #pragma unroll
       for (int r = 0; r < kHq; ++r) st.acc[n][r] *= ah[r];
   }
-  float p[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) p[t] = s[t] == -INFINITY ? 0.f : exp2f(s[t] - st.m);
-  st.z += (p[0] + p[1]) + (p[2] + p[3]);
-  unsigned hi[4], lo[4];
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const unsigned b = __float_as_uint(p[t]);
-    hi[t] = b >> 16;
-    lo[t] = f32_to_bf16(p[t] - __uint_as_float(b & 0xffff0000u));
-  }
   typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
-  const u32x2 uh = {hi[0] | hi[1] << 16, hi[2] | hi[3] << 16};
-  const u32x2 ul = {lo[0] | lo[1] << 16, lo[2] | lo[3] << 16};
-  const s16x4 ph = __builtin_bit_cast(s16x4, uh), pl = __builtin_bit_cast(s16x4, ul);
-#define PRISMKV_PV16(N)                                                                  \
-  {                                                                                      \
-    const u32x2 vu = {dim_pair<N>(vr[0], vr[1]), dim_pair<N>(vr[2], vr[3])};             \
-    const s16x4 vb = __builtin_bit_cast(s16x4, vu);                                      \
-    st.acc[N] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ph, vb, st.acc[N], 0, 0, 0);   \
-    st.acc[N] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pl, vb, st.acc[N], 0, 0, 0);   \
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    if (nvalid[i] <= 0) continue;  // uniform
+    float p[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) p[t] = s[i][t] == -INFINITY ? 0.f : exp2f(s[i][t] - st.m);
+    st.z += (p[0] + p[1]) + (p[2] + p[3]);
+    // P = head + remainder, both bf16: head = the top 16 bits, remainder rounded to nearest
+    unsigned hi[4], lo[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const unsigned b = __float_as_uint(p[t]);
+      hi[t] = b >> 16;
+      lo[t] = f32_to_bf16(p[t] - __uint_as_float(b & 0xffff0000u));
+    }
+    const u32x2 uh = {hi[0] | hi[1] << 16, hi[2] | hi[3] << 16};
+    const u32x2 ul = {lo[0] | lo[1] << 16, lo[2] | lo[3] << 16};
+    const s16x4 ph = __builtin_bit_cast(s16x4, uh), pl = __builtin_bit_cast(s16x4, ul);
+#define PRISMKV_PVB(N)                                                                   \
+    {                                                                                    \
+      const u32x2 vu = {dim_pair<N>(vr[i][0], vr[i][1]), dim_pair<N>(vr[i][2], vr[i][3])}; \
+      const s16x4 vb = __builtin_bit_cast(s16x4, vu);                                    \
+      st.acc[N] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ph, vb, st.acc[N], 0, 0, 0); \
+      st.acc[N] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pl, vb, st.acc[N], 0, 0, 0); \
+    }
+    PRISMKV_PVB(0) PRISMKV_PVB(1) PRISMKV_PVB(2) PRISMKV_PVB(3)
+    PRISMKV_PVB(4) PRISMKV_PVB(5) PRISMKV_PVB(6) PRISMKV_PVB(7)
+#undef PRISMKV_PVB
   }
-  PRISMKV_PV16(0) PRISMKV_PV16(1) PRISMKV_PV16(2) PRISMKV_PV16(3)
-  PRISMKV_PV16(4) PRISMKV_PV16(5) PRISMKV_PV16(6) PRISMKV_PV16(7)
-#undef PRISMKV_PV16
 }
 
 // Writes wave w's state (max, denominator, acc[4][128]) into LDS.

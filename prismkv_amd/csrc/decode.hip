@@ -773,10 +773,14 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
 #pragma unroll
   for (int c = 0; c < kMaxSplits / 64; ++c) lower[c] = (64 * c + lane < p) ? 0u : kReady;
 
-  // ---- 6. attention over the tile's tokens, then its tail rows: wave w
-  // takes the contiguous range [w * per, (w + 1) * per), per = ceil(rows / 8),
-  // in 16-row blocks, four blocks per round with every K/V load of the round
-  // issued up front
+  // ---- 6. attention over the tile's tokens, then its tail rows, in 16-row
+  // blocks dealt round-robin from the last wave down (block b to wave
+  // 7 - b % 8, so wave 0, which also sums the ids offset, gets the fewest),
+  // four blocks per round with every K/V load of the round issued up front
+  // and the round's blocks taken as one step of the online softmax.  Only
+  // the list's last block is partial: a wave's block whose lanes mostly
+  // repeat one row still costs about a third of a full block's load time,
+  // so whole blocks are dealt rather than equal row counts.
   const int n_sel = lds.nsel;
   const int T = a.tail_dev ? min(max(tail_word, 0), a.T) : a.T;
   const int tail_per = (T + a.S - 1) / a.S;
@@ -787,12 +791,12 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     const int last_row = a.H + T - 1;
     const uint16_t* kg = a.k + (size_t)g * a.ks;
     const uint16_t* vg = a.v + (size_t)g * a.vs;
-    const int per = (n_rows + kDT / 64 - 1) / (kDT / 64);
-    const int r0 = min(n_rows, w * per), r1 = min(n_rows, r0 + per);
-    // position of row r of the workgroup's list; rows past the wave's range
-    // repeat the range's first row (masked, same lines)
-    auto row_pos = [&](int r) {
-      r = r < r1 ? r : r0;
+    constexpr int kWaves = kDT / 64;
+    const int n_blocks = (n_rows + 15) >> 4;
+    // position of row r of the workgroup's list; rows past the list repeat
+    // the block's first row (masked, same lines)
+    auto row_pos = [&](int r, int base) {
+      r = r < n_rows ? r : base;
       int pos = r < n_sel ? rows[r] : a.H + t_lo + (r - n_sel);
       return pos < 0 ? 0 : (pos > last_row ? last_row : pos);
     };
@@ -820,45 +824,48 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     mfma_init(st, a.q + (size_t)g * kHq * kD);
 #endif
     constexpr int kPerRound = 4;
-    for (int b0 = r0; b0 < r1; b0 += kPerRound * 16) {
+    for (int k0 = kWaves - 1 - w; k0 < n_blocks; k0 += kPerRound * kWaves) {  // blocks k0 + 8 i
       uint4 kr[kPerRound][4], vr[kPerRound][4];
 #pragma unroll
       for (int i = 0; i < kPerRound; ++i) {
-        const int base = b0 + 16 * i;
-        if (base < r1) {  // uniform per wave
+        const int base = 16 * (k0 + kWaves * i);
+        if (base < n_rows) {  // uniform per wave
 #if PRISMKV_VALU_ATTENTION
 #pragma unroll
           for (int b = 0; b < 4; ++b) {
-            const size_t at = (size_t)row_pos(base + 4 * slot + b) * kD + 8 * q16;
+            const size_t at = (size_t)row_pos(base + 4 * slot + b, base) * kD + 8 * q16;
             kr[i][b] = load_nt16(kg + at);
             vr[i][b] = load_nt16(vg + at);
           }
 #else
-          const uint16_t* kp = kg + (size_t)row_pos(base + j) * kD + 8 * qd;
+          const uint16_t* kp = kg + (size_t)row_pos(base + j, base) * kD + 8 * qd;
 #pragma unroll
           for (int c = 0; c < 4; ++c) kr[i][c] = load_nt16(kp + 32 * c);
 #pragma unroll
-          for (int t = 0; t < 4; ++t) vr[i][t] = load_nt16(vg + (size_t)row_pos(base + 4 * qd + t) * kD + 8 * j);
+          for (int t = 0; t < 4; ++t) vr[i][t] = load_nt16(vg + (size_t)row_pos(base + 4 * qd + t, base) * kD + 8 * j);
 #endif
         }
       }
       asm volatile("" ::: "memory");  // every load of the round is in flight before any is used
-      if (b0 == r0 && w == 0) {
+      if (k0 == kWaves - 1 - w && w == 0) {
 #pragma unroll
         for (int c = 0; c < kMaxSplits / 64; ++c) {
           const int qq = 64 * c + lane;
           if (qq < p) lower[c] = ld_dev(&a.status[(size_t)g * a.S + qq]);
         }
       }
+#if PRISMKV_VALU_ATTENTION
 #pragma unroll
       for (int i = 0; i < kPerRound; ++i) {
-        const int base = b0 + 16 * i;
-#if PRISMKV_VALU_ATTENTION
-        if (base < r1) attend_step(qf, kr[i], vr[i], max(0, min(4, r1 - base - 4 * slot)), st);
-#else
-        if (base < r1) mfma_block16(st, kr[i], vr[i], min(16, r1 - base));
-#endif
+        const int base = 16 * (k0 + kWaves * i);
+        if (base < n_rows) attend_step(qf, kr[i], vr[i], max(0, min(4, n_rows - base - 4 * slot)), st);
       }
+#else
+      int nv[kPerRound];
+#pragma unroll
+      for (int i = 0; i < kPerRound; ++i) nv[i] = max(0, min(16, n_rows - 16 * (k0 + kWaves * i)));
+      mfma_blocks16<kPerRound>(st, kr, vr, nv);
+#endif
     }
 
     // ---- 7. the tile's global ids offset (ids are written after phase 8)
