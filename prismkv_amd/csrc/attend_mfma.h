@@ -174,38 +174,5 @@ __device__ __forceinline__ void mfma_stash(const MfmaAttn& st, MfmaLds<kWaves>& 
   }
 }
 
-// Merges the kWaves wave states (after a barrier) into one split state per
-// head, published at stp + h * hstride as complemented words: (max, den) as
-// one 64-bit word, then acc[128].  Thread = (head tid >> 7, dim tid & 127).
-template <int kWaves>
-__device__ __forceinline__ void mfma_publish(MfmaLds<kWaves>& lds, float* stp, size_t hstride) {
-  const int tid = threadIdx.x;
-  __syncthreads();
-  if (tid < kWaves * kHq) {
-    const int k = tid >> 2, h = tid & 3;
-    float M = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < kWaves; ++i) M = fmaxf(M, lds.sm[i][h]);
-    const float m = lds.sm[k][h];
-    lds.wt[k][h] = m == -INFINITY ? 0.f : exp2f(m - M);
-    if (k == 0) lds.mx[h] = M;
-  }
-  __syncthreads();
-  const int h = tid >> 7, d = tid & (kD - 1);
-  const float M = lds.mx[h];
-  float den = 0.f, v = 0.f;
-#pragma unroll
-  for (int k = 0; k < kWaves; ++k) {
-    const float wgt = lds.wt[k][h];
-    den = fmaf(wgt, lds.sz[k][h], den);
-    v = fmaf(wgt, lds.sacc[k][h][d], v);
-  }
-  float* sh = stp + (size_t)h * hstride;
-  if (d == 0)
-    st_dev(reinterpret_cast<unsigned long long*>(sh),
-           ~(((unsigned long long)__float_as_uint(den) << 32) | (unsigned long long)__float_as_uint(M)));
-  st_dev(reinterpret_cast<unsigned*>(sh + 2 + d), ~__float_as_uint(v));
-}
-
 }  // namespace
 }  // namespace prismkv

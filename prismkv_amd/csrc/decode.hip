@@ -178,7 +178,7 @@ __device__ __forceinline__ float2 unpub2(unsigned long long r) {
   return make_float2(__uint_as_float((unsigned)r), __uint_as_float((unsigned)(r >> 32)));
 }
 
-// Phase 8: merges the 8 wave states in LDS (as mfma_publish) and publishes
+// Phase 8: merges the 8 wave states stashed in LDS and publishes
 // them per (head, 32-dim slice) as complemented words {max, den, acc[32]}:
 // each slice has its own copy of (max, den), so every published word has
 // exactly one reader.  Thread = (head tid >> 7, dim tid & 127).
