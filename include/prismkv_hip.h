@@ -102,8 +102,15 @@ int prismkv_build_bits(uint64_t ids, uint64_t offsets, uint64_t bits, int groups
                        int64_t row_words, uint64_t stream);
 
 /* Stage 3 (replaces attention_tuned, src/prismkv/native8b.py:91-102;
- * semantics src/prismkv/core.py:170-183): split-K with the merge fused into
- * the last workgroup of each group; splits in [1,1024]. */
+ * semantics src/prismkv/core.py:170-183): when H + T <= 16384 x S (S =
+ * min(256, max(32, 256 / groups)) workgroups per group, all resident), the
+ * fused decode's attention phases over an even share of each group's
+ * count + T rows per workgroup; otherwise split-K with the merge fused into
+ * the last workgroup of each group.  splits in [1,1024] (the partition does
+ * not change the result).  `work` (prismkv_attend_work_bytes) is zero-filled
+ * once before first use and left zeroed; its first 32-bit word is the error
+ * word (nonzero if a bounded inter-workgroup wait gave up), with the
+ * optional host-word slot at byte 8. */
 size_t prismkv_attend_work_bytes(int groups, int splits);
 int prismkv_attend(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t count, uint64_t work,
                    uint64_t out, int groups, int H, int T, int64_t ks, int64_t vs, int64_t ids_stride,

@@ -425,4 +425,7 @@ def attend(q, keys, values, old_ids, history):
     lib.call("prismkv_attend", q1.data_ptr(), keys.data_ptr(), values.data_ptr(), ids.data_ptr(), count.data_ptr(),
              work.data_ptr(), out.data_ptr(), 1, history, L - history, L * DIM, L * DIM, ids.shape[1],
              ATTEND_SPLITS, stream=_stream())
+    if int(work[:4].view(torch.int32).item()):  # a bounded wait of the attention gave up
+        work.zero_()
+        raise RuntimeError("prismkv_attend: a bounded inter-workgroup wait gave up; the workspace was reset")
     return out[0].to(q.dtype)

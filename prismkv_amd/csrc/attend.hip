@@ -144,9 +144,13 @@ using namespace prismkv;
 
 extern "C" {
 
+// Work: the decode-phase region (attend_list_work_bytes: its error word
+// first), then this file's split states and arrival counters, disjoint, so
+// either launch finds its region as it left it.
 size_t prismkv_attend_work_bytes(int groups, int splits) {
   if (groups < 1 || splits < 1) return 0;
-  return (size_t)groups * kHq * splits * kStateW * sizeof(float) + (size_t)groups * sizeof(unsigned);
+  return attend_list_work_bytes(groups) + (size_t)groups * kHq * splits * kStateW * sizeof(float) +
+         (size_t)groups * sizeof(unsigned);
 }
 
 int prismkv_attend(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t count, uint64_t work, uint64_t out,
@@ -155,12 +159,15 @@ int prismkv_attend(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t co
   if (groups < 1 || groups > 65535 || H < 0 || T < 0 || splits < 1 || splits > 1024) return kBadSize;
   if (ks < (int64_t)(H + T) * kD || vs < (int64_t)(H + T) * kD || ids_stride < H) return kBadSize;
   if (!q || !k || !v || !ids || !count || !work || !out) return kBadSize;
+  // the decode's attention phases when the lists fit them; the split count
+  // does not change the result (exact softmax), only the partition
+  const int rc = attend_list(q, k, v, ids, count, work, out, groups, H, T, ks, vs, ids_stride, stream);
+  if (rc != kBadSize) return rc;
+  float* state = reinterpret_cast<float*>(reinterpret_cast<char*>(work) + attend_list_work_bytes(groups));
   AttendArgs a{reinterpret_cast<const uint16_t*>(q), reinterpret_cast<const uint16_t*>(k),
                reinterpret_cast<const uint16_t*>(v), reinterpret_cast<const int32_t*>(ids),
-               reinterpret_cast<const int32_t*>(count), ks, vs, ids_stride, H, T, splits,
-               reinterpret_cast<float*>(work)};
-  unsigned* sync = reinterpret_cast<unsigned*>(reinterpret_cast<float*>(work) +
-                                               (size_t)groups * kHq * splits * kStateW);
+               reinterpret_cast<const int32_t*>(count), ks, vs, ids_stride, H, T, splits, state};
+  unsigned* sync = reinterpret_cast<unsigned*>(state + (size_t)groups * kHq * splits * kStateW);
   hipLaunchKernelGGL(attend_fused, dim3(splits, groups), dim3(kAT), 0, (hipStream_t)stream, a, sync,
                      reinterpret_cast<uint16_t*>(out));
   return (int)hipGetLastError();

@@ -196,6 +196,14 @@ __device__ __forceinline__ unsigned block_incl_scan(unsigned v, unsigned* wsum) 
 constexpr int kSpinLimit = 1 << 20;
 int spin_limit();  // the current process-wide limit (defined in decode.hip)
 
+// Stage 3 on the fused decode's attention phases (defined in decode.hip):
+// the bytes its workspace region takes for `groups` groups, and the launch
+// over the given id lists; -1 when the geometry does not fit it (the caller
+// then uses its own split-K kernel).
+size_t attend_list_work_bytes(int groups);
+int attend_list(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t count, uint64_t work, uint64_t out,
+                int groups, int H, int T, int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream);
+
 // Error words.  A workspace's first 32-bit word is its sticky error word; its
 // 8-byte slot at byte offset 8 optionally holds the device address of a
 // host-mapped 32-bit word (0 = none), so a host binding can notice a wait that

@@ -112,6 +112,11 @@ struct DecodeArgs {
   int64_t ids_stride;
   int32_t* count;
   uint16_t* out;
+  // attention over a given id list (prismkv_attend; given-selection
+  // instantiation only): the group's ids [G][ids_stride] and counts [G]
+  // replace the selection and the union; ids / count are then not written
+  const int32_t* ids_in;
+  const int32_t* count_in;
 };
 
 // The tile's selected tokens live in dynamic LDS after this struct, sized
@@ -634,11 +639,13 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   // it has long landed when the attention first uses it.
   const int tail_word = ld_dev(a.tail_dev ? a.tail_dev : reinterpret_cast<const int*>(a.q));
 
+  // attention over a given id list: no selection, no union (uniform)
+  const bool id_list = kGiven && a.ids_in != nullptr;
   if constexpr (kGiven) {
     // ---- 1-4. the given selection: the valid, in-range buckets in order (an
     // out-of-range id selects nothing, as in union_kernel); no row is
     // prefetched, so the union loads every selected row
-    if (w == 0) {
+    if (w == 0 && !id_list) {
       bool ok = false;
       int f = 0;
       if (lane < kTop && a.valid[(size_t)g * kTop + lane] > 0.f) {
@@ -690,7 +697,19 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   // the chunks' counts give each its offset.  (Phase 4's final barrier
   // publishes need and sel_rows.)
   const int nw = (a.H + 31) / 32;
-  if (a.tw <= kTileWords) {
+  if (id_list) {
+    // ---- 5'. the workgroup's share of the group's list (count ids, then the
+    // T tail rows H .. H + T - 1): rows [p per, (p + 1) per) as positions
+    const int cnt = min(max(a.count_in[g], 0), a.H), total = cnt + a.T;
+    const int per = (total + a.S - 1) / a.S;
+    const int lo = min(total, p * per), n = min(total, lo + per) - lo;
+    const int32_t* idg = a.ids_in + (size_t)g * a.ids_stride;
+    for (int i = tid; i < n; i += kDT) {
+      const int j = lo + i;
+      rows[i] = j < cnt ? min(max(idg[j], 0), a.H - 1) : a.H + (j - cnt);
+    }
+    if (tid == 0) lds.nsel = n;
+  } else if (a.tw <= kTileWords) {
     if (w == 0) {
       const int nr = lds.need;
       const int wd = p * a.tw + lane;
@@ -783,7 +802,7 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   // so whole blocks are dealt rather than equal row counts.
   const int n_sel = lds.nsel;
   const int T = a.tail_dev ? min(max(tail_word, 0), a.T) : a.T;
-  const int tail_per = (T + a.S - 1) / a.S;
+  const int tail_per = id_list ? 0 : (T + a.S - 1) / a.S;  // an id list holds its tail rows
   const int t_lo = min(T, p * tail_per), t_hi = min(T, t_lo + tail_per);
   const int n_rows = n_sel + (t_hi - t_lo);
   {
@@ -847,7 +866,7 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
         }
       }
       asm volatile("" ::: "memory");  // every load of the round is in flight before any is used
-      if (k0 == kWaves - 1 - w && w == 0) {
+      if (k0 == kWaves - 1 - w && w == 0 && !id_list) {
 #pragma unroll
         for (int c = 0; c < kMaxSplits / 64; ++c) {
           const int qq = 64 * c + lane;
@@ -869,7 +888,7 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     }
 
     // ---- 7. the tile's global ids offset (ids are written after phase 8)
-    if (w == 0) {
+    if (w == 0 && !id_list) {
       const unsigned* tiles = a.status + (size_t)g * a.S;
       unsigned prefix = 0;
 #pragma unroll
@@ -928,7 +947,7 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
 #endif
     publish_sliced(lds.mf, a.state + (size_t)(g * a.S + p) * kHq * kSlices * kSliceW);
   }
-  {
+  if (!id_list) {
     int32_t* dst = a.ids + (size_t)g * a.ids_stride + lds.base;
     for (int i = tid; i < n_sel; i += kDT) dst[i] = rows[i];
   }
@@ -1093,6 +1112,8 @@ static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t b
   a.ids_stride = ids_stride;
   a.count = reinterpret_cast<int32_t*>(count);
   a.out = reinterpret_cast<uint16_t*>(out);
+  a.ids_in = nullptr;
+  a.count_in = nullptr;
   const dim3 grid(S, groups), block(kDT);
   hipStream_t s = (hipStream_t)stream;
   const size_t rows_bytes = (size_t)32 * a.tw * sizeof(int);  // the tile's row list (dynamic LDS)
@@ -1114,6 +1135,59 @@ static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t b
   }
   return (int)hipGetLastError();
 }
+
+// ---- stage 3 over a given id list ---------------------------------------
+// The decode's phases 6-9 with each workgroup's rows read from the group's id
+// list (an even share of count[g] + T rows per workgroup, the tail rows last)
+// instead of a union tile: round-robin 16-row MFMA blocks, the sliced split
+// states and the 16 merging workgroups, with the decode's bounded waits and
+// error word (word 0 of the region, its host-word slot at byte 8).
+namespace prismkv {
+
+size_t attend_list_work_bytes(int groups) {
+  return groups < 1 ? 0 : DecodeWorkLayout(groups, decode_splits(groups)).total;
+}
+
+int attend_list(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t count, uint64_t work, uint64_t out,
+                int groups, int H, int T, int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream) {
+  const int S = decode_splits(groups);
+  // every row of a workgroup's share must fit its dynamic LDS list
+  if (H + T < 1 || (int64_t)(H + T) > (int64_t)kTileTokens * S || S > resident_workgroups()) return kBadSize;
+  const DecodeWorkLayout L(groups, S);
+  char* w = reinterpret_cast<char*>(work);
+  DecodeArgs a{};
+  a.q = reinterpret_cast<const uint16_t*>(q);
+  a.k = reinterpret_cast<const uint16_t*>(k);
+  a.v = reinterpret_cast<const uint16_t*>(v);
+  a.ks = ks;
+  a.vs = vs;
+  a.H = H;
+  a.T = T;
+  a.S = S;
+  a.tw = 0;
+  a.stats = reinterpret_cast<unsigned long long*>(w + L.stats);
+  a.cand = reinterpret_cast<unsigned long long*>(w + L.cand);
+  a.status = reinterpret_cast<unsigned*>(w + L.status);
+  a.err = reinterpret_cast<unsigned*>(w + L.err);
+  a.err_host = error_host_slot(a.err);
+  a.spin = spin_limit();
+  a.state = reinterpret_cast<float*>(w + L.state);
+  a.walk = reinterpret_cast<unsigned*>(w + L.walk);
+  a.ids_stride = ids_stride;
+  a.out = reinterpret_cast<uint16_t*>(out);
+  a.ids_in = reinterpret_cast<const int32_t*>(ids);
+  a.count_in = reinterpret_cast<const int32_t*>(count);
+  const dim3 grid(S, groups), block(kDT);
+  hipStream_t s = (hipStream_t)stream;
+  const size_t rows_bytes = (size_t)((H + T + S - 1) / S) * sizeof(int);
+  if (S <= 32) hipLaunchKernelGGL((decode_kernel<1, true>), grid, block, rows_bytes, s, a);
+  else if (S <= 64) hipLaunchKernelGGL((decode_kernel<2, true>), grid, block, rows_bytes, s, a);
+  else if (S <= 128) hipLaunchKernelGGL((decode_kernel<4, true>), grid, block, rows_bytes, s, a);
+  else hipLaunchKernelGGL((decode_kernel<8, true>), grid, block, rows_bytes, s, a);
+  return (int)hipGetLastError();
+}
+
+}  // namespace prismkv
 
 // ---- the allocation-free decode ----------------------------------------
 // Callers that cannot allocate (code under graph capture, tight serving

@@ -294,7 +294,7 @@ class Native8B:
     def _attach_error_word(self):
         """Writes the host-mapped error word's device address into the
         host-word slot (bytes 8-15) of the workspaces whose kernels wait."""
-        for work in (self.decode_work, self.union_work):
+        for work in (self.decode_work, self.union_work, self.state):
             work[8:16].view(torch.int64).fill_(self._err_device_address)
 
     def check_errors(self):
@@ -422,8 +422,9 @@ class Native8B:
     def attention(self, q, k, v, *, splits=64, schedule=0):
         """Stage 3.  `splits` (1..128) and `schedule` (0, 1, 2) are validated and
         accepted for compatibility; the softmax is exact, so the partition does
-        not change the result, and the kernel always uses ATTEND_SPLITS
-        workgroups per group with rows dealt evenly to their waves."""
+        not change the result.  The launch is the fused decode's attention
+        phases over the selection's ids (an even share of each group's rows
+        per workgroup); a wait that gives up is reported at the next call."""
         self._check_kv(q, k, v, splits, schedule)
         self.check_errors()
         self.lib.call("prismkv_attend", q.data_ptr(), k.data_ptr(), v.data_ptr(), self.ids.data_ptr(),
@@ -610,11 +611,12 @@ class Native8B:
 
     def decode_errors(self):
         """Nonzero if a bounded inter-workgroup wait of any launch since the
-        last reset gave up (the decode and union workspaces' sticky error
-        words and the host-mapped word); synchronises, raises nothing."""
+        last reset gave up (the decode, union and attention workspaces'
+        sticky error words and the host-mapped word); synchronises, raises
+        nothing."""
         torch.cuda.synchronize(self.out.device)
         return (int(self.decode_work[:4].view(torch.int32).item()) | int(self.union_work[:4].view(torch.int32).item())
-                | int(self._err_host[0]))
+                | int(self.state[:4].view(torch.int32).item()) | int(self._err_host[0]))
 
     def buffer_bytes(self):
         """Live tensors owned here; excludes model/KV, caller indices and build temporaries."""
