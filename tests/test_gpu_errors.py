@@ -82,3 +82,48 @@ def test_route_give_up_raises_on_next_call():
         set_spin_limit(previous)
     assert raised
     _check_decode(op, q, k, v, case)
+
+
+def test_attention_give_up_raises_and_recovers():
+    """The separate attention (prismkv_attend on the decode's attention
+    phases) reports a give-up through its workspace's error word."""
+    case = cases.native_case(4096, 64, "random")
+    op, q, k, v = operator(case)
+    op.route(q)
+    op.attention(q, k, v)
+    torch.cuda.synchronize()
+    assert op.decode_errors() == 0
+    attempt = _forced_give_up(lambda: op.attention(q, k, v), op)
+    assert attempt is not None, "no wait gave up under spin limit 0"
+    assert op.decode_errors() == 0
+    op.route(q)
+    out = op.attention(q, k, v)
+    torch.cuda.synchronize()
+    groups = expect.expected(case)
+    err = expect.attention_errors(bf16_bits(out), expect.expected_attention(case, groups))
+    log(f"  attention after reset: {err}")
+    assert err["rel_l2"] <= 2e-3
+    assert op.decode_errors() == 0
+
+
+def test_core_attend_give_up_raises():
+    """core.attend checks the error word after its launch and raises."""
+    from prismkv_amd import core
+    case = cases.native_case(2048, 16, "random")
+    op, q, k, v = operator(case)
+    ids = torch.arange(0, 2048, 3, device="cuda")
+    previous = set_spin_limit(0)
+    try:
+        raised = False
+        for _ in range(4):
+            try:
+                core.attend(q[0], k[0], v[0], ids, 2048)
+            except RuntimeError as exc:
+                log(f"  core.attend raised: {exc}")
+                raised = True
+                break
+    finally:
+        set_spin_limit(previous)
+    assert raised
+    out = core.attend(q[0], k[0], v[0], ids, 2048)
+    assert torch.isfinite(out.float()).all()
