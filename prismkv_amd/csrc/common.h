@@ -162,7 +162,34 @@ __device__ __forceinline__ int wave_sum_dpp(int v) {
   return __builtin_amdgcn_readlane(v, 63);
 }
 
-// Inclusive prefix sum over the lanes of a wave64.
+// Wave sums of 8 integers at once by a transpose-reduce: pairs of lanes
+// 32, 16 and 8 apart swap halves of the set and add (permlane swaps, then a
+// DPP row rotation), which leaves lane l holding partial sums of value l >> 3
+// over its 8-lane group's partners; three in-row DPP steps then add the
+// group.  Returns, in lane 8j, the sum of p[j] over the wave (other lanes
+// hold the same sum for j = l >> 3).  Integer sums are exact in any order.
+__device__ __forceinline__ int wave_sum8(int (&p)[8]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const auto r = __builtin_amdgcn_permlane32_swap((unsigned)p[j], (unsigned)p[j + 4], false, false);
+    p[j] = (int)(r[0] + r[1]);  // bit 5 clear: value j, set: value j + 4
+  }
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const auto r = __builtin_amdgcn_permlane16_swap((unsigned)p[j], (unsigned)p[j + 2], false, false);
+    p[j] = (int)(r[0] + r[1]);  // bit 4 clear: value j (+4), set: value j + 2 (+4)
+  }
+  const bool b3 = lane & 8;
+  const int keep = b3 ? p[1] : p[0], send = b3 ? p[0] : p[1];
+  int v = keep + __float_as_int(xor8(__int_as_float(send)));  // value lane >> 3
+  v += __float_as_int(xor4(__int_as_float(v)));
+  v += __float_as_int(xor2(__int_as_float(v)));
+  v += __float_as_int(xor1(__int_as_float(v)));
+  return v;
+}
+
+// Inclusive prefix sum over the lanes of a wave64.// Inclusive prefix sum over the lanes of a wave64.
 __device__ __forceinline__ unsigned wave_incl_scan(unsigned v) {
   const int lane = threadIdx.x & 63;
 #pragma unroll

@@ -546,12 +546,10 @@ __device__ __forceinline__ uint32_t capped_walk(const DecodeArgs& a, int g, int 
       const int m0 = 2 * j + 1, m1 = 2 * j + 2;
       const int c0 = __popc(lo[m0 & 3] & hi[m0 >> 2]);
       const int c1 = m1 < 16 ? __popc(lo[m1 & 3] & hi[(m1 >> 2) & 3]) : 0;
-      packed[j] = wave_sum_dpp(c0 | c1 << 16);
+      packed[j] = c0 | c1 << 16;
     }
-    if (lane == 0) {
-#pragma unroll
-      for (int j = 0; j < kPacked; ++j) lds.walk_part[w][j] = packed[j];
-    }
+    const int wsum = wave_sum8(packed);  // lane 8j: the wave's packed word j
+    if ((lane & 7) == 0) lds.walk_part[w][lane >> 3] = wsum;
     __syncthreads();
     if (w == 0) {
       // the workgroup's counts (<= 16384 each: no carry between the halves),
