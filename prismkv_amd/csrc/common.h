@@ -142,11 +142,6 @@ __device__ __forceinline__ int wave_excl_small(int v, int* total) {
   return pre;
 }
 
-__device__ __forceinline__ int wave_sum_i(int v) {
-#pragma unroll
-  for (int o = 32; o; o >>= 1) v += __shfl_xor(v, o);
-  return v;
-}
 
 // Sum of v over the 64 lanes of a wave through DPP moves (no LDS round
 // trips): pairs, quads (quad_perm), 8 (row_half_mirror), 16 (row_mirror),
@@ -189,15 +184,21 @@ __device__ __forceinline__ int wave_sum8(int (&p)[8]) {
   return v;
 }
 
-// Inclusive prefix sum over the lanes of a wave64.// Inclusive prefix sum over the lanes of a wave64.
-__device__ __forceinline__ unsigned wave_incl_scan(unsigned v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    unsigned y = __shfl_up(v, o);
-    if (lane >= o) v += y;
-  }
-  return v;
+// Inclusive prefix sum over the lanes of a wave64.// The wave's integer sum, in every lane.
+__device__ __forceinline__ int wave_sum_i(int v) { return wave_sum_dpp(v); }
+
+// Inclusive prefix sum over the lanes of a wave64 by DPP (no LDS traffic):
+// in-row shifts by 1, 2, 4 and 8 (lanes without a source add 0), then row
+// 0's total into row 1 and row 2's into row 3, then rows 0-1's total into
+// rows 2 and 3.
+__device__ __forceinline__ unsigned wave_incl_scan(unsigned x) {
+  x += __builtin_amdgcn_update_dpp(0u, x, 0x111, 0xF, 0xF, false);  // row_shr:1
+  x += __builtin_amdgcn_update_dpp(0u, x, 0x112, 0xF, 0xF, false);  // row_shr:2
+  x += __builtin_amdgcn_update_dpp(0u, x, 0x114, 0xF, 0xF, false);  // row_shr:4
+  x += __builtin_amdgcn_update_dpp(0u, x, 0x118, 0xF, 0xF, false);  // row_shr:8
+  x += __builtin_amdgcn_update_dpp(0u, x, 0x142, 0xA, 0xF, false);  // row_bcast:15 into rows 1, 3
+  x += __builtin_amdgcn_update_dpp(0u, x, 0x143, 0xC, 0xF, false);  // row_bcast:31 into rows 2, 3
+  return x;
 }
 
 // Inclusive prefix sum over a workgroup of NT threads (NT a multiple of 64).

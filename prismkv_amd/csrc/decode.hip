@@ -741,7 +741,7 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
         rows[at++] = wd * 32 + (int)__builtin_ctz(m);
         m &= m - 1u;
       }
-      const int total = __shfl(incl, 63);
+      const int total = __builtin_amdgcn_readlane(incl, 63);
       if (lane == 0) {
         lds.nsel = total;
         st_dev(&a.status[(size_t)g * a.S + p], kReady | (unsigned)total);
