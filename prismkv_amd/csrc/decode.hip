@@ -583,11 +583,13 @@ __device__ __forceinline__ uint32_t capped_walk(const DecodeArgs& a, int g, int 
             s1 += (int)(c >> 16);
           }
       }
-#pragma unroll
-      for (int o = 8; o < 64; o <<= 1) {
-        s0 += __shfl_xor(s0, o);
-        s1 += __shfl_xor(s1, o);
-      }
+      // across lane bits 3, 4, 5 (DPP row rotation, then permlane swaps)
+      s0 += __float_as_int(xor8(__int_as_float(s0)));
+      s1 += __float_as_int(xor8(__int_as_float(s1)));
+      s0 += (int)xor16_u((unsigned)s0);
+      s1 += (int)xor16_u((unsigned)s1);
+      s0 += (int)xor32_u((unsigned)s0);
+      s1 += (int)xor32_u((unsigned)s1);
       // lane j < 8: the group's counts of patterns 2j + 1 (s0) and 2j + 2 (s1)
       int cnt[16];
       cnt[0] = 0;
