@@ -246,7 +246,8 @@ uint64_t prismkv_mapped_pointer(uint64_t host);
  *     table) <- Chan merge of the old moments with the block's population
  *     moments, in fp32 and the operation order of core.py:190-199.
  * `work` is prismkv_update_work_bytes(groups, N) bytes, zero-filled once
- * before first use and left zeroed.  N <= 4096; returns -1 on bad sizes.
+ * before first use and left zeroed.  N <= 4096; K rows, W and b 16-byte
+ * aligned; returns -1 on bad sizes.
  * The caller guarantees K holds rows [0, H+N) for every group. */
 size_t prismkv_update_work_bytes(int groups, int max_block);
 int prismkv_update(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
@@ -266,8 +267,8 @@ int prismkv_update(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t
  * directly.  Groups are processed `batch` at a time; `work` is
  * prismkv_build_work_bytes(batch, H) bytes (H x 3000 fp32 activations per
  * group of a batch), zero-filled once before first use and left zeroed.
- * H <= 2^20, row_words a multiple of 4 and >= (H+31)/32, bits and K rows
- * 16-byte aligned; -1 on bad sizes, -2 on unknown flags. */
+ * H <= 2^20, row_words a multiple of 4 and >= (H+31)/32, bits, W, b and K
+ * rows 16-byte aligned; -1 on bad sizes, -2 on unknown flags. */
 size_t prismkv_build_work_bytes(int batch, int H);
 int prismkv_build(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
                   uint64_t counts, uint64_t moments, uint64_t work, int groups, int batch, int H, int key_mean,

@@ -179,9 +179,15 @@ __global__ __launch_bounds__(kET) void encode_kernel(UpdateArgs a) {
     const bool more = ft + parts < kFTiles;
     if (more) load_w(ft + parts, wr);  // in flight while this tile is multiplied
     const int f0 = ft * kFT;
-    float bias[kFT / 16];
+    // the output is bucket-major (lane (i, q): buckets f0 + 16 j + 4 q .. + 3
+    // of token t0 + i), so each lane's 4 values of a j go out as one 16-byte
+    // store; kF is a multiple of 4, so those 4 buckets are live together
+    float4 bias[kFT / 16];
 #pragma unroll
-    for (int j = 0; j < kFT / 16; ++j) bias[j] = f0 + 16 * j + li < kF ? bg[f0 + 16 * j + li] : 0.f;
+    for (int j = 0; j < kFT / 16; ++j) {
+      const int f = f0 + 16 * j + 4 * lq;
+      bias[j] = f < kF ? *reinterpret_cast<const float4*>(bg + f) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     f32x4 acc[kFT / 16];
 #pragma unroll
     for (int j = 0; j < kFT / 16; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -192,31 +198,37 @@ __global__ __launch_bounds__(kET) void encode_kernel(UpdateArgs a) {
 #pragma unroll
       for (int j = 0; j < kFT / 16; ++j)
         bv[j] = *reinterpret_cast<const float4*>(&ws[buf][16 * j + li][16 * kb + 4 * lq]);
-      // the four accumulators interleaved: no MFMA waits on the one before it
+      // the four accumulators interleaved: no MFMA waits on the one before it.
+      // A = W (bucket rows), B = x (token columns): D[bucket][token], the
+      // same products in the same order as x W^T, transposed
 #pragma unroll
-      for (int j = 0; j < kFT / 16; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.x, bv[j].x, acc[j], 0, 0, 0);
+      for (int j = 0; j < kFT / 16; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].x, xa.x, acc[j], 0, 0, 0);
 #pragma unroll
-      for (int j = 0; j < kFT / 16; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.y, bv[j].y, acc[j], 0, 0, 0);
+      for (int j = 0; j < kFT / 16; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].y, xa.y, acc[j], 0, 0, 0);
 #pragma unroll
-      for (int j = 0; j < kFT / 16; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.z, bv[j].z, acc[j], 0, 0, 0);
+      for (int j = 0; j < kFT / 16; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].z, xa.z, acc[j], 0, 0, 0);
 #pragma unroll
-      for (int j = 0; j < kFT / 16; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(xa.w, bv[j].w, acc[j], 0, 0, 0);
+      for (int j = 0; j < kFT / 16; ++j) acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(bv[j].w, xa.w, acc[j], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
     // bias, relu, histogram of the positive values, store: lane (i, q) holds
-    // buckets f0 + 16 j + i of tokens t0 + 4 q + r
+    // buckets f0 + 16 j + 4 q + r of token t0 + i
+    const int tok = t0 + li;
 #pragma unroll
     for (int j = 0; j < kFT / 16; ++j) {
-      const int f = f0 + 16 * j + li;
+      const int f = f0 + 16 * j + 4 * lq;
+      const float b4[4] = {bias[j].x, bias[j].y, bias[j].z, bias[j].w};
+      float v[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int tok = t0 + 4 * lq + r;
-        const float x = acc[j][r] + bias[j];
-        const float v = x > 0.f ? x : 0.f;  // relu; non-positive values are never selected
-        if (tok < a.N && f < kF) {
-          ag[(size_t)tok * kF + f] = v;
-          if (v > 0.f) atomicAdd(&hist[__float_as_uint(v) >> 20], 1u);
-        }
+        const float x = acc[j][r] + b4[r];
+        v[r] = x > 0.f ? x : 0.f;  // relu; non-positive values are never selected
+      }
+      if (tok < a.N && f < kF) {
+        *reinterpret_cast<float4*>(&ag[(size_t)tok * kF + f]) = make_float4(v[0], v[1], v[2], v[3]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+          if (v[r] > 0.f) atomicAdd(&hist[__float_as_uint(v[r]) >> 20], 1u);
       }
     }
     if (more) {  // the other buffer was last read before the previous barrier
@@ -1092,7 +1104,7 @@ int prismkv_update(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t
     return kBadSize;
   if (ks < (int64_t)(H + N) * kD || row_words < (H + N + 31) / 32) return kBadSize;
   if (!k || !W || !b || !center || !scale || !bits || !counts || !moments || !work) return kBadSize;
-  if (!aligned16(k, ks)) return kBadSize;
+  if (!aligned16(k, ks) || ((W | b) & 15u)) return kBadSize;
   const UpdateLayout L(groups, N);
   const UpdateArgs a = make_args(k, W, b, center, scale, bits, counts, moments, work, groups, H, N, key_mean, ks,
                                  row_words, L);
@@ -1121,7 +1133,7 @@ int prismkv_build(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t 
   if (flags & ~kBuildCenter) return kBadMode;
   if (ks < (int64_t)H * kD || row_words < (H + 31) / 32 || (row_words & 3)) return kBadSize;
   if (!k || !W || !b || !center || !scale || !bits || !counts || !moments || !work) return kBadSize;
-  if (!aligned16(k, ks) || (bits & 15u)) return kBadSize;
+  if (!aligned16(k, ks) || ((bits | W | b) & 15u)) return kBadSize;
   const UpdateLayout L(batch, H);
   hipStream_t s = (hipStream_t)stream;
   for (int g0 = 0; g0 < groups; g0 += batch) {
