@@ -843,7 +843,10 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     mfma_init(st, a.q + (size_t)g * kHq * kD);
 #endif
     constexpr int kPerRound = 4;
-    for (int k0 = kWaves - 1 - w; k0 < n_blocks; k0 += kPerRound * kWaves) {  // blocks k0 + 8 i
+    // the wave index made explicitly uniform keeps the block indices in
+    // scalar registers (fewer VGPRs for the round's loads)
+    const int wu = __builtin_amdgcn_readfirstlane(w);
+    for (int k0 = kWaves - 1 - wu; k0 < n_blocks; k0 += kPerRound * kWaves) {  // blocks k0 + 8 i
       uint4 kr[kPerRound][4], vr[kPerRound][4];
 #pragma unroll
       for (int i = 0; i < kPerRound; ++i) {
@@ -866,7 +869,7 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
         }
       }
       asm volatile("" ::: "memory");  // every load of the round is in flight before any is used
-      if (k0 == kWaves - 1 - w && w == 0 && !id_list) {
+      if (k0 == kWaves - 1 - wu && wu == 0 && !id_list) {
 #pragma unroll
         for (int c = 0; c < kMaxSplits / 64; ++c) {
           const int qq = 64 * c + lane;
