@@ -120,7 +120,8 @@ int prismkv_attend(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t co
  * src/prismkv/native8b.py:104-106): ONE launch per layer for moment scoring,
  * selection, union and sparse attention; writes the same features / valid /
  * raw / ids / count as prismkv_route + prismkv_union and the same out as
- * prismkv_attend.  H <= 524288.  `work` is sized for the largest history the
+ * prismkv_attend.  H <= 524288, (H + T) * 256 < 2^31 (the K/V rows are
+ * read through 32-bit byte offsets).  `work` is sized for the largest history the
  * caller will use (`capacity` >= H) by prismkv_decode_work_bytes and is
  * zero-filled once before first use; its first 32-bit word is the error word
  * (nonzero if a bounded inter-workgroup wait gave up; see the bounded-wait

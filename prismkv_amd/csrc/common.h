@@ -41,6 +41,17 @@ __device__ __forceinline__ uint4 load_nt16(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// 16-byte streaming load through a raw buffer resource (gfx9 resource word 3
+// 0x00020000: 32-bit data format; aux 2: non-temporal).  The 32-bit offset
+// takes one address register per load instead of two.
+__device__ __forceinline__ uint4 load_nt16_buf(__amdgpu_buffer_rsrc_t r, unsigned byte_offset) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, 2);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_buffer(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
 // Per-lane select by a wave lane mask: lane i gets `if_set` when bit i of
 // `lanes` is set, else `if_clear` (one v_cndmask).  Written out so that the
 // compiler cannot fold `c ? x[a] : x[b]` over a register array into a

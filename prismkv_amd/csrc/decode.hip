@@ -841,6 +841,10 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
 #else
     MfmaAttn st;
     mfma_init(st, a.q + (size_t)g * kHq * kD);
+    // the group's K and V rows [0, last_row] as buffer resources (row
+    // positions are clamped into that range, so every offset is in bounds)
+    const int kv_bytes = __builtin_amdgcn_readfirstlane((last_row + 1) * 2 * kD);
+    const __amdgpu_buffer_rsrc_t kbuf = raw_buffer(kg, kv_bytes), vbuf = raw_buffer(vg, kv_bytes);
 #endif
     constexpr int kPerRound = 4;
     // the wave index made explicitly uniform keeps the block indices in
@@ -860,11 +864,12 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
             vr[i][b] = load_nt16(vg + at);
           }
 #else
-          const uint16_t* kp = kg + (size_t)row_pos(base + j, base) * kD + 8 * qd;
+          const unsigned ko = (unsigned)row_pos(base + j, base) * (2 * kD) + 16 * qd;
 #pragma unroll
-          for (int c = 0; c < 4; ++c) kr[i][c] = load_nt16(kp + 32 * c);
+          for (int c = 0; c < 4; ++c) kr[i][c] = load_nt16_buf(kbuf, ko + 64 * c);
 #pragma unroll
-          for (int t = 0; t < 4; ++t) vr[i][t] = load_nt16(vg + (size_t)row_pos(base + 4 * qd + t, base) * kD + 8 * j);
+          for (int t = 0; t < 4; ++t)
+            vr[i][t] = load_nt16_buf(vbuf, (unsigned)row_pos(base + 4 * qd + t, base) * (2 * kD) + 16 * j);
 #endif
         }
       }
@@ -1075,6 +1080,7 @@ static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t b
   if (given && limit >= 0) return kBadSize;
   if (row_words < (H + 31) / 32 || ids_stride < H) return kBadSize;
   if (ks < (int64_t)(H + T) * kD || vs < (int64_t)(H + T) * kD) return kBadSize;
+  if (((int64_t)H + T) * 2 * kD > INT32_MAX) return kBadSize;  // K/V rows are read through 32-bit buffer offsets
   // a given selection needs neither the moment tables nor raw
   if (!q || (!given && (!moments || !counts || !raw)) || !bits || !k || !v || !work || !features || !valid || !ids ||
       !count || !out)
