@@ -114,6 +114,15 @@ def test_native_error_codes(lib):
     assert call_raw(lib, "prismkv_build", *[16] * 9, 8, 8, 100, 8, 2, good, 4) == -2  # unknown flag
     assert call_raw(lib, "prismkv_build", *[0] * 9, 8, 8, 100, 8, 0, good, 4) == -1   # null pointers
     assert call_raw(lib, "prismkv_build", *[18] + [16] * 8, 8, 8, 100, 8, 0, good, 4) == -1  # misaligned K
+    assert call_raw(lib, "prismkv_build", 16, 20, *[16] * 7, 8, 8, 100, 8, 0, good, 4) == -1  # misaligned W
+    assert call_raw(lib, "prismkv_build", 16, 16, 24, *[16] * 6, 8, 8, 100, 8, 0, good, 4) == -1  # misaligned b
+    good = (100 + 64) * 128
+    assert call_raw(lib, "prismkv_update", 16, 20, *[16] * 7, 8, 100, 64, 8, good, 8) == -1  # misaligned W
+    assert call_raw(lib, "prismkv_update", 16, 16, 24, *[16] * 6, 8, 100, 64, 8, good, 8) == -1  # misaligned b
+    # prismkv_decode(13 buffers, groups, H, T, capacity, row_words, ks, vs, ids_stride, stream): K/V rows are
+    # addressed by 32-bit byte offsets, so (H + T) x 256 must stay below 2^31
+    big = (100 + (1 << 23)) * 128
+    assert call_raw(lib, "prismkv_decode", *[16] * 13, 8, 100, 1 << 23, 100, 4, big, big, 100) == -1
     # prismkv_decode_tail(13 buffers, tail, groups, H, max_tail, capacity, row_words, ks, vs, ids_stride)
     ok = (100 + 8) * 128
     assert call_raw(lib, "prismkv_decode_tail", *[16] * 13, 0, 8, 100, 8, 100, 4, ok, ok, 100) == -1   # no word
