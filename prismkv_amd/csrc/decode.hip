@@ -895,30 +895,9 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
 #endif
     }
 
-    // ---- 7. the tile's global ids offset (ids are written after phase 8)
-    if (w == 0 && !id_list) {
-      const unsigned* tiles = a.status + (size_t)g * a.S;
-      unsigned prefix = 0;
-#pragma unroll
-      for (int c = 0; c < kMaxSplits / 64; ++c) {
-        const int qq = 64 * c + lane;
-        unsigned v = lower[c];
-        wait_all([&] {
-          if (qq < p && !(v & kReady)) v = ld_dev(tiles + qq);
-          return (v & kReady) != 0u;
-        }, a);
-        prefix += (unsigned)wave_sum_i(qq < p ? (int)(v & ~kReady) : 0);
-      }
-      if (lane == 0) {
-        lds.base = (int)prefix;
-        if (p == a.S - 1) a.count[g] = (int32_t)(prefix + (unsigned)n_sel);
-      }
-    }
-
-    // ---- 8. the split state (after the look-back: its publication tells
-    // workgroup 0 that this workgroup no longer reads any published word);
-    // its barriers also publish lds.base to every wave
-    __syncthreads();  // the LDS union is free (the rows and base stay)
+    // each wave stashes its state as soon as its attention ends: the LDS
+    // union's earlier users (phases 1-5) are done, and no wave reads it
+    // during the attention
 #if PRISMKV_VALU_ATTENTION
     {
       // merge the wave's 4 slot states (lane bits 4, 5) into the stash layout
@@ -953,6 +932,31 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
 #else
     mfma_stash(st, lds.mf, w);
 #endif
+
+    // ---- 7. the tile's global ids offset (ids are written after phase 8)
+    if (w == 0 && !id_list) {
+      const unsigned* tiles = a.status + (size_t)g * a.S;
+      unsigned prefix = 0;
+#pragma unroll
+      for (int c = 0; c < kMaxSplits / 64; ++c) {
+        const int qq = 64 * c + lane;
+        unsigned v = lower[c];
+        wait_all([&] {
+          if (qq < p && !(v & kReady)) v = ld_dev(tiles + qq);
+          return (v & kReady) != 0u;
+        }, a);
+        prefix += (unsigned)wave_sum_i(qq < p ? (int)(v & ~kReady) : 0);
+      }
+      if (lane == 0) {
+        lds.base = (int)prefix;
+        if (p == a.S - 1) a.count[g] = (int32_t)(prefix + (unsigned)n_sel);
+      }
+    }
+
+    // ---- 8. the split state (after the look-back: its publication tells
+    // workgroup 0 that this workgroup no longer reads any published word);
+    // publish_sliced's first barrier waits for every wave's stash and also
+    // publishes lds.base to every wave
     publish_sliced(lds.mf, a.state + (size_t)(g * a.S + p) * kHq * kSlices * kSliceW);
   }
   if (!id_list) {
