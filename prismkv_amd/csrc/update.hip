@@ -104,13 +104,15 @@ __device__ __forceinline__ unsigned* hist_of(const UpdateArgs& a, int g, int lev
 // tile's W streams through LDS, double-buffered: the next tile's W is
 // requested into registers while the current tile is multiplied, then
 // stored to the other buffer.  Products run on fp32 MFMA
-// (v_mfma_f32_16x16x4f32: lane l feeds A[i = l % 16][k], B[k][j = l % 16] and
-// holds D[4 (l / 16) + r][l % 16]).  Lane (i, q) = (l % 16, l / 16) supplies
-// the dims 16 kb + 4 q + t of dim block kb to step t: its A values are x of
-// token row i at those 32 dims, its B values one 16-byte LDS read per
-// 16-bucket column and block.  A and B always pair the same dim, so the
-// steps only reorder the sum over the 128 dims (the same order for every
-// token and bucket).  P is the smallest count that gives the launch
+// (v_mfma_f32_16x16x4f32: lane l feeds A[i = l % 16][k = l / 16],
+// B[k][j = l % 16] and holds D[4 (l / 16) + r][l % 16]).  A is W (bucket
+// rows) and B is x (token columns), so D is [bucket][token] and lane (i, q)
+// ends with buckets 4 q .. 4 q + 3 of token i, stored as one 16-byte store.
+// Lane (i, q) = (l % 16, l / 16) supplies the dims 16 kb + 4 q + t of dim
+// block kb to step t: its W values are one 16-byte LDS read per 16-bucket
+// column and block, its x values those of token row i at its 32 dims.  A and
+// B always pair the same dim, so the steps only reorder the sum over the 128
+// dims (the same order for every token and bucket).  P is the smallest count that gives the launch
 // kEncMinWgs workgroups (two per CU), so the x of a token is computed P times
 // in all rather than once per bucket tile.
 // ---------------------------------------------------------------------------
