@@ -140,6 +140,21 @@ def test_append_full_block_4096():
     check_decode_after(case, op, k, got)
 
 
+@pytest.mark.parametrize("N", [1, 37, 100])
+def test_append_ragged_block(N):
+    # a block that fills neither a 16-row wave tile nor a 128-token encode
+    # workgroup: the rows past the block are masked at the activation store
+    case = cases.update_case("random", H=700, N=N, T=3, seed=50 + N)
+    log(f"update case kind=random H={case['H']} N={case['N']}")
+    op, k = run_append(case)
+    act = op.update_activations(case["N"]).cpu().numpy()
+    got = op.export_indices()
+    for g in range(8):
+        sel, moved, err = check_group(case, g, act[g], got[g])
+        log(f"  group {g}: selected={sel} moved_at_tau={moved} act_err={err:.2e}")
+    check_decode_after(case, op, k, got)
+
+
 def test_catch_up_two_blocks():
     # two consecutive appends equal two oracle append_index steps
     H, N, T = 300, 128, 5
