@@ -62,6 +62,11 @@ G, HQ, D, F, TOPK = 8, 4, 128, 3000, 16
 TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                                "decode_kernel_64k_hbm_traffic.md")
 STAGE_KERNEL = {"decode": "decode_kernel"}
+
+
+def nbytes(t):
+    """Bytes of a workspace tensor (the work_bytes argument beside its pointer)."""
+    return t.numel() * t.element_size()
 DEFAULT_STAGES = "chain,route,union,attend,dense,update,build,copy,long_history,capped"
 
 
@@ -241,7 +246,8 @@ def dense_control(layers, H, T, steps, warmup):
     def run():
         for _, q, k, v in layers:
             lib.call("prismkv_attend", q.data_ptr(), k.data_ptr(), v.data_ptr(), ids.data_ptr(), count.data_ptr(),
-                     work.data_ptr(), out.data_ptr(), G, H, T, k.stride(0), v.stride(0), H, splits, stream=stream())
+                     work.data_ptr(), out.data_ptr(), G, H, T, k.stride(0), v.stride(0), H, splits, nbytes(work),
+                     stream=stream())
     ms, _, _ = graph_time(run, steps, warmup)
     us = ms * 1e3 / len(layers)
     nbytes = G * (H + T) * 2 * D * 2 + G * H * 4 + 2 * G * HQ * D * 2
@@ -278,7 +284,7 @@ def update_timing(lib_path, H, blocks, steps, warmup, seed, device):
             op.lib.call("prismkv_update", k.data_ptr(), op.W_enc.data_ptr(), op.b_enc.data_ptr(),
                         op.center.data_ptr(), op.key_scale.data_ptr(), op.bits.data_ptr(), op.n.data_ptr(),
                         op.moments.data_ptr(), op.update_work.data_ptr(), G, h0, N, 8, k.stride(0), op.row_words,
-                        stream=stream())
+                        nbytes(op.update_work), stream=stream())
         ms, _, _ = graph_time(once, steps, warmup)
         us = ms * 1e3
         flops = 2.0 * G * N * F * D
@@ -310,7 +316,7 @@ def build_timing(lib_path, H, steps, warmup, seed, device):
         op.lib.call("prismkv_build", k.data_ptr(), op.W_enc.data_ptr(), op.b_enc.data_ptr(), op.center.data_ptr(),
                     op.key_scale.data_ptr(), op.bits.data_ptr(), op.n.data_ptr(), op.moments.data_ptr(),
                     op.build_work.data_ptr(), G, op.build_batch, H, 8, 1, k.stride(0), op.row_words,
-                    stream=stream())
+                    nbytes(op.build_work), stream=stream())
     ms, _, _ = graph_time(once, max(2, steps // 4), max(1, warmup // 4))
     flops = 2.0 * G * H * F * D
     out = dict(history=H, ms_per_layer=round(ms, 3), groups_per_batch=op.build_batch,
@@ -371,7 +377,7 @@ def capped(lib_path, steps, warmup, seed, device, layers_total, replicas=12, H=2
         op.unique_cap = None
         op.lib.call("prismkv_route_single", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(),
                     op.decode_work.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(), op.raw.data_ptr(), G,
-                    stream=stream())
+                    nbytes(op.decode_work), stream=stream())
         ranked.append((op.valid > 0).sum(1).cpu().numpy())
         op.unique_cap = cap
         op(q, k, v)
@@ -404,7 +410,7 @@ def capped(lib_path, steps, warmup, seed, device, layers_total, replicas=12, H=2
     def route_only(op, q, k, v):
         op.lib.call("prismkv_route_single", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(),
                     op.decode_work.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(), op.raw.data_ptr(), G,
-                    stream=stream())
+                    nbytes(op.decode_work), stream=stream())
 
     def walk_only(op, q, k, v):
         op.lib.call("prismkv_select_cap_n", op.bits.data_ptr(), op.n.data_ptr(), op.features.data_ptr(),
@@ -415,7 +421,7 @@ def capped(lib_path, steps, warmup, seed, device, layers_total, replicas=12, H=2
         op.lib.call("prismkv_union_attend", q.data_ptr(), op.bits.data_ptr(), k.data_ptr(), v.data_ptr(),
                     op.decode_work.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(), op.ids.data_ptr(),
                     op.count.data_ptr(), op.out.data_ptr(), G, op.history, k.shape[1] - op.history, op.capacity,
-                    op.row_words, k.stride(0), v.stride(0), op.capacity, stream=stream())
+                    op.row_words, k.stride(0), v.stride(0), op.capacity, nbytes(op.decode_work), stream=stream())
     us_route = stage(route_only)
     # the walk re-reads the route's ranking: restore it before timing the walk
     for op, q, k, v in layers:
@@ -586,13 +592,13 @@ def main():
         for op, q, k, v in layers:
             op.lib.call("prismkv_route_single", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(),
                         op.decode_work.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(),
-                        op.raw.data_ptr(), G, stream=stream())
+                        op.raw.data_ptr(), G, nbytes(op.decode_work), stream=stream())
 
     def union_only():
         for op, q, k, v in layers:
             op.lib.call("prismkv_union", op.bits.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(),
                         op.union_work.data_ptr(), op.ids.data_ptr(), op.count.data_ptr(), G, op.history,
-                        op.row_words, op.capacity, stream=stream())
+                        op.row_words, op.capacity, nbytes(op.union_work), stream=stream())
 
     def attend_only():
         for op, q, k, v in layers:

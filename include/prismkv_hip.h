@@ -14,6 +14,12 @@
  *     matching *_work_bytes() call, zero-filled once before first use; the
  *     kernels leave their counters at zero again, so launches can be replayed
  *     from a captured graph.  Calls sharing a work buffer must not overlap.
+ *     Every entry point that takes `work` also takes its size, `work_bytes`
+ *     (the last argument before the stream), and returns -1 without enqueuing
+ *     anything when it is below what the matching *_work_bytes() query returns
+ *     for the call's own sizes: an undersized or stale workspace is refused
+ *     instead of being written past its end.  (No reference counterpart: the
+ *     reference's kernels take no workspace.)
  *
  * Geometry is the native 8B specialisation: F = 3000 buckets, d = 128,
  * 4 query heads per KV group, Top-16 buckets (src/prismkv/native8b.py:1-6).
@@ -71,7 +77,7 @@ int attention_tuned(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t c
  * candidates and the final Top-16, three launches for G groups. */
 size_t prismkv_route_work_bytes(int groups);
 int prismkv_route(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
-                  uint64_t valid, uint64_t raw, int groups, uint64_t stream);
+                  uint64_t valid, uint64_t raw, int groups, size_t work_bytes, uint64_t stream);
 /* Stage 1 in ONE launch (the same replacement and semantics as prismkv_route,
  * identical features / valid / raw): the selection phases of prismkv_decode
  * alone.  `work` is prismkv_decode's workspace (prismkv_decode_work_bytes,
@@ -79,13 +85,14 @@ int prismkv_route(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, 
  * same error word; -1 when one group's workgroups cannot be resident at once,
  * as for prismkv_decode. */
 int prismkv_route_single(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
-                         uint64_t valid, uint64_t raw, int groups, uint64_t stream);
+                         uint64_t valid, uint64_t raw, int groups, size_t work_bytes, uint64_t stream);
 
 /* Stage 2 (replaces launch_union_warp, src/prismkv/native8b.py:88-89;
  * semantics kernels/ppu_8b/union.cu:14-27): one launch, any H up to 2^29. */
 size_t prismkv_union_work_bytes(int groups, int H);
 int prismkv_union(uint64_t bits, uint64_t features, uint64_t valid, uint64_t work, uint64_t ids,
-                  uint64_t count, int groups, int H, int64_t row_words, int64_t ids_stride, uint64_t stream);
+                  uint64_t count, int groups, int H, int64_t row_words, int64_t ids_stride, size_t work_bytes,
+                  uint64_t stream);
 
 /* Stage 2, strict unique-ID budget (src/prismkv/core.py:149-163, select_buckets
  * with unique_cap): walks the ranked buckets (rows with valid > 0, in rank
@@ -109,12 +116,15 @@ int prismkv_build_bits(uint64_t ids, uint64_t offsets, uint64_t bits, int groups
  * the last workgroup of each group.  splits in [1,1024] (the partition does
  * not change the result).  `work` (prismkv_attend_work_bytes) is zero-filled
  * once before first use and left zeroed; its first 32-bit word is the error
- * word (nonzero if a bounded inter-workgroup wait gave up), with the
- * optional host-word slot at byte 8. */
+ * word (1 if a bounded inter-workgroup wait gave up; 2 if an id outside
+ * [0, H) or a count outside [0, H] was found, which is then read clamped into
+ * range), with the optional host-word slot at byte 8.  The ids of a group
+ * must be distinct (the reference's attend rejects duplicates on the host,
+ * src/prismkv/core.py:176-179). */
 size_t prismkv_attend_work_bytes(int groups, int splits);
 int prismkv_attend(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t count, uint64_t work,
                    uint64_t out, int groups, int H, int T, int64_t ks, int64_t vs, int64_t ids_stride,
-                   int splits, uint64_t stream);
+                   int splits, size_t work_bytes, uint64_t stream);
 
 /* Stages 1-3 fused (replaces Native8B.__call__ = route + attention,
  * src/prismkv/native8b.py:104-106): ONE launch per layer for moment scoring,
@@ -133,7 +143,7 @@ size_t prismkv_decode_work_bytes(int groups, int capacity);
 int prismkv_decode(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
                    uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
                    uint64_t out, int groups, int H, int T, int capacity, int64_t row_words, int64_t ks, int64_t vs,
-                   int64_t ids_stride, uint64_t stream);
+                   int64_t ids_stride, size_t work_bytes, uint64_t stream);
 /* prismkv_decode with the tail length read from device memory at launch
  * (`tail`: one int32, 4-byte aligned), clamped to [0, max_tail]; the K/V
  * extents are checked for max_tail.  For a decode step captured once in a
@@ -144,7 +154,7 @@ int prismkv_decode(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits,
 int prismkv_decode_tail(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
                         uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
                         uint64_t out, uint64_t tail, int groups, int H, int max_tail, int capacity, int64_t row_words,
-                        int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream);
+                        int64_t ks, int64_t vs, int64_t ids_stride, size_t work_bytes, uint64_t stream);
 /* Stages 2-3 fused from a given selection (replaces launch_union_warp +
  * attention_tuned, src/prismkv/native8b.py:88-89 and :100-101): ONE launch
  * for the union and the sparse attention of prismkv_decode, over the
@@ -156,7 +166,8 @@ int prismkv_decode_tail(uint64_t q, uint64_t moments, uint64_t counts, uint64_t 
  * a group that cannot be resident are prismkv_decode's. */
 int prismkv_union_attend(uint64_t q, uint64_t bits, uint64_t k, uint64_t v, uint64_t work, uint64_t features,
                          uint64_t valid, uint64_t ids, uint64_t count, uint64_t out, int groups, int H, int T,
-                         int capacity, int64_t row_words, int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream);
+                         int capacity, int64_t row_words, int64_t ks, int64_t vs, int64_t ids_stride,
+                         size_t work_bytes, uint64_t stream);
 /* prismkv_union_attend with the tail length read from device memory at
  * launch (`tail`: one int32, 4-byte aligned), clamped to [0, max_tail], as
  * prismkv_decode_tail: the capped step (route, budgeted walk, union +
@@ -166,7 +177,7 @@ int prismkv_union_attend(uint64_t q, uint64_t bits, uint64_t k, uint64_t v, uint
 int prismkv_union_attend_tail(uint64_t q, uint64_t bits, uint64_t k, uint64_t v, uint64_t work, uint64_t features,
                               uint64_t valid, uint64_t ids, uint64_t count, uint64_t out, uint64_t tail, int groups, int H,
                               int max_tail, int capacity, int64_t row_words, int64_t ks, int64_t vs, int64_t ids_stride,
-                              uint64_t stream);
+                              size_t work_bytes, uint64_t stream);
 /* The capped step in ONE launch (replaces the strict unique cap branch of
  * select_buckets, src/prismkv/core.py:149-163, between route and union,
  * src/prismkv/native8b.py:104-106 with a cap): prismkv_decode with the
@@ -181,7 +192,7 @@ int prismkv_union_attend_tail(uint64_t q, uint64_t bits, uint64_t k, uint64_t v,
 int prismkv_decode_capped(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
                           uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
                           uint64_t out, int groups, int H, int T, int capacity, int64_t limit, int64_t row_words,
-                          int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream);
+                          int64_t ks, int64_t vs, int64_t ids_stride, size_t work_bytes, uint64_t stream);
 /* prismkv_decode_capped with the tail length read from device memory at
  * launch, as prismkv_decode_tail (no reference counterpart: a captured capped
  * step replayed as the tail grows). */
@@ -189,7 +200,7 @@ int prismkv_decode_capped_tail(uint64_t q, uint64_t moments, uint64_t counts, ui
                                uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids,
                                uint64_t count, uint64_t out, uint64_t tail, int groups, int H, int max_tail,
                                int capacity, int64_t limit, int64_t row_words, int64_t ks, int64_t vs,
-                               int64_t ids_stride, uint64_t stream);
+                               int64_t ids_stride, size_t work_bytes, uint64_t stream);
 
 /* The allocation-free decode.  No counterpart in the reference: for callers
  * that cannot allocate device memory (code under HIP graph capture, tight
@@ -247,13 +258,17 @@ uint64_t prismkv_mapped_pointer(uint64_t host);
  *     table) <- Chan merge of the old moments with the block's population
  *     moments, in fp32 and the operation order of core.py:190-199.
  * `work` is prismkv_update_work_bytes(groups, N) bytes, zero-filled once
- * before first use and left zeroed.  N <= 4096; K rows, W and b 16-byte
- * aligned; returns -1 on bad sizes.
+ * before first use and left zeroed; a workspace sized for the largest block
+ * serves every smaller one.  N <= 4096; K rows, W and b 16-byte aligned;
+ * returns -1 on bad sizes.  The block's dense activations [G][N][3000] f32
+ * stay in the workspace from byte prismkv_update_act_offset(groups) on until
+ * the next call (the same offset, for `batch` groups, in prismkv_build's).
  * The caller guarantees K holds rows [0, H+N) for every group. */
 size_t prismkv_update_work_bytes(int groups, int max_block);
+size_t prismkv_update_act_offset(int groups);
 int prismkv_update(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
                    uint64_t counts, uint64_t moments, uint64_t work, int groups, int H, int N, int key_mean,
-                   int64_t ks, int64_t row_words, uint64_t stream);
+                   int64_t ks, int64_t row_words, size_t work_bytes, uint64_t stream);
 
 /* ---- prefill index build -----------------------------------------------
  * build_index (src/prismkv/core.py:92-103) of every group from K rows
@@ -273,14 +288,15 @@ int prismkv_update(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t
 size_t prismkv_build_work_bytes(int batch, int H);
 int prismkv_build(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
                   uint64_t counts, uint64_t moments, uint64_t work, int groups, int batch, int H, int key_mean,
-                  int flags, int64_t ks, int64_t row_words, uint64_t stream);
+                  int flags, int64_t ks, int64_t row_words, size_t work_bytes, uint64_t stream);
 
 /* ---- the prismkv.core surface (src/prismkv/core.py) ---------------------
  * Stage 1 with the score vector of bucket_scores (core.py:106-130): as
  * prismkv_route, and scores f32 [G][3000] <- the per-head softmax
  * probabilities' mean over the 4 heads (0 for a dead bucket). */
 int prismkv_route_scores(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
-                         uint64_t valid, uint64_t raw, uint64_t scores, int groups, uint64_t stream);
+                         uint64_t valid, uint64_t raw, uint64_t scores, int groups, size_t work_bytes,
+                         uint64_t stream);
 
 /* Stage 1 by query activations (router "q_activation", core.py:131-139):
  * a = relu((q / qscale[g]) W[g]^T + b[g]) for the 4 heads (W f32 [G][3000][128],
@@ -293,12 +309,14 @@ int prismkv_route_scores(uint64_t q, uint64_t moments, uint64_t counts, uint64_t
  * with width 64. */
 size_t prismkv_route_qact_work_bytes(int groups);
 int prismkv_route_qact(uint64_t q, uint64_t W, uint64_t b, uint64_t qscale, uint64_t counts, uint64_t work,
-                       uint64_t features, uint64_t valid, uint64_t raw, uint64_t scores, int groups, uint64_t stream);
+                       uint64_t features, uint64_t valid, uint64_t raw, uint64_t scores, int groups, size_t work_bytes,
+                       uint64_t stream);
 
 /* prismkv_union / prismkv_select_cap over selections of `width` rows per
  * group (features / valid [G][width]), width 16 or 64. */
 int prismkv_union_n(uint64_t bits, uint64_t features, uint64_t valid, uint64_t work, uint64_t ids, uint64_t count,
-                    int groups, int H, int64_t row_words, int64_t ids_stride, int width, uint64_t stream);
+                    int groups, int H, int64_t row_words, int64_t ids_stride, int width, size_t work_bytes,
+                    uint64_t stream);
 int prismkv_select_cap_n(uint64_t bits, uint64_t counts, uint64_t features, uint64_t valid, uint64_t raw, int groups,
                          int H, int64_t limit, int64_t row_words, int width, uint64_t stream);
 
@@ -310,7 +328,8 @@ int prismkv_select_cap_n(uint64_t bits, uint64_t counts, uint64_t features, uint
  * fewer are positive); out_len i32 [1] <- how many were written.  `work` is
  * prismkv_topk_work_bytes() bytes, zero-filled once and left zeroed. */
 size_t prismkv_topk_work_bytes(void);
-int prismkv_topk(uint64_t act, uint64_t out, uint64_t out_len, uint64_t work, int N, int64_t count, uint64_t stream);
+int prismkv_topk(uint64_t act, uint64_t out, uint64_t out_len, uint64_t work, int N, int64_t count,
+                 size_t work_bytes, uint64_t stream);
 
 /* summarize (core.py:76-89) of every group from its bitmap rows: counts and
  * the tiled moments get each bucket's member count and the population mean
@@ -319,7 +338,8 @@ int prismkv_topk(uint64_t act, uint64_t out, uint64_t out_len, uint64_t work, in
  * prismkv_summarize_work_bytes(groups) bytes, zero-filled once. */
 size_t prismkv_summarize_work_bytes(int groups);
 int prismkv_summarize(uint64_t k, uint64_t bits, uint64_t center, uint64_t counts, uint64_t moments, uint64_t work,
-                      int groups, int H, int flags, int64_t ks, int64_t row_words, uint64_t stream);
+                      int groups, int H, int flags, int64_t ks, int64_t row_words, size_t work_bytes,
+                      uint64_t stream);
 
 #ifdef __cplusplus
 }

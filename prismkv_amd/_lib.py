@@ -24,34 +24,37 @@ SIGNATURES = {
     "attention_tuned": ([_U64] * 7 + [_I32] * 6, True, _I32),
     # MI355X-native symbols
     "prismkv_route_work_bytes": ([_I32], False, _SZ),
-    "prismkv_route": ([_U64] * 7 + [_I32], True, _I32),
-    "prismkv_route_single": ([_U64] * 7 + [_I32], True, _I32),
+    "prismkv_route": ([_U64] * 7 + [_I32, _SZ], True, _I32),
+    "prismkv_route_single": ([_U64] * 7 + [_I32, _SZ], True, _I32),
     "prismkv_union_work_bytes": ([_I32, _I32], False, _SZ),
-    "prismkv_union": ([_U64] * 6 + [_I32, _I32, _I64, _I64], True, _I32),
+    "prismkv_union": ([_U64] * 6 + [_I32, _I32, _I64, _I64, _SZ], True, _I32),
     "prismkv_build_bits": ([_U64] * 3 + [_I32, _I64, _I64], True, _I32),
     "prismkv_attend_work_bytes": ([_I32, _I32], False, _SZ),
-    "prismkv_attend": ([_U64] * 7 + [_I32, _I32, _I32, _I64, _I64, _I64, _I32], True, _I32),
+    "prismkv_attend": ([_U64] * 7 + [_I32, _I32, _I32, _I64, _I64, _I64, _I32, _SZ], True, _I32),
     "prismkv_decode_work_bytes": ([_I32, _I32], False, _SZ),
-    "prismkv_decode": ([_U64] * 13 + [_I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64], True, _I32),
-    "prismkv_union_attend": ([_U64] * 10 + [_I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64], True, _I32),
-    "prismkv_decode_tail": ([_U64] * 14 + [_I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64], True, _I32),
-    "prismkv_union_attend_tail": ([_U64] * 11 + [_I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64], True, _I32),
-    "prismkv_decode_capped": ([_U64] * 13 + [_I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64, _I64], True, _I32),
-    "prismkv_decode_capped_tail": ([_U64] * 14 + [_I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64, _I64], True,
-                                   _I32),
+    "prismkv_decode": ([_U64] * 13 + [_I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64, _SZ], True, _I32),
+    "prismkv_union_attend": ([_U64] * 10 + [_I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64, _SZ], True, _I32),
+    "prismkv_decode_tail": ([_U64] * 14 + [_I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64, _SZ], True, _I32),
+    "prismkv_union_attend_tail": ([_U64] * 11 + [_I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64, _SZ], True,
+                                  _I32),
+    "prismkv_decode_capped": ([_U64] * 13 + [_I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64, _I64, _SZ], True,
+                              _I32),
+    "prismkv_decode_capped_tail": ([_U64] * 14 + [_I32, _I32, _I32, _I32, _I64, _I64, _I64, _I64, _I64, _SZ],
+                                   True, _I32),
     "prismkv_select_cap": ([_U64] * 5 + [_I32, _I32, _I64, _I64], True, _I32),
     "prismkv_update_work_bytes": ([_I32, _I32], False, _SZ),
-    "prismkv_update": ([_U64] * 9 + [_I32] * 4 + [_I64, _I64], True, _I32),
+    "prismkv_update_act_offset": ([_I32], False, _SZ),
+    "prismkv_update": ([_U64] * 9 + [_I32] * 4 + [_I64, _I64, _SZ], True, _I32),
     "prismkv_build_work_bytes": ([_I32, _I32], False, _SZ),
-    "prismkv_build": ([_U64] * 9 + [_I32] * 5 + [_I64, _I64], True, _I32),
-    "prismkv_route_scores": ([_U64] * 8 + [_I32], True, _I32),
+    "prismkv_build": ([_U64] * 9 + [_I32] * 5 + [_I64, _I64, _SZ], True, _I32),
+    "prismkv_route_scores": ([_U64] * 8 + [_I32, _SZ], True, _I32),
     "prismkv_topk_work_bytes": ([], False, _SZ),
-    "prismkv_topk": ([_U64] * 4 + [_I32, _I64], True, _I32),
+    "prismkv_topk": ([_U64] * 4 + [_I32, _I64, _SZ], True, _I32),
     "prismkv_summarize_work_bytes": ([_I32], False, _SZ),
-    "prismkv_summarize": ([_U64] * 6 + [_I32, _I32, _I32, _I64, _I64], True, _I32),
+    "prismkv_summarize": ([_U64] * 6 + [_I32, _I32, _I32, _I64, _I64, _SZ], True, _I32),
     "prismkv_route_qact_work_bytes": ([_I32], False, _SZ),
-    "prismkv_route_qact": ([_U64] * 10 + [_I32], True, _I32),
-    "prismkv_union_n": ([_U64] * 6 + [_I32, _I32, _I64, _I64, _I32], True, _I32),
+    "prismkv_route_qact": ([_U64] * 10 + [_I32, _SZ], True, _I32),
+    "prismkv_union_n": ([_U64] * 6 + [_I32, _I32, _I64, _I64, _I32, _SZ], True, _I32),
     "prismkv_select_cap_n": ([_U64] * 5 + [_I32, _I32, _I64, _I64, _I32], True, _I32),
     # error handling of the bounded inter-workgroup waits
     "prismkv_set_spin_limit": ([_I32], False, _I32),
@@ -94,6 +97,12 @@ class Library:
 
     def query(self, name: str, *args) -> int:
         return int(getattr(self.cdll, name)(*args))
+
+
+def nbytes(t) -> int:
+    """Size in bytes of a workspace tensor: the `work_bytes` argument that
+    accompanies its pointer."""
+    return t.numel() * t.element_size()
 
 
 def load(path=None) -> Library:

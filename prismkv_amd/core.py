@@ -21,8 +21,8 @@ from dataclasses import dataclass
 import torch
 
 from . import _lib
-from .native8b import (CHUNK, CHUNKS, DIM, FEATURES, HEADS, PADDED, TOPK, FeatureIndex, bitmap_row_words,
-                       tile_moments, untile_moments)
+from .native8b import (CHUNK, CHUNKS, DIM, ERR_WAIT, ERROR_MESSAGES, FEATURES, HEADS, PADDED, TOPK, FeatureIndex,
+                       bitmap_row_words, tile_moments, untile_moments)
 from .weights import SharedSAE
 
 __all__ = ["FeatureIndex", "SharedSAE", "positive_global_topk", "summarize", "build_index", "bucket_scores",
@@ -64,8 +64,8 @@ def _work(name, nbytes, device):
 
 
 def _fresh_work(nbytes, device):
-    """A new zero-filled workspace: the build and update keep the block's
-    activations in theirs, at offsets that depend on the block size."""
+    """A new zero-filled workspace of its own for one build or update, whose
+    activations stay readable in it (index.native keeps no workspace)."""
     return torch.zeros(max(nbytes, 1), dtype=torch.uint8, device=device)
 
 
@@ -178,7 +178,7 @@ def positive_global_topk(a: torch.Tensor, count: int):
     out_len = torch.zeros(1, dtype=torch.int32, device=a.device)
     work = _work("topk", lib.query("prismkv_topk_work_bytes"), a.device)
     lib.call("prismkv_topk", a.data_ptr(), out.data_ptr(), out_len.data_ptr(), work.data_ptr(), a.shape[0], count,
-             stream=_stream())
+             _lib.nbytes(work), stream=_stream())
     return out[:int(out_len.item())]
 
 
@@ -198,7 +198,7 @@ def summarize(keys, lists, center=None):
     work = _work("summarize", lib.query("prismkv_summarize_work_bytes", 1), keys.device)
     lib.call("prismkv_summarize", keys.data_ptr(), t.bits.data_ptr(), c.data_ptr(), t.n.data_ptr(),
              t.moments.data_ptr(), work.data_ptr(), 1, n, 1 if center is None else 0, keys.stride(0) * n, t.row_words,
-             stream=_stream())
+             _lib.nbytes(work), stream=_stream())
     mean, var = untile_moments(t.moments)
     counts = torch.tensor([len(x) for x in lists], device=keys.device, dtype=torch.long)
     out = FeatureIndex(n, c[0] if center is None else center, counts, mean[0].contiguous(), var[0].contiguous(),
@@ -233,7 +233,7 @@ def build_index(keys, sae, key_scale, *, center=None):
     work = _fresh_work(lib.query("prismkv_build_work_bytes", 1, n), device)
     lib.call("prismkv_build", keys.data_ptr(), W.data_ptr(), b.data_ptr(), c.data_ptr(), scale.data_ptr(),
              t.bits.data_ptr(), t.n.data_ptr(), t.moments.data_ptr(), work.data_ptr(), 1, 1, n, int(sae.key_mean),
-             1 if center is None else 0, keys.stride(0) * n, t.row_words, stream=_stream())
+             1 if center is None else 0, keys.stride(0) * n, t.row_words, _lib.nbytes(work), stream=_stream())
     mean, var = untile_moments(t.moments)
     out = FeatureIndex(n, c[0] if center is None else torch.as_tensor(center).to(device), t.n[0, :FEATURES].long(),
                        mean[0].contiguous(), var[0].contiguous(), _lists_from_bits(t.bits, 0, n))
@@ -267,7 +267,7 @@ def append_index(index, new_keys, sae, key_scale):
     base = new_keys.data_ptr() - H * row_bytes
     lib.call("prismkv_update", base, W.data_ptr(), b.data_ptr(), c.data_ptr(), scale.data_ptr(), t.bits.data_ptr(),
              t.n.data_ptr(), t.moments.data_ptr(), work.data_ptr(), 1, H, N, int(sae.key_mean), (H + N) * DIM,
-             t.row_words, stream=_stream())
+             t.row_words, _lib.nbytes(work), stream=_stream())
     mean, var = untile_moments(t.moments)
     new_lists = _lists_from_bits(t.bits, H, H + N)
     lists = [torch.cat((torch.as_tensor(old).to(device=device, dtype=torch.long), new))
@@ -304,7 +304,7 @@ def _route_qact(q, index, sae, query_scale, scores):
     work = _work("route_qact", lib.query("prismkv_route_qact_work_bytes", 1), device)
     lib.call("prismkv_route_qact", q1.data_ptr(), W.data_ptr(), b.data_ptr(), qs.data_ptr(), t.n.data_ptr(),
              work.data_ptr(), features.data_ptr(), valid.data_ptr(), raw.data_ptr(), scores.data_ptr(), 1,
-             stream=_stream())
+             _lib.nbytes(work), stream=_stream())
     return t, features, valid, raw
 
 
@@ -318,7 +318,8 @@ def _route(q, index, scores):
     raw = torch.zeros(1, dtype=torch.int32, device=device)
     work = _work("route", lib.query("prismkv_route_work_bytes", 1), device)
     lib.call("prismkv_route_scores", q1.data_ptr(), t.moments.data_ptr(), t.n.data_ptr(), work.data_ptr(),
-             features.data_ptr(), valid.data_ptr(), raw.data_ptr(), scores.data_ptr(), 1, stream=_stream())
+             features.data_ptr(), valid.data_ptr(), raw.data_ptr(), scores.data_ptr(), 1, _lib.nbytes(work),
+             stream=_stream())
     return t, features, valid, raw
 
 
@@ -380,7 +381,8 @@ def select_buckets(q, index, *, unique_cap=None, **kwargs):
     count = torch.zeros(1, dtype=torch.int32, device=q.device)
     work = _work("union", lib.query("prismkv_union_work_bytes", 1, H), q.device)
     lib.call("prismkv_union_n", t.bits.data_ptr(), features.data_ptr(), valid.data_ptr(), work.data_ptr(),
-             ids.data_ptr(), count.data_ptr(), 1, H, t.row_words, ids.shape[1], width, stream=_stream())
+             ids.data_ptr(), count.data_ptr(), 1, H, t.row_words, ids.shape[1], width, _lib.nbytes(work),
+             stream=_stream())
     n = int(count.item())
     if int(work[:4].view(torch.int32).item()):  # a bounded wait of the union gave up
         work.zero_()
@@ -424,8 +426,10 @@ def attend(q, keys, values, old_ids, history):
     work = _work("attend", lib.query("prismkv_attend_work_bytes", 1, ATTEND_SPLITS), q.device)
     lib.call("prismkv_attend", q1.data_ptr(), keys.data_ptr(), values.data_ptr(), ids.data_ptr(), count.data_ptr(),
              work.data_ptr(), out.data_ptr(), 1, history, L - history, L * DIM, L * DIM, ids.shape[1],
-             ATTEND_SPLITS, stream=_stream())
-    if int(work[:4].view(torch.int32).item()):  # a bounded wait of the attention gave up
+             ATTEND_SPLITS, _lib.nbytes(work), stream=_stream())
+    code = int(work[:4].view(torch.int32).item())
+    if code:  # a bounded wait of the attention gave up (ids were checked above)
         work.zero_()
-        raise RuntimeError("prismkv_attend: a bounded inter-workgroup wait gave up; the workspace was reset")
+        raise RuntimeError(f"prismkv_attend: {ERROR_MESSAGES.get(code, ERROR_MESSAGES[ERR_WAIT])}; "
+                           "the workspace was reset")
     return out[0].to(q.dtype)

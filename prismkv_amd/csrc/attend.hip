@@ -62,6 +62,7 @@ __device__ void attend_split(const AttendArgs& a, int g, int p, AttendLds& lds) 
     for (int i = 0; i < 8; ++i) s.acc[h][i] = 0.f;
 
   int n_old = -1, total = 0;
+  bool bad = false;  // an id outside [0, H) or a count outside [0, H]
   for (int round = 0;; ++round) {
     // row i of this lane's slot in the round: list index j[i]
     int jr[kSlotRows], idv[kSlotRows];
@@ -72,8 +73,9 @@ __device__ void attend_split(const AttendArgs& a, int g, int p, AttendLds& lds) 
       idv[i] = a.H > 0 ? idg[j < a.H ? j : a.H - 1] : 0;  // speculative: meaningful only if j < count
     }
     if (n_old < 0) {
-      n_old = a.cnt[g];
-      n_old = n_old < 0 ? 0 : (n_old > a.H ? a.H : n_old);
+      const int given = a.cnt[g];
+      n_old = given < 0 ? 0 : (given > a.H ? a.H : given);
+      bad = given != n_old;
       total = n_old + a.T;
     }
     if (!__ballot(jr[0] < total)) break;  // rows grow with i and round: nothing left for this wave
@@ -85,6 +87,7 @@ __device__ void attend_split(const AttendArgs& a, int g, int p, AttendLds& lds) 
     for (int i = 0; i < kSlotRows; ++i) {
       const int j = jr[i];
       const int p = j < n_old ? idv[i] : a.H + (j - n_old);
+      bad |= j < n_old && (p < 0 || p >= a.H);
       const int pos = (j < total && p >= 0) ? (p > last_row ? last_row : p) : 0;
       kr[i] = load_nt16(kg + (size_t)pos * kD);
       vr[i] = load_nt16(vg + (size_t)pos * kD);
@@ -107,6 +110,7 @@ __device__ void attend_split(const AttendArgs& a, int g, int p, AttendLds& lds) 
     asm volatile("" ::: "memory");  // LDS reads of this round precede the next round's gathers
   }
 
+  if (a.err && __ballot(bad) && lane == 0) report_error(a.err, error_host_slot(a.err), kErrIds);
   store_wg_state(s, lds, a.state + (((size_t)g * kHq) * a.S + p) * kStateW, (size_t)a.S * kStateW);
 }
 
@@ -155,10 +159,11 @@ size_t prismkv_attend_work_bytes(int groups, int splits) {
 
 int prismkv_attend(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t count, uint64_t work, uint64_t out,
                    int groups, int H, int T, int64_t ks, int64_t vs, int64_t ids_stride, int splits,
-                   uint64_t stream) {
+                   size_t work_bytes, uint64_t stream) {
   if (groups < 1 || groups > 65535 || H < 0 || T < 0 || splits < 1 || splits > 1024) return kBadSize;
   if (ks < (int64_t)(H + T) * kD || vs < (int64_t)(H + T) * kD || ids_stride < H) return kBadSize;
   if (!q || !k || !v || !ids || !count || !work || !out) return kBadSize;
+  if (work_bytes < prismkv_attend_work_bytes(groups, splits)) return kBadSize;
   // the decode's attention phases when the lists fit them; the split count
   // does not change the result (exact softmax), only the partition
   const int rc = attend_list(q, k, v, ids, count, work, out, groups, H, T, ks, vs, ids_stride, stream);
@@ -167,6 +172,7 @@ int prismkv_attend(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t co
   AttendArgs a{reinterpret_cast<const uint16_t*>(q), reinterpret_cast<const uint16_t*>(k),
                reinterpret_cast<const uint16_t*>(v), reinterpret_cast<const int32_t*>(ids),
                reinterpret_cast<const int32_t*>(count), ks, vs, ids_stride, H, T, splits, state};
+  a.err = reinterpret_cast<unsigned*>(work);  // the decode-phase region's error word comes first
   unsigned* sync = reinterpret_cast<unsigned*>(state + (size_t)groups * kHq * splits * kStateW);
   hipLaunchKernelGGL(attend_fused, dim3(splits, groups), dim3(kAT), 0, (hipStream_t)stream, a, sync,
                      reinterpret_cast<uint16_t*>(out));

@@ -22,6 +22,7 @@ struct AttendArgs {
   int64_t ks, vs, ids_stride;
   int H, T, S;
   float* state;
+  unsigned* err = nullptr;  // error word (kErrIds for an id or count out of range), or none
 };
 
 __device__ __forceinline__ void unpack8(const uint4 r, float (&f)[8]) {

@@ -195,7 +195,7 @@ __device__ __forceinline__ int wave_sum8(int (&p)[8]) {
   return v;
 }
 
-// Inclusive prefix sum over the lanes of a wave64.// The wave's integer sum, in every lane.
+// The wave's integer sum, in every lane.
 __device__ __forceinline__ int wave_sum_i(int v) { return wave_sum_dpp(v); }
 
 // Inclusive prefix sum over the lanes of a wave64 by DPP (no LDS traffic):
@@ -245,14 +245,17 @@ int attend_list(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t count
 
 // Error words.  A workspace's first 32-bit word is its sticky error word; its
 // 8-byte slot at byte offset 8 optionally holds the device address of a
-// host-mapped 32-bit word (0 = none), so a host binding can notice a wait that
-// gave up without copying or synchronising.  A wait that gives up writes 1 to
-// both (system scope: the host word lives in host memory).
-__device__ __forceinline__ void report_error(unsigned* err, unsigned* const* host_slot) {
-  __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+// host-mapped 32-bit word (0 = none), so a host binding can notice an error
+// without copying or synchronising.  A wait that gives up writes kErrWait to
+// both (system scope: the host word lives in host memory); an attention over
+// a caller's id list that finds an id outside [0, H) or a count outside
+// [0, H] writes kErrIds (and reads the id clamped into range).
+constexpr unsigned kErrWait = 1u, kErrIds = 2u;
+__device__ __forceinline__ void report_error(unsigned* err, unsigned* const* host_slot, unsigned code = kErrWait) {
+  __hip_atomic_store(err, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   if (host_slot) {
     unsigned* host = __hip_atomic_load(host_slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (host) __hip_atomic_store(host, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    if (host) __hip_atomic_store(host, code, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
   }
 }
 // The host-pointer slot of a workspace whose error word is `err`.

@@ -700,14 +700,23 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   if (id_list) {
     // ---- 5'. the workgroup's share of the group's list (count ids, then the
     // T tail rows H .. H + T - 1): rows [p per, (p + 1) per) as positions
-    const int cnt = min(max(a.count_in[g], 0), a.H), total = cnt + a.T;
+    const int given_cnt = a.count_in[g];
+    const int cnt = min(max(given_cnt, 0), a.H), total = cnt + a.T;
     const int per = (total + a.S - 1) / a.S;
     const int lo = min(total, p * per), n = min(total, lo + per) - lo;
     const int32_t* idg = a.ids_in + (size_t)g * a.ids_stride;
+    bool bad = p == 0 && tid == 0 && given_cnt != cnt;
     for (int i = tid; i < n; i += kDT) {
       const int j = lo + i;
-      rows[i] = j < cnt ? min(max(idg[j], 0), a.H - 1) : a.H + (j - cnt);
+      int r = a.H + (j - cnt);
+      if (j < cnt) {
+        const int id = idg[j];
+        bad |= id < 0 || id >= a.H;
+        r = min(max(id, 0), a.H - 1);
+      }
+      rows[i] = r;
     }
+    if (bad) report_error(a.err, a.err_host, kErrIds);  // the rows stay in range (clamped)
     if (tid == 0) lds.nsel = n;
   } else if (a.tw <= kTileWords) {
     if (w == 0) {
@@ -1074,12 +1083,13 @@ static int resident_workgroups() {
   return cached[dev];
 }
 
-static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
-                       uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
-                       uint64_t out, const int* tail_dev, bool given, int groups, int H, int T, int capacity,
-                       int64_t row_words, int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream,
-                       unsigned* err = nullptr, int64_t limit = -1) {
-  // limit >= 0: the capped launch (route, the strict unique cap's walk, union + attention)
+// Every host-side check of a decode launch, before anything is enqueued:
+// 0, or -1 for a size, range, pointer or residency the launch cannot take.
+// limit >= 0: the capped launch (route, the strict unique cap's walk, union + attention).
+static int decode_check(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
+                        uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
+                        uint64_t out, bool given, int groups, int H, int T, int capacity, int64_t row_words,
+                        int64_t ks, int64_t vs, int64_t ids_stride, int64_t limit) {
   if (groups < 1 || groups > 65535 || H < 1 || H > kFusedMaxHistory || T < 0 || capacity < H) return kBadSize;
   if (given && limit >= 0) return kBadSize;
   if (row_words < (H + 31) / 32 || ids_stride < H) return kBadSize;
@@ -1089,8 +1099,16 @@ static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t b
   if (!q || (!given && (!moments || !counts || !raw)) || !bits || !k || !v || !work || !features || !valid || !ids ||
       !count || !out)
     return kBadSize;
+  if (decode_splits(groups) > resident_workgroups()) return kBadSize;  // a group's workgroups must be resident together
+  return 0;
+}
+
+// Enqueues a decode launch whose arguments decode_check accepted.
+static int decode_launch(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
+                         uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
+                         uint64_t out, const int* tail_dev, bool given, int groups, int H, int T, int64_t row_words,
+                         int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream, unsigned* err, int64_t limit) {
   const int S = decode_splits(groups);
-  if (S > resident_workgroups()) return kBadSize;  // a group's workgroups must be resident together
   const DecodeWorkLayout L(groups, S);
   char* w = reinterpret_cast<char*>(work);
   DecodeArgs a;
@@ -1147,6 +1165,22 @@ static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t b
     else hipLaunchKernelGGL(decode_kernel<8>, grid, block, rows_bytes, s, a);
   }
   return (int)hipGetLastError();
+}
+
+// A decode launch on a caller's workspace of work_bytes bytes, which must
+// hold prismkv_decode_work_bytes(groups, capacity).
+static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
+                       uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
+                       uint64_t out, const int* tail_dev, bool given, int groups, int H, int T, int capacity,
+                       int64_t row_words, int64_t ks, int64_t vs, int64_t ids_stride, size_t work_bytes,
+                       uint64_t stream, int64_t limit = -1) {
+  if (groups < 1 || groups > 65535) return kBadSize;
+  if (work_bytes < DecodeWorkLayout(groups, decode_splits(groups)).total) return kBadSize;
+  const int rc = decode_check(q, moments, counts, bits, k, v, work, features, valid, raw, ids, count, out, given,
+                              groups, H, T, capacity, row_words, ks, vs, ids_stride, limit);
+  if (rc) return rc;
+  return decode_launch(q, moments, counts, bits, k, v, work, features, valid, raw, ids, count, out, tail_dev, given,
+                       groups, H, T, row_words, ks, vs, ids_stride, stream, nullptr, limit);
 }
 
 // ---- stage 3 over a given id list ---------------------------------------
@@ -1248,14 +1282,18 @@ int prismkv_decode_noalloc(uint64_t q, uint64_t moments, uint64_t counts, uint64
   if (L.walk > kScratchBytes) return kBadSize;  // the workspace of more than 13 groups does not fit
   char* work = scratch_address();
   if (!work) return (int)hipErrorInvalidSymbol;
+  // every check before the clear: a rejected call enqueues nothing
+  int rc = decode_check(q, moments, counts, bits, k, v, reinterpret_cast<uint64_t>(work), features, valid, raw, ids,
+                        count, out, false, groups, H, T, capacity, row_words, ks, vs, ids_stride, -1);
+  if (rc) return rc;
   // a call that gave up may have left published words behind: start from zero
   hipLaunchKernelGGL(clear_words, dim3((unsigned)std::min<size_t>(1024, (L.walk / 16 + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, reinterpret_cast<uint4*>(work), L.walk / 16);
-  const int rc = (int)hipGetLastError();
+  rc = (int)hipGetLastError();
   if (rc) return rc;
-  return decode_impl(q, moments, counts, bits, k, v, reinterpret_cast<uint64_t>(work), features, valid, raw, ids,
-                     count, out, nullptr, false, groups, H, T, capacity, row_words, ks, vs, ids_stride, stream,
-                     reinterpret_cast<unsigned*>(err));
+  return decode_launch(q, moments, counts, bits, k, v, reinterpret_cast<uint64_t>(work), features, valid, raw, ids,
+                       count, out, nullptr, false, groups, H, T, row_words, ks, vs, ids_stride, stream,
+                       reinterpret_cast<unsigned*>(err), -1);
 }
 
 int prismkv_set_spin_limit(int limit) {
@@ -1272,41 +1310,43 @@ uint64_t prismkv_mapped_pointer(uint64_t host) {
 }
 
 size_t prismkv_decode_work_bytes(int groups, int capacity) {
-  if (groups < 1 || capacity < 1) return 0;
+  if (groups < 1 || groups > 65535 || capacity < 1) return 0;
   return DecodeWorkLayout(groups, decode_splits(groups)).total;
 }
 
 int prismkv_decode(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
                    uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
                    uint64_t out, int groups, int H, int T, int capacity, int64_t row_words, int64_t ks, int64_t vs,
-                   int64_t ids_stride, uint64_t stream) {
+                   int64_t ids_stride, size_t work_bytes, uint64_t stream) {
   return decode_impl(q, moments, counts, bits, k, v, work, features, valid, raw, ids, count, out, nullptr, false, groups,
-                     H, T, capacity, row_words, ks, vs, ids_stride, stream);
+                     H, T, capacity, row_words, ks, vs, ids_stride, work_bytes, stream);
 }
 
 int prismkv_union_attend(uint64_t q, uint64_t bits, uint64_t k, uint64_t v, uint64_t work, uint64_t features,
                          uint64_t valid, uint64_t ids, uint64_t count, uint64_t out, int groups, int H, int T,
-                         int capacity, int64_t row_words, int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream) {
+                         int capacity, int64_t row_words, int64_t ks, int64_t vs, int64_t ids_stride,
+                         size_t work_bytes, uint64_t stream) {
   return decode_impl(q, 0, 0, bits, k, v, work, features, valid, 0, ids, count, out, nullptr, true, groups, H, T,
-                     capacity, row_words, ks, vs, ids_stride, stream);
+                     capacity, row_words, ks, vs, ids_stride, work_bytes, stream);
 }
 
 int prismkv_union_attend_tail(uint64_t q, uint64_t bits, uint64_t k, uint64_t v, uint64_t work, uint64_t features,
                               uint64_t valid, uint64_t ids, uint64_t count, uint64_t out, uint64_t tail, int groups, int H,
                               int max_tail, int capacity, int64_t row_words, int64_t ks, int64_t vs, int64_t ids_stride,
-                              uint64_t stream) {
+                              size_t work_bytes, uint64_t stream) {
   if (!tail || tail % 4) return kBadSize;
   return decode_impl(q, 0, 0, bits, k, v, work, features, valid, 0, ids, count, out, reinterpret_cast<const int*>(tail),
-                     true, groups, H, max_tail, capacity, row_words, ks, vs, ids_stride, stream);
+                     true, groups, H, max_tail, capacity, row_words, ks, vs, ids_stride, work_bytes, stream);
 }
 
 int prismkv_route_single(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
-                         uint64_t valid, uint64_t raw, int groups, uint64_t stream) {
+                         uint64_t valid, uint64_t raw, int groups, size_t work_bytes, uint64_t stream) {
   if (groups < 1 || groups > 65535) return kBadSize;
   if (!q || !moments || !counts || !work || !features || !valid || !raw) return kBadSize;
   const int S = decode_splits(groups);
-  if (S > resident_workgroups()) return kBadSize;  // a group's workgroups must be resident together
   const DecodeWorkLayout L(groups, S);
+  if (work_bytes < L.total) return kBadSize;  // prismkv_decode_work_bytes(groups, .)
+  if (S > resident_workgroups()) return kBadSize;  // a group's workgroups must be resident together
   char* w = reinterpret_cast<char*>(work);
   DecodeArgs a{};  // no bitmap, K/V, ids or split states: phases 1-4 only
   a.q = reinterpret_cast<const uint16_t*>(q);
@@ -1336,31 +1376,31 @@ int prismkv_route_single(uint64_t q, uint64_t moments, uint64_t counts, uint64_t
 int prismkv_decode_tail(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
                         uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
                         uint64_t out, uint64_t tail, int groups, int H, int max_tail, int capacity, int64_t row_words,
-                        int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream) {
+                        int64_t ks, int64_t vs, int64_t ids_stride, size_t work_bytes, uint64_t stream) {
   if (!tail || tail % 4) return kBadSize;
   return decode_impl(q, moments, counts, bits, k, v, work, features, valid, raw, ids, count, out,
                      reinterpret_cast<const int*>(tail), false, groups, H, max_tail, capacity, row_words, ks, vs,
-                     ids_stride, stream);
+                     ids_stride, work_bytes, stream);
 }
 
 int prismkv_decode_capped(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
                           uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
                           uint64_t out, int groups, int H, int T, int capacity, int64_t limit, int64_t row_words,
-                          int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream) {
+                          int64_t ks, int64_t vs, int64_t ids_stride, size_t work_bytes, uint64_t stream) {
   if (limit < 0) return kBadSize;
   return decode_impl(q, moments, counts, bits, k, v, work, features, valid, raw, ids, count, out, nullptr, false, groups,
-                     H, T, capacity, row_words, ks, vs, ids_stride, stream, nullptr, limit);
+                     H, T, capacity, row_words, ks, vs, ids_stride, work_bytes, stream, limit);
 }
 
 int prismkv_decode_capped_tail(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
                                uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids,
                                uint64_t count, uint64_t out, uint64_t tail, int groups, int H, int max_tail,
                                int capacity, int64_t limit, int64_t row_words, int64_t ks, int64_t vs,
-                               int64_t ids_stride, uint64_t stream) {
+                               int64_t ids_stride, size_t work_bytes, uint64_t stream) {
   if (!tail || tail % 4 || limit < 0) return kBadSize;
   return decode_impl(q, moments, counts, bits, k, v, work, features, valid, raw, ids, count, out,
                      reinterpret_cast<const int*>(tail), false, groups, H, max_tail, capacity, row_words, ks, vs,
-                     ids_stride, stream, nullptr, limit);
+                     ids_stride, work_bytes, stream, limit);
 }
 
 }  // extern "C"

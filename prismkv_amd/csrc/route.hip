@@ -366,9 +366,10 @@ size_t prismkv_route_work_bytes(int groups) {
 }
 
 static int route_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
-                      uint64_t valid, uint64_t raw, float* scores, int groups, uint64_t stream) {
+                      uint64_t valid, uint64_t raw, float* scores, int groups, size_t work_bytes, uint64_t stream) {
   if (groups < 1 || groups > 65535) return kBadSize;
   if (!q || !moments || !counts || !work || !features || !valid || !raw) return kBadSize;
+  if (work_bytes < prismkv_route_work_bytes(groups)) return kBadSize;
   char* base = reinterpret_cast<char*>(work);
   RouteWork rw{reinterpret_cast<float*>(base), reinterpret_cast<float*>(base + route_logits_bytes(groups))};
   hipStream_t s = (hipStream_t)stream;
@@ -384,15 +385,16 @@ static int route_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t wo
 }
 
 int prismkv_route(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features, uint64_t valid,
-                  uint64_t raw, int groups, uint64_t stream) {
-  return route_impl(q, moments, counts, work, features, valid, raw, nullptr, groups, stream);
+                  uint64_t raw, int groups, size_t work_bytes, uint64_t stream) {
+  return route_impl(q, moments, counts, work, features, valid, raw, nullptr, groups, work_bytes, stream);
 }
 
 int prismkv_route_scores(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
-                         uint64_t valid, uint64_t raw, uint64_t scores, int groups, uint64_t stream) {
+                         uint64_t valid, uint64_t raw, uint64_t scores, int groups, size_t work_bytes,
+                         uint64_t stream) {
   if (!scores) return kBadSize;
   return route_impl(q, moments, counts, work, features, valid, raw, reinterpret_cast<float*>(scores), groups,
-                    stream);
+                    work_bytes, stream);
 }
 
 size_t prismkv_route_qact_work_bytes(int groups) {
@@ -401,9 +403,11 @@ size_t prismkv_route_qact_work_bytes(int groups) {
 }
 
 int prismkv_route_qact(uint64_t q, uint64_t W, uint64_t b, uint64_t qscale, uint64_t counts, uint64_t work,
-                       uint64_t features, uint64_t valid, uint64_t raw, uint64_t scores, int groups, uint64_t stream) {
+                       uint64_t features, uint64_t valid, uint64_t raw, uint64_t scores, int groups, size_t work_bytes,
+                       uint64_t stream) {
   if (groups < 1 || groups > 65535) return kBadSize;
   if (!q || !W || !b || !qscale || !counts || !work || !features || !valid || !raw || (W & 15u)) return kBadSize;
+  if (work_bytes < prismkv_route_qact_work_bytes(groups)) return kBadSize;
   hipStream_t s = (hipStream_t)stream;
   unsigned long long* cand = reinterpret_cast<unsigned long long*>(work);
   hipLaunchKernelGGL(qact_part_kernel, dim3(kQaParts, groups), dim3(kRT), 0, s, reinterpret_cast<const uint16_t*>(q),

@@ -627,10 +627,12 @@ static void launch_union(const uint32_t* b, int64_t row_words, const int64_t* f,
 }
 
 static int union_impl(uint64_t bits, uint64_t features, uint64_t valid, uint64_t work, uint64_t ids, uint64_t count,
-                      int groups, int H, int64_t row_words, int64_t ids_stride, int width, uint64_t stream) {
+                      int groups, int H, int64_t row_words, int64_t ids_stride, int width, size_t work_bytes,
+                      uint64_t stream) {
   if (groups < 1 || groups > 65535 || H < 1 || H > (1 << 29)) return kBadSize;
   if (row_words < (H + 31) / 32 || ids_stride < H || (width != kTop && width != 64)) return kBadSize;
   if (!bits || !features || !valid || !work || !ids || !count) return kBadSize;
+  if (work_bytes < prismkv_union_work_bytes(groups, H)) return kBadSize;
   const int wpt = union_wpt(H, row_words);
   const int tiles = union_tiles(H, wpt);
   // fixed layout for any H: err word, its host-word slot (bytes 8-15),
@@ -653,13 +655,16 @@ static int union_impl(uint64_t bits, uint64_t features, uint64_t valid, uint64_t
 extern "C" {
 
 int prismkv_union(uint64_t bits, uint64_t features, uint64_t valid, uint64_t work, uint64_t ids, uint64_t count,
-                  int groups, int H, int64_t row_words, int64_t ids_stride, uint64_t stream) {
-  return union_impl(bits, features, valid, work, ids, count, groups, H, row_words, ids_stride, kTop, stream);
+                  int groups, int H, int64_t row_words, int64_t ids_stride, size_t work_bytes, uint64_t stream) {
+  return union_impl(bits, features, valid, work, ids, count, groups, H, row_words, ids_stride, kTop, work_bytes,
+                    stream);
 }
 
 int prismkv_union_n(uint64_t bits, uint64_t features, uint64_t valid, uint64_t work, uint64_t ids, uint64_t count,
-                    int groups, int H, int64_t row_words, int64_t ids_stride, int width, uint64_t stream) {
-  return union_impl(bits, features, valid, work, ids, count, groups, H, row_words, ids_stride, width, stream);
+                    int groups, int H, int64_t row_words, int64_t ids_stride, int width, size_t work_bytes,
+                    uint64_t stream) {
+  return union_impl(bits, features, valid, work, ids, count, groups, H, row_words, ids_stride, width, work_bytes,
+                    stream);
 }
 
 int prismkv_build_bits(uint64_t ids, uint64_t offsets, uint64_t bits, int groups, int64_t cap, int64_t row_words,

@@ -1025,17 +1025,23 @@ __global__ __launch_bounds__(kUT) void flat_emit_kernel(UpdateArgs a, int64_t* o
 
 using namespace prismkv;
 
+// Work layout (bytes) for `groups` groups and blocks of N keys: the regions
+// that must start at zero (histograms, control words) and the other scratch
+// first, at offsets that depend on the group count only, then the block's
+// activations [groups][N][3000] f32 last.  A workspace sized for the largest
+// block therefore serves every smaller block: no call finds another call's
+// activations where it expects zeroed histograms.
 struct UpdateLayout {
-  size_t act, hist, ctl, tcount, part, list, total;
+  size_t hist, ctl, tcount, part, list, act, total;
   UpdateLayout(int groups, int N) {
     size_t o = 0;
     auto take = [&](size_t n) { const size_t at = o; o += (n + 255) & ~(size_t)255; return at; };
-    act = take((size_t)groups * N * kF * sizeof(float));
     hist = take((size_t)groups * kLevels * kRep * kBins * sizeof(unsigned));
     ctl = take((size_t)groups * kCtl * sizeof(unsigned));
     tcount = take((size_t)groups * kMaxTieBlocks * 2 * sizeof(unsigned));
     part = take((size_t)groups * kCenterParts * kD * sizeof(double));
     list = take((size_t)groups * kListCap * sizeof(uint2));
+    act = take((size_t)groups * N * kF * sizeof(float));
     total = o;
   }
 };
@@ -1095,19 +1101,25 @@ static bool aligned16(uint64_t p, int64_t stride_elems) { return ((p | (uint64_t
 extern "C" {
 
 size_t prismkv_update_work_bytes(int groups, int max_block) {
-  if (groups < 1 || max_block < 1 || max_block > kMaxBlock) return 0;
+  if (groups < 1 || groups > 65535 || max_block < 1 || max_block > kMaxBlock) return 0;
   return UpdateLayout(groups, max_block).total;
+}
+
+size_t prismkv_update_act_offset(int groups) {
+  if (groups < 1 || groups > 65535) return 0;
+  return UpdateLayout(groups, 0).act;
 }
 
 int prismkv_update(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
                    uint64_t counts, uint64_t moments, uint64_t work, int groups, int H, int N, int key_mean,
-                   int64_t ks, int64_t row_words, uint64_t stream) {
+                   int64_t ks, int64_t row_words, size_t work_bytes, uint64_t stream) {
   if (groups < 1 || groups > 65535 || H < 0 || N < 1 || N > kMaxBlock || key_mean < 1 || key_mean > kF)
     return kBadSize;
   if (ks < (int64_t)(H + N) * kD || row_words < (H + N + 31) / 32) return kBadSize;
   if (!k || !W || !b || !center || !scale || !bits || !counts || !moments || !work) return kBadSize;
   if (!aligned16(k, ks) || ((W | b) & 15u)) return kBadSize;
   const UpdateLayout L(groups, N);
+  if (work_bytes < L.total) return kBadSize;  // prismkv_update_work_bytes(groups, N)
   const UpdateArgs a = make_args(k, W, b, center, scale, bits, counts, moments, work, groups, H, N, key_mean, ks,
                                  row_words, L);
   hipStream_t s = (hipStream_t)stream;
@@ -1128,7 +1140,7 @@ size_t prismkv_build_work_bytes(int batch, int H) {
 
 int prismkv_build(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
                   uint64_t counts, uint64_t moments, uint64_t work, int groups, int batch, int H, int key_mean,
-                  int flags, int64_t ks, int64_t row_words, uint64_t stream) {
+                  int flags, int64_t ks, int64_t row_words, size_t work_bytes, uint64_t stream) {
   if (groups < 1 || groups > 65535 || batch < 1 || batch > groups || H < 1 || H > kMaxBuild || key_mean < 1 ||
       key_mean > kF)
     return kBadSize;
@@ -1137,6 +1149,7 @@ int prismkv_build(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t 
   if (!k || !W || !b || !center || !scale || !bits || !counts || !moments || !work) return kBadSize;
   if (!aligned16(k, ks) || ((bits | W | b) & 15u)) return kBadSize;
   const UpdateLayout L(batch, H);
+  if (work_bytes < L.total) return kBadSize;  // prismkv_build_work_bytes(batch, H)
   hipStream_t s = (hipStream_t)stream;
   for (int g0 = 0; g0 < groups; g0 += batch) {
     const int nb = std::min(batch, groups - g0);
@@ -1164,10 +1177,11 @@ int prismkv_build(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t 
 size_t prismkv_topk_work_bytes(void) { return UpdateLayout(1, 0).total; }
 
 int prismkv_topk(uint64_t act, uint64_t out, uint64_t out_len, uint64_t work, int N, int64_t count,
-                 uint64_t stream) {
+                 size_t work_bytes, uint64_t stream) {
   if (N < 1 || N > kMaxBuild || count < 0) return kBadSize;
   if (!act || !out || !out_len || !work || (act & 15u)) return kBadSize;
   const UpdateLayout L(1, 0);
+  if (work_bytes < L.total) return kBadSize;  // prismkv_topk_work_bytes()
   const int64_t n = (int64_t)N * kF;
   UpdateArgs a = make_args(0, 0, 0, 0, 0, 0, 0, 0, work, 1, 0, N, 1, 0, 0, L);
   a.act = reinterpret_cast<float*>(act);  // read only here
@@ -1192,12 +1206,14 @@ size_t prismkv_summarize_work_bytes(int groups) {
 }
 
 int prismkv_summarize(uint64_t k, uint64_t bits, uint64_t center, uint64_t counts, uint64_t moments, uint64_t work,
-                      int groups, int H, int flags, int64_t ks, int64_t row_words, uint64_t stream) {
+                      int groups, int H, int flags, int64_t ks, int64_t row_words, size_t work_bytes,
+                      uint64_t stream) {
   if (groups < 1 || groups > 65535 || H < 1 || H > kMaxBuild) return kBadSize;
   if (flags & ~kBuildCenter) return kBadMode;
   if (ks < (int64_t)H * kD || row_words < (H + 31) / 32) return kBadSize;
   if (!k || !bits || !center || !counts || !moments || !work || !aligned16(k, ks)) return kBadSize;
   const UpdateLayout L(groups, 0);
+  if (work_bytes < L.total) return kBadSize;  // prismkv_summarize_work_bytes(groups)
   const UpdateArgs a = make_args(k, 0, 0, center, 0, bits, counts, moments, work, groups, 0, H, 1, ks, row_words, L);
   hipStream_t s = (hipStream_t)stream;
   if (flags & kBuildCenter) {

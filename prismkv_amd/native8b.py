@@ -64,6 +64,11 @@ BUILD_WORK_LIMIT = 8 << 30
 ATTEND_SPLITS = 32
 CHUNK = 32
 CHUNKS = (FEATURES + CHUNK - 1) // CHUNK
+# Codes of a workspace's error word (and the host-mapped word), as the kernels write them.
+ERR_WAIT, ERR_IDS = 1, 2
+ERROR_MESSAGES = {ERR_WAIT: "prismkv decode: a bounded inter-workgroup wait gave up",
+                  ERR_IDS: "prismkv attention: an id outside [0, history) or a count outside [0, history] "
+                           "reached the attention"}
 PADDED = CHUNKS * CHUNK
 
 
@@ -210,7 +215,7 @@ class Native8B:
             obj.lib.call("prismkv_build", k.data_ptr(), obj.W_enc.data_ptr(), obj.b_enc.data_ptr(),
                          obj.center.data_ptr(), obj.key_scale.data_ptr(), obj.bits.data_ptr(), obj.n.data_ptr(),
                          obj.moments.data_ptr(), work.data_ptr(), GROUPS, batch, history, obj.key_mean, flags,
-                         k.stride(0), obj.row_words, stream=obj._stream())
+                         k.stride(0), obj.row_words, _lib.nbytes(work), stream=obj._stream())
             obj.build_work = work if keep_activations else None
             obj.build_batch = batch
         obj.unique_cap = unique_cap
@@ -232,7 +237,8 @@ class Native8B:
         if getattr(self, "build_work", None) is None:
             raise ValueError("build with keep_activations=True first")
         n = self.build_batch * self.history * FEATURES
-        return self.build_work[:4 * n].view(torch.float32).view(self.build_batch, self.history, FEATURES)
+        at = self.lib.query("prismkv_update_act_offset", self.build_batch)
+        return self.build_work[at:at + 4 * n].view(torch.float32).view(self.build_batch, self.history, FEATURES)
 
     def _setup(self, h, capacity, library, counts, mean, variance, csr, offsets, center=None):
         if csr.numel() and (int(csr.max()) >= h or int(csr.min()) < 0):
@@ -298,16 +304,20 @@ class Native8B:
             work[8:16].view(torch.int64).fill_(self._err_device_address)
 
     def check_errors(self):
-        """Raise RuntimeError if a bounded inter-workgroup wait of an earlier
-        launch gave up (its results are invalid).  Reads the host-mapped error
-        word, so it neither synchronises nor sees launches that have not run
-        yet; on an error the device is synchronised, every workspace is
-        zeroed (a late workgroup may have left published words behind) and the
-        error words are cleared before raising."""
-        if int(self._err_host[0]) == 0:
+        """Raise RuntimeError if an earlier launch reported an error: a
+        bounded inter-workgroup wait gave up, or the attention found an id
+        outside [0, history) in `ids` (or a count outside [0, history]) and
+        read it clamped.  Either way the results of the launches since the
+        last check are invalid.  Reads the host-mapped error word, so it
+        neither synchronises nor sees launches that have not run yet; on an
+        error the device is synchronised, every workspace is zeroed (a late
+        workgroup may have left published words behind) and the error words
+        are cleared before raising."""
+        code = int(self._err_host[0])
+        if code == 0:
             return
         self.reset_workspaces()
-        raise RuntimeError("prismkv decode: a bounded inter-workgroup wait gave up; the results of the launches "
+        raise RuntimeError(ERROR_MESSAGES.get(code, ERROR_MESSAGES[ERR_WAIT]) + "; the results of the launches "
                            "since the last check are invalid (the workspaces have been reset)")
 
     def reset_workspaces(self):
@@ -336,7 +346,7 @@ class Native8B:
         width = self._select(q)
         self.lib.call("prismkv_union_n", self.bits.data_ptr(), self.features.data_ptr(), self.valid.data_ptr(),
                       self.union_work.data_ptr(), self.ids.data_ptr(), self.count.data_ptr(), GROUPS, self.history,
-                      self.row_words, self.capacity, width, stream=self._stream())
+                      self.row_words, self.capacity, width, _lib.nbytes(self.union_work), stream=self._stream())
 
     def _select(self, q):
         """Stage 1 and the optional strict unique cap: features / valid / raw.
@@ -349,12 +359,13 @@ class Native8B:
         if self.router == "q_activation":
             self.lib.call("prismkv_route_qact", q.data_ptr(), self.W_query.data_ptr(), self.b_query.data_ptr(),
                           self.query_scale.data_ptr(), self.n.data_ptr(), self.qact_work.data_ptr(),
-                          self.features.data_ptr(), self.valid.data_ptr(), self.raw.data_ptr(), 0, GROUPS, stream=s)
+                          self.features.data_ptr(), self.valid.data_ptr(), self.raw.data_ptr(), 0, GROUPS,
+                          _lib.nbytes(self.qact_work), stream=s)
         else:
             # one launch: the selection phases of the decode, on its workspace
             self.lib.call("prismkv_route_single", q.data_ptr(), self.moments.data_ptr(), self.n.data_ptr(),
                           self.decode_work.data_ptr(), self.features.data_ptr(), self.valid.data_ptr(),
-                          self.raw.data_ptr(), GROUPS, stream=s)
+                          self.raw.data_ptr(), GROUPS, _lib.nbytes(self.decode_work), stream=s)
         width = self.features.shape[1]
         if self.unique_cap is not None:
             self.lib.call("prismkv_select_cap_n", self.bits.data_ptr(), self.n.data_ptr(), self.features.data_ptr(),
@@ -430,7 +441,7 @@ class Native8B:
         self.lib.call("prismkv_attend", q.data_ptr(), k.data_ptr(), v.data_ptr(), self.ids.data_ptr(),
                       self.count.data_ptr(), self.state.data_ptr(), self.out.data_ptr(), GROUPS, self.history,
                       k.shape[1] - self.history, k.stride(0), v.stride(0), self.capacity, ATTEND_SPLITS,
-                      stream=self._stream())
+                      _lib.nbytes(self.state), stream=self._stream())
         return self.out
 
     def __call__(self, q, k, v, *, tail=None, **kwargs):
@@ -465,14 +476,14 @@ class Native8B:
                               self.raw.data_ptr(), self.ids.data_ptr(), self.count.data_ptr(), self.out.data_ptr(),
                               tail.data_ptr(), GROUPS, self.history, k.shape[1] - self.history, self.capacity,
                               self._cap_limit(), self.row_words, k.stride(0), v.stride(0), self.capacity,
-                              stream=self._stream())
+                              _lib.nbytes(self.decode_work), stream=self._stream())
                 return self.out
             self.lib.call("prismkv_decode_tail", q.data_ptr(), self.moments.data_ptr(), self.n.data_ptr(),
                           self.bits.data_ptr(), k.data_ptr(), v.data_ptr(), self.decode_work.data_ptr(),
                           self.features.data_ptr(), self.valid.data_ptr(), self.raw.data_ptr(), self.ids.data_ptr(),
                           self.count.data_ptr(), self.out.data_ptr(), tail.data_ptr(), GROUPS, self.history,
                           k.shape[1] - self.history, self.capacity, self.row_words, k.stride(0), v.stride(0),
-                          self.capacity, stream=self._stream())
+                          self.capacity, _lib.nbytes(self.decode_work), stream=self._stream())
             return self.out
         if self.history > FUSED_MAX_HISTORY or self.router != "moments":
             # very long histories exceed one launch's group size; the q_activation
@@ -486,13 +497,14 @@ class Native8B:
                           self.features.data_ptr(), self.valid.data_ptr(), self.raw.data_ptr(), self.ids.data_ptr(),
                           self.count.data_ptr(), self.out.data_ptr(), GROUPS, self.history,
                           k.shape[1] - self.history, self.capacity, self._cap_limit(), self.row_words, k.stride(0),
-                          v.stride(0), self.capacity, stream=self._stream())
+                          v.stride(0), self.capacity, _lib.nbytes(self.decode_work), stream=self._stream())
             return self.out
         self.lib.call("prismkv_decode", q.data_ptr(), self.moments.data_ptr(), self.n.data_ptr(), self.bits.data_ptr(),
                       k.data_ptr(), v.data_ptr(), self.decode_work.data_ptr(), self.features.data_ptr(),
                       self.valid.data_ptr(), self.raw.data_ptr(), self.ids.data_ptr(), self.count.data_ptr(),
                       self.out.data_ptr(), GROUPS, self.history, k.shape[1] - self.history, self.capacity,
-                      self.row_words, k.stride(0), v.stride(0), self.capacity, stream=self._stream())
+                      self.row_words, k.stride(0), v.stride(0), self.capacity, _lib.nbytes(self.decode_work),
+                      stream=self._stream())
         return self.out
 
     # ------------------------------------------------------------ stage 4
@@ -549,7 +561,8 @@ class Native8B:
         self.lib.call("prismkv_update", k.data_ptr(), self.W_enc.data_ptr(), self.b_enc.data_ptr(),
                       self.center.data_ptr(), self.key_scale.data_ptr(), self.bits.data_ptr(), self.n.data_ptr(),
                       self.moments.data_ptr(), self.update_work.data_ptr(), GROUPS, self.history, block,
-                      self.key_mean, k.stride(0), self.row_words, stream=self._stream())
+                      self.key_mean, k.stride(0), self.row_words, _lib.nbytes(self.update_work),
+                      stream=self._stream())
         self.history += block
 
     def update_activations(self, block):
@@ -558,7 +571,8 @@ class Native8B:
         if self.update_work is None or not 1 <= block <= self.update_block:
             raise ValueError("no append with this block size")
         n = GROUPS * block * FEATURES
-        return self.update_work[:4 * n].view(torch.float32).view(GROUPS, block, FEATURES)
+        at = self.lib.query("prismkv_update_act_offset", GROUPS)
+        return self.update_work[at:at + 4 * n].view(torch.float32).view(GROUPS, block, FEATURES)
 
     def catch_up(self, k, total=None, update_interval=MAX_BLOCK):
         """Index complete old tail blocks while more than `update_interval`

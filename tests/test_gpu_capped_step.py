@@ -16,6 +16,7 @@ import torch
 
 import oracle
 from oracle import cases, expect
+from prismkv_amd._lib import nbytes
 from tests.gpu_util import bf16_bits, log, route_outputs
 
 pytestmark = pytest.mark.gpu
@@ -93,7 +94,7 @@ def test_capped_step_graph_36_layers():
         groups = expect.expected(case)
         op.lib.call("prismkv_route_single", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(),
                     op.decode_work.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(), op.raw.data_ptr(), 8,
-                    stream=torch.cuda.current_stream().cuda_stream)
+                    nbytes(op.decode_work), stream=torch.cuda.current_stream().cuda_stream)
         features, valid, raw, _, _ = route_outputs(op)
         for g in range(8):  # the ranked order, before the walk, is the oracle's
             n = len(groups[g]["order"])

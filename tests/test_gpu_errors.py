@@ -127,3 +127,72 @@ def test_core_attend_give_up_raises():
     assert raised
     out = core.attend(q[0], k[0], v[0], ids, 2048)
     assert torch.isfinite(out.float()).all()
+
+
+def test_undersized_workspace_is_refused_before_any_launch():
+    # a workspace one byte short of prismkv_decode_work_bytes (e.g. one sized
+    # under an older layout) is refused with -1 by every decode variant and
+    # nothing is enqueued: the outputs keep the sentinel written before
+    from prismkv_amd._lib import nbytes
+    case = cases.native_case(2048, 16, "random", seed=17)
+    op, q, k, v = operator(case)
+    out = op(q, k, v).clone()
+    torch.cuda.synchronize()
+    short = nbytes(op.decode_work) - 1
+    s = torch.cuda.current_stream().cuda_stream
+    tail = torch.tensor([16], dtype=torch.int32, device="cuda")
+    T = k.shape[1] - op.history
+    common = (op.row_words, k.stride(0), v.stride(0), op.capacity, short)
+    head = (q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(), op.bits.data_ptr(), k.data_ptr(), v.data_ptr(),
+            op.decode_work.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(), op.raw.data_ptr(),
+            op.ids.data_ptr(), op.count.data_ptr(), op.out.data_ptr())
+    given = (q.data_ptr(), op.bits.data_ptr(), k.data_ptr(), v.data_ptr(), op.decode_work.data_ptr(),
+             op.features.data_ptr(), op.valid.data_ptr(), op.ids.data_ptr(), op.count.data_ptr(), op.out.data_ptr())
+    calls = {
+        "prismkv_decode": (*head, 8, op.history, T, op.capacity, *common),
+        "prismkv_decode_tail": (*head, tail.data_ptr(), 8, op.history, T, op.capacity, *common),
+        "prismkv_decode_capped": (*head, 8, op.history, T, op.capacity, 100, *common),
+        "prismkv_decode_capped_tail": (*head, tail.data_ptr(), 8, op.history, T, op.capacity, 100, *common),
+        "prismkv_union_attend": (*given, 8, op.history, T, op.capacity, *common),
+        "prismkv_union_attend_tail": (*given, tail.data_ptr(), 8, op.history, T, op.capacity, *common),
+        "prismkv_route_single": (*head[:3], op.decode_work.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(),
+                                 op.raw.data_ptr(), 8, short),
+    }
+    for name, args in calls.items():
+        op.out.fill_(7.0)
+        op.count.fill_(-5)
+        op.features.fill_(-3)
+        torch.cuda.synchronize()
+        assert getattr(op.lib.cdll, name)(*args, s) == -1, name
+        torch.cuda.synchronize()
+        assert bool((op.out == 7.0).all()) and bool((op.count == -5).all()) and bool((op.features == -3).all()), name
+    log(f"  refused without a launch: {sorted(calls)}")
+    assert torch.equal(op(q, k, v), out)
+    assert op.decode_errors() == 0
+
+
+def test_attention_reports_ids_out_of_range():
+    # Native8B.attention reads `ids` / `count` as route() left them; an id
+    # outside [0, history) (or a count outside [0, history]) is read clamped,
+    # so every access stays in range, and the error word makes the next check
+    # raise instead of returning a plausible but wrong output
+    case = cases.native_case(4096, 40, "random", seed=23)
+    op, q, k, v = operator(case)
+    op.route(q)
+    good = op.attention(q, k, v).clone()
+    torch.cuda.synchronize()
+    assert op.decode_errors() == 0
+    for what in ("id", "count"):
+        op.route(q)
+        if what == "id":
+            op.ids[3, 0] = op.history + 5
+        else:
+            op.count[5] = op.history + 1
+        op.attention(q, k, v)
+        torch.cuda.synchronize()
+        with pytest.raises(RuntimeError, match="outside"):
+            op.check_errors()
+        log(f"  {what} out of range: reported")
+    op.route(q)
+    assert torch.equal(op.attention(q, k, v), good)
+    assert op.decode_errors() == 0

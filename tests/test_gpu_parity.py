@@ -10,6 +10,7 @@ import torch
 
 import oracle
 from oracle import cases, expect
+from prismkv_amd._lib import nbytes
 from tests.gpu_util import bf16_bits, device_layer, log, operator, route_outputs
 
 pytestmark = pytest.mark.gpu
@@ -205,12 +206,12 @@ def test_single_launch_route_matches_three_launch_route(H):
 
     def three():
         lib.call("prismkv_route", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(), work.data_ptr(),
-                 op.features.data_ptr(), op.valid.data_ptr(), op.raw.data_ptr(), 8, stream=s)
+                 op.features.data_ptr(), op.valid.data_ptr(), op.raw.data_ptr(), 8, nbytes(work), stream=s)
 
     def one():
         lib.call("prismkv_route_single", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(),
                  op.decode_work.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(), op.raw.data_ptr(), 8,
-                 stream=s)
+                 nbytes(op.decode_work), stream=s)
 
     def selection():
         torch.cuda.synchronize()
@@ -309,13 +310,13 @@ def three_launch_capped(op, q, k, v, groups=8, work=None):
     s = torch.cuda.current_stream().cuda_stream
     work = op.decode_work if work is None else work
     op.lib.call("prismkv_route_single", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(), work.data_ptr(),
-                op.features.data_ptr(), op.valid.data_ptr(), op.raw.data_ptr(), groups, stream=s)
+                op.features.data_ptr(), op.valid.data_ptr(), op.raw.data_ptr(), groups, nbytes(work), stream=s)
     op.lib.call("prismkv_select_cap", op.bits.data_ptr(), op.n.data_ptr(), op.features.data_ptr(),
                 op.valid.data_ptr(), op.raw.data_ptr(), groups, op.history, op._cap_limit(), op.row_words, stream=s)
     op.lib.call("prismkv_union_attend", q.data_ptr(), op.bits.data_ptr(), k.data_ptr(), v.data_ptr(),
                 work.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(), op.ids.data_ptr(),
                 op.count.data_ptr(), op.out.data_ptr(), groups, op.history, k.shape[1] - op.history, op.capacity,
-                op.row_words, k.stride(0), v.stride(0), op.capacity, stream=s)
+                op.row_words, k.stride(0), v.stride(0), op.capacity, nbytes(work), stream=s)
     torch.cuda.synchronize()
     return bf16_bits(op.out).copy()
 
@@ -402,7 +403,7 @@ def test_capped_decode_groups(groups):
                     op.bits.data_ptr(), k.data_ptr(), v.data_ptr(), work.data_ptr(), op.features.data_ptr(),
                     op.valid.data_ptr(), op.raw.data_ptr(), op.ids.data_ptr(), op.count.data_ptr(),
                     op.out.data_ptr(), groups, op.history, k.shape[1] - op.history, op.capacity, op._cap_limit(),
-                    op.row_words, k.stride(0), v.stride(0), op.capacity, stream=s)
+                    op.row_words, k.stride(0), v.stride(0), op.capacity, nbytes(work), stream=s)
         torch.cuda.synchronize()
         assert int(work[:4].view(torch.int32)[0]) == 0  # no bounded wait gave up
         got = (op.features, op.valid, op.raw, op.ids, op.count)
@@ -437,7 +438,7 @@ def test_fused_decode_fewer_groups(groups):
     op.lib.call("prismkv_decode", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(), op.bits.data_ptr(),
                 k.data_ptr(), v.data_ptr(), work.data_ptr(), feats.data_ptr(), valid.data_ptr(), raw.data_ptr(),
                 ids.data_ptr(), count.data_ptr(), out.data_ptr(), groups, op.history, k.shape[1] - op.history,
-                op.capacity, op.row_words, k.stride(0), v.stride(0), op.capacity,
+                op.capacity, op.row_words, k.stride(0), v.stride(0), op.capacity, nbytes(work),
                 stream=torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
     assert int(work[:4].view(torch.int32)[0]) == 0  # no bounded wait gave up

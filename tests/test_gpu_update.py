@@ -188,3 +188,30 @@ def test_catch_up_two_blocks():
             assert np.array_equal(got[g].counts.cpu().numpy(), idx.counts)
             assert np.allclose(got[g].mean.cpu().numpy(), idx.mean, rtol=1e-4, atol=1e-4)
             assert np.allclose(got[g].variance.cpu().numpy(), idx.variance, rtol=1e-4, atol=1e-4)
+
+
+def test_append_smaller_block_after_larger():
+    # one workspace serves blocks of different sizes (the zeroed histograms
+    # and control words sit at offsets that do not move with the block size):
+    # a 256-key block, then a 37-key block, each against the oracle
+    from prismkv_amd import Native8B
+    H, N1, N2, T = 700, 256, 37, 3
+    case = cases.update_case("random", H=H, N=N1 + N2, T=T, seed=57)
+    op = Native8B(device_indices(case), capacity=H + N1 + N2 + T)
+    op.set_encoder_tables(torch.from_numpy(case["W"]), torch.from_numpy(case["b"]), torch.from_numpy(case["scale"]),
+                          case["key_mean"])
+    k = bf16_tensor(case["k"])
+    op.append(k, N1)
+    torch.cuda.synchronize()
+    mid = [oracle.Index(H + N1, i.center.cpu().numpy(), i.counts.cpu().numpy(), i.mean.cpu().numpy(),
+                        i.variance.cpu().numpy(), [l.numpy() for l in i.lists]) for i in op.export_indices()]
+    op.append(k, N2)
+    torch.cuda.synchronize()
+    assert op.history == H + N1 + N2
+    act = op.update_activations(N2).cpu().numpy()
+    got = op.export_indices()
+    case2 = dict(case, H=H + N1, N=N2, indices=mid)
+    for g in range(8):
+        sel, moved, err = check_group(case2, g, act[g], got[g])
+        log(f"  group {g}: second block selected={sel} moved_at_tau={moved} act_err={err:.2e}")
+        assert sel == N2 * case["key_mean"]

@@ -17,8 +17,9 @@ from tests.gpu_util import log, operator
 pytestmark = pytest.mark.gpu
 
 
-def _noalloc(op, q, k, v, groups=8):
+def _noalloc(op, q, k, v, groups=8, history=None):
     """prismkv_decode_noalloc into fresh output buffers; returns them and the error word."""
+    history = op.history if history is None else history
     dev = q.device
     out = dict(features=torch.zeros(groups, 16, dtype=torch.int64, device=dev),
                valid=torch.zeros(groups, 16, device=dev), raw=torch.zeros(groups, dtype=torch.int32, device=dev),
@@ -29,8 +30,8 @@ def _noalloc(op, q, k, v, groups=8):
     rc = op.lib.cdll.prismkv_decode_noalloc(
         q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(), op.bits.data_ptr(), k.data_ptr(), v.data_ptr(),
         out["features"].data_ptr(), out["valid"].data_ptr(), out["raw"].data_ptr(), out["ids"].data_ptr(),
-        out["count"].data_ptr(), out["out"].data_ptr(), out["err"].data_ptr(), groups, op.history,
-        k.shape[1] - op.history, op.capacity, op.row_words, k.stride(0), v.stride(0), op.capacity,
+        out["count"].data_ptr(), out["out"].data_ptr(), out["err"].data_ptr(), groups, history,
+        k.shape[1] - history, op.capacity, op.row_words, k.stride(0), v.stride(0), op.capacity,
         torch.cuda.current_stream().cuda_stream)
     return rc, out
 
@@ -68,3 +69,12 @@ def test_noalloc_rejects_too_many_groups():
     op, q, k, v = operator(case)
     rc, _ = _noalloc(op, q, k, v, groups=14)  # the workspace of 14 groups exceeds the 1 MiB array
     assert rc == -1
+    # a history the decode cannot take is refused by the same host checks as
+    # prismkv_decode's, before the array is cleared: nothing is enqueued, and
+    # the next call still matches prismkv_decode
+    for bad in (0, op.capacity + 1):
+        rc, got = _noalloc(op, q, k, v, history=bad)
+        torch.cuda.synchronize()
+        assert rc == -1, bad
+        assert int(got["count"].abs().sum()) == 0 and int(got["err"].item()) == 0
+    _compare(op, q, k, v)
