@@ -48,6 +48,14 @@ __device__ __forceinline__ uint4 load_nt16_buf(__amdgpu_buffer_rsrc_t r, unsigne
   const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, byte_offset, 0, 2);
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+// 4-byte streaming load through a raw buffer resource.
+__device__ __forceinline__ uint32_t load_nt4_buf(__amdgpu_buffer_rsrc_t r, unsigned byte_offset) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, byte_offset, 0, 2);
+}
+// A raw buffer resource over [base, base + bytes).  Reads past `bytes` return
+// 0 without a memory access, so a resource of 0 bytes turns a load into a
+// no-op that still counts as issued (kernels use this to keep a load sequence
+// unconditional, so the compiler's wait counts stay exact).
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_buffer(const void* base, int bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
 }

@@ -83,6 +83,7 @@ constexpr unsigned kReady = 1u << 31;
 constexpr int kSlices = 4;                    // 32-dim slices of a head's output
 constexpr int kSliceW = 2 + kD / kSlices;     // {max, den, acc[32]} per (split, head, slice)
 constexpr int kMergers = kHq * kSlices;       // workgroups 0..15 each merge one (head, slice)
+constexpr int kEarlyRows = 16 * (kAT / 64);   // early tail rows per workgroup: one 16-row block per wave
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -336,9 +337,22 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int g, int h, i
 // lds.cover[w]; the union loads only the winners no wave prefetched.
 // Without kPrefetchRows (the route-only and the capped launch) nothing is
 // prefetched.
+//
+// `early` lets the fused decode request its early tail rows here (phase 6
+// consumes them): prepare() once the candidates have landed, issue() after
+// the barrier that follows the bitmap-word requests -- so every wave's words
+// are ahead of every wave's tail rows in the CU's memory queue and the
+// selection never waits for the tail -- and wait_words() before the words
+// are used (a wait that leaves the tail rows in flight).
 constexpr int kPrefetch = 6;
-template <int KW, bool kPrefetchRows = true>
-__device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, DecodeLds& lds) {
+struct NoEarly {
+  __device__ void prepare() {}
+  __device__ void barrier() { __syncthreads(); }
+  __device__ void issue() {}
+  __device__ void wait_words() const {}
+};
+template <int KW, bool kPrefetchRows = true, class Early = NoEarly>
+__device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, DecodeLds& lds, Early& early) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int nk = a.S * kTop;
   const unsigned long long* cg = a.cand + (size_t)g * a.S * kTop;
@@ -353,21 +367,28 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, D
     }, a);
     v[k] = i < nk ? ~r : 0ull;
   }
+  early.prepare();
   const unsigned long long best = sorted_rows_top16<KW>(v);
   if (lane < kTop) lds.sel.best[kTop * w + lane] = best;
   if (threadIdx.x < kTop) lds.win[threadIdx.x] = 0ull;  // ranks no key fills stay empty
   const int nw = (a.H + 31) / 32;
   const int wd = p * a.tw + lane;
   const bool word = lane < a.tw && wd < nw;
-  const uint32_t* gb = a.bits + (size_t)g * kF * a.row_words + min(wd, nw - 1);
   unsigned long long pk[kPrefetch];
   uint32_t pw[kPrefetch];
 #pragma unroll
   for (int r = 0; r < kPrefetch; ++r) {
     pk[r] = readlane_u64(best, r);  // rank r of this wave's list (uniform)
-    pw[r] = (kPrefetchRows && pk[r]) ? __builtin_nontemporal_load(gb + (size_t)row_of(pk[r]) * a.row_words) : 0u;
+    pw[r] = 0u;
+    if constexpr (kPrefetchRows) {
+      // every rank issues its load (an empty key's through an empty resource),
+      // so the loads after these are counted exactly when pw is waited for
+      const uint32_t* row = a.bits + ((size_t)g * kF + row_of(pk[r])) * a.row_words;
+      pw[r] = load_nt4_buf(raw_buffer(row, pk[r] ? (int)a.row_words * 4 : 0), (unsigned)min(wd, nw - 1) * 4u);
+    }
   }
-  __syncthreads();
+  early.barrier();
+  early.issue();
   constexpr int kListed = kDT / 64 * kTop;  // 128
   if (threadIdx.x < kListed) {
     const unsigned long long x = lds.sel.best[threadIdx.x];
@@ -392,6 +413,7 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, D
   const unsigned long long last = need ? readlane_u64(win, need - 1) : ~0ull;
   uint32_t part = 0u;
   unsigned covered = 0u;
+  early.wait_words();
 #pragma unroll
   for (int r = 0; r < kPrefetch; ++r)
     if (pk[r] != 0ull && pk[r] >= last) {  // uniform
@@ -410,8 +432,8 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, D
 // Phases 1-4: the group's Top-16 (rank order) into lds.win (every wave) and
 // lds.sel_rows / lds.need.  Without kUnion only workgroup 0 runs phase 4;
 // kPrefetchRows requests the union's bitmap words in phase 4.
-template <int KW, bool kUnion = true, bool kPrefetchRows = kUnion>
-__device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p, DecodeLds& lds) {
+template <int KW, bool kUnion = true, bool kPrefetchRows = kUnion, class Early = NoEarly>
+__device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p, DecodeLds& lds, Early& early) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int S = a.S;
   // moment tiles kper * p + j, j < own: contiguous 32 KB tiles, one stream per workgroup
@@ -490,7 +512,12 @@ __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p,
   if constexpr (!kUnion) {
     if (p != 0) return;
   }
-  final_top16<KW, kUnion && kPrefetchRows>(a, g, p, lds);
+  final_top16<KW, kUnion && kPrefetchRows>(a, g, p, lds, early);
+}
+template <int KW, bool kUnion = true, bool kPrefetchRows = kUnion>
+__device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p, DecodeLds& lds) {
+  NoEarly none;
+  decode_select<KW, kUnion, kPrefetchRows>(a, g, p, lds, none);
 }
 
 // ---- 4b. (capped launch) the strict unique cap's budgeted walk over the
@@ -628,7 +655,50 @@ __device__ __forceinline__ uint32_t capped_walk(const DecodeArgs& a, int g, int 
 // a strict unique cap leaves them) and phases 5-9 run on it.  With kCap the
 // strict unique cap's walk (phase 4b) runs between the selection and the
 // union, on the same launch.
-template <int KW, bool kGiven = false, bool kCap = false>
+// The early tail request of the fused decode: wave w's 16-row block of the
+// workgroup's tail rows, [t_lo + 16 w, t_lo + 16 w + 16) clipped to its share
+// [t_lo, t_hi), into ek / ev in the MFMA operand layouts of mfma_blocks16.
+// prepare() derives the rows from the tail word (long landed by then);
+// issue() requests them: 8 loads in every wave, through empty resources
+// for a wave without early rows.  A load costs its CU issue time even then,
+// so the host takes this kernel only for tails that give most waves a block.
+struct EarlyTail {
+  const DecodeArgs& a;
+  int g, p, tail_word;
+  int& n;  // this wave's early rows (uniform), for phase 6
+  uint4 (&ek)[1][4];
+  uint4 (&ev)[1][4];
+  int r0 = 0, T = 0;
+  __device__ void prepare() {
+    T = a.tail_dev ? min(max(tail_word, 0), a.T) : a.T;
+    const int per = (T + a.S - 1) / a.S;
+    const int lo = min(T, p * per), hi = min(T, lo + per);
+    const int wu = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+    n = __builtin_amdgcn_readfirstlane(max(0, min(16, hi - (lo + 16 * wu))));
+    r0 = a.H + lo + 16 * wu;  // the K/V row of the block's first row
+  }
+  __device__ void issue() {
+    {  // every wave (an empty resource for a wave without early rows: no memory access)
+      const int lane = threadIdx.x & 63, j = lane & 15, qd = lane >> 4;
+      const int kv_bytes = __builtin_amdgcn_readfirstlane(n > 0 ? (a.H + T) * 2 * kD : 0);
+      const __amdgpu_buffer_rsrc_t kb = raw_buffer(a.k + (size_t)g * a.ks, kv_bytes);
+      const __amdgpu_buffer_rsrc_t vb = raw_buffer(a.v + (size_t)g * a.vs, kv_bytes);
+      const unsigned ko = (unsigned)(r0 + (j < n ? j : 0)) * (2 * kD) + 16 * qd;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) ek[0][c] = load_nt16_buf(kb, ko + 64 * c);
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        ev[0][t] = load_nt16_buf(vb, (unsigned)(r0 + (4 * qd + t < n ? 4 * qd + t : 0)) * (2 * kD) + 16 * j);
+    }
+  }
+  __device__ void barrier() { __syncthreads(); }
+  // Loads complete in order: with at most the 8 early loads outstanding,
+  // everything requested before them (the bitmap words) has landed.  The
+  // explicit wait keeps the compiler from waiting for every load instead.
+  __device__ void wait_words() const { __builtin_amdgcn_s_waitcnt(8 | (0x7 << 4) | (0xf << 8)); }
+};
+
+template <int KW, bool kGiven = false, bool kCap = false, bool kEarlyTail = false>
 __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   const int p = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   __shared__ DecodeLds lds;
@@ -638,6 +708,13 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   // no branch (without a device word the load reads q and is ignored), so
   // it has long landed when the attention first uses it.
   const int tail_word = ld_dev(a.tail_dev ? a.tail_dev : reinterpret_cast<const int*>(a.q));
+  // Early tail (the uncapped decode): each wave's 16-row block of the
+  // workgroup's tail rows is requested in phase 4, behind the bitmap words,
+  // so it streams in while the selection finishes and the union is built
+  // (HBM is otherwise idle then); phase 6 attends it first.
+  constexpr bool kEarly = kEarlyTail && !kGiven && !kCap && !PRISMKV_VALU_ATTENTION;
+  int early_n = 0;
+  uint4 ek[1][4], ev[1][4];
 
   // attention over a given id list: no selection, no union (uniform)
   const bool id_list = kGiven && a.ids_in != nullptr;
@@ -661,11 +738,13 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     if (lane == 0) lds.cover[w] = 0u;
     __syncthreads();
   } else if constexpr (!kCap) {
-    // ---- 1-4. the group's Top-16
-    decode_select<KW>(a, g, p, lds);
-    if (p == 0 && w == 0)
-      write_selection(lds.win, lds.need, a.counts + (size_t)g * kFP, a.features + (size_t)g * kTop,
-                      a.valid + (size_t)g * kTop, a.raw + g);
+    // ---- 1-4. the group's Top-16 (and the early tail rows requested)
+    if constexpr (kEarly) {
+      EarlyTail early{a, g, p, tail_word, early_n, ek, ev};
+      decode_select<KW>(a, g, p, lds, early);
+    } else {
+      decode_select<KW>(a, g, p, lds);
+    }
   }
   // ---- 1-4b. the group's Top-16, then the budgeted walk over it: this
   // thread's word of the kept rows' union, and the kept buckets (in rank
@@ -813,7 +892,9 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   const int T = a.tail_dev ? min(max(tail_word, 0), a.T) : a.T;
   const int tail_per = id_list ? 0 : (T + a.S - 1) / a.S;  // an id list holds its tail rows
   const int t_lo = min(T, p * tail_per), t_hi = min(T, t_lo + tail_per);
-  const int n_rows = n_sel + (t_hi - t_lo);
+  // the list: the tile's tokens, then the tail rows the early blocks did not take
+  const int early_rows = kEarly ? min(t_hi - t_lo, kEarlyRows) : 0;
+  const int n_rows = n_sel + (t_hi - t_lo) - early_rows;
   {
     const int j = lane & 15, qd = lane >> 4;
     const int last_row = a.H + T - 1;
@@ -825,7 +906,7 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     // the block's first row (masked, same lines)
     auto row_pos = [&](int r, int base) {
       r = r < n_rows ? r : base;
-      int pos = r < n_sel ? rows[r] : a.H + t_lo + (r - n_sel);
+      int pos = r < n_sel ? rows[r] : a.H + t_lo + early_rows + (r - n_sel);
       return pos < 0 ? 0 : (pos > last_row ? last_row : pos);
     };
 #if PRISMKV_VALU_ATTENTION
@@ -859,6 +940,14 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     // the wave index made explicitly uniform keeps the block indices in
     // scalar registers (fewer VGPRs for the round's loads)
     const int wu = __builtin_amdgcn_readfirstlane(w);
+#if !PRISMKV_VALU_ATTENTION
+    // the early tail block, requested in phase 4, has landed: attend it first
+    // (its registers are free again before the rounds' loads need theirs)
+    if (early_n > 0) {  // uniform
+      const int early_nv[1] = {early_n};
+      mfma_blocks16<1>(st, ek, ev, early_nv);
+    }
+#endif
     for (int k0 = kWaves - 1 - wu; k0 < n_blocks; k0 += kPerRound * kWaves) {  // blocks k0 + 8 i
       uint4 kr[kPerRound][4], vr[kPerRound][4];
 #pragma unroll
@@ -972,6 +1061,13 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     int32_t* dst = a.ids + (size_t)g * a.ids_stride + lds.base;
     for (int i = tid; i < n_sel; i += kDT) dst[i] = rows[i];
   }
+  // the selection (features / valid / raw) is written here, after the
+  // attention, by the group's last workgroup (not a merger), so that its
+  // bucket-size loads neither wait behind the early tail rows nor delay a merge
+  if constexpr (!kGiven && !kCap)
+    if (p == a.S - 1 && w == 0)
+      write_selection(lds.win, lds.need, a.counts + (size_t)g * kFP, a.features + (size_t)g * kTop,
+                      a.valid + (size_t)g * kTop, a.raw + g);
 
   // ---- 9. workgroups 0..15 each merge one (head, 32-dim slice) of the S
   // split states into out[g] and clear the words they read; workgroup 0
@@ -1068,7 +1164,11 @@ static int resident_workgroups() {
                          reinterpret_cast<const void*>(decode_kernel<1, false, true>),
                          reinterpret_cast<const void*>(decode_kernel<2, false, true>),
                          reinterpret_cast<const void*>(decode_kernel<4, false, true>),
-                         reinterpret_cast<const void*>(decode_kernel<8, false, true>)};
+                         reinterpret_cast<const void*>(decode_kernel<8, false, true>),
+                         reinterpret_cast<const void*>(decode_kernel<1, false, false, true>),
+                         reinterpret_cast<const void*>(decode_kernel<2, false, false, true>),
+                         reinterpret_cast<const void*>(decode_kernel<4, false, false, true>),
+                         reinterpret_cast<const void*>(decode_kernel<8, false, false, true>)};
     for (const void* fn : fns) {
       if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kTileTokens * (int)sizeof(int)) !=
           hipSuccess)
@@ -1158,6 +1258,12 @@ static int decode_launch(uint64_t q, uint64_t moments, uint64_t counts, uint64_t
     else if (S <= 64) hipLaunchKernelGGL((decode_kernel<2, true>), grid, block, rows_bytes, s, a);
     else if (S <= 128) hipLaunchKernelGGL((decode_kernel<4, true>), grid, block, rows_bytes, s, a);
     else hipLaunchKernelGGL((decode_kernel<8, true>), grid, block, rows_bytes, s, a);
+  } else if ((T + S - 1) / S >= kEarlyRows / 2) {
+    // tails that give most waves an early block: the early-tail variant
+    if (S <= 32) hipLaunchKernelGGL((decode_kernel<1, false, false, true>), grid, block, rows_bytes, s, a);
+    else if (S <= 64) hipLaunchKernelGGL((decode_kernel<2, false, false, true>), grid, block, rows_bytes, s, a);
+    else if (S <= 128) hipLaunchKernelGGL((decode_kernel<4, false, false, true>), grid, block, rows_bytes, s, a);
+    else hipLaunchKernelGGL((decode_kernel<8, false, false, true>), grid, block, rows_bytes, s, a);
   } else {
     if (S <= 32) hipLaunchKernelGGL(decode_kernel<1>, grid, block, rows_bytes, s, a);
     else if (S <= 64) hipLaunchKernelGGL(decode_kernel<2>, grid, block, rows_bytes, s, a);
