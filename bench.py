@@ -67,7 +67,7 @@ STAGE_KERNEL = {"decode": "decode_kernel"}
 def nbytes(t):
     """Bytes of a workspace tensor (the work_bytes argument beside its pointer)."""
     return t.numel() * t.element_size()
-DEFAULT_STAGES = "chain,route,union,attend,dense,update,build,copy,long_history,capped"
+DEFAULT_STAGES = "chain,route,union,attend,dense,update,build,copy,long_history,capped,tails,amortised"
 
 
 def parse():
@@ -250,8 +250,8 @@ def dense_control(layers, H, T, steps, warmup):
                      stream=stream())
     ms, _, _ = graph_time(run, steps, warmup)
     us = ms * 1e3 / len(layers)
-    nbytes = G * (H + T) * 2 * D * 2 + G * H * 4 + 2 * G * HQ * D * 2
-    return us, nbytes
+    dense_bytes = G * (H + T) * 2 * D * 2 + G * H * 4 + 2 * G * HQ * D * 2
+    return us, dense_bytes
 
 
 @torch.no_grad()
@@ -352,6 +352,71 @@ def long_history(lib_path, steps, warmup, seed, device, layers_total, replicas=1
     out["update_1024"] = upd
     # per token and layer: one decode plus 1/1024 of a block update
     out["us_per_token_per_layer_with_update"] = round(us + upd["us_per_block"] / 1024, 3)
+    return out
+
+
+@torch.no_grad()
+def tails(lib_path, steps, warmup, seed, device, layers_total, H=65536, tails_=(2048, 4096)):
+    """The headline history with the longer tails the update policy leaves:
+    with the reference's default interval of 4096 tokens
+    (configs/submitted_8b.json:14) the unindexed tail runs from 0 to 4096
+    rows between updates.  36 distinct layers built with the longest tail;
+    each tail length is timed on views of the same layers."""
+    T_max = max(tails_)
+    log(f"tails: building {layers_total} layers H={H} T={T_max} ...")
+    layers = [make_layer(lib_path, 200 + i, H, T_max, seed, device) for i in range(layers_total)]
+    torch.cuda.synchronize()
+    out = {}
+    for T in tails_:
+        views = [(op, q, k[:, :H + T], v[:, :H + T]) for op, q, k, v in layers]
+        run = chain_of(views, layers_total)
+        run()
+        torch.cuda.synchronize()
+        errors = max(l[0].decode_errors() for l in views)
+        ms, _, _ = graph_time(run, steps, warmup)
+        us = ms * 1e3 / layers_total
+        r, u, a, uniq = stage_bytes([l[0] for l in views], H, T)
+        out[str(T)] = dict(decode=rate(r + u + a, us), mean_unique_ids_per_group=round(uniq, 1), wait_errors=errors)
+        log(f"tails: {us:.2f} us/layer decode at H={H} T={T}")
+    del layers
+    torch.cuda.empty_cache()
+    return dict(history=H, layers=layers_total, by_tail=out)
+
+
+@torch.no_grad()
+def amortised(lib_path, steps, warmup, seed, device, layers_total, replicas=12, histories=(32768, 65536),
+              intervals=(512, 2048, 4096)):
+    """Decode with the index update amortised, as the reference reports it
+    (reviewer_guide/results/hyperparameter_sensitivity/README.md:49-58, the
+    update intervals 512 / 2048 / 4096 at 32K and 64K): per token and layer,
+    one decode at the window's mean tail (interval / 2 rows; the decode time
+    grows linearly with the tail) plus 1/interval of one block update of
+    `interval` keys on a table of that history."""
+    out = {}
+    for H in histories:
+        T_max = max(intervals) // 2
+        log(f"amortised: building {replicas} layers H={H} T={T_max} ...")
+        layers = [make_layer(lib_path, 300 + i, H, T_max, seed, device) for i in range(replicas)]
+        torch.cuda.synchronize()
+        dec = {}
+        for n in intervals:
+            T = n // 2
+            views = [(op, q, k[:, :H + T], v[:, :H + T]) for op, q, k, v in layers]
+            run = chain_of(views, layers_total)
+            run()
+            torch.cuda.synchronize()
+            ms, _, _ = graph_time(run, steps, warmup)
+            dec[n] = ms * 1e3 / layers_total
+        del layers, views, run
+        torch.cuda.empty_cache()
+        upd = update_timing(lib_path, H, list(intervals), steps, warmup, seed, device)
+        for n in intervals:
+            u = upd[str(n)]["us_per_block"]
+            out[f"{H}/{n}"] = dict(history=H, interval=n, decode_us_per_layer_at_mean_tail=round(dec[n], 3),
+                                   mean_tail=n // 2, update_us_per_block=u,
+                                   update_us_per_token_per_layer=round(u / n, 4),
+                                   us_per_token_per_layer=round(dec[n] + u / n, 3))
+            log(f"amortised H={H} interval {n}: decode {dec[n]:.2f} + update {u / n:.3f} us per token and layer")
     return out
 
 
@@ -575,7 +640,10 @@ def main():
                    capped=capped(lib_path, a.steps, a.warmup, a.seed, device, a.layers) if "capped" in stages else None,
                    update=update_timing(lib_path, H, [int(x) for x in a.update_blocks.split(",") if x], a.steps,
                                         a.warmup, a.seed, device) if "update" in stages else None,
-                   build=build_timing(lib_path, H, a.steps, a.warmup, a.seed, device) if "build" in stages else None)
+                   build=build_timing(lib_path, H, a.steps, a.warmup, a.seed, device) if "build" in stages else None,
+                   tails=tails(lib_path, a.steps, a.warmup, a.seed, device, a.layers, H) if "tails" in stages else None,
+                   amortised=amortised(lib_path, a.steps, a.warmup, a.seed, device, a.layers)
+                   if "amortised" in stages else None)
         print(json.dumps(out), flush=True)
         return
     log(f"building {a.layers} layers H={H} T={T} ...")
@@ -620,8 +688,8 @@ def main():
     torch.cuda.synchronize()
     wait_errors = max(l[0].decode_errors() for l in layers)
     b_route, b_union, b_av, uniq = stage_bytes([l[0] for l in layers], H, T)
-    nbytes = {"decode": b_route + b_union + b_av, "route": b_route, "union": b_union, "attend": b_av}
-    stage_report = {name: rate(nbytes[name], us) for name, us in per_stage.items()}
+    stage_nbytes = {"decode": b_route + b_union + b_av, "route": b_route, "union": b_union, "attend": b_av}
+    stage_report = {name: rate(stage_nbytes[name], us) for name, us in per_stage.items()}
     dense = None
     if "dense" in stages:
         d_us, d_bytes = dense_control(layers, H, T, a.steps, a.warmup)
@@ -673,14 +741,20 @@ def main():
     roofline = None
     if dominant:
         d = stage_report[dominant]
+        traffic = measured_traffic(dominant, H, T)
         roofline = dict(bound="hbm", achieved=d["achieved_GBps"], peak=HBM_PEAK_GBS, unit="GB/s",
-                        frac=d["frac_of_peak"], traffic=measured_traffic(dominant, H, T),
+                        frac=d["frac_of_peak"], traffic=traffic,
+                        traffic_source=None if traffic is None else
+                        "profile-derived, not collected by this run: FETCH_SIZE and WRITE_SIZE passes over this "
+                        "workload, scaled by the copy kernel's factors (profiles/decode_kernel_64k_hbm_traffic.md)",
                         kernel=STAGE_KERNEL.get(dominant, dominant), algorithmic_bytes=d["algorithmic_bytes"])
     n_layers = a.layers
     del layers
     torch.cuda.empty_cache()
     long_h = long_history(lib_path, a.steps, a.warmup, a.seed, device, n_layers) if "long_history" in stages else None
     cap = capped(lib_path, a.steps, a.warmup, a.seed, device, n_layers) if "capped" in stages else None
+    tail_lines = tails(lib_path, a.steps, a.warmup, a.seed, device, n_layers, H) if "tails" in stages else None
+    amort = amortised(lib_path, a.steps, a.warmup, a.seed, device, n_layers) if "amortised" in stages else None
     value = ms * 1e3 / a.layers
     result = {
         "metric": METRIC, "value": round(value, 3), "unit": "us/layer", "n_gpus": 1, "steps": a.steps,
@@ -696,7 +770,8 @@ def main():
                    "kv_dtype": "bf16", "mean_unique_ids_per_group": round(uniq, 1), "parallelism": "single GPU"},
         "wall_ms_per_step": round(wall, 4), "wait_errors": wait_errors, "stages": stage_report, "dense": dense,
         "copy_probe_GBps": copy_gbs and round(copy_gbs, 1), "update": update, "build": build,
-        "long_history": long_h, "capped": cap, "roofline": roofline, "cpu_baseline": cpu,
+        "long_history": long_h, "capped": cap, "tails": tail_lines, "amortised": amort, "roofline": roofline,
+        "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
 
