@@ -656,11 +656,9 @@ def main():
         for op, q, k, v in layers:
             op(q, k, v)
 
-    def route_only():  # moment scoring + Top-16, one launch (Native8B.route also runs the union)
+    def route_only():  # Native8B.route(): moment scoring, Top-16, union and ids in one launch
         for op, q, k, v in layers:
-            op.lib.call("prismkv_route_single", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(),
-                        op.decode_work.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(),
-                        op.raw.data_ptr(), G, nbytes(op.decode_work), stream=stream())
+            op.route(q)
 
     def union_only():
         for op, q, k, v in layers:
@@ -688,7 +686,8 @@ def main():
     torch.cuda.synchronize()
     wait_errors = max(l[0].decode_errors() for l in layers)
     b_route, b_union, b_av, uniq = stage_bytes([l[0] for l in layers], H, T)
-    stage_nbytes = {"decode": b_route + b_union + b_av, "route": b_route, "union": b_union, "attend": b_av}
+    stage_nbytes = {"decode": b_route + b_union + b_av, "route": b_route + b_union, "union": b_union,
+                    "attend": b_av}
     stage_report = {name: rate(stage_nbytes[name], us) for name, us in per_stage.items()}
     dense = None
     if "dense" in stages:

@@ -86,6 +86,17 @@ int prismkv_route(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, 
  * as for prismkv_decode. */
 int prismkv_route_single(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
                          uint64_t valid, uint64_t raw, int groups, size_t work_bytes, uint64_t stream);
+/* Stages 1-2 in ONE launch (replaces Native8B.route = pack + torch.bmm +
+ * fused_norm_top + launch_union_warp, src/prismkv/native8b.py:82-89;
+ * semantics src/prismkv/core.py:106-130, :142-148 with cap None): the
+ * selection, union and id phases of prismkv_decode without the attention.
+ * Writes the same features / valid / raw / ids / count as prismkv_decode;
+ * no K/V is read and no output written.  The limits, workspace and -1 are
+ * prismkv_decode's. */
+int prismkv_route_union(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t work,
+                        uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count, int groups,
+                        int H, int capacity, int64_t row_words, int64_t ids_stride, size_t work_bytes,
+                        uint64_t stream);
 
 /* Stage 2 (replaces launch_union_warp, src/prismkv/native8b.py:88-89;
  * semantics kernels/ppu_8b/union.cu:14-27): one launch, any H up to 2^29. */

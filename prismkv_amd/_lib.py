@@ -26,6 +26,7 @@ SIGNATURES = {
     "prismkv_route_work_bytes": ([_I32], False, _SZ),
     "prismkv_route": ([_U64] * 7 + [_I32, _SZ], True, _I32),
     "prismkv_route_single": ([_U64] * 7 + [_I32, _SZ], True, _I32),
+    "prismkv_route_union": ([_U64] * 10 + [_I32, _I32, _I32, _I64, _I64, _SZ], True, _I32),
     "prismkv_union_work_bytes": ([_I32, _I32], False, _SZ),
     "prismkv_union": ([_U64] * 6 + [_I32, _I32, _I64, _I64, _SZ], True, _I32),
     "prismkv_build_bits": ([_U64] * 3 + [_I32, _I64, _I64], True, _I32),

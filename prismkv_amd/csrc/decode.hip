@@ -105,6 +105,7 @@ struct DecodeArgs {
   int spin;                       // bound of every wait (sleeps), prismkv_set_spin_limit
   float* state;  // [G][S][4 heads][4 slices][34] published split states
   unsigned* walk;  // [G][4 windows][S][8] published pattern counts (capped launch)
+  unsigned* done;  // [G] workgroups past their last read of published words (route-and-union launch)
   int limit;       // the strict unique cap's limit (capped launch)
   int64_t* features;
   float* valid;
@@ -311,7 +312,8 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int g, int h, i
     float acc = 0.f;
 #pragma unroll
     for (int i = 0; i < kGroups; ++i) acc += lds.fin.part[i][tid];
-    a.out[((size_t)g * kHq + h) * kD + c * (kD / kSlices) + tid] = f32_to_bf16(den > 0.f ? acc / den : 0.f);
+    if (a.out)  // the route-and-union launch merges only to clear (no output)
+      a.out[((size_t)g * kHq + h) * kD + c * (kD / kSlices) + tid] = f32_to_bf16(den > 0.f ? acc / den : 0.f);
   }
   // every word read above has been consumed (the barrier follows the last use)
   for (int i = tid; i < S * kSliceW; i += kDT) {
@@ -698,7 +700,12 @@ struct EarlyTail {
   __device__ void wait_words() const { __builtin_amdgcn_s_waitcnt(8 | (0x7 << 4) | (0xf << 8)); }
 };
 
-template <int KW, bool kGiven = false, bool kCap = false, bool kEarlyTail = false>
+// kRouteOnly: stages 1-2 alone (what Native8B.route() runs): the selection,
+// the union tiles and the ids, with no attention; the empty split states are
+// still published and merged (without writing out), since that hand-off is
+// what tells workgroup 0 that every workgroup is done with the published
+// words it then clears.
+template <int KW, bool kGiven = false, bool kCap = false, bool kEarlyTail = false, bool kRouteOnly = false>
 __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   const int p = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   __shared__ DecodeLds lds;
@@ -712,7 +719,7 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   // workgroup's tail rows is requested in phase 4, behind the bitmap words,
   // so it streams in while the selection finishes and the union is built
   // (HBM is otherwise idle then); phase 6 attends it first.
-  constexpr bool kEarly = kEarlyTail && !kGiven && !kCap && !PRISMKV_VALU_ATTENTION;
+  constexpr bool kEarly = kEarlyTail && !kGiven && !kCap && !kRouteOnly && !PRISMKV_VALU_ATTENTION;
   int early_n = 0;
   uint4 ek[1][4], ev[1][4];
 
@@ -894,7 +901,7 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   const int t_lo = min(T, p * tail_per), t_hi = min(T, t_lo + tail_per);
   // the list: the tile's tokens, then the tail rows the early blocks did not take
   const int early_rows = kEarly ? min(t_hi - t_lo, kEarlyRows) : 0;
-  const int n_rows = n_sel + (t_hi - t_lo) - early_rows;
+  const int n_rows = kRouteOnly ? 0 : n_sel + (t_hi - t_lo) - early_rows;
   {
     const int j = lane & 15, qd = lane >> 4;
     const int last_row = a.H + T - 1;
@@ -1055,7 +1062,10 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     // workgroup 0 that this workgroup no longer reads any published word);
     // publish_sliced's first barrier waits for every wave's stash and also
     // publishes lds.base to every wave
-    publish_sliced(lds.mf, a.state + (size_t)(g * a.S + p) * kHq * kSlices * kSliceW);
+    if constexpr (kRouteOnly)
+      __syncthreads();  // lds.base to every wave
+    else
+      publish_sliced(lds.mf, a.state + (size_t)(g * a.S + p) * kHq * kSlices * kSliceW);
   }
   if (!id_list) {
     int32_t* dst = a.ids + (size_t)g * a.ids_stride + lds.base;
@@ -1068,6 +1078,21 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     if (p == a.S - 1 && w == 0)
       write_selection(lds.win, lds.need, a.counts + (size_t)g * kFP, a.features + (size_t)g * kTop,
                       a.valid + (size_t)g * kTop, a.raw + g);
+  if constexpr (kRouteOnly) {
+    // no attention: the group's last workgroup past its look-back (a ticket
+    // per workgroup) clears the statistics, candidates and tile counts, which
+    // no workgroup reads any more, and resets the ticket counter
+    __syncthreads();  // wave 0's look-back reads are done
+    if (tid == 0) lds.nsel = (int)inc_dev(&a.done[g]);
+    __syncthreads();
+    if (lds.nsel == a.S - 1) {
+      for (int i = tid; i < kChunks * kHq; i += kDT) st_dev(&a.stats[(size_t)g * kChunks * kHq + i], 0ull);
+      for (int i = tid; i < a.S * kTop; i += kDT) st_dev(&a.cand[(size_t)g * a.S * kTop + i], 0ull);
+      for (int i = tid; i < a.S; i += kDT) st_dev(&a.status[(size_t)g * a.S + i], 0u);
+      if (tid == 0) st_dev(&a.done[g], 0u);
+    }
+    return;
+  }
 
   // ---- 9. workgroups 0..15 each merge one (head, 32-dim slice) of the S
   // split states into out[g] and clear the words they read; workgroup 0
@@ -1121,11 +1146,11 @@ int spin_limit() { return __atomic_load_n(&g_spin_limit, __ATOMIC_RELAXED); }
 }  // namespace prismkv
 
 // Work layout (bytes) for the split count of `groups` groups:
-// err (the error word, then the host-word slot at byte 8) | stats | candidates | status | state | walk.
-// The walk's records come last: only the capped launch uses them, so the
-// other launches touch the first `walk` bytes only.
+// err (the error word, then the host-word slot at byte 8) | stats | candidates | status | state | walk | done.
+// The walk's records and the route-and-union launch's ticket counters come
+// last: the other launches touch the first `walk` bytes only.
 struct DecodeWorkLayout {
-  size_t err, stats, cand, status, state, walk, total;
+  size_t err, stats, cand, status, state, walk, done, total;
   DecodeWorkLayout(int groups, int S) {
     size_t o = 0;
     auto take = [&](size_t n) { const size_t at = o; o += (n + 255) & ~(size_t)255; return at; };
@@ -1135,6 +1160,7 @@ struct DecodeWorkLayout {
     status = take((size_t)groups * S * sizeof(unsigned));
     state = take((size_t)groups * S * kHq * kSlices * kSliceW * sizeof(float));
     walk = take((size_t)groups * kWindows * S * kPacked * sizeof(unsigned));
+    done = take((size_t)groups * sizeof(unsigned));
     total = o;
   }
 };
@@ -1168,7 +1194,11 @@ static int resident_workgroups() {
                          reinterpret_cast<const void*>(decode_kernel<1, false, false, true>),
                          reinterpret_cast<const void*>(decode_kernel<2, false, false, true>),
                          reinterpret_cast<const void*>(decode_kernel<4, false, false, true>),
-                         reinterpret_cast<const void*>(decode_kernel<8, false, false, true>)};
+                         reinterpret_cast<const void*>(decode_kernel<8, false, false, true>),
+                         reinterpret_cast<const void*>(decode_kernel<1, false, false, false, true>),
+                         reinterpret_cast<const void*>(decode_kernel<2, false, false, false, true>),
+                         reinterpret_cast<const void*>(decode_kernel<4, false, false, false, true>),
+                         reinterpret_cast<const void*>(decode_kernel<8, false, false, false, true>)};
     for (const void* fn : fns) {
       if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kTileTokens * (int)sizeof(int)) !=
           hipSuccess)
@@ -1189,15 +1219,17 @@ static int resident_workgroups() {
 static int decode_check(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
                         uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
                         uint64_t out, bool given, int groups, int H, int T, int capacity, int64_t row_words,
-                        int64_t ks, int64_t vs, int64_t ids_stride, int64_t limit) {
+                        int64_t ks, int64_t vs, int64_t ids_stride, int64_t limit, bool route_only = false) {
   if (groups < 1 || groups > 65535 || H < 1 || H > kFusedMaxHistory || T < 0 || capacity < H) return kBadSize;
   if (given && limit >= 0) return kBadSize;
   if (row_words < (H + 31) / 32 || ids_stride < H) return kBadSize;
-  if (ks < (int64_t)(H + T) * kD || vs < (int64_t)(H + T) * kD) return kBadSize;
-  if (((int64_t)H + T) * 2 * kD > INT32_MAX) return kBadSize;  // K/V rows are read through 32-bit buffer offsets
+  if (!route_only) {  // the route-and-union launch reads no K/V and writes no out
+    if (ks < (int64_t)(H + T) * kD || vs < (int64_t)(H + T) * kD) return kBadSize;
+    if (((int64_t)H + T) * 2 * kD > INT32_MAX) return kBadSize;  // K/V rows are read through 32-bit buffer offsets
+    if (!k || !v || !out) return kBadSize;
+  }
   // a given selection needs neither the moment tables nor raw
-  if (!q || (!given && (!moments || !counts || !raw)) || !bits || !k || !v || !work || !features || !valid || !ids ||
-      !count || !out)
+  if (!q || (!given && (!moments || !counts || !raw)) || !bits || !work || !features || !valid || !ids || !count)
     return kBadSize;
   if (decode_splits(groups) > resident_workgroups()) return kBadSize;  // a group's workgroups must be resident together
   return 0;
@@ -1207,7 +1239,8 @@ static int decode_check(uint64_t q, uint64_t moments, uint64_t counts, uint64_t 
 static int decode_launch(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t k, uint64_t v,
                          uint64_t work, uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count,
                          uint64_t out, const int* tail_dev, bool given, int groups, int H, int T, int64_t row_words,
-                         int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream, unsigned* err, int64_t limit) {
+                         int64_t ks, int64_t vs, int64_t ids_stride, uint64_t stream, unsigned* err, int64_t limit,
+                         bool route_only = false) {
   const int S = decode_splits(groups);
   const DecodeWorkLayout L(groups, S);
   char* w = reinterpret_cast<char*>(work);
@@ -1235,6 +1268,7 @@ static int decode_launch(uint64_t q, uint64_t moments, uint64_t counts, uint64_t
   a.spin = spin_limit();
   a.state = reinterpret_cast<float*>(w + L.state);
   a.walk = reinterpret_cast<unsigned*>(w + L.walk);
+  a.done = reinterpret_cast<unsigned*>(w + L.done);
   a.limit = (int)std::min<int64_t>(limit, H);
   a.features = reinterpret_cast<int64_t*>(features);
   a.valid = reinterpret_cast<float*>(valid);
@@ -1248,7 +1282,12 @@ static int decode_launch(uint64_t q, uint64_t moments, uint64_t counts, uint64_t
   const dim3 grid(S, groups), block(kDT);
   hipStream_t s = (hipStream_t)stream;
   const size_t rows_bytes = (size_t)32 * a.tw * sizeof(int);  // the tile's row list (dynamic LDS)
-  if (limit >= 0) {
+  if (route_only) {
+    if (S <= 32) hipLaunchKernelGGL((decode_kernel<1, false, false, false, true>), grid, block, rows_bytes, s, a);
+    else if (S <= 64) hipLaunchKernelGGL((decode_kernel<2, false, false, false, true>), grid, block, rows_bytes, s, a);
+    else if (S <= 128) hipLaunchKernelGGL((decode_kernel<4, false, false, false, true>), grid, block, rows_bytes, s, a);
+    else hipLaunchKernelGGL((decode_kernel<8, false, false, false, true>), grid, block, rows_bytes, s, a);
+  } else if (limit >= 0) {
     if (S <= 32) hipLaunchKernelGGL((decode_kernel<1, false, true>), grid, block, rows_bytes, s, a);
     else if (S <= 64) hipLaunchKernelGGL((decode_kernel<2, false, true>), grid, block, rows_bytes, s, a);
     else if (S <= 128) hipLaunchKernelGGL((decode_kernel<4, false, true>), grid, block, rows_bytes, s, a);
@@ -1443,6 +1482,19 @@ int prismkv_union_attend_tail(uint64_t q, uint64_t bits, uint64_t k, uint64_t v,
   if (!tail || tail % 4) return kBadSize;
   return decode_impl(q, 0, 0, bits, k, v, work, features, valid, 0, ids, count, out, reinterpret_cast<const int*>(tail),
                      true, groups, H, max_tail, capacity, row_words, ks, vs, ids_stride, work_bytes, stream);
+}
+
+int prismkv_route_union(uint64_t q, uint64_t moments, uint64_t counts, uint64_t bits, uint64_t work,
+                        uint64_t features, uint64_t valid, uint64_t raw, uint64_t ids, uint64_t count, int groups,
+                        int H, int capacity, int64_t row_words, int64_t ids_stride, size_t work_bytes,
+                        uint64_t stream) {
+  if (groups < 1 || groups > 65535) return kBadSize;
+  if (work_bytes < DecodeWorkLayout(groups, decode_splits(groups)).total) return kBadSize;
+  const int rc = decode_check(q, moments, counts, bits, 0, 0, work, features, valid, raw, ids, count, 0, false,
+                              groups, H, 0, capacity, row_words, 0, 0, ids_stride, -1, true);
+  if (rc) return rc;
+  return decode_launch(q, moments, counts, bits, 0, 0, work, features, valid, raw, ids, count, 0, nullptr, false,
+                       groups, H, 0, row_words, 0, 0, ids_stride, stream, nullptr, -1, true);
 }
 
 int prismkv_route_single(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,

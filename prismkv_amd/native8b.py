@@ -342,7 +342,22 @@ class Native8B:
         self.__dict__["_unique_cap"] = cap
 
     def route(self, q):
+        """Stages 1-2: features / valid / raw and the union's ids / count.
+        With the moments router, no unique cap and a history the fused
+        decode serves, ONE launch (prismkv_route_union: the decode's
+        selection, union and id phases without the attention)."""
         self.check_errors()
+        if self.router == "moments" and self.unique_cap is None and self.history <= FUSED_MAX_HISTORY:
+            if tuple(q.shape) != (GROUPS, HEADS, DIM) or q.dtype != torch.bfloat16 or not q.is_contiguous():
+                raise ValueError("contiguous BF16 Q[8,4,128] required")
+            if q.device != self.out.device:
+                raise ValueError("Q must live on the index device")
+            self.lib.call("prismkv_route_union", q.data_ptr(), self.moments.data_ptr(), self.n.data_ptr(),
+                          self.bits.data_ptr(), self.decode_work.data_ptr(), self.features.data_ptr(),
+                          self.valid.data_ptr(), self.raw.data_ptr(), self.ids.data_ptr(), self.count.data_ptr(),
+                          GROUPS, self.history, self.capacity, self.row_words, self.capacity,
+                          _lib.nbytes(self.decode_work), stream=self._stream())
+            return
         width = self._select(q)
         self.lib.call("prismkv_union_n", self.bits.data_ptr(), self.features.data_ptr(), self.valid.data_ptr(),
                       self.union_work.data_ptr(), self.ids.data_ptr(), self.count.data_ptr(), GROUPS, self.history,

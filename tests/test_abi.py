@@ -165,6 +165,7 @@ WORK_CASES = {
     "prismkv_topk": ((*[16] * 4, 100, 800), ("prismkv_topk_work_bytes",)),
     "prismkv_summarize": ((*[16] * 6, 8, H, 1, KS, 32), ("prismkv_summarize_work_bytes", 8)),
     "prismkv_route_single": ((*[16] * 7, 8), ("prismkv_decode_work_bytes", 8, H)),
+    "prismkv_route_union": ((*[16] * 10, 8, H, H, 32, H), ("prismkv_decode_work_bytes", 8, H)),
     "prismkv_decode": ((*[16] * 13, 8, H, T, H, 32, KS, KS, H), ("prismkv_decode_work_bytes", 8, H)),
     "prismkv_decode_tail": ((*[16] * 14, 8, H, T, H, 32, KS, KS, H), ("prismkv_decode_work_bytes", 8, H)),
     "prismkv_decode_capped": ((*[16] * 13, 8, H, T, H, 62, 32, KS, KS, H), ("prismkv_decode_work_bytes", 8, H)),
@@ -173,7 +174,7 @@ WORK_CASES = {
     "prismkv_union_attend": ((*[16] * 10, 8, H, T, H, 32, KS, KS, H), ("prismkv_decode_work_bytes", 8, H)),
     "prismkv_union_attend_tail": ((*[16] * 11, 8, H, T, H, 32, KS, KS, H), ("prismkv_decode_work_bytes", 8, H)),
 }
-WAITING = {"prismkv_route_single", "prismkv_decode", "prismkv_decode_tail", "prismkv_decode_capped",
+WAITING = {"prismkv_route_single", "prismkv_route_union", "prismkv_decode", "prismkv_decode_tail", "prismkv_decode_capped",
            "prismkv_decode_capped_tail", "prismkv_union_attend", "prismkv_union_attend_tail"}
 
 

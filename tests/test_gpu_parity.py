@@ -451,3 +451,47 @@ def test_fused_decode_fewer_groups(groups):
     log(f"  groups={groups}: {err}")
     assert err["rel_l2"] <= AV_TOL and err["max_abs"] < 0.05, err
 
+
+
+@pytest.mark.parametrize("H", [4096, 65536, 200000])
+def test_route_union_one_launch(H):
+    # Native8B.route() runs prismkv_route_union (stages 1-2 in one launch):
+    # features / valid / raw / ids / count bit-identical to the two-launch
+    # route (prismkv_route_single, then prismkv_union_n), on repeated calls
+    # and after a decode on the same workspace, which is left zero
+    op, q, k, v = device_layer(H, 16, seed=12)
+    lib, s = op.lib, torch.cuda.current_stream().cuda_stream
+
+    def two():
+        lib.call("prismkv_route_single", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(),
+                 op.decode_work.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(), op.raw.data_ptr(), 8,
+                 nbytes(op.decode_work), stream=s)
+        lib.call("prismkv_union_n", op.bits.data_ptr(), op.features.data_ptr(), op.valid.data_ptr(),
+                 op.union_work.data_ptr(), op.ids.data_ptr(), op.count.data_ptr(), 8, op.history, op.row_words,
+                 op.capacity, 16, nbytes(op.union_work), stream=s)
+
+    def outputs():
+        torch.cuda.synchronize()
+        f, va, r, ids, c = route_outputs(op)
+        out = (f.copy(), va.copy(), r.copy(), [ids[g][:c[g]].copy() for g in range(8)], c.copy())
+        for x in (op.features, op.valid, op.raw, op.ids, op.count):
+            x.zero_()
+        return out
+
+    two()
+    want = outputs()
+    for step in range(3):
+        op.route(q)
+        got = outputs()
+        for a, b in zip(want[:3], got[:3]):
+            assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), step
+        assert np.array_equal(want[4], got[4]), step
+        for g in range(8):
+            assert np.array_equal(want[3][g], got[3][g]), (step, g)
+        if step == 1:
+            op(q, k, v)
+            torch.cuda.synchronize()
+    assert int(op.decode_work.view(torch.int32)[0]) == 0
+    assert op.decode_errors() == 0
+    assert not bool(op.decode_work[16:].any()), "the workspace is left zero"
+    log(f"  H={H}: one-launch route equals route + union over 3 calls; unique ids {want[4].tolist()}")
