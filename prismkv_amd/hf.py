@@ -250,6 +250,8 @@ class HFNative:
     # ------------------------------------------------------------ lifecycle
 
     def begin_request(self):
+        if getattr(self, "_static", None) is not None:  # the finished request's steps join its records
+            self._static.flush_records()
         self.prefix_lengths, self.ops = {}, {}
         self._log = _Records(self.mode, self.detailed_records)
 
@@ -282,6 +284,8 @@ class HFNative:
         """Per-(layer, group) decode records in the reference's fields (reads
         the pending device tensors back; raises if a decode's bounded wait
         gave up)."""
+        if self._static is not None:
+            self._static.flush_records()
         if self._log.pending:
             torch.cuda.synchronize()
             self.check_errors()
@@ -380,6 +384,7 @@ class HFNative:
             raise RuntimeError("static-cache decode steps run through DecodeGraph")
         tail = (pos[-1:] + 1 - op.history).to(torch.int32)
         out = op(q[0, :, 0].reshape(GROUPS, HEADS, DIM).contiguous(), k[0], v[0], tail=tail)
+        self._static._record(layer, op)
         return out.reshape(1, 1, queries, q.shape[-1]), None
 
 
@@ -401,13 +406,25 @@ class DecodeGraph:
     device): one launch per layer, or with a unique cap the route, the
     budgeted walk and the union + attention launch.  With graph=False every
     step runs eagerly through the same code.  Sparse mode and the moments
-    router only; records are not kept."""
+    router only.
 
-    def __init__(self, session, cache, *, graph=True):
+    Records (the session's `records`, hf_reference.py:216-231): each step's
+    decode writes its count, raw and selection of every layer into a device
+    ring of `record_steps` slots, indexed by the step's position on the
+    device, inside the captured step; the host notes each step's histories
+    and reads the ring back when `records` is read or the ring is full (one
+    synchronisation per `record_steps` steps).  The detailed fields are not
+    kept here (detailed_records raises)."""
+
+    def __init__(self, session, cache, *, graph=True, record_steps=1024):
         if session.mode != "sparse" or session.router != "moments":
             raise NotImplementedError("DecodeGraph drives the fused decode: sparse mode, moments router")
+        if session.detailed_records:
+            raise NotImplementedError("DecodeGraph keeps the basic records (detailed_records=False)")
         if session._static is not None:
             raise ValueError("the session already drives a static cache")
+        if int(record_steps) < 1:
+            raise ValueError("record_steps must be positive")
         device = next(session.model.parameters()).device
         self.session, self.cache, self.position = session, cache, None
         self.max_length = int(cache.max_cache_len)
@@ -416,12 +433,48 @@ class DecodeGraph:
         self.pos = torch.zeros((1, 1), dtype=torch.long, device=device)
         self.graph, self.logits, self.stale = None, None, True
         self.eager_steps = 0
+        self.record_steps = int(record_steps)
+        self._slot = torch.zeros(1, dtype=torch.long, device=device)  # ring slot of the current step
+        self._rings = {}   # layer -> device ring of (count, raw, valid) per step
+        self._steps = []   # (position, {layer: history}) of the steps in the rings, oldest first
         session._static = self
 
     def close(self):
+        self.flush_records()
         if self.session._static is self:
             self.session._static = None
         self.graph = self.logits = None
+
+    def _record(self, layer, op):
+        """Copies the layer's count / raw / valid into the step's ring slot
+        (device-side index, so a captured step records every replay)."""
+        ring = self._rings.get(layer)
+        if ring is None:
+            if torch.cuda.is_current_stream_capturing():
+                raise RuntimeError("record rings are created by an eager step")
+            R, dev = self.record_steps, op.out.device
+            ring = self._rings[layer] = (torch.zeros(R, GROUPS, dtype=torch.int32, device=dev),
+                                         torch.zeros(R, GROUPS, dtype=torch.int32, device=dev),
+                                         torch.zeros(R, *op.valid.shape, dtype=op.valid.dtype, device=dev))
+        for dst, src in zip(ring, (op.count, op.raw, op.valid)):
+            dst.index_copy_(0, self._slot, src[None])
+
+    def flush_records(self):
+        """Moves the recorded steps into the session's records (synchronises)."""
+        if not self._steps:
+            return
+        torch.cuda.synchronize()
+        self.session.check_errors()
+        host = {layer: [x.cpu() for x in ring] for layer, ring in self._rings.items()}
+        log = self.session._log
+        for position, histories in self._steps:
+            slot, total = position % self.record_steps, position + 1
+            for layer in sorted(histories):
+                count, raw, valid = (x[slot] for x in host[layer])
+                log.pending.append(dict(layer=layer, history=histories[layer], total=total,
+                                        prefix=self.session.prefix_lengths[layer], unique=count, raw=raw,
+                                        buckets=(valid > 0).sum(1)))
+        self._steps = []
 
     def _prepare(self, total):
         """Lazy builds and updates for a step that ends with `total` tokens;
@@ -437,6 +490,7 @@ class DecodeGraph:
         return moved
 
     def _forward(self):
+        torch.remainder(self.pos.reshape(1), self.record_steps, out=self._slot)
         out = self.session.model(self.ids, position_ids=self.pos, attention_mask={"full_attention": None},
                                  past_key_values=self.cache, use_cache=True, logits_to_keep=1)
         return out.logits
@@ -473,5 +527,8 @@ class DecodeGraph:
                 self._capture()
             self.graph.replay()
             logits = self.logits
+        self._steps.append((self.position, {layer: op.history for layer, op in self.session.ops.items()}))
+        if len(self._steps) == self.record_steps:
+            self.flush_records()
         self.position += 1
         return logits

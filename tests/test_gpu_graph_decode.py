@@ -10,7 +10,8 @@
     the oracle's route + attention (src/prismkv/core.py:106-183) over the
     index the device holds, the update policy (hf_reference.py:205-211)
     moves the history across the run, and the graph-replayed steps give
-    bit-identical logits to the eager ones.
+    bit-identical logits to the eager ones and the same records (read back
+    from the per-step device ring) as the eager steps' operators held.
 """
 import numpy as np
 import pytest
@@ -98,18 +99,27 @@ def test_static_cache_decode_graph():
     model = tiny_qwen3(layers)
     session = HFNative(model, encoders(layers), update_interval=interval)
     ids = torch.randint(0, 256, (1, P + N), generator=torch.Generator().manual_seed(9)).cuda()
-    logits = {}
+    logits, records, expected = {}, {}, []
     checks = {0, 64, N - 1}
     for use_graph in (False, True):
         session.begin_request()
         cache = StaticCache(config=model.config, max_cache_len=P + N + 16)
-        step = DecodeGraph(session, cache, graph=use_graph)
+        # a 32-step record ring: read back twice during the run and once at the end
+        step = DecodeGraph(session, cache, graph=use_graph, record_steps=32)
         _prefill(session, model, cache, ids, P)
         cap = Capture(session) if not use_graph else None
         out = []
         for s in range(N):
             n_calls = len(cap.calls) if cap else 0
             out.append(step(ids[:, P + s:P + s + 1]).clone())
+            if cap:  # the records each eager step must leave, read from the operators
+                torch.cuda.synchronize()
+                for layer in sorted(session.ops):
+                    op = session.ops[layer]
+                    for g, (u, r, b) in enumerate(zip(op.count.tolist(), op.raw.tolist(),
+                                                      (op.valid > 0).sum(1).tolist())):
+                        expected.append(dict(layer=layer, group=g, history=op.history, unique=u, raw=r, buckets=b,
+                                             tail=P + s + 1 - op.history, routing_policy="sparse"))
             if cap and s in checks:
                 torch.cuda.synchronize()
                 for layer, q, K, V, o in cap.calls[n_calls:]:
@@ -126,9 +136,13 @@ def test_static_cache_decode_graph():
             assert op.decode_errors() == 0
         step.close()
         logits[use_graph] = torch.stack(out)
+        records[use_graph] = [dict(r) for r in session.records]
         log(f"graph={use_graph}: {N} steps, histories {[op.history for op in session.ops.values()]}")
     assert torch.isfinite(logits[False]).all()
     assert torch.equal(logits[False], logits[True])
+    assert len(expected) == N * layers * 8
+    assert records[False] == expected
+    assert records[True] == expected
     session.close()
 
 
