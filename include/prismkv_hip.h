@@ -352,6 +352,38 @@ int prismkv_summarize(uint64_t k, uint64_t bits, uint64_t center, uint64_t count
                       int groups, int H, int flags, int64_t ks, int64_t row_words, size_t work_bytes,
                       uint64_t stream);
 
+/* ---- fp32 inputs ---------------------------------------------------------
+ * The reference's core functions take tensors of any float dtype and compute
+ * in fp32 (src/prismkv/core.py:92-103,106-139,170-183; examples/replay.py:15-21
+ * runs them on fp32 keys, queries and values).  These entry points are the
+ * ones above with fp32 in place of bf16: the same arguments, work sizes,
+ * error words and results, except that
+ *   prismkv_build_f32 / prismkv_update_f32 / prismkv_summarize_f32: K rows are
+ *     fp32 (ks in elements; rows 16-byte aligned);
+ *   prismkv_route_scores_f32 / prismkv_route_qact_f32: q is fp32 [G][4][128];
+ *   prismkv_attend_f32: q, K and V rows are fp32 and out is fp32 [G][4][128]
+ *     (always the split-K kernel; q, K, V and the row strides 16-byte
+ *     aligned).
+ * Every key, query and value is used at full fp32 precision. */
+int prismkv_build_f32(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
+                      uint64_t counts, uint64_t moments, uint64_t work, int groups, int batch, int H, int key_mean,
+                      int flags, int64_t ks, int64_t row_words, size_t work_bytes, uint64_t stream);
+int prismkv_update_f32(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
+                       uint64_t counts, uint64_t moments, uint64_t work, int groups, int H, int N, int key_mean,
+                       int64_t ks, int64_t row_words, size_t work_bytes, uint64_t stream);
+int prismkv_summarize_f32(uint64_t k, uint64_t bits, uint64_t center, uint64_t counts, uint64_t moments,
+                          uint64_t work, int groups, int H, int flags, int64_t ks, int64_t row_words,
+                          size_t work_bytes, uint64_t stream);
+int prismkv_route_scores_f32(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
+                             uint64_t valid, uint64_t raw, uint64_t scores, int groups, size_t work_bytes,
+                             uint64_t stream);
+int prismkv_route_qact_f32(uint64_t q, uint64_t W, uint64_t b, uint64_t qscale, uint64_t counts, uint64_t work,
+                           uint64_t features, uint64_t valid, uint64_t raw, uint64_t scores, int groups,
+                           size_t work_bytes, uint64_t stream);
+int prismkv_attend_f32(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t count, uint64_t work,
+                       uint64_t out, int groups, int H, int T, int64_t ks, int64_t vs, int64_t ids_stride,
+                       int splits, size_t work_bytes, uint64_t stream);
+
 #ifdef __cplusplus
 }
 #endif

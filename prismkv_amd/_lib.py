@@ -55,6 +55,12 @@ SIGNATURES = {
     "prismkv_summarize": ([_U64] * 6 + [_I32, _I32, _I32, _I64, _I64, _SZ], True, _I32),
     "prismkv_route_qact_work_bytes": ([_I32], False, _SZ),
     "prismkv_route_qact": ([_U64] * 10 + [_I32, _SZ], True, _I32),
+    "prismkv_build_f32": ([_U64] * 9 + [_I32] * 5 + [_I64, _I64, _SZ], True, _I32),
+    "prismkv_update_f32": ([_U64] * 9 + [_I32] * 4 + [_I64, _I64, _SZ], True, _I32),
+    "prismkv_summarize_f32": ([_U64] * 6 + [_I32, _I32, _I32, _I64, _I64, _SZ], True, _I32),
+    "prismkv_route_scores_f32": ([_U64] * 8 + [_I32, _SZ], True, _I32),
+    "prismkv_route_qact_f32": ([_U64] * 10 + [_I32, _SZ], True, _I32),
+    "prismkv_attend_f32": ([_U64] * 7 + [_I32, _I32, _I32, _I64, _I64, _I64, _I32, _SZ], True, _I32),
     "prismkv_union_n": ([_U64] * 6 + [_I32, _I32, _I64, _I64, _I32, _SZ], True, _I32),
     "prismkv_select_cap_n": ([_U64] * 5 + [_I32, _I32, _I64, _I64, _I32], True, _I32),
     # error handling of the bounded inter-workgroup waits

@@ -4,8 +4,12 @@ package's HIP kernels.
 
 The kernels are specialised to the native geometry of the decode path
 (src/prismkv/native8b.py:42-43): head_dim 128, F = 3000 buckets, GQA groups
-of 4 query heads, bf16 keys / values / queries on the device.  Inputs of
-another geometry raise NotImplementedError; there is no CPU path.
+of 4 query heads, on the device.  Like the reference, which computes on
+`.float()` of its inputs, keys / queries / values may be of any float dtype:
+bf16 inputs run the bf16 kernels, any other dtype is taken as `.float()`
+(exact for fp16, the reference's own rounding for fp64) and runs the fp32
+entry points, and outputs come back in the input's dtype.  Inputs of another
+geometry raise NotImplementedError; there is no CPU path.
 
 A FeatureIndex made here carries its device tables (tiled moments, bucket
 sizes, membership bitmap) in `index.native`, so routing, selection and
@@ -139,15 +143,24 @@ def _lists_from_bits(bits, lo, hi, offset=0):
     return list(torch.split(t + (lo + offset), per))
 
 
+def _native_rows(x, what):
+    """Rows of head_dim 128 for the kernels and the entry-point suffix: bf16
+    stays bf16 (""), any other float dtype becomes x.float() ("_f32")."""
+    _native(x.device.type == "cuda", f"{what} on the device")
+    _native(x.dtype.is_floating_point, f"floating-point {what}")
+    _native(x.shape[-1] == DIM, "head_dim 128")
+    suffix = ""
+    if x.dtype != torch.bfloat16:
+        x, suffix = x.float(), "_f32"
+    x = x if x.stride(-1) == 1 and (x.ndim == 1 or x.stride(-2) == DIM) else x.contiguous()
+    if x.data_ptr() % 16:
+        x = x.clone()
+    return x, suffix
+
+
 def _check_keys(keys):
-    _native(keys.device.type == "cuda", "keys on the device")
-    _native(keys.dtype == torch.bfloat16, "bf16 keys (the model's K cache dtype)")
-    _native(keys.shape[-1] == DIM, "head_dim 128")
     _native(len(keys) <= MAX_KEYS, f"at most {MAX_KEYS} keys per call")
-    keys = keys if keys.stride(-1) == 1 and keys.stride(0) == DIM else keys.contiguous()
-    if keys.data_ptr() % 16:
-        keys = keys.clone()
-    return keys
+    return _native_rows(keys, "keys")
 
 
 def _check_sae(sae):
@@ -188,7 +201,7 @@ def summarize(keys, lists, center=None):
     keys over each bucket's list (two passes), center = keys.float().mean(0)
     unless given."""
     n, d = keys.shape
-    keys = _check_keys(keys)
+    keys, suffix = _check_keys(keys)
     _native(len(lists) == FEATURES, "3000 bucket lists")
     lib = _lib_()
     t = NativeTables.empty(n, keys.device)
@@ -196,7 +209,7 @@ def summarize(keys, lists, center=None):
     c = torch.zeros(1, DIM, device=keys.device) if center is None else \
         torch.as_tensor(center).to(device=keys.device, dtype=torch.float32).reshape(1, DIM).clone()
     work = _work("summarize", lib.query("prismkv_summarize_work_bytes", 1), keys.device)
-    lib.call("prismkv_summarize", keys.data_ptr(), t.bits.data_ptr(), c.data_ptr(), t.n.data_ptr(),
+    lib.call("prismkv_summarize" + suffix, keys.data_ptr(), t.bits.data_ptr(), c.data_ptr(), t.n.data_ptr(),
              t.moments.data_ptr(), work.data_ptr(), 1, n, 1 if center is None else 0, keys.stride(0) * n, t.row_words,
              _lib.nbytes(work), stream=_stream())
     mean, var = untile_moments(t.moments)
@@ -222,7 +235,7 @@ def build_index(keys, sae, key_scale, *, center=None):
     if keys.shape[-1] != sae.head_dim:
         raise ValueError("SAE and attention head dimensions differ")
     _check_sae(sae)
-    keys = _check_keys(keys)
+    keys, suffix = _check_keys(keys)
     n, device = len(keys), keys.device
     lib = _lib_()
     t = NativeTables.empty(n, device)
@@ -231,7 +244,7 @@ def build_index(keys, sae, key_scale, *, center=None):
     c = torch.zeros(1, DIM, device=device) if center is None else \
         torch.as_tensor(center).to(device=device, dtype=torch.float32).reshape(1, DIM).clone()
     work = _fresh_work(lib.query("prismkv_build_work_bytes", 1, n), device)
-    lib.call("prismkv_build", keys.data_ptr(), W.data_ptr(), b.data_ptr(), c.data_ptr(), scale.data_ptr(),
+    lib.call("prismkv_build" + suffix, keys.data_ptr(), W.data_ptr(), b.data_ptr(), c.data_ptr(), scale.data_ptr(),
              t.bits.data_ptr(), t.n.data_ptr(), t.moments.data_ptr(), work.data_ptr(), 1, 1, n, int(sae.key_mean),
              1 if center is None else 0, keys.stride(0) * n, t.row_words, _lib.nbytes(work), stream=_stream())
     mean, var = untile_moments(t.moments)
@@ -253,7 +266,7 @@ def append_index(index, new_keys, sae, key_scale):
     if new_keys.shape[-1] != sae.head_dim:
         raise ValueError("SAE and attention head dimensions differ")
     _check_sae(sae)
-    new_keys = _check_keys(new_keys)
+    new_keys, suffix = _check_keys(new_keys)
     N, H, device = len(new_keys), index.history, new_keys.device
     _native(N <= MAX_BLOCK, f"append blocks of at most {MAX_BLOCK} keys")
     lib = _lib_()
@@ -265,9 +278,9 @@ def append_index(index, new_keys, sae, key_scale):
     # the kernels read K rows [H, H + N) of the buffer: address the block as those rows
     row_bytes = DIM * new_keys.element_size()
     base = new_keys.data_ptr() - H * row_bytes
-    lib.call("prismkv_update", base, W.data_ptr(), b.data_ptr(), c.data_ptr(), scale.data_ptr(), t.bits.data_ptr(),
-             t.n.data_ptr(), t.moments.data_ptr(), work.data_ptr(), 1, H, N, int(sae.key_mean), (H + N) * DIM,
-             t.row_words, _lib.nbytes(work), stream=_stream())
+    lib.call("prismkv_update" + suffix, base, W.data_ptr(), b.data_ptr(), c.data_ptr(), scale.data_ptr(),
+             t.bits.data_ptr(), t.n.data_ptr(), t.moments.data_ptr(), work.data_ptr(), 1, H, N, int(sae.key_mean),
+             (H + N) * DIM, t.row_words, _lib.nbytes(work), stream=_stream())
     mean, var = untile_moments(t.moments)
     new_lists = _lists_from_bits(t.bits, H, H + N)
     lists = [torch.cat((torch.as_tensor(old).to(device=device, dtype=torch.long), new))
@@ -281,10 +294,10 @@ def append_index(index, new_keys, sae, key_scale):
 # ------------------------------------------------------------------ stages 1-3
 
 def _check_q(q):
-    _native(q.device.type == "cuda", "queries on the device")
+    """[1, 4, 128] queries for the kernels and the entry-point suffix."""
     _native(tuple(q.shape) == (HEADS, DIM), "GQA groups of 4 query heads of head_dim 128")
-    _native(q.dtype == torch.bfloat16, "bf16 queries")
-    return q.contiguous().reshape(1, HEADS, DIM)
+    q, suffix = _native_rows(q, "queries")
+    return q.reshape(1, HEADS, DIM), suffix
 
 
 QA_WIDTH = 64  # the q_activation selection: up to 4 heads x 16 buckets
@@ -292,7 +305,7 @@ QA_WIDTH = 64  # the q_activation selection: up to 4 heads x 16 buckets
 
 def _route_qact(q, index, sae, query_scale, scores):
     t = _tables(index)
-    q1 = _check_q(q)
+    q1, suffix = _check_q(q)
     _check_sae(sae)
     lib = _lib_()
     device = q1.device
@@ -302,7 +315,7 @@ def _route_qact(q, index, sae, query_scale, scores):
     valid = torch.zeros(1, QA_WIDTH, device=device)
     raw = torch.zeros(1, dtype=torch.int32, device=device)
     work = _work("route_qact", lib.query("prismkv_route_qact_work_bytes", 1), device)
-    lib.call("prismkv_route_qact", q1.data_ptr(), W.data_ptr(), b.data_ptr(), qs.data_ptr(), t.n.data_ptr(),
+    lib.call("prismkv_route_qact" + suffix, q1.data_ptr(), W.data_ptr(), b.data_ptr(), qs.data_ptr(), t.n.data_ptr(),
              work.data_ptr(), features.data_ptr(), valid.data_ptr(), raw.data_ptr(), scores.data_ptr(), 1,
              _lib.nbytes(work), stream=_stream())
     return t, features, valid, raw
@@ -310,14 +323,14 @@ def _route_qact(q, index, sae, query_scale, scores):
 
 def _route(q, index, scores):
     t = _tables(index)
-    q1 = _check_q(q)
+    q1, suffix = _check_q(q)
     lib = _lib_()
     device = q1.device
     features = torch.zeros(1, TOPK, dtype=torch.int64, device=device)
     valid = torch.zeros(1, TOPK, device=device)
     raw = torch.zeros(1, dtype=torch.int32, device=device)
     work = _work("route", lib.query("prismkv_route_work_bytes", 1), device)
-    lib.call("prismkv_route_scores", q1.data_ptr(), t.moments.data_ptr(), t.n.data_ptr(), work.data_ptr(),
+    lib.call("prismkv_route_scores" + suffix, q1.data_ptr(), t.moments.data_ptr(), t.n.data_ptr(), work.data_ptr(),
              features.data_ptr(), valid.data_ptr(), raw.data_ptr(), scores.data_ptr(), 1, _lib.nbytes(work),
              stream=_stream())
     return t, features, valid, raw
@@ -406,30 +419,30 @@ def attend(q, keys, values, old_ids, history):
         raise ValueError("deduplicate history before attention")
     if len(old_ids) + len(keys) - history == 0:
         return q.new_zeros(q.shape)
-    q1 = _check_q(q)
-    for x in (keys, values):
-        _native(x.device.type == "cuda" and x.dtype == torch.bfloat16 and x.shape[-1] == DIM,
-                "bf16 K/V rows of head_dim 128 on the device")
-    keys = keys if keys.stride(-1) == 1 and keys.stride(0) == DIM else keys.contiguous()
-    values = values if values.stride(-1) == 1 and values.stride(0) == DIM else values.contiguous()
-    if keys.data_ptr() % 16:
-        keys = keys.clone()
-    if values.data_ptr() % 16:
-        values = values.clone()
+    _native(tuple(q.shape) == (HEADS, DIM), "GQA groups of 4 query heads of head_dim 128")
+    # q @ K^T and P @ V of core.py:182-183 on .float() of each operand: all
+    # bf16 runs the bf16 kernel, anything else the fp32 one on fp32 copies
+    for x, name in ((q, "queries"), (keys, "keys"), (values, "values")):
+        _native(x.dtype.is_floating_point, f"floating-point {name}")
+    bf16 = all(x.dtype == torch.bfloat16 for x in (q, keys, values))
+    dtype, suffix = (torch.bfloat16, "") if bf16 else (torch.float32, "_f32")
+    q1, keys, values = (_native_rows(x.to(dtype), name)[0] for x, name in
+                        ((q, "queries"), (keys, "keys"), (values, "values")))
+    q1 = q1.reshape(1, HEADS, DIM)
     L = len(keys)
     lib = _lib_()
     # an id row as wide as the history (the entry point's row stride), first len(old_ids) used
     ids = torch.zeros(1, max(history, len(old_ids), 1), dtype=torch.int32, device=q.device)
     ids[0, :len(old_ids)] = old_ids.to(device=q.device, dtype=torch.int32)
     count = torch.tensor([len(old_ids)], dtype=torch.int32, device=q.device)
-    out = torch.empty(1, HEADS, DIM, dtype=torch.bfloat16, device=q.device)
+    out = torch.empty(1, HEADS, DIM, dtype=dtype, device=q.device)
     work = _work("attend", lib.query("prismkv_attend_work_bytes", 1, ATTEND_SPLITS), q.device)
-    lib.call("prismkv_attend", q1.data_ptr(), keys.data_ptr(), values.data_ptr(), ids.data_ptr(), count.data_ptr(),
-             work.data_ptr(), out.data_ptr(), 1, history, L - history, L * DIM, L * DIM, ids.shape[1],
-             ATTEND_SPLITS, _lib.nbytes(work), stream=_stream())
+    lib.call("prismkv_attend" + suffix, q1.data_ptr(), keys.data_ptr(), values.data_ptr(), ids.data_ptr(),
+             count.data_ptr(), work.data_ptr(), out.data_ptr(), 1, history, L - history, L * DIM, L * DIM,
+             ids.shape[1], ATTEND_SPLITS, _lib.nbytes(work), stream=_stream())
     code = int(work[:4].view(torch.int32).item())
     if code:  # a bounded wait of the attention gave up (ids were checked above)
         work.zero_()
-        raise RuntimeError(f"prismkv_attend: {ERROR_MESSAGES.get(code, ERROR_MESSAGES[ERR_WAIT])}; "
+        raise RuntimeError(f"prismkv_attend{suffix}: {ERROR_MESSAGES.get(code, ERROR_MESSAGES[ERR_WAIT])}; "
                            "the workspace was reset")
     return out[0].to(q.dtype)

@@ -23,6 +23,10 @@
 // counter, restored to zero afterwards) merges the S split states and writes
 // the bf16 output; the compat entry point uses a separate merge launch.
 // Split states cross workgroups through write-through stores, not fences.
+//
+// prismkv_attend_f32 runs the same kernel on fp32 q / K / V (fp32 output):
+// each lane's 8 dims of a row are two 16-byte loads, and a slot takes 5 rows
+// per round instead of 9 so the rows in flight fit the same registers.
 #include "attend_core.h"
 
 namespace prismkv {
@@ -37,19 +41,23 @@ namespace {
 // count[g], so the id loads are issued together with the count load; then
 // every K and V row of the round (up to 36 per wave, 16 bytes per lane per
 // row) is requested before any is consumed.
-__device__ void attend_split(const AttendArgs& a, int g, int p, AttendLds& lds) {
+template <typename E>
+__device__ void attend_split(const AttendArgs<E>& a, int g, int p, AttendLds& lds) {
+  typedef Row8<E> RL;
+  constexpr int kRows = sizeof(E) == 2 ? kSlotRows : 5;  // rows per slot per round
+  constexpr int kRoundRows = 4 * kRows;                  // rows per wave per round
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int q16 = lane & 15, slot = lane >> 4;
   const int last_row = a.H + a.T - 1;
   const int nwaves = (kAT / 64) * a.S, gw = (kAT / 64) * p + w;
   const int32_t* idg = a.ids + (size_t)g * a.ids_stride;
-  const uint16_t* kg = a.k + (size_t)g * a.ks + 8 * q16;
-  const uint16_t* vg = a.v + (size_t)g * a.vs + 8 * q16;
+  const E* kg = a.k + (size_t)g * a.ks + 8 * q16;
+  const E* vg = a.v + (size_t)g * a.vs + 8 * q16;
 
   float qf[kHq][8];
 #pragma unroll
   for (int h = 0; h < kHq; ++h) {
-    unpack8(*reinterpret_cast<const uint4*>(a.q + ((size_t)g * kHq + h) * kD + 8 * q16), qf[h]);
+    unpack8(RL::load(a.q + ((size_t)g * kHq + h) * kD + 8 * q16), qf[h]);
 #pragma unroll
     for (int i = 0; i < 8; ++i) qf[h][i] *= kLog2eScale;
   }
@@ -65,10 +73,10 @@ __device__ void attend_split(const AttendArgs& a, int g, int p, AttendLds& lds) 
   bool bad = false;  // an id outside [0, H) or a count outside [0, H]
   for (int round = 0;; ++round) {
     // row i of this lane's slot in the round: list index j[i]
-    int jr[kSlotRows], idv[kSlotRows];
+    int jr[kRows], idv[kRows];
 #pragma unroll
-    for (int i = 0; i < kSlotRows; ++i) {
-      const int j = gw + nwaves * (round * kWaveRows + i * 4 + slot);
+    for (int i = 0; i < kRows; ++i) {
+      const int j = gw + nwaves * (round * kRoundRows + i * 4 + slot);
       jr[i] = j;
       idv[i] = a.H > 0 ? idg[j < a.H ? j : a.H - 1] : 0;  // speculative: meaningful only if j < count
     }
@@ -79,31 +87,31 @@ __device__ void attend_split(const AttendArgs& a, int g, int p, AttendLds& lds) 
       total = n_old + a.T;
     }
     if (!__ballot(jr[0] < total)) break;  // rows grow with i and round: nothing left for this wave
-    // every lane issues all 2 * kSlotRows gathers at once (rows past the end
+    // every lane issues all 2 * kRows gathers at once (rows past the end
     // re-read row 0 and are masked); the compiler waits per load, so step st
     // computes as soon as its own rows have landed, while later rows fly
-    uint4 kr[kSlotRows], vr[kSlotRows];
+    typename RL::Raw kr[kRows], vr[kRows];
 #pragma unroll
-    for (int i = 0; i < kSlotRows; ++i) {
+    for (int i = 0; i < kRows; ++i) {
       const int j = jr[i];
       const int p = j < n_old ? idv[i] : a.H + (j - n_old);
       bad |= j < n_old && (p < 0 || p >= a.H);
       const int pos = (j < total && p >= 0) ? (p > last_row ? last_row : p) : 0;
-      kr[i] = load_nt16(kg + (size_t)pos * kD);
-      vr[i] = load_nt16(vg + (size_t)pos * kD);
+      kr[i] = RL::load(kg + (size_t)pos * kD);
+      vr[i] = RL::load(vg + (size_t)pos * kD);
       if ((i & 3) == 3) asm volatile("" ::: "memory");  // issue the rows step by step, in order
     }
-    const int base = gw + nwaves * (round * kWaveRows + slot);  // list index of row i: base + 4 * nwaves * i
+    const int base = gw + nwaves * (round * kRoundRows + slot);  // list index of row i: base + 4 * nwaves * i
 #pragma unroll
-    for (int st = 0; st < (kSlotRows + 3) / 4; ++st) {
+    for (int st = 0; st < (kRows + 3) / 4; ++st) {
       int nv = 0;
-      uint4 ks[4], vs[4];
+      typename RL::Raw ks[4], vs[4];
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
         const int i = st * 4 + b;
-        nv += (i < kSlotRows) && (base + 4 * nwaves * i < total);
-        ks[b] = kr[i < kSlotRows ? i : kSlotRows - 1];
-        vs[b] = vr[i < kSlotRows ? i : kSlotRows - 1];
+        nv += (i < kRows) && (base + 4 * nwaves * i < total);
+        ks[b] = kr[i < kRows ? i : kRows - 1];
+        vs[b] = vr[i < kRows ? i : kRows - 1];
       }
       if (__ballot(nv > 0)) attend_step(qf, ks, vs, nv, s);
     }
@@ -114,8 +122,8 @@ __device__ void attend_split(const AttendArgs& a, int g, int p, AttendLds& lds) 
   store_wg_state(s, lds, a.state + (((size_t)g * kHq) * a.S + p) * kStateW, (size_t)a.S * kStateW);
 }
 
-__global__ __launch_bounds__(kAT) void attend_fused(AttendArgs a, unsigned* __restrict__ sync,
-                                                    uint16_t* __restrict__ out) {
+template <typename E>
+__global__ __launch_bounds__(kAT) void attend_fused(AttendArgs<E> a, unsigned* __restrict__ sync, E* __restrict__ out) {
   const int p = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
   __shared__ AttendLds lds;
   __shared__ int is_last;
@@ -129,7 +137,7 @@ __global__ __launch_bounds__(kAT) void attend_fused(AttendArgs a, unsigned* __re
   merge_group(a.state, a.S, g, out, lds.wts);
 }
 
-__global__ __launch_bounds__(kAT) void attend_split_only(AttendArgs a) {
+__global__ __launch_bounds__(kAT) void attend_split_only(AttendArgs<uint16_t> a) {
   __shared__ AttendLds lds;
   attend_split(a, blockIdx.y, blockIdx.x, lds);
 }
@@ -145,6 +153,25 @@ __global__ __launch_bounds__(kAT) void attend_merge(const float* __restrict__ st
 }  // namespace prismkv
 
 using namespace prismkv;
+
+extern "C" size_t prismkv_attend_work_bytes(int groups, int splits);
+
+// The split kernel with the last-arriving workgroup's merge over the work's
+// split states (after the decode-phase region, whose error word comes first).
+template <typename E>
+static int attend_split_launch(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t count, uint64_t work,
+                               uint64_t out, int groups, int H, int T, int64_t ks, int64_t vs, int64_t ids_stride,
+                               int splits, uint64_t stream) {
+  float* state = reinterpret_cast<float*>(reinterpret_cast<char*>(work) + attend_list_work_bytes(groups));
+  AttendArgs<E> a{reinterpret_cast<const E*>(q), reinterpret_cast<const E*>(k), reinterpret_cast<const E*>(v),
+                  reinterpret_cast<const int32_t*>(ids), reinterpret_cast<const int32_t*>(count), ks, vs, ids_stride,
+                  H, T, splits, state};
+  a.err = reinterpret_cast<unsigned*>(work);
+  unsigned* sync = reinterpret_cast<unsigned*>(state + (size_t)groups * kHq * splits * kStateW);
+  hipLaunchKernelGGL(attend_fused<E>, dim3(splits, groups), dim3(kAT), 0, (hipStream_t)stream, a, sync,
+                     reinterpret_cast<E*>(out));
+  return (int)hipGetLastError();
+}
 
 extern "C" {
 
@@ -168,15 +195,20 @@ int prismkv_attend(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t co
   // does not change the result (exact softmax), only the partition
   const int rc = attend_list(q, k, v, ids, count, work, out, groups, H, T, ks, vs, ids_stride, stream);
   if (rc != kBadSize) return rc;
-  float* state = reinterpret_cast<float*>(reinterpret_cast<char*>(work) + attend_list_work_bytes(groups));
-  AttendArgs a{reinterpret_cast<const uint16_t*>(q), reinterpret_cast<const uint16_t*>(k),
-               reinterpret_cast<const uint16_t*>(v), reinterpret_cast<const int32_t*>(ids),
-               reinterpret_cast<const int32_t*>(count), ks, vs, ids_stride, H, T, splits, state};
-  a.err = reinterpret_cast<unsigned*>(work);  // the decode-phase region's error word comes first
-  unsigned* sync = reinterpret_cast<unsigned*>(state + (size_t)groups * kHq * splits * kStateW);
-  hipLaunchKernelGGL(attend_fused, dim3(splits, groups), dim3(kAT), 0, (hipStream_t)stream, a, sync,
-                     reinterpret_cast<uint16_t*>(out));
-  return (int)hipGetLastError();
+  return attend_split_launch<uint16_t>(q, k, v, ids, count, work, out, groups, H, T, ks, vs, ids_stride, splits,
+                                      stream);
+}
+
+// fp32 q / K / V rows and fp32 output; the same work layout (error word first).
+int prismkv_attend_f32(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t count, uint64_t work, uint64_t out,
+                       int groups, int H, int T, int64_t ks, int64_t vs, int64_t ids_stride, int splits,
+                       size_t work_bytes, uint64_t stream) {
+  if (groups < 1 || groups > 65535 || H < 0 || T < 0 || splits < 1 || splits > 1024) return kBadSize;
+  if (ks < (int64_t)(H + T) * kD || vs < (int64_t)(H + T) * kD || ids_stride < H) return kBadSize;
+  if (!q || !k || !v || !ids || !count || !work || !out || ((q | k | v | (uint64_t)(ks | vs) * 4) & 15u))
+    return kBadSize;
+  if (work_bytes < prismkv_attend_work_bytes(groups, splits)) return kBadSize;
+  return attend_split_launch<float>(q, k, v, ids, count, work, out, groups, H, T, ks, vs, ids_stride, splits, stream);
 }
 
 // kernels/ppu_8b/av_tuned.cu:62-67 contract; state is the caller's
@@ -185,9 +217,9 @@ int attention_tuned(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t c
                     int H, int T, int KS, int VS, int S, int mode, uint64_t stream) {
   if (S < 1 || S > 128 || H < 1 || T < 0 || KS < (H + T) * kD || VS < (H + T) * kD) return kBadSize;
   if (mode < 0 || mode > 2) return kBadMode;
-  AttendArgs a{reinterpret_cast<const uint16_t*>(q), reinterpret_cast<const uint16_t*>(k),
-               reinterpret_cast<const uint16_t*>(v), reinterpret_cast<const int32_t*>(ids),
-               reinterpret_cast<const int32_t*>(cnt), KS, VS, H, H, T, S, reinterpret_cast<float*>(state)};
+  AttendArgs<uint16_t> a{reinterpret_cast<const uint16_t*>(q), reinterpret_cast<const uint16_t*>(k),
+                         reinterpret_cast<const uint16_t*>(v), reinterpret_cast<const int32_t*>(ids),
+                         reinterpret_cast<const int32_t*>(cnt), KS, VS, H, H, T, S, reinterpret_cast<float*>(state)};
   hipLaunchKernelGGL(attend_split_only, dim3(S, 8), dim3(kAT), 0, (hipStream_t)stream, a);
   hipLaunchKernelGGL(attend_merge, dim3(8), dim3(kAT), 0, (hipStream_t)stream,
                      reinterpret_cast<const float*>(state), reinterpret_cast<uint16_t*>(out), S);

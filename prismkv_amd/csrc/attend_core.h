@@ -13,10 +13,12 @@ constexpr float kLog2eScale = 0.12751743082459868f;  // log2(e) / sqrt(128): sco
 constexpr float kSlack = 8.0f;                     // lazy-rescale threshold (log2 units)
 constexpr int kStepRows = 16;                      // rows per wave step (4 slots x 4 rows)
 
+// E: the element type of q, K, V and the output (uint16_t = bf16 bits, or float).
+template <typename E>
 struct AttendArgs {
-  const uint16_t* q;
-  const uint16_t* k;
-  const uint16_t* v;
+  const E* q;
+  const E* k;
+  const E* v;
   const int32_t* ids;
   const int32_t* cnt;
   int64_t ks, vs, ids_stride;
@@ -31,6 +33,33 @@ __device__ __forceinline__ void unpack8(const uint4 r, float (&f)[8]) {
   f[4] = bf16_lo(r.z); f[5] = bf16_hi(r.z);
   f[6] = bf16_lo(r.w); f[7] = bf16_hi(r.w);
 }
+
+// 8 consecutive fp32 dims as loaded (two 16-byte loads).
+struct F32x8 {
+  uint4 a, b;
+};
+__device__ __forceinline__ void unpack8(const F32x8& r, float (&f)[8]) {
+  f[0] = __uint_as_float(r.a.x); f[1] = __uint_as_float(r.a.y);
+  f[2] = __uint_as_float(r.a.z); f[3] = __uint_as_float(r.a.w);
+  f[4] = __uint_as_float(r.b.x); f[5] = __uint_as_float(r.b.y);
+  f[6] = __uint_as_float(r.b.z); f[7] = __uint_as_float(r.b.w);
+}
+
+// The raw 8-dim load of one element type, and the output conversion.
+template <typename E>
+struct Row8;
+template <>
+struct Row8<uint16_t> {
+  typedef uint4 Raw;
+  static __device__ __forceinline__ Raw load(const uint16_t* p) { return load_nt16(p); }
+  static __device__ __forceinline__ uint16_t out(float x) { return f32_to_bf16(x); }
+};
+template <>
+struct Row8<float> {
+  typedef F32x8 Raw;
+  static __device__ __forceinline__ Raw load(const float* p) { return F32x8{load_nt16(p), load_nt16(p + 4)}; }
+  static __device__ __forceinline__ float out(float x) { return x; }
+};
 
 __device__ __forceinline__ float exp2_or_zero(float x) { return x == -INFINITY ? 0.f : exp2f(x); }
 
@@ -58,8 +87,9 @@ struct SlotState {
 };
 
 // One step: 4 rows per slot (row b of slot = rows[b]); kr/vr hold the loaded
-// lines; ok[b] marks real rows.
-__device__ __forceinline__ void attend_step(const float (&qf)[kHq][8], const uint4 (&kr)[4], const uint4 (&vr)[4],
+// lines (R: uint4 of 8 bf16 dims or F32x8); rows b >= nvalid are masked.
+template <typename R>
+__device__ __forceinline__ void attend_step(const float (&qf)[kHq][8], const R (&kr)[4], const R (&vr)[4],
                                             int nvalid, SlotState& s) {
   const int lane = threadIdx.x & 63, q16 = lane & 15, slot0 = lane & 48;
   float x[16];
@@ -182,11 +212,12 @@ __device__ void store_wg_state(const SlotState& s, AttendLds& lds, float* stp, s
 }
 
 // Merges the S split states of group g into out[g] (thread = head tid >> 7,
-// dim tid & 127).  Splits go in batches of 32: each thread issues its 32
+// dim tid & 127; out of element type E).  Splits go in batches of 32: each thread issues its 32
 // accumulator loads and each wave its 32 (max, den) loads before any is
 // used, so S <= 32 costs one memory round trip.  The caller has seen every
 // split's arrival (the states are complete when this runs).
-__device__ void merge_group(const float* state, int S, int g, uint16_t* out, float (&wts)[kAT / 64][64]) {
+template <typename E>
+__device__ void merge_group(const float* state, int S, int g, E* out, float (&wts)[kAT / 64][64]) {
   const int tid = threadIdx.x, h = tid >> 7, d = tid & (kD - 1), w = tid >> 6, lane = tid & 63;
   const float* st = state + (size_t)(g * kHq + h) * S * kStateW;
   float M = -INFINITY, den = 0.f, v = 0.f;
@@ -213,7 +244,7 @@ __device__ void merge_group(const float* state, int S, int g, uint16_t* out, flo
 #pragma unroll
     for (int i = 0; i < 32; ++i) v = fmaf(wts[w][i], av[i], v);
   }
-  out[((size_t)g * kHq + h) * kD + d] = f32_to_bf16(den > 0.f ? v / den : 0.f);
+  out[((size_t)g * kHq + h) * kD + d] = Row8<E>::out(den > 0.f ? v / den : 0.f);
 }
 
 }  // namespace

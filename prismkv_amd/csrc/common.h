@@ -24,6 +24,9 @@ constexpr int kBadMode = -2;
 __device__ __forceinline__ float bf16_lo(uint32_t u) { return __uint_as_float(u << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+// An input element (bf16 bits or fp32) as fp32: the widening is exact.
+__device__ __forceinline__ float to_f32(uint16_t h) { return bf16_to_f32(h); }
+__device__ __forceinline__ float to_f32(float x) { return x; }
 
 // fp32 -> bf16, round to nearest even, NaN kept quiet.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {

@@ -45,7 +45,8 @@ struct RouteWork {
   float* stats;   // [G][kChunks][4][2] (chunk max, chunk sum of exp)
 };
 
-__global__ __launch_bounds__(kRT) void route_score_kernel(const uint16_t* __restrict__ q,
+template <typename QT>
+__global__ __launch_bounds__(kRT) void route_score_kernel(const QT* __restrict__ q,
                                                           const float* __restrict__ moments,
                                                           const int* __restrict__ counts, RouteWork work) {
   const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
@@ -164,14 +165,15 @@ __global__ __launch_bounds__(64) void route_final_kernel(const unsigned long lon
 constexpr int kQaParts = (kF + kRT - 1) / kRT;  // 12
 constexpr int kQaSel = kHq * kTop;               // 64
 
-__global__ __launch_bounds__(kRT) void qact_part_kernel(const uint16_t* __restrict__ q, const float* __restrict__ W,
+template <typename QT>
+__global__ __launch_bounds__(kRT) void qact_part_kernel(const QT* __restrict__ q, const float* __restrict__ W,
                                                         const float* __restrict__ b, const float* __restrict__ qscale,
                                                         unsigned long long* __restrict__ cand) {
   const int j = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   __shared__ float xs[kHq][kD];
   __shared__ __align__(16) unsigned long long keys[kHq][kRT];
   const float qs = qscale[g];
-  for (int i = tid; i < kHq * kD; i += kRT) xs[i / kD][i % kD] = bf16_to_f32(q[(size_t)g * kHq * kD + i]) / qs;
+  for (int i = tid; i < kHq * kD; i += kRT) xs[i / kD][i % kD] = to_f32(q[(size_t)g * kHq * kD + i]) / qs;
   __syncthreads();
   const int f = j * kRT + tid;
   float acc[kHq] = {0.f, 0.f, 0.f, 0.f};
@@ -347,9 +349,10 @@ __global__ void pack_kernel(const uint16_t* __restrict__ q, float* __restrict__ 
 
 using namespace prismkv;
 
-static void launch_route_score(const uint16_t* q, const float* moments, const int* counts, float* logits,
-                               float* stats, int groups, hipStream_t stream) {
-  hipLaunchKernelGGL(route_score_kernel, dim3(kChunks, groups), dim3(kRT), 0, stream, q, moments, counts,
+template <typename QT>
+static void launch_route_score(const QT* q, const float* moments, const int* counts, float* logits, float* stats,
+                               int groups, hipStream_t stream) {
+  hipLaunchKernelGGL(route_score_kernel<QT>, dim3(kChunks, groups), dim3(kRT), 0, stream, q, moments, counts,
                      RouteWork{logits, stats});
 }
 
@@ -365,6 +368,9 @@ size_t prismkv_route_work_bytes(int groups) {
   return route_logits_bytes(groups) + route_stats_bytes(groups) + route_cand_bytes(groups);
 }
 
+}  // extern "C"
+
+template <typename QT>
 static int route_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
                       uint64_t valid, uint64_t raw, float* scores, int groups, size_t work_bytes, uint64_t stream) {
   if (groups < 1 || groups > 65535) return kBadSize;
@@ -373,7 +379,7 @@ static int route_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t wo
   char* base = reinterpret_cast<char*>(work);
   RouteWork rw{reinterpret_cast<float*>(base), reinterpret_cast<float*>(base + route_logits_bytes(groups))};
   hipStream_t s = (hipStream_t)stream;
-  launch_route_score(reinterpret_cast<const uint16_t*>(q), reinterpret_cast<const float*>(moments),
+  launch_route_score(reinterpret_cast<const QT*>(q), reinterpret_cast<const float*>(moments),
                      reinterpret_cast<const int*>(counts), rw.logits, rw.stats, groups, s);
   unsigned long long* cand =
       reinterpret_cast<unsigned long long*>(base + route_logits_bytes(groups) + route_stats_bytes(groups));
@@ -384,17 +390,27 @@ static int route_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t wo
   return (int)hipGetLastError();
 }
 
+extern "C" {
+
 int prismkv_route(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features, uint64_t valid,
                   uint64_t raw, int groups, size_t work_bytes, uint64_t stream) {
-  return route_impl(q, moments, counts, work, features, valid, raw, nullptr, groups, work_bytes, stream);
+  return route_impl<uint16_t>(q, moments, counts, work, features, valid, raw, nullptr, groups, work_bytes, stream);
 }
 
 int prismkv_route_scores(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
                          uint64_t valid, uint64_t raw, uint64_t scores, int groups, size_t work_bytes,
                          uint64_t stream) {
   if (!scores) return kBadSize;
-  return route_impl(q, moments, counts, work, features, valid, raw, reinterpret_cast<float*>(scores), groups,
-                    work_bytes, stream);
+  return route_impl<uint16_t>(q, moments, counts, work, features, valid, raw, reinterpret_cast<float*>(scores),
+                              groups, work_bytes, stream);
+}
+
+int prismkv_route_scores_f32(uint64_t q, uint64_t moments, uint64_t counts, uint64_t work, uint64_t features,
+                             uint64_t valid, uint64_t raw, uint64_t scores, int groups, size_t work_bytes,
+                             uint64_t stream) {
+  if (!scores) return kBadSize;
+  return route_impl<float>(q, moments, counts, work, features, valid, raw, reinterpret_cast<float*>(scores), groups,
+                           work_bytes, stream);
 }
 
 size_t prismkv_route_qact_work_bytes(int groups) {
@@ -402,21 +418,40 @@ size_t prismkv_route_qact_work_bytes(int groups) {
   return (size_t)groups * kHq * kQaParts * kTop * sizeof(unsigned long long);
 }
 
-int prismkv_route_qact(uint64_t q, uint64_t W, uint64_t b, uint64_t qscale, uint64_t counts, uint64_t work,
-                       uint64_t features, uint64_t valid, uint64_t raw, uint64_t scores, int groups, size_t work_bytes,
-                       uint64_t stream) {
+}  // extern "C"
+
+template <typename QT>
+static int route_qact_impl(uint64_t q, uint64_t W, uint64_t b, uint64_t qscale, uint64_t counts, uint64_t work,
+                           uint64_t features, uint64_t valid, uint64_t raw, uint64_t scores, int groups,
+                           size_t work_bytes, uint64_t stream) {
   if (groups < 1 || groups > 65535) return kBadSize;
   if (!q || !W || !b || !qscale || !counts || !work || !features || !valid || !raw || (W & 15u)) return kBadSize;
   if (work_bytes < prismkv_route_qact_work_bytes(groups)) return kBadSize;
   hipStream_t s = (hipStream_t)stream;
   unsigned long long* cand = reinterpret_cast<unsigned long long*>(work);
-  hipLaunchKernelGGL(qact_part_kernel, dim3(kQaParts, groups), dim3(kRT), 0, s, reinterpret_cast<const uint16_t*>(q),
+  hipLaunchKernelGGL(qact_part_kernel<QT>, dim3(kQaParts, groups), dim3(kRT), 0, s, reinterpret_cast<const QT*>(q),
                      reinterpret_cast<const float*>(W), reinterpret_cast<const float*>(b),
                      reinterpret_cast<const float*>(qscale), cand);
   hipLaunchKernelGGL(qact_final_kernel, dim3(groups), dim3(kRT), 0, s, cand, reinterpret_cast<const int*>(counts),
                      reinterpret_cast<int64_t*>(features), reinterpret_cast<float*>(valid),
                      reinterpret_cast<int*>(raw), reinterpret_cast<float*>(scores));
   return (int)hipGetLastError();
+}
+
+extern "C" {
+
+int prismkv_route_qact(uint64_t q, uint64_t W, uint64_t b, uint64_t qscale, uint64_t counts, uint64_t work,
+                       uint64_t features, uint64_t valid, uint64_t raw, uint64_t scores, int groups, size_t work_bytes,
+                       uint64_t stream) {
+  return route_qact_impl<uint16_t>(q, W, b, qscale, counts, work, features, valid, raw, scores, groups, work_bytes,
+                                   stream);
+}
+
+int prismkv_route_qact_f32(uint64_t q, uint64_t W, uint64_t b, uint64_t qscale, uint64_t counts, uint64_t work,
+                           uint64_t features, uint64_t valid, uint64_t raw, uint64_t scores, int groups,
+                           size_t work_bytes, uint64_t stream) {
+  return route_qact_impl<float>(q, W, b, qscale, counts, work, features, valid, raw, scores, groups, work_bytes,
+                                stream);
 }
 
 int pack(uint64_t q, uint64_t a, uint64_t stream) {

@@ -51,12 +51,14 @@ struct TileLds {
   float dots[2][kHq][kChunk];   // [part][head][bucket]
 };
 
-// q (rows k < 128) and q*q (rows k >= 128) of group g, 4 heads per float4:
-// thread t of nt stages entries t, t + nt, ... of the 512.
-__device__ __forceinline__ void stage_query(const uint16_t* q, int g, float4* qq, int t, int nt) {
+// q (rows k < 128) and q*q (rows k >= 128) of group g, 4 heads per float4,
+// from bf16 or fp32 queries: thread t of nt stages entries t, t + nt, ... of
+// the 512.
+template <typename QT>
+__device__ __forceinline__ void stage_query(const QT* q, int g, float4* qq, int t, int nt) {
   for (int i = t; i < kHq * kD; i += nt) {
     const int h = i >> 7, k = i & (kD - 1);
-    const float x = bf16_to_f32(q[((size_t)g * kHq + h) * kD + k]);
+    const float x = to_f32(q[((size_t)g * kHq + h) * kD + k]);
     reinterpret_cast<float*>(&qq[k])[h] = x;
     reinterpret_cast<float*>(&qq[kD + k])[h] = x * x;  // core.py:127 q.square() in fp32
   }

@@ -38,7 +38,11 @@
 //   ties     only when ties overflow the budget: per contiguous range of a,
 //            count the ties, then take the first `need` in flat order;
 //   moments  per 32-bucket tile: new members from the bitmap, two-pass
-//            moments of their bf16 keys, merge, counts += new.
+//            moments of their keys, merge, counts += new.
+// Keys are the model's bf16 K cache or fp32 rows (the `_f32` entry points):
+// the kernels that read keys take the element type as a template argument
+// and widen every key to fp32 at the load, so both compute the same fp32 /
+// double arithmetic on the values they are given.
 // The build runs the same selection over all H keys of a group (in batches
 // of groups, so the activations of one batch fit the workspace) after a
 // center pass and a bitmap clear, and computes every bucket's moments from
@@ -70,8 +74,47 @@ constexpr int kBuildCenter = 1;      // prismkv_build flag: compute the center (
 enum { kMode = 0, kPrefix, kRem, kTau, kNeed, kTies, kOrdered, kCount, kListed, kListLen, kCtl = 16 };
 enum { kModeTopK = 0, kModeAllPositive = 1 };
 
+// Key loads of the two key element types: 2, 4 or 8 consecutive dims as the
+// raw loaded bits (kept packed while in flight) and their fp32 values.
+template <typename KT>
+struct KeyLoad;
+
+template <>
+struct KeyLoad<uint16_t> {  // bf16
+  typedef uint32_t Raw2;
+  typedef uint2 Raw4;
+  static __device__ __forceinline__ Raw2 load2(const uint16_t* p) { return *reinterpret_cast<const uint32_t*>(p); }
+  static __device__ __forceinline__ float lo(Raw2 r) { return bf16_lo(r); }
+  static __device__ __forceinline__ float hi(Raw2 r) { return bf16_hi(r); }
+  static __device__ __forceinline__ Raw4 load4(const uint16_t* p) { return *reinterpret_cast<const uint2*>(p); }
+  static __device__ __forceinline__ float4 f4(Raw4 r) {
+    return make_float4(bf16_lo(r.x), bf16_hi(r.x), bf16_lo(r.y), bf16_hi(r.y));
+  }
+  static __device__ __forceinline__ void load8(const uint16_t* p, float (&x)[8]) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    x[0] = bf16_lo(v.x); x[1] = bf16_hi(v.x); x[2] = bf16_lo(v.y); x[3] = bf16_hi(v.y);
+    x[4] = bf16_lo(v.z); x[5] = bf16_hi(v.z); x[6] = bf16_lo(v.w); x[7] = bf16_hi(v.w);
+  }
+};
+
+template <>
+struct KeyLoad<float> {
+  typedef float2 Raw2;
+  typedef float4 Raw4;
+  static __device__ __forceinline__ Raw2 load2(const float* p) { return *reinterpret_cast<const float2*>(p); }
+  static __device__ __forceinline__ float lo(Raw2 r) { return r.x; }
+  static __device__ __forceinline__ float hi(Raw2 r) { return r.y; }
+  static __device__ __forceinline__ Raw4 load4(const float* p) { return *reinterpret_cast<const float4*>(p); }
+  static __device__ __forceinline__ float4 f4(Raw4 r) { return r; }
+  static __device__ __forceinline__ void load8(const float* p, float (&x)[8]) {
+    const float4 a = reinterpret_cast<const float4*>(p)[0], b = reinterpret_cast<const float4*>(p)[1];
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w;
+    x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+  }
+};
+
 struct UpdateArgs {
-  const uint16_t* k;  // K cache; the block is rows [H, H+N) of each group
+  const void* k;      // K rows (bf16 or fp32); the block is rows [H, H+N) of each group
   int64_t ks;         // group stride (elements)
   const float* W;     // [G][F][128]
   const float* b;     // [G][F]
@@ -123,13 +166,16 @@ constexpr int kEncTokens = kET / 64 * kRowTile;   // tokens per workgroup (128)
 constexpr int kEncMinWgs = 512;                   // workgroups the bucket-tile parts aim for
 constexpr int kWLoads = kFT * kD / 4 / kET;       // float4 of a W tile per thread (4)
 
-// K chunk kb (4 bf16 dims 16 kb + 4 q ..) of token row t0 + i for lane (i, q).
-__device__ __forceinline__ uint2 key_chunk(const UpdateArgs& a, int g, int t0, int kb) {
+// K chunk kb (4 dims 16 kb + 4 q ..) of token row t0 + i for lane (i, q).
+template <typename KT>
+__device__ __forceinline__ typename KeyLoad<KT>::Raw4 key_chunk(const UpdateArgs& a, int g, int t0, int kb) {
   const int li = threadIdx.x & 15, lq = (threadIdx.x >> 4) & 3;
   const int row = min(t0 + li, a.N - 1);  // rows past the block repeat the last one (masked at the store)
-  return *reinterpret_cast<const uint2*>(a.k + (size_t)g * a.ks + (size_t)(a.H + row) * kD + 16 * kb + 4 * lq);
+  const KT* k = static_cast<const KT*>(a.k);
+  return KeyLoad<KT>::load4(k + (size_t)g * a.ks + (size_t)(a.H + row) * kD + 16 * kb + 4 * lq);
 }
 
+template <typename KT>
 __global__ __launch_bounds__(kET) void encode_kernel(UpdateArgs a) {
   const int y = blockIdx.x, part = blockIdx.y, parts = gridDim.y, g = blockIdx.z, tid = threadIdx.x;
   const int w = tid >> 6, lane = tid & 63, li = lane & 15, lq = lane >> 4;
@@ -137,9 +183,9 @@ __global__ __launch_bounds__(kET) void encode_kernel(UpdateArgs a) {
   __shared__ __align__(16) float cs[kD];              // center
   __shared__ unsigned hist[kBins];
   const int t0 = y * kEncTokens + w * kRowTile;  // the wave's first token
-  uint2 kr[kD / 16];
+  typename KeyLoad<KT>::Raw4 kr[kD / 16];
 #pragma unroll
-  for (int kb = 0; kb < kD / 16; ++kb) kr[kb] = key_chunk(a, g, t0, kb);
+  for (int kb = 0; kb < kD / 16; ++kb) kr[kb] = key_chunk<KT>(a, g, t0, kb);
   const float* wg = a.W + (size_t)g * kF * kD;
   // thread tid moves float4 tid + kET u of a 64 x 128 W tile (bucket i / 32, dims 4 (i % 32) ..)
   auto load_w = [&](int ft, float4 (&r)[kWLoads]) {
@@ -167,10 +213,9 @@ __global__ __launch_bounds__(kET) void encode_kernel(UpdateArgs a) {
   float4 xs[kD / 16];
 #pragma unroll
   for (int kb = 0; kb < kD / 16; ++kb) {
-    const uint2 r = kr[kb];
+    const float4 r = KeyLoad<KT>::f4(kr[kb]);
     const float4 c = *reinterpret_cast<const float4*>(&cs[16 * kb + 4 * lq]);
-    xs[kb] = make_float4((bf16_lo(r.x) - c.x) / sc, (bf16_hi(r.x) - c.y) / sc, (bf16_lo(r.y) - c.z) / sc,
-                         (bf16_hi(r.y) - c.w) / sc);
+    xs[kb] = make_float4((r.x - c.x) / sc, (r.y - c.y) / sc, (r.z - c.z) / sc, (r.w - c.w) / sc);
   }
   store_w(0, wr);
   __syncthreads();
@@ -566,6 +611,7 @@ __device__ __forceinline__ float merge_var(float a, float b, float den, float ma
   return v + ((a * b) / (den * den)) * (d * d);
 }
 
+template <typename KT>
 __global__ __launch_bounds__(kUT) void moments_kernel(UpdateArgs a) {
   const int c = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   __shared__ float nm[kChunk][kD], nv[kChunk][kD];
@@ -575,7 +621,8 @@ __global__ __launch_bounds__(kUT) void moments_kernel(UpdateArgs a) {
   extern __shared__ int toks_all[];
   int* toks = toks_all + (size_t)w * a.N;
   const int w_lo = a.H >> 5, w_hi = (a.H + a.N - 1) >> 5;
-  const uint16_t* kg = a.k + (size_t)g * a.ks;
+  typedef KeyLoad<KT> KL;
+  const KT* kg = static_cast<const KT*>(a.k) + (size_t)g * a.ks;
   // the first 64 bitmap words of the wave's 8 buckets, all requested at once
   // (the whole block's words up to 2016 tokens)
   constexpr int kCols = kChunk / 4;
@@ -613,18 +660,18 @@ __global__ __launch_bounds__(kUT) void moments_kernel(UpdateArgs a) {
     // 2l, 2l+1.  Members are summed in ascending order; their key words are
     // requested kMomBatch at a time, and a bucket of at most kMomBatch members
     // keeps them in registers for the second pass.
-    auto key_word = [&](int i) { return *reinterpret_cast<const uint32_t*>(kg + (size_t)toks[i] * kD + 2 * lane); };
+    auto key_word = [&](int i) { return KL::load2(kg + (size_t)toks[i] * kD + 2 * lane); };
     float s0 = 0.f, s1 = 0.f;
-    uint32_t kept[kMomBatch];
+    typename KL::Raw2 kept[kMomBatch];
     for (int i0 = 0; i0 < b; i0 += kMomBatch) {  // uniform
-      uint32_t r[kMomBatch];
+      typename KL::Raw2 r[kMomBatch];
 #pragma unroll
       for (int u = 0; u < kMomBatch; ++u) r[u] = key_word(min(i0 + u, b - 1));  // unconditional: one round trip
 #pragma unroll
       for (int u = 0; u < kMomBatch; ++u) {
         if (i0 + u < b) {
-          s0 += bf16_lo(r[u]);
-          s1 += bf16_hi(r[u]);
+          s0 += KL::lo(r[u]);
+          s1 += KL::hi(r[u]);
         }
         kept[u] = r[u];
       }
@@ -635,19 +682,19 @@ __global__ __launch_bounds__(kUT) void moments_kernel(UpdateArgs a) {
 #pragma unroll
       for (int u = 0; u < kMomBatch; ++u)
         if (u < b) {
-          const float d0 = bf16_lo(kept[u]) - m0, d1 = bf16_hi(kept[u]) - m1;
+          const float d0 = KL::lo(kept[u]) - m0, d1 = KL::hi(kept[u]) - m1;
           q0 += d0 * d0;
           q1 += d1 * d1;
         }
     } else {
       for (int i0 = 0; i0 < b; i0 += kMomBatch) {
-        uint32_t r[kMomBatch];
+        typename KL::Raw2 r[kMomBatch];
 #pragma unroll
         for (int u = 0; u < kMomBatch; ++u) r[u] = key_word(min(i0 + u, b - 1));
 #pragma unroll
         for (int u = 0; u < kMomBatch; ++u)
           if (i0 + u < b) {
-            const float d0 = bf16_lo(r[u]) - m0, d1 = bf16_hi(r[u]) - m1;
+            const float d0 = KL::lo(r[u]) - m0, d1 = KL::hi(r[u]) - m1;
             q0 += d0 * d0;
             q1 += d1 * d1;
           }
@@ -695,20 +742,22 @@ __global__ __launch_bounds__(kUT) void moments_kernel(UpdateArgs a) {
 // (thread = row step tid >> 4 of 16, dims 8 (tid & 15) ..);
 // center_final_kernel: grid G x 128 adds the parts in order, divides by N.
 // ---------------------------------------------------------------------------
+template <typename KT>
 __global__ __launch_bounds__(kUT) void center_part_kernel(UpdateArgs a, double* part) {
   const int p = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
   __shared__ double red[kUT / 16][kD];
   const int R = (a.N + kCenterParts - 1) / kCenterParts;
   const int lo = min(a.N, p * R), hi = min(a.N, lo + R);
   const int r = tid >> 4, d0 = (tid & 15) * 8;
-  const uint16_t* kg = a.k + (size_t)g * a.ks + (size_t)a.H * kD;
+  const KT* kg = static_cast<const KT*>(a.k) + (size_t)g * a.ks + (size_t)a.H * kD;
   double acc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0.0;
   for (int t = lo + r; t < hi; t += kUT / 16) {
-    const uint4 v = *reinterpret_cast<const uint4*>(kg + (size_t)t * kD + d0);
-    acc[0] += bf16_lo(v.x); acc[1] += bf16_hi(v.x); acc[2] += bf16_lo(v.y); acc[3] += bf16_hi(v.y);
-    acc[4] += bf16_lo(v.z); acc[5] += bf16_hi(v.z); acc[6] += bf16_lo(v.w); acc[7] += bf16_hi(v.w);
+    float x[8];
+    KeyLoad<KT>::load8(kg + (size_t)t * kD + d0, x);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] += x[j];
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) red[r][d0 + j] = acc[j];
@@ -781,14 +830,13 @@ __device__ __forceinline__ unsigned compact_chunk(const uint32_t* row, int w0, i
   return total;
 }
 
-template <bool kDev>
-__device__ __forceinline__ void accumulate_rows(const uint16_t* kg, const int* toks, unsigned n, int slot, int d0,
+template <bool kDev, typename KT>
+__device__ __forceinline__ void accumulate_rows(const KT* kg, const int* toks, unsigned n, int slot, int d0,
                                                 const float (&m)[8], double (&acc)[8]) {
 #pragma unroll 4
   for (unsigned i = slot; i < n; i += kSlots) {
-    const uint4 v = *reinterpret_cast<const uint4*>(kg + (size_t)toks[i] * kD + d0);
-    const float x[8] = {bf16_lo(v.x), bf16_hi(v.x), bf16_lo(v.y), bf16_hi(v.y),
-                        bf16_lo(v.z), bf16_hi(v.z), bf16_lo(v.w), bf16_hi(v.w)};
+    float x[8];
+    KeyLoad<KT>::load8(kg + (size_t)toks[i] * kD + d0, x);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       if constexpr (kDev) {
@@ -803,8 +851,8 @@ __device__ __forceinline__ void accumulate_rows(const uint16_t* kg, const int* t
 
 // One pass over the members (kDev: squared deviations from m), reduced over
 // the slots into red[0][..] order-fixed sums for tid < kD (returned).
-template <bool kDev>
-__device__ double bucket_pass(BuildMomentsLds& L, const uint32_t* row, const uint16_t* kg, int nw, int N, bool kept,
+template <bool kDev, typename KT>
+__device__ double bucket_pass(BuildMomentsLds& L, const uint32_t* row, const KT* kg, int nw, int N, bool kept,
                               unsigned n, const float (&m)[8]) {
   const int tid = threadIdx.x, slot = tid >> 4, d0 = (tid & 15) * 8;
   double acc[8];
@@ -831,11 +879,12 @@ __device__ double bucket_pass(BuildMomentsLds& L, const uint32_t* row, const uin
   return t;
 }
 
+template <typename KT>
 __global__ __launch_bounds__(kUT) void build_moments_kernel(UpdateArgs a) {
   const int f = blockIdx.x, g = blockIdx.y, tid = threadIdx.x;
   __shared__ BuildMomentsLds L;
   const uint32_t* row = a.bits + ((size_t)g * kF + f) * a.row_words;
-  const uint16_t* kg = a.k + (size_t)g * a.ks;
+  const KT* kg = static_cast<const KT*>(a.k) + (size_t)g * a.ks;
   const int nw = (a.N + 31) >> 5;
   // count the members, keeping the list while it fits
   unsigned n = 0;
@@ -1051,7 +1100,7 @@ static UpdateArgs make_args(uint64_t k, uint64_t W, uint64_t b, uint64_t center,
                             int64_t ks, int64_t row_words, const UpdateLayout& L) {
   char* w = reinterpret_cast<char*>(work);
   UpdateArgs a;
-  a.k = reinterpret_cast<const uint16_t*>(k);
+  a.k = reinterpret_cast<const void*>(k);
   a.ks = ks;
   a.W = reinterpret_cast<const float*>(W);
   a.b = reinterpret_cast<const float*>(b);
@@ -1081,10 +1130,11 @@ static UpdateArgs make_args(uint64_t k, uint64_t W, uint64_t b, uint64_t center,
 
 // encode .. ties: the exact batch-wide positive Top-k of the N keys' activations
 // and their bitmap bits.
+template <typename KT>
 static void launch_selection(const UpdateArgs& a, int groups, hipStream_t s) {
   const int token_tiles = (a.N + kEncTokens - 1) / kEncTokens;
   const int parts = std::max(1, std::min(kFTiles, (kEncMinWgs + token_tiles * groups - 1) / (token_tiles * groups)));
-  hipLaunchKernelGGL(encode_kernel, dim3(token_tiles, parts, groups), dim3(kET), 0, s, a);
+  hipLaunchKernelGGL(encode_kernel<KT>, dim3(token_tiles, parts, groups), dim3(kET), 0, s, a);
   hipLaunchKernelGGL(digit_kernel, dim3(groups), dim3(kUT), 0, s, a, 0);
   for (int level = 1; level < kLevels; ++level) {
     hipLaunchKernelGGL(refine_kernel, dim3(kRefineBlocks, groups), dim3(kUT), 0, s, a, level);
@@ -1096,7 +1146,94 @@ static void launch_selection(const UpdateArgs& a, int groups, hipStream_t s) {
   hipLaunchKernelGGL(tie_take_kernel, dim3(tie_grid, groups), dim3(kUT), 0, s, a);
 }
 
-static bool aligned16(uint64_t p, int64_t stride_elems) { return ((p | (uint64_t)(stride_elems * 2)) & 15u) == 0; }
+template <typename KT>
+static bool aligned16(uint64_t p, int64_t stride_elems) {
+  return ((p | (uint64_t)(stride_elems * (int64_t)sizeof(KT))) & 15u) == 0;
+}
+
+template <typename KT>
+static int update_impl(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
+                       uint64_t counts, uint64_t moments, uint64_t work, int groups, int H, int N, int key_mean,
+                       int64_t ks, int64_t row_words, size_t work_bytes, uint64_t stream) {
+  if (groups < 1 || groups > 65535 || H < 0 || N < 1 || N > kMaxBlock || key_mean < 1 || key_mean > kF)
+    return kBadSize;
+  if (ks < (int64_t)(H + N) * kD || row_words < (H + N + 31) / 32) return kBadSize;
+  if (!k || !W || !b || !center || !scale || !bits || !counts || !moments || !work) return kBadSize;
+  if (!aligned16<KT>(k, ks) || ((W | b) & 15u)) return kBadSize;
+  const UpdateLayout L(groups, N);
+  if (work_bytes < L.total) return kBadSize;  // prismkv_update_work_bytes(groups, N)
+  const UpdateArgs a = make_args(k, W, b, center, scale, bits, counts, moments, work, groups, H, N, key_mean, ks,
+                                 row_words, L);
+  hipStream_t s = (hipStream_t)stream;
+  launch_selection<KT>(a, groups, s);
+  // member lists: N ints per wave of dynamic LDS (up to 64 KB, allowed once per key type)
+  static const hipError_t lds_ok = hipFuncSetAttribute(reinterpret_cast<const void*>(moments_kernel<KT>),
+                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                       (int)(kUT / 64 * kMaxBlock * sizeof(int)));
+  if (lds_ok != hipSuccess) return (int)lds_ok;
+  hipLaunchKernelGGL(moments_kernel<KT>, dim3(kChunks, groups), dim3(kUT), (size_t)(kUT / 64) * N * sizeof(int), s,
+                     a);
+  return (int)hipGetLastError();
+}
+
+template <typename KT>
+static int build_impl(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
+                      uint64_t counts, uint64_t moments, uint64_t work, int groups, int batch, int H, int key_mean,
+                      int flags, int64_t ks, int64_t row_words, size_t work_bytes, uint64_t stream) {
+  if (groups < 1 || groups > 65535 || batch < 1 || batch > groups || H < 1 || H > kMaxBuild || key_mean < 1 ||
+      key_mean > kF)
+    return kBadSize;
+  if (flags & ~kBuildCenter) return kBadMode;
+  if (ks < (int64_t)H * kD || row_words < (H + 31) / 32 || (row_words & 3)) return kBadSize;
+  if (!k || !W || !b || !center || !scale || !bits || !counts || !moments || !work) return kBadSize;
+  if (!aligned16<KT>(k, ks) || ((bits | W | b) & 15u)) return kBadSize;
+  const UpdateLayout L(batch, H);
+  if (work_bytes < L.total) return kBadSize;  // prismkv_build_work_bytes(batch, H)
+  hipStream_t s = (hipStream_t)stream;
+  for (int g0 = 0; g0 < groups; g0 += batch) {
+    const int nb = std::min(batch, groups - g0);
+    const uint64_t kg = k + (uint64_t)g0 * ks * sizeof(KT);
+    const uint64_t cg = center + (uint64_t)g0 * kD * sizeof(float);
+    UpdateArgs a = make_args(kg, W + (uint64_t)g0 * kF * kD * sizeof(float), b + (uint64_t)g0 * kF * sizeof(float),
+                             cg, scale + (uint64_t)g0 * sizeof(float),
+                             bits + (uint64_t)g0 * kF * row_words * sizeof(uint32_t),
+                             counts + (uint64_t)g0 * kFP * sizeof(int),
+                             moments + (uint64_t)g0 * kChunks * kRow * kChunk * sizeof(float), work, nb, 0, H,
+                             key_mean, ks, row_words, L);
+    if (flags & kBuildCenter) {
+      double* part = reinterpret_cast<double*>(reinterpret_cast<char*>(work) + L.part);
+      hipLaunchKernelGGL(center_part_kernel<KT>, dim3(kCenterParts, nb), dim3(kUT), 0, s, a, part);
+      hipLaunchKernelGGL(center_final_kernel, dim3(nb), dim3(kD), 0, s, a, (const double*)part,
+                         reinterpret_cast<float*>(cg));
+    }
+    hipLaunchKernelGGL(clear_bits_kernel, dim3(512, nb), dim3(kUT), 0, s, a);
+    launch_selection<KT>(a, nb, s);
+    hipLaunchKernelGGL(build_moments_kernel<KT>, dim3(kF, nb), dim3(kUT), 0, s, a);
+  }
+  return (int)hipGetLastError();
+}
+
+template <typename KT>
+static int summarize_impl(uint64_t k, uint64_t bits, uint64_t center, uint64_t counts, uint64_t moments,
+                          uint64_t work, int groups, int H, int flags, int64_t ks, int64_t row_words,
+                          size_t work_bytes, uint64_t stream) {
+  if (groups < 1 || groups > 65535 || H < 1 || H > kMaxBuild) return kBadSize;
+  if (flags & ~kBuildCenter) return kBadMode;
+  if (ks < (int64_t)H * kD || row_words < (H + 31) / 32) return kBadSize;
+  if (!k || !bits || !center || !counts || !moments || !work || !aligned16<KT>(k, ks)) return kBadSize;
+  const UpdateLayout L(groups, 0);
+  if (work_bytes < L.total) return kBadSize;  // prismkv_summarize_work_bytes(groups)
+  const UpdateArgs a = make_args(k, 0, 0, center, 0, bits, counts, moments, work, groups, 0, H, 1, ks, row_words, L);
+  hipStream_t s = (hipStream_t)stream;
+  if (flags & kBuildCenter) {
+    double* part = reinterpret_cast<double*>(reinterpret_cast<char*>(work) + L.part);
+    hipLaunchKernelGGL(center_part_kernel<KT>, dim3(kCenterParts, groups), dim3(kUT), 0, s, a, part);
+    hipLaunchKernelGGL(center_final_kernel, dim3(groups), dim3(kD), 0, s, a, (const double*)part,
+                       reinterpret_cast<float*>(center));
+  }
+  hipLaunchKernelGGL(build_moments_kernel<KT>, dim3(kF, groups), dim3(kUT), 0, s, a);
+  return (int)hipGetLastError();
+}
 
 extern "C" {
 
@@ -1113,24 +1250,15 @@ size_t prismkv_update_act_offset(int groups) {
 int prismkv_update(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
                    uint64_t counts, uint64_t moments, uint64_t work, int groups, int H, int N, int key_mean,
                    int64_t ks, int64_t row_words, size_t work_bytes, uint64_t stream) {
-  if (groups < 1 || groups > 65535 || H < 0 || N < 1 || N > kMaxBlock || key_mean < 1 || key_mean > kF)
-    return kBadSize;
-  if (ks < (int64_t)(H + N) * kD || row_words < (H + N + 31) / 32) return kBadSize;
-  if (!k || !W || !b || !center || !scale || !bits || !counts || !moments || !work) return kBadSize;
-  if (!aligned16(k, ks) || ((W | b) & 15u)) return kBadSize;
-  const UpdateLayout L(groups, N);
-  if (work_bytes < L.total) return kBadSize;  // prismkv_update_work_bytes(groups, N)
-  const UpdateArgs a = make_args(k, W, b, center, scale, bits, counts, moments, work, groups, H, N, key_mean, ks,
-                                 row_words, L);
-  hipStream_t s = (hipStream_t)stream;
-  launch_selection(a, groups, s);
-  // member lists: N ints per wave of dynamic LDS (up to 64 KB, allowed once)
-  static const hipError_t lds_ok = hipFuncSetAttribute(reinterpret_cast<const void*>(moments_kernel),
-                                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                       (int)(kUT / 64 * kMaxBlock * sizeof(int)));
-  if (lds_ok != hipSuccess) return (int)lds_ok;
-  hipLaunchKernelGGL(moments_kernel, dim3(kChunks, groups), dim3(kUT), (size_t)(kUT / 64) * N * sizeof(int), s, a);
-  return (int)hipGetLastError();
+  return update_impl<uint16_t>(k, W, b, center, scale, bits, counts, moments, work, groups, H, N, key_mean, ks,
+                               row_words, work_bytes, stream);
+}
+
+int prismkv_update_f32(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
+                       uint64_t counts, uint64_t moments, uint64_t work, int groups, int H, int N, int key_mean,
+                       int64_t ks, int64_t row_words, size_t work_bytes, uint64_t stream) {
+  return update_impl<float>(k, W, b, center, scale, bits, counts, moments, work, groups, H, N, key_mean, ks,
+                            row_words, work_bytes, stream);
 }
 
 size_t prismkv_build_work_bytes(int batch, int H) {
@@ -1141,37 +1269,15 @@ size_t prismkv_build_work_bytes(int batch, int H) {
 int prismkv_build(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
                   uint64_t counts, uint64_t moments, uint64_t work, int groups, int batch, int H, int key_mean,
                   int flags, int64_t ks, int64_t row_words, size_t work_bytes, uint64_t stream) {
-  if (groups < 1 || groups > 65535 || batch < 1 || batch > groups || H < 1 || H > kMaxBuild || key_mean < 1 ||
-      key_mean > kF)
-    return kBadSize;
-  if (flags & ~kBuildCenter) return kBadMode;
-  if (ks < (int64_t)H * kD || row_words < (H + 31) / 32 || (row_words & 3)) return kBadSize;
-  if (!k || !W || !b || !center || !scale || !bits || !counts || !moments || !work) return kBadSize;
-  if (!aligned16(k, ks) || ((bits | W | b) & 15u)) return kBadSize;
-  const UpdateLayout L(batch, H);
-  if (work_bytes < L.total) return kBadSize;  // prismkv_build_work_bytes(batch, H)
-  hipStream_t s = (hipStream_t)stream;
-  for (int g0 = 0; g0 < groups; g0 += batch) {
-    const int nb = std::min(batch, groups - g0);
-    const uint64_t kg = k + (uint64_t)g0 * ks * sizeof(uint16_t);
-    const uint64_t cg = center + (uint64_t)g0 * kD * sizeof(float);
-    UpdateArgs a = make_args(kg, W + (uint64_t)g0 * kF * kD * sizeof(float), b + (uint64_t)g0 * kF * sizeof(float),
-                             cg, scale + (uint64_t)g0 * sizeof(float),
-                             bits + (uint64_t)g0 * kF * row_words * sizeof(uint32_t),
-                             counts + (uint64_t)g0 * kFP * sizeof(int),
-                             moments + (uint64_t)g0 * kChunks * kRow * kChunk * sizeof(float), work, nb, 0, H,
-                             key_mean, ks, row_words, L);
-    if (flags & kBuildCenter) {
-      double* part = reinterpret_cast<double*>(reinterpret_cast<char*>(work) + L.part);
-      hipLaunchKernelGGL(center_part_kernel, dim3(kCenterParts, nb), dim3(kUT), 0, s, a, part);
-      hipLaunchKernelGGL(center_final_kernel, dim3(nb), dim3(kD), 0, s, a, (const double*)part,
-                         reinterpret_cast<float*>(cg));
-    }
-    hipLaunchKernelGGL(clear_bits_kernel, dim3(512, nb), dim3(kUT), 0, s, a);
-    launch_selection(a, nb, s);
-    hipLaunchKernelGGL(build_moments_kernel, dim3(kF, nb), dim3(kUT), 0, s, a);
-  }
-  return (int)hipGetLastError();
+  return build_impl<uint16_t>(k, W, b, center, scale, bits, counts, moments, work, groups, batch, H, key_mean, flags,
+                              ks, row_words, work_bytes, stream);
+}
+
+int prismkv_build_f32(uint64_t k, uint64_t W, uint64_t b, uint64_t center, uint64_t scale, uint64_t bits,
+                      uint64_t counts, uint64_t moments, uint64_t work, int groups, int batch, int H, int key_mean,
+                      int flags, int64_t ks, int64_t row_words, size_t work_bytes, uint64_t stream) {
+  return build_impl<float>(k, W, b, center, scale, bits, counts, moments, work, groups, batch, H, key_mean, flags,
+                           ks, row_words, work_bytes, stream);
 }
 
 size_t prismkv_topk_work_bytes(void) { return UpdateLayout(1, 0).total; }
@@ -1208,22 +1314,15 @@ size_t prismkv_summarize_work_bytes(int groups) {
 int prismkv_summarize(uint64_t k, uint64_t bits, uint64_t center, uint64_t counts, uint64_t moments, uint64_t work,
                       int groups, int H, int flags, int64_t ks, int64_t row_words, size_t work_bytes,
                       uint64_t stream) {
-  if (groups < 1 || groups > 65535 || H < 1 || H > kMaxBuild) return kBadSize;
-  if (flags & ~kBuildCenter) return kBadMode;
-  if (ks < (int64_t)H * kD || row_words < (H + 31) / 32) return kBadSize;
-  if (!k || !bits || !center || !counts || !moments || !work || !aligned16(k, ks)) return kBadSize;
-  const UpdateLayout L(groups, 0);
-  if (work_bytes < L.total) return kBadSize;  // prismkv_summarize_work_bytes(groups)
-  const UpdateArgs a = make_args(k, 0, 0, center, 0, bits, counts, moments, work, groups, 0, H, 1, ks, row_words, L);
-  hipStream_t s = (hipStream_t)stream;
-  if (flags & kBuildCenter) {
-    double* part = reinterpret_cast<double*>(reinterpret_cast<char*>(work) + L.part);
-    hipLaunchKernelGGL(center_part_kernel, dim3(kCenterParts, groups), dim3(kUT), 0, s, a, part);
-    hipLaunchKernelGGL(center_final_kernel, dim3(groups), dim3(kD), 0, s, a, (const double*)part,
-                       reinterpret_cast<float*>(center));
-  }
-  hipLaunchKernelGGL(build_moments_kernel, dim3(kF, groups), dim3(kUT), 0, s, a);
-  return (int)hipGetLastError();
+  return summarize_impl<uint16_t>(k, bits, center, counts, moments, work, groups, H, flags, ks, row_words, work_bytes,
+                                  stream);
+}
+
+int prismkv_summarize_f32(uint64_t k, uint64_t bits, uint64_t center, uint64_t counts, uint64_t moments,
+                          uint64_t work, int groups, int H, int flags, int64_t ks, int64_t row_words,
+                          size_t work_bytes, uint64_t stream) {
+  return summarize_impl<float>(k, bits, center, counts, moments, work, groups, H, flags, ks, row_words, work_bytes,
+                               stream);
 }
 
 }  // extern "C"

@@ -106,6 +106,12 @@ def test_native_error_codes(lib):
     assert call_raw(lib, "prismkv_union", *[1] * 6, 8, 100, 4, 99, BIG) == -1   # ids stride too small
     assert call_raw(lib, "prismkv_attend", *[1] * 7, 8, 10, 2, 12 * 128, 12 * 128, 10, 0, BIG) == -1  # splits
     assert call_raw(lib, "prismkv_attend", *[1] * 7, 8, 10, 2, 11 * 128, 12 * 128, 10, 4, BIG) == -1  # ks
+    assert call_raw(lib, "prismkv_attend_f32", *[16] * 7, 8, 10, 2, 11 * 128, 12 * 128, 10, 4, BIG) == -1  # ks
+    assert call_raw(lib, "prismkv_attend_f32", 20, *[16] * 6, 8, 10, 2, 12 * 128, 12 * 128, 10, 4, BIG) == -1  # q
+    assert call_raw(lib, "prismkv_attend_f32", *[16] * 7, 8, 10, 2, 12 * 128 + 1, 12 * 128, 10, 4, BIG) == -1  # ks
+    assert call_raw(lib, "prismkv_build_f32", *[16] * 9, 8, 8, 100, 8, 0, 100 * 128 + 2, 4, BIG) == -1  # K stride
+    assert call_raw(lib, "prismkv_build_f32", *[0] * 9, 8, 8, 100, 8, 0, 100 * 128, 4, BIG) == -1  # null pointers
+    assert call_raw(lib, "prismkv_route_scores_f32", *[16] * 7, 0, 8, BIG) == -1  # no score vector
     # prismkv_update(k, W, b, center, scale, bits, counts, moments, work, groups, H, N, key_mean, ks, row_words,
     # work_bytes)
     good = (100 + 64) * 128
@@ -164,6 +170,12 @@ WORK_CASES = {
     "prismkv_build": ((*[16] * 9, 8, 4, H, 8, 1, KS, 32), ("prismkv_build_work_bytes", 4, H)),
     "prismkv_topk": ((*[16] * 4, 100, 800), ("prismkv_topk_work_bytes",)),
     "prismkv_summarize": ((*[16] * 6, 8, H, 1, KS, 32), ("prismkv_summarize_work_bytes", 8)),
+    "prismkv_route_scores_f32": ((*[16] * 8, 8), ("prismkv_route_work_bytes", 8)),
+    "prismkv_route_qact_f32": ((*[16] * 10, 8), ("prismkv_route_qact_work_bytes", 8)),
+    "prismkv_attend_f32": ((*[16] * 7, 8, H, T, KS, KS, H, 32), ("prismkv_attend_work_bytes", 8, 32)),
+    "prismkv_update_f32": ((*[16] * 9, 8, H, T, 8, KS, 32), ("prismkv_update_work_bytes", 8, T)),
+    "prismkv_build_f32": ((*[16] * 9, 8, 4, H, 8, 1, KS, 32), ("prismkv_build_work_bytes", 4, H)),
+    "prismkv_summarize_f32": ((*[16] * 6, 8, H, 1, KS, 32), ("prismkv_summarize_work_bytes", 8)),
     "prismkv_route_single": ((*[16] * 7, 8), ("prismkv_decode_work_bytes", 8, H)),
     "prismkv_route_union": ((*[16] * 10, 8, H, H, 32, H), ("prismkv_decode_work_bytes", 8, H)),
     "prismkv_decode": ((*[16] * 13, 8, H, T, H, 32, KS, KS, H), ("prismkv_decode_work_bytes", 8, H)),
