@@ -745,7 +745,8 @@ def main():
                         frac=d["frac_of_peak"], traffic=traffic,
                         traffic_source=None if traffic is None else
                         "profile-derived, not collected by this run: FETCH_SIZE and WRITE_SIZE passes over this "
-                        "workload, scaled by the copy kernel's factors (profiles/decode_kernel_64k_hbm_traffic.md)",
+                        "workload, scaled by the copy kernel's factors, which the dense control's gather of known "
+                        "size confirms to 1.1% (profiles/decode_kernel_64k_hbm_traffic.md)",
                         kernel=STAGE_KERNEL.get(dominant, dominant), algorithmic_bytes=d["algorithmic_bytes"])
     n_layers = a.layers
     del layers
