@@ -450,6 +450,7 @@ __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p,
   {
     const int half = tid >> 8, t = tid & 255;
     unsigned qv = load_query512(a.q, g, tid);
+    asm volatile("" ::: "memory");  // q is issued first, whatever the scheduler's pressure estimate
     const int c0 = min(tile(half), kChunks - 1), c2 = min(tile(2), kChunks - 1);
     const int* cg = a.counts + (size_t)g * kFP + (t & 31);
     const int n0 = __builtin_nontemporal_load(cg + c0 * kChunk), n2 = __builtin_nontemporal_load(cg + c2 * kChunk);
@@ -533,39 +534,57 @@ __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p,
 // tokens whose pattern holds i and no row kept before it in the window,
 // which decides the window's rows in rank order exactly as the
 // one-bucket-at-a-time walk does, and every workgroup decides the same from
-// the same sums.  Returns this thread's word of U (0 past the tile) and the
-// kept ranks in *keep.
+// the same sums.
+// The greedy walk never drops a kept row, so the union only grows: the
+// tokens a window adds are final once it is decided.  Each window's new
+// tokens are appended to the workgroup's row list (rows[], in window order)
+// and attended by segment(lo, n) while the NEXT window's counts cross
+// between the workgroups (segment(-1, 0), the tail share, goes with the
+// first window), so the gather runs during the walk's hand-offs instead of
+// after the last one.  Returns this thread's word of U (0 past the tile),
+// the kept ranks in *keep, the rows listed in *listed and the first row not
+// yet attended in *attended (the caller attends [*attended, *listed) after a
+// barrier).
 constexpr int kWindow = 4;
 constexpr int kWindows = kTop / kWindow;
 constexpr int kPacked = 8;  // 15 pattern counts, two 16-bit counts per word
+// The ranked rows' words of the tile wait in dynamic LDS after the row list
+// ([kTop][kDT], thread t's at t), not in registers: the attention between
+// the windows needs those.
+constexpr int kWalkWordsBytes = kTop * kDT * (int)sizeof(uint32_t);
 
-__device__ __forceinline__ uint32_t capped_walk(const DecodeArgs& a, int g, int p, DecodeLds& lds, unsigned* keep) {
+template <typename Segment>
+__device__ __forceinline__ uint32_t capped_walk(const DecodeArgs& a, int g, int p, DecodeLds& lds, int* rows,
+                                                unsigned* keep, int* listed_out, int* attended_out,
+                                                Segment&& segment) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int nr = lds.need;
   const int nw = (a.H + 31) / 32, wd = p * a.tw + tid;
   const bool col = tid < a.tw && wd < nw;
   const uint32_t wmask = !col ? 0u : (wd == nw - 1 && (a.H & 31)) ? (1u << (a.H & 31)) - 1u : ~0u;
-  // every ranked row's word, all requested at once
-  uint32_t v[kTop];
+  // every ranked row's word, all requested at once, kept in LDS
+  uint32_t* words = reinterpret_cast<uint32_t*>(rows + 32 * a.tw);
   {
+    uint32_t v[kTop];
     const uint32_t* gb = a.bits + (size_t)g * kF * a.row_words + (col ? wd : 0);
 #pragma unroll
     for (int r = 0; r < kTop; ++r)
       v[r] = nr > 0 ? __builtin_nontemporal_load(gb + (size_t)lds.sel_rows[r < nr ? r : nr - 1] * a.row_words) : 0u;
 #pragma unroll
-    for (int r = 0; r < kTop; ++r) v[r] &= r < nr ? wmask : 0u;
+    for (int r = 0; r < kTop; ++r) words[r * kDT + tid] = v[r] & (r < nr ? wmask : 0u);
   }
   const int lim = a.limit < a.H ? a.limit : a.H;  // a union never exceeds H
   unsigned* rec = a.walk + (size_t)g * kWindows * a.S * kPacked;
   uint32_t U = 0u;
-  int total = 0;
+  int total = 0, listed = 0, attended = 0;
   unsigned kept = 0u;
+  bool tail_done = false;
 #pragma unroll
   for (int k = 0; k < kWindows; ++k) {
     if (kWindow * k >= nr) break;  // uniform
     uint32_t x[kWindow];
 #pragma unroll
-    for (int i = 0; i < kWindow; ++i) x[i] = v[kWindow * k + i] & ~U;
+    for (int i = 0; i < kWindow; ++i) x[i] = words[(kWindow * k + i) * kDT + tid] & ~U;
     // pattern m = (rows 0, 1: m & 3) x (rows 2, 3: m >> 2)
     const uint32_t lo[4] = {~x[0] & ~x[1], x[0] & ~x[1], ~x[0] & x[1], x[0] & x[1]};
     const uint32_t hi[4] = {~x[2] & ~x[3], x[2] & ~x[3], ~x[2] & x[3], x[2] & x[3]};
@@ -580,16 +599,26 @@ __device__ __forceinline__ uint32_t capped_walk(const DecodeArgs& a, int g, int 
     const int wsum = wave_sum8(packed);  // lane 8j: the wave's packed word j
     if ((lane & 7) == 0) lds.walk_part[w][lane >> 3] = wsum;
     __syncthreads();
-    if (w == 0) {
-      // the workgroup's counts (<= 16384 each: no carry between the halves),
-      // published complemented; then every workgroup's, lane l summing word
-      // l & 7 of workgroups (l >> 3) + 8 i
-      if (lane < kPacked) {
-        unsigned sum = 0u;
+    // the workgroup's counts (<= 16384 each: no carry between the halves),
+    // published complemented
+    if (w == 0 && lane < kPacked) {
+      unsigned sum = 0u;
 #pragma unroll
-        for (int ww = 0; ww < kDT / 64; ++ww) sum += (unsigned)lds.walk_part[ww][lane];
-        st_dev(&rec[((size_t)k * a.S + p) * kPacked + lane], ~sum);
-      }
+      for (int ww = 0; ww < kDT / 64; ++ww) sum += (unsigned)lds.walk_part[ww][lane];
+      st_dev(&rec[((size_t)k * a.S + p) * kPacked + lane], ~sum);
+    }
+    // while they cross: the rows decided so far (before the first window,
+    // the tail share), by every wave
+    if (!tail_done) {
+      segment(-1, 0);
+      tail_done = true;
+    } else {
+      segment(attended, listed - attended);
+      attended = listed;
+    }
+    if (w == 0) {
+      // every workgroup's counts, lane l summing word l & 7 of workgroups
+      // (l >> 3) + 8 i
       const int j = lane & 7;
       int s0 = 0, s1 = 0;
       for (int q0 = lane >> 3; q0 < a.S; q0 += 32) {
@@ -643,11 +672,31 @@ __device__ __forceinline__ uint32_t capped_walk(const DecodeArgs& a, int g, int 
     }
     __syncthreads();
     const unsigned kw = lds.walk_keep;
+    uint32_t inc = 0u;  // this word's tokens the window adds
 #pragma unroll
-    for (int i = 0; i < kWindow; ++i) U |= (kw >> i) & 1u ? x[i] : 0u;
+    for (int i = 0; i < kWindow; ++i) inc |= (kw >> i) & 1u ? x[i] : 0u;
+    U |= inc;
     kept |= kw << (kWindow * k);
+    // append them to the row list (the next segment reads it after the
+    // next window's first barrier; the caller barriers after the last)
+    const int c = __popc(inc), incl = wave_scan_i(c);
+    if (lane == 63) lds.chunk_rows[w] = incl;
+    __syncthreads();
+    int at = listed, add = 0;
+#pragma unroll
+    for (int ww = 0; ww < kDT / 64; ++ww) {
+      const int t = lds.chunk_rows[ww];
+      at += ww < w ? t : 0;
+      add += t;
+    }
+    at += incl - c;
+    for (uint32_t m = inc; m; m &= m - 1u) rows[at++] = wd * 32 + (int)__builtin_ctz(m);
+    listed += add;
   }
+  if (!tail_done) segment(-1, 0);  // nothing ranked: the tail share alone
   *keep = kept;
+  *listed_out = listed;
+  *attended_out = attended;
   return U;
 }
 
@@ -753,28 +802,9 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
       decode_select<KW>(a, g, p, lds);
     }
   }
-  // ---- 1-4b. the group's Top-16, then the budgeted walk over it: this
-  // thread's word of the kept rows' union, and the kept buckets (in rank
-  // order, compacted) into features / valid / raw
-  uint32_t walked = 0u;
-  if constexpr (kCap) {
-    decode_select<KW, true, false>(a, g, p, lds);
-    unsigned keep = 0u;
-    walked = capped_walk(a, g, p, lds, &keep);
-    if (p == 0 && w == 0) {
-      const int nkept = __popc(keep);
-      const bool kept = lane < kTop && ((keep >> lane) & 1u);
-      const int b = lane < kTop ? lds.sel_rows[lane] : 0;
-      if (lane < kTop) {
-        int64_t* fg = a.features + (size_t)g * kTop;
-        if (kept) fg[__popc(keep & ((1u << lane) - 1u))] = b;
-        if (lane >= nkept) fg[lane] = 0;
-        a.valid[(size_t)g * kTop + lane] = lane < nkept ? 1.f : 0.f;
-      }
-      const int n = wave_sum_i(kept ? a.counts[(size_t)g * kFP + b] : 0);
-      if (lane == 0) a.raw[g] = n;
-    }
-  }
+  // ---- 1-4b. (capped) the group's Top-16; the budgeted walk over it runs
+  // in phase 6, interleaved with the attention of the rows it has decided
+  if constexpr (kCap) decode_select<KW, true, false>(a, g, p, lds);
 
   // ---- 5. union tile: OR the selected rows over words [tw p, tw (p + 1)), compact.
   // One 64-word chunk (histories up to 64K at 8 groups): wave 0 ORs the rows
@@ -783,7 +813,9 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   // the chunks' counts give each its offset.  (Phase 4's final barrier
   // publishes need and sel_rows.)
   const int nw = (a.H + 31) / 32;
-  if (id_list) {
+  if constexpr (kCap) {
+    // the capped launch lists its rows during the walk (phase 6)
+  } else if (id_list) {
     // ---- 5'. the workgroup's share of the group's list (count ids, then the
     // T tail rows H .. H + T - 1): rows [p per, (p + 1) per) as positions
     const int given_cnt = a.count_in[g];
@@ -808,16 +840,14 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     if (w == 0) {
       const int nr = lds.need;
       const int wd = p * a.tw + lane;
-      uint32_t m = walked;  // the capped launch's union word (lane = tile word)
+      uint32_t m = 0u;
       unsigned covered = 0u;
-      if constexpr (!kCap) {
 #pragma unroll
-        for (int k = 0; k < kDT / 64; ++k) {
-          m |= lds.sel.ors[k][lane];
-          covered |= lds.cover[k];
-        }
+      for (int k = 0; k < kDT / 64; ++k) {
+        m |= lds.sel.ors[k][lane];
+        covered |= lds.cover[k];
       }
-      const unsigned missing = kCap ? 0u : ((1u << nr) - 1u) & ~covered;  // winners' ranks no wave prefetched (uniform)
+      const unsigned missing = ((1u << nr) - 1u) & ~covered;  // winners' ranks no wave prefetched (uniform)
       if (missing && lane < a.tw && wd < nw) {
         // one round of loads: every rank loads (a covered one repeats the first
         // missing row) and only the missing ones are kept
@@ -848,10 +878,10 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     const int chunks = (a.tw + kTileWords - 1) / kTileWords;  // <= 8
     const int cw = w * kTileWords + lane, wd = p * a.tw + cw;
     const int nr = lds.need;
-    uint32_t m = walked;  // the capped launch's union word (thread = tile word)
+    uint32_t m = 0u;
     int n = 0, incl = 0;
     if (w < chunks) {
-      if (!kCap && nr > 0 && cw < a.tw && wd < nw) {
+      if (nr > 0 && cw < a.tw && wd < nw) {
         const uint32_t* gb = a.bits + (size_t)g * kF * a.row_words + wd;
         uint32_t v[kTop];
 #pragma unroll
@@ -895,27 +925,20 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   // the list's last block is partial: a wave's block whose lanes mostly
   // repeat one row still costs about a third of a full block's load time,
   // so whole blocks are dealt rather than equal row counts.
-  const int n_sel = lds.nsel;
   const int T = a.tail_dev ? min(max(tail_word, 0), a.T) : a.T;
   const int tail_per = id_list ? 0 : (T + a.S - 1) / a.S;  // an id list holds its tail rows
   const int t_lo = min(T, p * tail_per), t_hi = min(T, t_lo + tail_per);
   // the list: the tile's tokens, then the tail rows the early blocks did not take
   const int early_rows = kEarly ? min(t_hi - t_lo, kEarlyRows) : 0;
-  const int n_rows = kRouteOnly ? 0 : n_sel + (t_hi - t_lo) - early_rows;
+  int n_sel = kCap ? 0 : lds.nsel;  // the capped launch's: the walk's final list
+  uint32_t walked = 0u;             // the capped launch's word of the kept rows' union (thread = tile word)
+  int walked_at = 0;                // ... and its tokens' offset in the tile's ascending ids
   {
     const int j = lane & 15, qd = lane >> 4;
     const int last_row = a.H + T - 1;
     const uint16_t* kg = a.k + (size_t)g * a.ks;
     const uint16_t* vg = a.v + (size_t)g * a.vs;
     constexpr int kWaves = kDT / 64;
-    const int n_blocks = (n_rows + 15) >> 4;
-    // position of row r of the workgroup's list; rows past the list repeat
-    // the block's first row (masked, same lines)
-    auto row_pos = [&](int r, int base) {
-      r = r < n_rows ? r : base;
-      int pos = r < n_sel ? rows[r] : a.H + t_lo + early_rows + (r - n_sel);
-      return pos < 0 ? 0 : (pos > last_row ? last_row : pos);
-    };
 #if PRISMKV_VALU_ATTENTION
     // VALU attention (the A/B alternative, built with -DPRISMKV_VALU_ATTENTION=1):
     // lane (q16, slot) holds dims 8 q16 .. 8 q16 + 8 of the rows of its slot
@@ -943,61 +966,116 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     const int kv_bytes = __builtin_amdgcn_readfirstlane((last_row + 1) * 2 * kD);
     const __amdgpu_buffer_rsrc_t kbuf = raw_buffer(kg, kv_bytes), vbuf = raw_buffer(vg, kv_bytes);
 #endif
-    constexpr int kPerRound = 4;
+    // blocks per wave per round (the capped launch keeps the walk's state
+    // live across its segments: two blocks, 256 rows per workgroup in
+    // flight, still cover HBM's latency)
+    constexpr int kPerRound = kCap ? 2 : 4;
     // the wave index made explicitly uniform keeps the block indices in
     // scalar registers (fewer VGPRs for the round's loads)
     const int wu = __builtin_amdgcn_readfirstlane(w);
-#if !PRISMKV_VALU_ATTENTION
-    // the early tail block, requested in phase 4, has landed: attend it first
-    // (its registers are free again before the rounds' loads need theirs)
-    if (early_n > 0) {  // uniform
-      const int early_nv[1] = {early_n};
-      mfma_blocks16<1>(st, ek, ev, early_nv);
-    }
-#endif
-    for (int k0 = kWaves - 1 - wu; k0 < n_blocks; k0 += kPerRound * kWaves) {  // blocks k0 + 8 i
-      uint4 kr[kPerRound][4], vr[kPerRound][4];
+    // attends n rows, row r at K/V row pos_of(r) (clamped into the group's
+    // rows; rows past n repeat the block's first row and are masked); with
+    // `look`, wave 0 requests the lower tiles' counts once its first K/V
+    // loads are in flight
+    auto attend_rows = [&](auto&& pos_of, int n, bool look) {
+      const int n_blocks = (n + 15) >> 4;
+      auto row_pos = [&](int r, int base) {
+        const int pos = pos_of(r < n ? r : base);
+        return pos < 0 ? 0 : (pos > last_row ? last_row : pos);
+      };
+      for (int k0 = kWaves - 1 - wu; k0 < n_blocks; k0 += kPerRound * kWaves) {  // blocks k0 + 8 i
+        uint4 kr[kPerRound][4], vr[kPerRound][4];
 #pragma unroll
-      for (int i = 0; i < kPerRound; ++i) {
-        const int base = 16 * (k0 + kWaves * i);
-        if (base < n_rows) {  // uniform per wave
+        for (int i = 0; i < kPerRound; ++i) {
+          const int base = 16 * (k0 + kWaves * i);
+          if (base < n) {  // uniform per wave
 #if PRISMKV_VALU_ATTENTION
 #pragma unroll
-          for (int b = 0; b < 4; ++b) {
-            const size_t at = (size_t)row_pos(base + 4 * slot + b, base) * kD + 8 * q16;
-            kr[i][b] = load_nt16(kg + at);
-            vr[i][b] = load_nt16(vg + at);
+            for (int b = 0; b < 4; ++b) {
+              const size_t at = (size_t)row_pos(base + 4 * slot + b, base) * kD + 8 * q16;
+              kr[i][b] = load_nt16(kg + at);
+              vr[i][b] = load_nt16(vg + at);
+            }
+#else
+            const unsigned ko = (unsigned)row_pos(base + j, base) * (2 * kD) + 16 * qd;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) kr[i][c] = load_nt16_buf(kbuf, ko + 64 * c);
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+              vr[i][t] = load_nt16_buf(vbuf, (unsigned)row_pos(base + 4 * qd + t, base) * (2 * kD) + 16 * j);
+#endif
           }
-#else
-          const unsigned ko = (unsigned)row_pos(base + j, base) * (2 * kD) + 16 * qd;
-#pragma unroll
-          for (int c = 0; c < 4; ++c) kr[i][c] = load_nt16_buf(kbuf, ko + 64 * c);
-#pragma unroll
-          for (int t = 0; t < 4; ++t)
-            vr[i][t] = load_nt16_buf(vbuf, (unsigned)row_pos(base + 4 * qd + t, base) * (2 * kD) + 16 * j);
-#endif
         }
-      }
-      asm volatile("" ::: "memory");  // every load of the round is in flight before any is used
-      if (k0 == kWaves - 1 - wu && wu == 0 && !id_list) {
+        asm volatile("" ::: "memory");  // every load of the round is in flight before any is used
+        if (look && k0 == kWaves - 1 - wu && wu == 0) {
 #pragma unroll
-        for (int c = 0; c < kMaxSplits / 64; ++c) {
-          const int qq = 64 * c + lane;
-          if (qq < p) lower[c] = ld_dev(&a.status[(size_t)g * a.S + qq]);
+          for (int c = 0; c < kMaxSplits / 64; ++c) {
+            const int qq = 64 * c + lane;
+            if (qq < p) lower[c] = ld_dev(&a.status[(size_t)g * a.S + qq]);
+          }
         }
-      }
 #if PRISMKV_VALU_ATTENTION
 #pragma unroll
-      for (int i = 0; i < kPerRound; ++i) {
-        const int base = 16 * (k0 + kWaves * i);
-        if (base < n_rows) attend_step(qf, kr[i], vr[i], max(0, min(4, n_rows - base - 4 * slot)), st);
-      }
+        for (int i = 0; i < kPerRound; ++i) {
+          const int base = 16 * (k0 + kWaves * i);
+          if (base < n) attend_step(qf, kr[i], vr[i], max(0, min(4, n - base - 4 * slot)), st);
+        }
 #else
-      int nv[kPerRound];
+        int nv[kPerRound];
 #pragma unroll
-      for (int i = 0; i < kPerRound; ++i) nv[i] = max(0, min(16, n_rows - 16 * (k0 + kWaves * i)));
-      mfma_blocks16<kPerRound>(st, kr, vr, nv);
+        for (int i = 0; i < kPerRound; ++i) nv[i] = max(0, min(16, n - 16 * (k0 + kWaves * i)));
+        mfma_blocks16<kPerRound>(st, kr, vr, nv);
 #endif
+      }
+    };
+    if constexpr (kCap) {
+      // ---- 4b + 6. the walk, each window's hand-off overlapped with the
+      // attention of the rows decided before it (the tail share first)
+      unsigned keep = 0u;
+      int listed = 0, attended = 0;
+      walked = capped_walk(a, g, p, lds, rows, &keep, &listed, &attended, [&](int lo, int n) {
+        if (lo < 0)
+          attend_rows([&](int r) { return a.H + t_lo + r; }, t_hi - t_lo, false);
+        else
+          attend_rows([&](int r) { return rows[lo + r]; }, n, false);
+      });
+      // the tile's count for the look-back, and its ascending ids' offsets
+      const int c = __popc(walked), incl = wave_scan_i(c);
+      if (lane == 63) lds.chunk_rows[w] = incl;
+      __syncthreads();  // also: the last window's rows are listed
+#pragma unroll
+      for (int ww = 0; ww < kWaves; ++ww) walked_at += ww < w ? lds.chunk_rows[ww] : 0;
+      walked_at += incl - c;
+      n_sel = listed;
+      if (tid == 0) st_dev(&a.status[(size_t)g * a.S + p], kReady | (unsigned)listed);
+      attend_rows([&](int r) { return rows[attended + r]; }, listed - attended, true);
+      // the kept buckets (in rank order, compacted) into features / valid /
+      // raw, by a workgroup that merges nothing
+      if (p == a.S - 1 && w == 0) {
+        const int nkept = __popc(keep);
+        const bool kept = lane < kTop && ((keep >> lane) & 1u);
+        const int b = lane < kTop ? lds.sel_rows[lane] : 0;
+        if (lane < kTop) {
+          int64_t* fg = a.features + (size_t)g * kTop;
+          if (kept) fg[__popc(keep & ((1u << lane) - 1u))] = b;
+          if (lane >= nkept) fg[lane] = 0;
+          a.valid[(size_t)g * kTop + lane] = lane < nkept ? 1.f : 0.f;
+        }
+        const int nb = wave_sum_i(kept ? a.counts[(size_t)g * kFP + b] : 0);
+        if (lane == 0) a.raw[g] = nb;
+      }
+    } else {
+#if !PRISMKV_VALU_ATTENTION
+      // the early tail block, requested in phase 4, has landed: attend it first
+      // (its registers are free again before the rounds' loads need theirs)
+      if (early_n > 0) {  // uniform
+        const int early_nv[1] = {early_n};
+        mfma_blocks16<1>(st, ek, ev, early_nv);
+      }
+#endif
+      const int n_rows = kRouteOnly ? 0 : n_sel + (t_hi - t_lo) - early_rows;
+      attend_rows([&](int r) { return r < n_sel ? rows[r] : a.H + t_lo + early_rows + (r - n_sel); }, n_rows,
+                  !id_list);
     }
 
     // each wave stashes its state as soon as its attention ends: the LDS
@@ -1067,7 +1145,12 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     else
       publish_sliced(lds.mf, a.state + (size_t)(g * a.S + p) * kHq * kSlices * kSliceW);
   }
-  if (!id_list) {
+  if constexpr (kCap) {
+    // ascending, from the union word: rows[] holds them in window order
+    int32_t* dst = a.ids + (size_t)g * a.ids_stride + lds.base + walked_at;
+    const int wd = p * a.tw + tid;
+    for (uint32_t m = walked; m; m &= m - 1u) *dst++ = wd * 32 + (int)__builtin_ctz(m);
+  } else if (!id_list) {
     int32_t* dst = a.ids + (size_t)g * a.ids_stride + lds.base;
     for (int i = tid; i < n_sel; i += kDT) dst[i] = rows[i];
   }
@@ -1166,8 +1249,9 @@ struct DecodeWorkLayout {
 };
 
 // Workgroups of decode_kernel resident on device `dev` at once (CUs x blocks
-// per CU) with the largest row list (64 KB of dynamic LDS), queried once per
-// device; the instantiations are allowed that much dynamic LDS here.  The
+// per CU) with the largest row list (64 KB of dynamic LDS) and the capped
+// walk's words (32 KB), queried once per device; the instantiations are
+// allowed that much dynamic LDS here.  The
 // route-only kernels (no dynamic LDS) are counted at the same size, which
 // can only understate them.
 static int resident_workgroups() {
@@ -1199,12 +1283,11 @@ static int resident_workgroups() {
                          reinterpret_cast<const void*>(decode_kernel<2, false, false, false, true>),
                          reinterpret_cast<const void*>(decode_kernel<4, false, false, false, true>),
                          reinterpret_cast<const void*>(decode_kernel<8, false, false, false, true>)};
+    // (the capped launches' row list is followed by the walk's words)
+    const int dyn = kTileTokens * (int)sizeof(int) + kWalkWordsBytes;
     for (const void* fn : fns) {
-      if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kTileTokens * (int)sizeof(int)) !=
-          hipSuccess)
-        return 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kDT, kTileTokens * sizeof(int)) != hipSuccess)
-        return 0;
+      if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, dyn) != hipSuccess) return 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, kDT, dyn) != hipSuccess) return 0;
       least = std::min(least, per_cu);
     }
     per_cu = least;
@@ -1288,10 +1371,11 @@ static int decode_launch(uint64_t q, uint64_t moments, uint64_t counts, uint64_t
     else if (S <= 128) hipLaunchKernelGGL((decode_kernel<4, false, false, false, true>), grid, block, rows_bytes, s, a);
     else hipLaunchKernelGGL((decode_kernel<8, false, false, false, true>), grid, block, rows_bytes, s, a);
   } else if (limit >= 0) {
-    if (S <= 32) hipLaunchKernelGGL((decode_kernel<1, false, true>), grid, block, rows_bytes, s, a);
-    else if (S <= 64) hipLaunchKernelGGL((decode_kernel<2, false, true>), grid, block, rows_bytes, s, a);
-    else if (S <= 128) hipLaunchKernelGGL((decode_kernel<4, false, true>), grid, block, rows_bytes, s, a);
-    else hipLaunchKernelGGL((decode_kernel<8, false, true>), grid, block, rows_bytes, s, a);
+    const size_t dyn = rows_bytes + kWalkWordsBytes;
+    if (S <= 32) hipLaunchKernelGGL((decode_kernel<1, false, true>), grid, block, dyn, s, a);
+    else if (S <= 64) hipLaunchKernelGGL((decode_kernel<2, false, true>), grid, block, dyn, s, a);
+    else if (S <= 128) hipLaunchKernelGGL((decode_kernel<4, false, true>), grid, block, dyn, s, a);
+    else hipLaunchKernelGGL((decode_kernel<8, false, true>), grid, block, dyn, s, a);
   } else if (given) {
     if (S <= 32) hipLaunchKernelGGL((decode_kernel<1, true>), grid, block, rows_bytes, s, a);
     else if (S <= 64) hipLaunchKernelGGL((decode_kernel<2, true>), grid, block, rows_bytes, s, a);

@@ -295,12 +295,22 @@ def test_strict_unique_cap(H, tail, kind, cap):
     err = expect.attention_errors(bf16_bits(out), expected)
     log(f"  capped call, one launch: {err}")
     assert err["rel_l2"] <= AV_TOL and err["max_abs"] < 0.05, err
-    # ... and bit for bit the three launches (route, prismkv_select_cap,
-    # prismkv_union_attend over the walked selection)
+    # ... and the three launches (route, prismkv_select_cap,
+    # prismkv_union_attend over the walked selection): the same rows, attended
+    # in another order (the one launch takes each window's rows as the walk
+    # decides them), so the outputs agree to rounding
     fused = bf16_bits(out).copy()
     three = three_launch_capped(op, q, k, v)
-    assert np.array_equal(fused, three), "capped: one launch vs three"
+    assert same_rows_close(fused, three), "capped: one launch vs three"
     assert op.decode_errors() == 0
+
+
+def same_rows_close(a_bits, b_bits, tol=1e-3):
+    """Two bf16 outputs of attention over the same rows in different orders:
+    within `tol` relative L2 (fp32 accumulation order, then bf16 rounding)."""
+    a = oracle.bf16_to_f32(a_bits).astype(np.float64)
+    b = oracle.bf16_to_f32(b_bits).astype(np.float64)
+    return oracle.rel_l2(a, b) <= tol
 
 
 def three_launch_capped(op, q, k, v, groups=8, work=None):
@@ -385,8 +395,9 @@ def test_cap_walk_layouts(H, pad):
 def test_capped_decode_groups(groups):
     # prismkv_decode_capped on the first `groups` groups (32 .. 256 workgroups
     # per group, so 32 .. 256 records per walk window): features / valid /
-    # raw / ids / count and out bit for bit as the three launches on the same
-    # groups, at caps that keep from none to all of the ranked buckets
+    # raw / ids / count bit for bit as the three launches on the same groups,
+    # and out to rounding (the same rows in window order), at caps that keep
+    # from none to all of the ranked buckets
     case = cases.native_case(32768, 40, "random", seed=17)
     op, q, k, v = operator(case)
     s = torch.cuda.current_stream().cuda_stream
@@ -412,7 +423,7 @@ def test_capped_decode_groups(groups):
                 assert torch.equal(a[g], b[g]), (cap, g)
             n = int(ref[4][g])
             assert int(got[4][g]) == n and torch.equal(got[3][g][:n], ref[3][g][:n]), (cap, g)
-        assert np.array_equal(bf16_bits(op.out)[:groups], three[:groups]), cap
+        assert same_rows_close(bf16_bits(op.out)[:groups], three[:groups]), cap
         kept.append([int((op.valid[g] > 0).sum()) for g in range(groups)])
     log(f"  groups={groups}: kept buckets per cap {kept}")
 
