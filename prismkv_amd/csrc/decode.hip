@@ -233,7 +233,9 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int g, int h, i
   // Polled with two generations of loads in flight: a word that lands just
   // after one generation was issued is seen by the next, half a round trip
   // later.  Every load is unconditional (published words keep their value
-  // until this merge clears them), so the waits between generations stay exact.
+  // until this merge clears them), and nothing else is in flight (drained
+  // first), so the explicit wait for a generation leaves the other one
+  // outstanding; the compiler's own waits would otherwise take both.
   constexpr int kPer = 2 * KW;  // S <= 32 KW splits: thread (d, sg) reads splits sg + 16 i, i < kPer
   const unsigned long long* mzp =
       reinterpret_cast<const unsigned long long*>(base + (size_t)min(tid, S - 1) * stride);
@@ -264,11 +266,17 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int g, int h, i
       }
     return ok;
   };
+  // s_waitcnt with vmcnt = one generation's loads (lgkmcnt, expcnt left open)
+  constexpr int kGen = 1 + kPer;
+  constexpr int kWaitGen = (kGen & 0xF) | ((kGen >> 4) << 14) | (0x7 << 4) | (0xF << 8);
+  drain();
   issue(0);
   for (int spins = 0;; spins += 2) {
     issue(1);
+    __builtin_amdgcn_s_waitcnt(kWaitGen);  // generation 0 has landed, generation 1 is in flight
     if (__syncthreads_and(take(0))) break;
     issue(0);
+    __builtin_amdgcn_s_waitcnt(kWaitGen);
     if (__syncthreads_and(take(1))) break;
     if (spins >= a.spin) {
       if (tid == 0) report_error(a.err, a.err_host);
