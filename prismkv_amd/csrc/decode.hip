@@ -171,6 +171,10 @@ __device__ __forceinline__ void wait_all(Pred pred, const Args& a) {
   }
 }
 
+// s_waitcnt immediate waiting until at most n vector memory operations of
+// the wave are outstanding (expcnt and lgkmcnt left open).
+constexpr int vmcnt_wait(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+
 // Bitmap row of a candidate key.  Landed keys always name a bucket below
 // 3000; the clamp keeps a key read after a wait gave up in range too.
 __device__ __forceinline__ int row_of(unsigned long long key) { return min(key_bucket(key), kF - 1); }
@@ -267,8 +271,7 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int g, int h, i
     return ok;
   };
   // s_waitcnt with vmcnt = one generation's loads (lgkmcnt, expcnt left open)
-  constexpr int kGen = 1 + kPer;
-  constexpr int kWaitGen = (kGen & 0xF) | ((kGen >> 4) << 14) | (0x7 << 4) | (0xF << 8);
+  constexpr int kWaitGen = vmcnt_wait(1 + kPer);
   drain();
   issue(0);
   for (int spins = 0;; spins += 2) {
@@ -367,15 +370,42 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, D
   const int nk = a.S * kTop;
   const unsigned long long* cg = a.cand + (size_t)g * a.S * kTop;
   unsigned long long v[KW];
+  {
+    // two generations of unconditional loads in flight (nothing else is,
+    // after the drain), each waited for explicitly: a key that lands just
+    // after one generation was issued is seen by the next
+    unsigned long long r[KW], gen[2][KW];
+    auto issue = [&](int gg) {
 #pragma unroll
-  for (int k = 0; k < KW; ++k) {
-    const int i = (w * KW + k) * 64 + lane;
-    unsigned long long r = 0;
-    wait_all([&] {
-      if (i < nk && r == 0) r = ld_dev(cg + i);
-      return i >= nk || r != 0;
-    }, a);
-    v[k] = i < nk ? ~r : 0ull;
+      for (int k = 0; k < KW; ++k) gen[gg][k] = ld_dev(cg + min((w * KW + k) * 64 + lane, nk - 1));
+    };
+    auto take = [&](int gg) {
+      bool ok = true;
+#pragma unroll
+      for (int k = 0; k < KW; ++k) {
+        r[k] = r[k] ? r[k] : gen[gg][k];
+        ok = ok && ((w * KW + k) * 64 + lane >= nk || r[k] != 0);
+      }
+      return __ballot(!ok) == 0;
+    };
+#pragma unroll
+    for (int k = 0; k < KW; ++k) r[k] = 0;
+    drain();
+    issue(0);
+    for (int spins = 0;; spins += 2) {
+      issue(1);
+      __builtin_amdgcn_s_waitcnt(vmcnt_wait(KW));  // generation 0 has landed
+      if (take(0)) break;
+      issue(0);
+      __builtin_amdgcn_s_waitcnt(vmcnt_wait(KW));
+      if (take(1)) break;
+      if (spins >= a.spin) {
+        if (lane == 0) report_error(a.err, a.err_host);
+        break;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < KW; ++k) v[k] = (w * KW + k) * 64 + lane < nk ? ~r[k] : 0ull;
   }
   early.prepare();
   const unsigned long long best = sorted_rows_top16<KW>(v);
@@ -487,12 +517,31 @@ __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p,
   if (w < kHq) {
     const int h = w;
     const unsigned long long* st = a.stats + (size_t)g * kChunks * kHq + h;
-    unsigned long long r0 = 0, r1 = 0;
-    wait_all([&] {
-      if (lane < kChunks && r0 == 0) r0 = ld_dev(st + lane * kHq);
-      if (lane + 64 < kChunks && r1 == 0) r1 = ld_dev(st + (lane + 64) * kHq);
-      return (lane >= kChunks || r0 != 0) && (lane + 64 >= kChunks || r1 != 0);
-    }, a);
+    // two generations of unconditional loads in flight, as in final_top16
+    unsigned long long r0 = 0, r1 = 0, gen[2][2];
+    auto issue = [&](int gg) {
+      gen[gg][0] = ld_dev(st + min(lane, kChunks - 1) * kHq);
+      gen[gg][1] = ld_dev(st + min(lane + 64, kChunks - 1) * kHq);
+    };
+    auto take = [&](int gg) {
+      r0 = r0 ? r0 : gen[gg][0];
+      r1 = r1 ? r1 : gen[gg][1];
+      return __ballot(!((lane >= kChunks || r0 != 0) && (lane + 64 >= kChunks || r1 != 0))) == 0;
+    };
+    drain();
+    issue(0);
+    for (int spins = 0;; spins += 2) {
+      issue(1);
+      __builtin_amdgcn_s_waitcnt(vmcnt_wait(2));  // generation 0 has landed
+      if (take(0)) break;
+      issue(0);
+      __builtin_amdgcn_s_waitcnt(vmcnt_wait(2));
+      if (take(1)) break;
+      if (spins >= a.spin) {
+        if (lane == 0) report_error(a.err, a.err_host);
+        break;
+      }
+    }
     const float2 mz = merge_chunk_stats([&](int ch) { return unpub2(ch == lane ? r0 : r1); });
     if (lane == 0) {
       lds.gmax[h] = mz.x;
