@@ -679,17 +679,38 @@ __device__ __forceinline__ uint32_t capped_walk(const DecodeArgs& a, int g, int 
       const int j = lane & 7;
       int s0 = 0, s1 = 0;
       for (int q0 = lane >> 3; q0 < a.S; q0 += 32) {
-        unsigned r[4] = {0u, 0u, 0u, 0u};
-        wait_all([&] {
+        // two generations of unconditional loads in flight (nothing else
+        // is, after the drain), each waited for explicitly, as in the
+        // final merge
+        unsigned r[4] = {0u, 0u, 0u, 0u}, gen[2][4];
+        auto issue = [&](int gg) {
+#pragma unroll
+          for (int t = 0; t < 4; ++t)
+            gen[gg][t] = ld_dev(&rec[((size_t)k * a.S + min(q0 + 8 * t, a.S - 1)) * kPacked + j]);
+        };
+        auto take = [&](int gg) {
           bool done = true;
 #pragma unroll
           for (int t = 0; t < 4; ++t) {
-            const int q = q0 + 8 * t;
-            if (q < a.S && r[t] == 0u) r[t] = ld_dev(&rec[((size_t)k * a.S + q) * kPacked + j]);
-            done = done && (q >= a.S || r[t] != 0u);
+            r[t] = r[t] ? r[t] : gen[gg][t];
+            done = done && (q0 + 8 * t >= a.S || r[t] != 0u);
           }
-          return done;
-        }, a);
+          return __ballot(!done) == 0;
+        };
+        drain();
+        issue(0);
+        for (int spins = 0;; spins += 2) {
+          issue(1);
+          __builtin_amdgcn_s_waitcnt(vmcnt_wait(4));  // generation 0 has landed
+          if (take(0)) break;
+          issue(0);
+          __builtin_amdgcn_s_waitcnt(vmcnt_wait(4));
+          if (take(1)) break;
+          if (spins >= a.spin) {
+            if ((threadIdx.x & 63) == 0) report_error(a.err, a.err_host);
+            break;
+          }
+        }
 #pragma unroll
         for (int t = 0; t < 4; ++t)
           if (q0 + 8 * t < a.S) {
