@@ -175,6 +175,19 @@ __device__ __forceinline__ void wait_all(Pred pred, const Args& a) {
 // the wave are outstanding (expcnt and lgkmcnt left open).
 constexpr int vmcnt_wait(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
 
+#ifndef PRISMKV_POLL_STAGGER
+#define PRISMKV_POLL_STAGGER 16
+#endif
+// The two generations of a poll: after the first is issued, the second waits
+// PRISMKV_POLL_STAGGER x 64 cycles (about 0.4 us), so that thereafter they
+// land that far apart and a published word is seen a quarter of a round trip
+// after it lands on average, not half of one.  Measured at 64K (36 layers,
+// four alternations): 0 -> 25.28, 8 -> 25.13, 12 -> 24.97, 16 -> 24.90,
+// 20 -> 24.95, 24 -> 25.11, 32 -> 25.63 us per layer.
+__device__ __forceinline__ void poll_stagger() {
+  if constexpr (PRISMKV_POLL_STAGGER > 0) __builtin_amdgcn_s_sleep(PRISMKV_POLL_STAGGER);
+}
+
 // Bitmap row of a candidate key.  Landed keys always name a bucket below
 // 3000; the clamp keeps a key read after a wait gave up in range too.
 __device__ __forceinline__ int row_of(unsigned long long key) { return min(key_bucket(key), kF - 1); }
@@ -274,6 +287,7 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int g, int h, i
   constexpr int kWaitGen = vmcnt_wait(1 + kPer);
   drain();
   issue(0);
+  poll_stagger();  // the second generation trails the first by part of a round trip
   for (int spins = 0;; spins += 2) {
     issue(1);
     __builtin_amdgcn_s_waitcnt(kWaitGen);  // generation 0 has landed, generation 1 is in flight
@@ -392,6 +406,7 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, D
     for (int k = 0; k < KW; ++k) r[k] = 0;
     drain();
     issue(0);
+    poll_stagger();  // the second generation trails the first by part of a round trip
     for (int spins = 0;; spins += 2) {
       issue(1);
       __builtin_amdgcn_s_waitcnt(vmcnt_wait(KW));  // generation 0 has landed
@@ -530,6 +545,7 @@ __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p,
     };
     drain();
     issue(0);
+    poll_stagger();  // the second generation trails the first by part of a round trip
     for (int spins = 0;; spins += 2) {
       issue(1);
       __builtin_amdgcn_s_waitcnt(vmcnt_wait(2));  // generation 0 has landed
@@ -699,6 +715,7 @@ __device__ __forceinline__ uint32_t capped_walk(const DecodeArgs& a, int g, int 
         };
         drain();
         issue(0);
+        poll_stagger();  // the second generation trails the first by part of a round trip
         for (int spins = 0;; spins += 2) {
           issue(1);
           __builtin_amdgcn_s_waitcnt(vmcnt_wait(4));  // generation 0 has landed
