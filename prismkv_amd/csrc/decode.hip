@@ -188,6 +188,44 @@ __device__ __forceinline__ void poll_stagger() {
   if constexpr (PRISMKV_POLL_STAGGER > 0) __builtin_amdgcn_s_sleep(PRISMKV_POLL_STAGGER);
 }
 
+#ifndef PRISMKV_POLL_GENS
+#define PRISMKV_POLL_GENS 2
+#endif
+constexpr int kPollGens = PRISMKV_POLL_GENS;  // generations of a poll's loads in flight
+
+// Polls published words with kPollGens generations of kLoads unconditional
+// loads each in flight (issue(g) requests generation g, ready(g) takes it
+// and returns the caller's uniform verdict).  Nothing else is in flight
+// after the drain, so each generation is waited for exactly with
+// vmcnt((kPollGens - 1) kLoads), leaving the later ones outstanding; the
+// generations are issued poll_stagger() apart and so keep landing apart.
+// Gives up (report(), once) after `limit` generations.
+template <int kLoads, typename Issue, typename Ready, typename Report>
+__device__ __forceinline__ void poll_generations(Issue&& issue, Ready&& ready, Report&& report, int limit) {
+  drain();
+#pragma unroll
+  for (int g = 0; g + 1 < kPollGens; ++g) {
+    issue(g);
+    poll_stagger();
+  }
+  for (int spins = 0;; spins += kPollGens) {
+    bool done = false;
+#pragma unroll
+    for (int g = 0; g < kPollGens; ++g) {
+      if (!done) {
+        issue((g + kPollGens - 1) % kPollGens);
+        __builtin_amdgcn_s_waitcnt(vmcnt_wait((kPollGens - 1) * kLoads));  // generation g has landed
+        done = ready(g);
+      }
+    }
+    if (done) return;
+    if (spins >= limit) {
+      report();
+      return;
+    }
+  }
+}
+
 // Bitmap row of a candidate key.  Landed keys always name a bucket below
 // 3000; the clamp keeps a key read after a wait gave up in range too.
 __device__ __forceinline__ int row_of(unsigned long long key) { return min(key_bucket(key), kF - 1); }
@@ -260,8 +298,8 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int g, int h, i
 #pragma unroll
   for (int i = 0; i < kPer; ++i)
     accp[i] = reinterpret_cast<const unsigned*>(base + (size_t)min(sg + kGroups * i, S - 1) * stride + 2 + d);
-  unsigned long long rmz = 0, gmz[2];
-  unsigned racc[kPer], gacc[2][kPer];
+  unsigned long long rmz = 0, gmz[kPollGens];
+  unsigned racc[kPer], gacc[kPollGens][kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) racc[i] = 0u;
   auto issue = [&](int gen) {
@@ -283,23 +321,8 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int g, int h, i
       }
     return ok;
   };
-  // s_waitcnt with vmcnt = one generation's loads (lgkmcnt, expcnt left open)
-  constexpr int kWaitGen = vmcnt_wait(1 + kPer);
-  drain();
-  issue(0);
-  poll_stagger();  // the second generation trails the first by part of a round trip
-  for (int spins = 0;; spins += 2) {
-    issue(1);
-    __builtin_amdgcn_s_waitcnt(kWaitGen);  // generation 0 has landed, generation 1 is in flight
-    if (__syncthreads_and(take(0))) break;
-    issue(0);
-    __builtin_amdgcn_s_waitcnt(kWaitGen);
-    if (__syncthreads_and(take(1))) break;
-    if (spins >= a.spin) {
-      if (tid == 0) report_error(a.err, a.err_host);
-      break;
-    }
-  }
+  poll_generations<1 + kPer>(issue, [&](int gen) { return __syncthreads_and(take(gen)) != 0; },
+                              [&] { if (tid == 0) report_error(a.err, a.err_host); }, a.spin);
   // M = max over splits, den = sum of weighted denominators (fixed order)
   float2 mz = make_float2(-INFINITY, 0.f);
   if (tid < S) {
@@ -388,7 +411,7 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, D
     // two generations of unconditional loads in flight (nothing else is,
     // after the drain), each waited for explicitly: a key that lands just
     // after one generation was issued is seen by the next
-    unsigned long long r[KW], gen[2][KW];
+    unsigned long long r[KW], gen[kPollGens][KW];
     auto issue = [&](int gg) {
 #pragma unroll
       for (int k = 0; k < KW; ++k) gen[gg][k] = ld_dev(cg + min((w * KW + k) * 64 + lane, nk - 1));
@@ -404,21 +427,7 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, D
     };
 #pragma unroll
     for (int k = 0; k < KW; ++k) r[k] = 0;
-    drain();
-    issue(0);
-    poll_stagger();  // the second generation trails the first by part of a round trip
-    for (int spins = 0;; spins += 2) {
-      issue(1);
-      __builtin_amdgcn_s_waitcnt(vmcnt_wait(KW));  // generation 0 has landed
-      if (take(0)) break;
-      issue(0);
-      __builtin_amdgcn_s_waitcnt(vmcnt_wait(KW));
-      if (take(1)) break;
-      if (spins >= a.spin) {
-        if (lane == 0) report_error(a.err, a.err_host);
-        break;
-      }
-    }
+    poll_generations<KW>(issue, take, [&] { if (lane == 0) report_error(a.err, a.err_host); }, a.spin);
 #pragma unroll
     for (int k = 0; k < KW; ++k) v[k] = (w * KW + k) * 64 + lane < nk ? ~r[k] : 0ull;
   }
@@ -533,7 +542,7 @@ __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p,
     const int h = w;
     const unsigned long long* st = a.stats + (size_t)g * kChunks * kHq + h;
     // two generations of unconditional loads in flight, as in final_top16
-    unsigned long long r0 = 0, r1 = 0, gen[2][2];
+    unsigned long long r0 = 0, r1 = 0, gen[kPollGens][2];
     auto issue = [&](int gg) {
       gen[gg][0] = ld_dev(st + min(lane, kChunks - 1) * kHq);
       gen[gg][1] = ld_dev(st + min(lane + 64, kChunks - 1) * kHq);
@@ -543,21 +552,7 @@ __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p,
       r1 = r1 ? r1 : gen[gg][1];
       return __ballot(!((lane >= kChunks || r0 != 0) && (lane + 64 >= kChunks || r1 != 0))) == 0;
     };
-    drain();
-    issue(0);
-    poll_stagger();  // the second generation trails the first by part of a round trip
-    for (int spins = 0;; spins += 2) {
-      issue(1);
-      __builtin_amdgcn_s_waitcnt(vmcnt_wait(2));  // generation 0 has landed
-      if (take(0)) break;
-      issue(0);
-      __builtin_amdgcn_s_waitcnt(vmcnt_wait(2));
-      if (take(1)) break;
-      if (spins >= a.spin) {
-        if (lane == 0) report_error(a.err, a.err_host);
-        break;
-      }
-    }
+    poll_generations<2>(issue, take, [&] { if (lane == 0) report_error(a.err, a.err_host); }, a.spin);
     const float2 mz = merge_chunk_stats([&](int ch) { return unpub2(ch == lane ? r0 : r1); });
     if (lane == 0) {
       lds.gmax[h] = mz.x;
@@ -698,7 +693,7 @@ __device__ __forceinline__ uint32_t capped_walk(const DecodeArgs& a, int g, int 
         // two generations of unconditional loads in flight (nothing else
         // is, after the drain), each waited for explicitly, as in the
         // final merge
-        unsigned r[4] = {0u, 0u, 0u, 0u}, gen[2][4];
+        unsigned r[4] = {0u, 0u, 0u, 0u}, gen[kPollGens][4];
         auto issue = [&](int gg) {
 #pragma unroll
           for (int t = 0; t < 4; ++t)
@@ -713,21 +708,7 @@ __device__ __forceinline__ uint32_t capped_walk(const DecodeArgs& a, int g, int 
           }
           return __ballot(!done) == 0;
         };
-        drain();
-        issue(0);
-        poll_stagger();  // the second generation trails the first by part of a round trip
-        for (int spins = 0;; spins += 2) {
-          issue(1);
-          __builtin_amdgcn_s_waitcnt(vmcnt_wait(4));  // generation 0 has landed
-          if (take(0)) break;
-          issue(0);
-          __builtin_amdgcn_s_waitcnt(vmcnt_wait(4));
-          if (take(1)) break;
-          if (spins >= a.spin) {
-            if ((threadIdx.x & 63) == 0) report_error(a.err, a.err_host);
-            break;
-          }
-        }
+        poll_generations<4>(issue, take, [&] { if (lane == 0) report_error(a.err, a.err_host); }, a.spin);
 #pragma unroll
         for (int t = 0; t < 4; ++t)
           if (q0 + 8 * t < a.S) {
