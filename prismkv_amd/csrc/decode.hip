@@ -199,7 +199,7 @@ constexpr int kPollGens = PRISMKV_POLL_GENS;  // generations of a poll's loads i
 // after the drain, so each generation is waited for exactly with
 // vmcnt((kPollGens - 1) kLoads), leaving the later ones outstanding; the
 // generations are issued poll_stagger() apart and so keep landing apart.
-// Gives up (report(), once) after `limit` generations.
+// Gives up (report(), once) after `limit` + 1 generations found short.
 template <int kLoads, typename Issue, typename Ready, typename Report>
 __device__ __forceinline__ void poll_generations(Issue&& issue, Ready&& ready, Report&& report, int limit) {
   drain();
@@ -208,20 +208,16 @@ __device__ __forceinline__ void poll_generations(Issue&& issue, Ready&& ready, R
     issue(g);
     poll_stagger();
   }
-  for (int spins = 0;; spins += kPollGens) {
-    bool done = false;
+  for (int tries = 0;;) {
 #pragma unroll
     for (int g = 0; g < kPollGens; ++g) {
-      if (!done) {
-        issue((g + kPollGens - 1) % kPollGens);
-        __builtin_amdgcn_s_waitcnt(vmcnt_wait((kPollGens - 1) * kLoads));  // generation g has landed
-        done = ready(g);
+      issue((g + kPollGens - 1) % kPollGens);
+      __builtin_amdgcn_s_waitcnt(vmcnt_wait((kPollGens - 1) * kLoads));  // generation g has landed
+      if (ready(g)) return;
+      if (tries++ >= limit) {  // (a limit of 0 gives up at the first generation found short)
+        report();
+        return;
       }
-    }
-    if (done) return;
-    if (spins >= limit) {
-      report();
-      return;
     }
   }
 }
