@@ -453,15 +453,26 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, D
   if (threadIdx.x < kListed) {
     const unsigned long long x = lds.sel.best[threadIdx.x];
     if (x != 0ull) {  // nonzero keys are unique, so their ranks are
+      // binary searches of the 8 descending lists, step by step across the
+      // lists, so each step's 8 LDS reads are in flight together
+      constexpr int kLists = kDT / 64;
+      int pos[kLists];
+#pragma unroll
+      for (int L = 0; L < kLists; ++L) pos[L] = 0;
+#pragma unroll
+      for (int step = kTop / 2; step > 0; step >>= 1) {
+        unsigned long long y[kLists];
+#pragma unroll
+        for (int L = 0; L < kLists; ++L) y[L] = lds.sel.best[kTop * L + pos[L] + step - 1];
+#pragma unroll
+        for (int L = 0; L < kLists; ++L) pos[L] += y[L] > x ? step : 0;
+      }
+      unsigned long long y[kLists];
+#pragma unroll
+      for (int L = 0; L < kLists; ++L) y[L] = lds.sel.best[kTop * L + pos[L]];
       int rank = 0;
 #pragma unroll
-      for (int L = 0; L < kDT / 64; ++L) {
-        const unsigned long long* lst = lds.sel.best + kTop * L;  // descending
-        int pos = 0;
-#pragma unroll
-        for (int step = kTop / 2; step > 0; step >>= 1) pos += lst[pos + step - 1] > x ? step : 0;
-        rank += pos + (lst[pos] > x ? 1 : 0);  // pos <= 15 here; 16 when the whole list is greater
-      }
+      for (int L = 0; L < kLists; ++L) rank += pos[L] + (y[L] > x ? 1 : 0);  // 16 when the whole list is greater
       if (rank < kTop) lds.win[rank] = x;
     }
   }
