@@ -74,6 +74,7 @@ namespace {
 
 constexpr int kDT = kAT;           // 512 threads, 8 waves
 constexpr int kTileWords = 64;     // bitmap words per union chunk (one wave, one word per lane)
+constexpr int kPrefetchChunks = 2; // union chunks the wide variant requests in phase 4 (tiles of 65-128 words)
 constexpr int kMaxTileWords = 512; // bitmap words per workgroup at most (8 chunks, one per wave)
 constexpr int kTileTokens = 32 * kMaxTileWords;
 constexpr int kMinSplits = 32;     // at least one workgroup per CU for the scoring
@@ -144,6 +145,7 @@ struct DecodeLds {
       alignas(16) unsigned long long own[2 * 64];  // this workgroup's keys (<= 96 used)
       alignas(16) unsigned long long best[kDT / 64 * kTop];
       unsigned ors[kDT / 64][kTileWords];  // per wave: OR of its prefetched winning rows over the tile's words
+      unsigned ors2[kDT / 64][kTileWords];  // the same over the second chunk (wide variant)
     } sel;
     MfmaLds<kDT / 64> mf;
     struct {
@@ -397,7 +399,7 @@ struct NoEarly {
   __device__ void issue() {}
   __device__ void wait_words() const {}
 };
-template <int KW, bool kPrefetchRows = true, class Early = NoEarly>
+template <int KW, bool kPrefetchRows = true, class Early = NoEarly, int kPfChunks = 1>
 __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, DecodeLds& lds, Early& early) {
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int nk = a.S * kTop;
@@ -434,17 +436,24 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, D
   const int nw = (a.H + 31) / 32;
   const int wd = p * a.tw + lane;
   const bool word = lane < a.tw && wd < nw;
+  // kPfChunks = 2 (tiles of more than one chunk): the second chunk's words
+  // are requested too
+  constexpr bool two = kPrefetchRows && kPfChunks > 1;
+  const bool word2 = kTileWords + lane < a.tw && wd + kTileWords < nw;
   unsigned long long pk[kPrefetch];
-  uint32_t pw[kPrefetch];
+  uint32_t pw[kPrefetch], pw2[kPrefetch];
 #pragma unroll
   for (int r = 0; r < kPrefetch; ++r) {
     pk[r] = readlane_u64(best, r);  // rank r of this wave's list (uniform)
     pw[r] = 0u;
+    pw2[r] = 0u;
     if constexpr (kPrefetchRows) {
-      // every rank issues its load (an empty key's through an empty resource),
+      // every rank issues its loads (an empty key's through an empty resource),
       // so the loads after these are counted exactly when pw is waited for
       const uint32_t* row = a.bits + ((size_t)g * kF + row_of(pk[r])) * a.row_words;
-      pw[r] = load_nt4_buf(raw_buffer(row, pk[r] ? (int)a.row_words * 4 : 0), (unsigned)min(wd, nw - 1) * 4u);
+      const __amdgpu_buffer_rsrc_t res = raw_buffer(row, pk[r] ? (int)a.row_words * 4 : 0);
+      pw[r] = load_nt4_buf(res, (unsigned)min(wd, nw - 1) * 4u);
+      if constexpr (two) pw2[r] = load_nt4_buf(res, (unsigned)min(wd + kTileWords, nw - 1) * 4u);
     }
   }
   early.barrier();
@@ -482,17 +491,19 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, D
   const unsigned long long win = lane < kTop ? lds.win[lane] : 0ull;
   const int need = __popcll(__ballot(win != 0ull));
   const unsigned long long last = need ? readlane_u64(win, need - 1) : ~0ull;
-  uint32_t part = 0u;
+  uint32_t part = 0u, part2 = 0u;
   unsigned covered = 0u;
   early.wait_words();
 #pragma unroll
   for (int r = 0; r < kPrefetch; ++r)
     if (pk[r] != 0ull && pk[r] >= last) {  // uniform
       part |= pw[r];
+      part2 |= pw2[r];
       covered |= 1u << __popcll(__ballot(lane < need && win > pk[r]));
     }
   lds.sel.ors[w][lane] = word ? part : 0u;
-  if (lane == 0) lds.cover[w] = covered;
+  if constexpr (two) lds.sel.ors2[w][lane] = word2 ? part2 : 0u;
+  if (lane == 0) lds.cover[w] = kPrefetchRows ? covered : 0u;
   if (w == 0) {
     if (lane < kTop) lds.sel_rows[lane] = lane < need ? row_of(win) : 0;  // the union reads rows < need only
     if (lane == 0) lds.need = need;
@@ -503,7 +514,7 @@ __device__ __forceinline__ void final_top16(const DecodeArgs& a, int g, int p, D
 // Phases 1-4: the group's Top-16 (rank order) into lds.win (every wave) and
 // lds.sel_rows / lds.need.  Without kUnion only workgroup 0 runs phase 4;
 // kPrefetchRows requests the union's bitmap words in phase 4.
-template <int KW, bool kUnion = true, bool kPrefetchRows = kUnion, class Early = NoEarly>
+template <int KW, bool kUnion = true, bool kPrefetchRows = kUnion, class Early = NoEarly, int kPfChunks = 1>
 __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p, DecodeLds& lds, Early& early) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int S = a.S;
@@ -590,7 +601,7 @@ __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p,
   if constexpr (!kUnion) {
     if (p != 0) return;
   }
-  final_top16<KW, kUnion && kPrefetchRows>(a, g, p, lds, early);
+  final_top16<KW, kUnion && kPrefetchRows, Early, kPfChunks>(a, g, p, lds, early);
 }
 template <int KW, bool kUnion = true, bool kPrefetchRows = kUnion>
 __device__ __forceinline__ void decode_select(const DecodeArgs& a, int g, int p, DecodeLds& lds) {
@@ -837,7 +848,10 @@ struct EarlyTail {
 // still published and merged (without writing out), since that hand-off is
 // what tells workgroup 0 that every workgroup is done with the published
 // words it then clears.
-template <int KW, bool kGiven = false, bool kCap = false, bool kEarlyTail = false, bool kRouteOnly = false>
+// kWide: union tiles of 65-128 words (the host's choice when tw > 64), whose
+// two chunks' words phase 4 requests.
+template <int KW, bool kGiven = false, bool kCap = false, bool kEarlyTail = false, bool kRouteOnly = false,
+          bool kWide = false>
 __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   const int p = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   __shared__ DecodeLds lds;
@@ -852,6 +866,7 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   // so it streams in while the selection finishes and the union is built
   // (HBM is otherwise idle then); phase 6 attends it first.
   constexpr bool kEarly = kEarlyTail && !kGiven && !kCap && !kRouteOnly && !PRISMKV_VALU_ATTENTION;
+  constexpr int kPfChunks = kWide && !kGiven && !kCap ? 2 : 1;  // union chunks prefetched in phase 4
   int early_n = 0;
   uint4 ek[1][4], ev[1][4];
 
@@ -880,9 +895,10 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     // ---- 1-4. the group's Top-16 (and the early tail rows requested)
     if constexpr (kEarly) {
       EarlyTail early{a, g, p, tail_word, early_n, ek, ev};
-      decode_select<KW>(a, g, p, lds, early);
+      decode_select<KW, true, true, EarlyTail, kPfChunks>(a, g, p, lds, early);
     } else {
-      decode_select<KW>(a, g, p, lds);
+      NoEarly none;
+      decode_select<KW, true, true, NoEarly, kPfChunks>(a, g, p, lds, none);
     }
   }
   // ---- 1-4b. (capped) the group's Top-16; the budgeted walk over it runs
@@ -892,9 +908,10 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   // ---- 5. union tile: OR the selected rows over words [tw p, tw (p + 1)), compact.
   // One 64-word chunk (histories up to 64K at 8 groups): wave 0 ORs the rows
   // the waves prefetched in phase 4 and loads any winner none prefetched.
-  // More chunks: wave w < ceil(tw / 64) loads chunk w of every selected row;
-  // the chunks' counts give each its offset.  (Phase 4's final barrier
-  // publishes need and sel_rows.)
+  // More chunks: wave w < ceil(tw / 64) takes chunk w -- in the wide variant
+  // (two chunks, both prefetched) as wave 0 does its one chunk, otherwise by
+  // loading every selected row; the chunks' counts give each its offset.
+  // (Phase 4's final barrier publishes need and sel_rows.)
   const int nw = (a.H + 31) / 32;
   if constexpr (kCap) {
     // the capped launch lists its rows during the walk (phase 6)
@@ -964,7 +981,29 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     uint32_t m = 0u;
     int n = 0, incl = 0;
     if (w < chunks) {
-      if (nr > 0 && cw < a.tw && wd < nw) {
+      if constexpr (kPfChunks > 1) {
+        // chunk w < 2 (both prefetched): the waves' ORs, then one round of
+        // loads for the winners no wave prefetched (every rank loads, a
+        // covered one repeating the first missing row, and only the missing
+        // ones are kept)
+        unsigned covered = 0u;
+#pragma unroll
+        for (int k = 0; k < kDT / 64; ++k) {
+          m |= w ? lds.sel.ors2[k][lane] : lds.sel.ors[k][lane];
+          covered |= lds.cover[k];
+        }
+        const unsigned missing = ((1u << nr) - 1u) & ~covered;  // uniform
+        if (missing && cw < a.tw && wd < nw) {
+          const uint32_t* gb = a.bits + (size_t)g * kF * a.row_words + wd;
+          const int first = __builtin_ctz(missing);
+          uint32_t v[kTop];
+#pragma unroll
+          for (int r = 0; r < kTop; ++r)
+            v[r] = __builtin_nontemporal_load(gb + (size_t)lds.sel_rows[(missing >> r) & 1u ? r : first] * a.row_words);
+#pragma unroll
+          for (int r = 0; r < kTop; ++r) m |= (missing >> r) & 1u ? v[r] : 0u;
+        }
+      } else if (nr > 0 && cw < a.tw && wd < nw) {
         const uint32_t* gb = a.bits + (size_t)g * kF * a.row_words + wd;
         uint32_t v[kTop];
 #pragma unroll
@@ -1365,7 +1404,16 @@ static int resident_workgroups() {
                          reinterpret_cast<const void*>(decode_kernel<1, false, false, false, true>),
                          reinterpret_cast<const void*>(decode_kernel<2, false, false, false, true>),
                          reinterpret_cast<const void*>(decode_kernel<4, false, false, false, true>),
-                         reinterpret_cast<const void*>(decode_kernel<8, false, false, false, true>)};
+                         reinterpret_cast<const void*>(decode_kernel<8, false, false, false, true>),
+                         reinterpret_cast<const void*>(decode_kernel<1, false, false, false, false, true>),
+                         reinterpret_cast<const void*>(decode_kernel<2, false, false, false, false, true>),
+                         reinterpret_cast<const void*>(decode_kernel<4, false, false, false, false, true>),
+                         reinterpret_cast<const void*>(decode_kernel<1, false, false, true, false, true>),
+                         reinterpret_cast<const void*>(decode_kernel<2, false, false, true, false, true>),
+                         reinterpret_cast<const void*>(decode_kernel<4, false, false, true, false, true>),
+                         reinterpret_cast<const void*>(decode_kernel<1, false, false, false, true, true>),
+                         reinterpret_cast<const void*>(decode_kernel<2, false, false, false, true, true>),
+                         reinterpret_cast<const void*>(decode_kernel<4, false, false, false, true, true>)};
     // (the capped launches' row list is followed by the walk's words)
     const int dyn = kTileTokens * (int)sizeof(int) + kWalkWordsBytes;
     for (const void* fn : fns) {
@@ -1399,6 +1447,18 @@ static int decode_check(uint64_t q, uint64_t moments, uint64_t counts, uint64_t 
     return kBadSize;
   if (decode_splits(groups) > resident_workgroups()) return kBadSize;  // a group's workgroups must be resident together
   return 0;
+}
+
+// One fused variant's launch for S workgroups per group: KW = ceil(S / 32)
+// 64-key candidate sets per wave (the wide variant is never taken above
+// S = 128, so it has no KW = 8 instantiation).
+template <bool kGiven, bool kCap, bool kEarlyTail, bool kRouteOnly, bool kWide>
+static void launch_decode(int S, dim3 grid, size_t dyn, hipStream_t s, const DecodeArgs& a) {
+  const dim3 block(kDT);
+  if (S <= 32) hipLaunchKernelGGL((decode_kernel<1, kGiven, kCap, kEarlyTail, kRouteOnly, kWide>), grid, block, dyn, s, a);
+  else if (S <= 64) hipLaunchKernelGGL((decode_kernel<2, kGiven, kCap, kEarlyTail, kRouteOnly, kWide>), grid, block, dyn, s, a);
+  else if (S <= 128) hipLaunchKernelGGL((decode_kernel<4, kGiven, kCap, kEarlyTail, kRouteOnly, kWide>), grid, block, dyn, s, a);
+  else if constexpr (!kWide) hipLaunchKernelGGL((decode_kernel<8, kGiven, kCap, kEarlyTail, kRouteOnly, false>), grid, block, dyn, s, a);
 }
 
 // Enqueues a decode launch whose arguments decode_check accepted.
@@ -1445,36 +1505,26 @@ static int decode_launch(uint64_t q, uint64_t moments, uint64_t counts, uint64_t
   a.out = reinterpret_cast<uint16_t*>(out);
   a.ids_in = nullptr;
   a.count_in = nullptr;
-  const dim3 grid(S, groups), block(kDT);
+  const dim3 grid(S, groups);
   hipStream_t s = (hipStream_t)stream;
   const size_t rows_bytes = (size_t)32 * a.tw * sizeof(int);  // the tile's row list (dynamic LDS)
+  // wide: union tiles of 65-128 words, both chunks prefetched (S <= 128 at
+  // every history the single launch takes, 8 groups above 64K)
+  const bool wide = a.tw > kTileWords && a.tw <= kPrefetchChunks * kTileWords && S <= 128;
   if (route_only) {
-    if (S <= 32) hipLaunchKernelGGL((decode_kernel<1, false, false, false, true>), grid, block, rows_bytes, s, a);
-    else if (S <= 64) hipLaunchKernelGGL((decode_kernel<2, false, false, false, true>), grid, block, rows_bytes, s, a);
-    else if (S <= 128) hipLaunchKernelGGL((decode_kernel<4, false, false, false, true>), grid, block, rows_bytes, s, a);
-    else hipLaunchKernelGGL((decode_kernel<8, false, false, false, true>), grid, block, rows_bytes, s, a);
+    if (wide) launch_decode<false, false, false, true, true>(S, grid, rows_bytes, s, a);
+    else launch_decode<false, false, false, true, false>(S, grid, rows_bytes, s, a);
   } else if (limit >= 0) {
-    const size_t dyn = rows_bytes + kWalkWordsBytes;
-    if (S <= 32) hipLaunchKernelGGL((decode_kernel<1, false, true>), grid, block, dyn, s, a);
-    else if (S <= 64) hipLaunchKernelGGL((decode_kernel<2, false, true>), grid, block, dyn, s, a);
-    else if (S <= 128) hipLaunchKernelGGL((decode_kernel<4, false, true>), grid, block, dyn, s, a);
-    else hipLaunchKernelGGL((decode_kernel<8, false, true>), grid, block, dyn, s, a);
+    launch_decode<false, true, false, false, false>(S, grid, rows_bytes + kWalkWordsBytes, s, a);
   } else if (given) {
-    if (S <= 32) hipLaunchKernelGGL((decode_kernel<1, true>), grid, block, rows_bytes, s, a);
-    else if (S <= 64) hipLaunchKernelGGL((decode_kernel<2, true>), grid, block, rows_bytes, s, a);
-    else if (S <= 128) hipLaunchKernelGGL((decode_kernel<4, true>), grid, block, rows_bytes, s, a);
-    else hipLaunchKernelGGL((decode_kernel<8, true>), grid, block, rows_bytes, s, a);
+    launch_decode<true, false, false, false, false>(S, grid, rows_bytes, s, a);
   } else if ((T + S - 1) / S >= kEarlyRows / 2) {
     // tails that give most waves an early block: the early-tail variant
-    if (S <= 32) hipLaunchKernelGGL((decode_kernel<1, false, false, true>), grid, block, rows_bytes, s, a);
-    else if (S <= 64) hipLaunchKernelGGL((decode_kernel<2, false, false, true>), grid, block, rows_bytes, s, a);
-    else if (S <= 128) hipLaunchKernelGGL((decode_kernel<4, false, false, true>), grid, block, rows_bytes, s, a);
-    else hipLaunchKernelGGL((decode_kernel<8, false, false, true>), grid, block, rows_bytes, s, a);
+    if (wide) launch_decode<false, false, true, false, true>(S, grid, rows_bytes, s, a);
+    else launch_decode<false, false, true, false, false>(S, grid, rows_bytes, s, a);
   } else {
-    if (S <= 32) hipLaunchKernelGGL(decode_kernel<1>, grid, block, rows_bytes, s, a);
-    else if (S <= 64) hipLaunchKernelGGL(decode_kernel<2>, grid, block, rows_bytes, s, a);
-    else if (S <= 128) hipLaunchKernelGGL(decode_kernel<4>, grid, block, rows_bytes, s, a);
-    else hipLaunchKernelGGL(decode_kernel<8>, grid, block, rows_bytes, s, a);
+    if (wide) launch_decode<false, false, false, false, true>(S, grid, rows_bytes, s, a);
+    else launch_decode<false, false, false, false, false>(S, grid, rows_bytes, s, a);
   }
   return (int)hipGetLastError();
 }
