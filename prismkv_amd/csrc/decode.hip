@@ -106,7 +106,6 @@ struct DecodeArgs {
   int spin;                       // bound of every wait (sleeps), prismkv_set_spin_limit
   float* state;  // [G][S][4 heads][4 slices][34] published split states
   unsigned* walk;  // [G][4 windows][S][8] published pattern counts (capped launch)
-  unsigned* done;  // [G] workgroups past their last read of published words (route-and-union launch)
   int limit;       // the strict unique cap's limit (capped launch)
   int64_t* features;
   float* valid;
@@ -393,6 +392,23 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int g, int h, i
 // selection never waits for the tail -- and wait_words() before the words
 // are used (a wait that leaves the tail rows in flight).
 constexpr int kPrefetch = 6;
+
+// Phase 5's tile count, published for the ids offsets.  The decode publishes
+// one status word per tile (cleared by workgroup 0 after the final merge).
+// The route-only launch has no final hand-off, so it publishes the count to
+// each later tile r in a slot of r's own ([G][S][S] words in the split-state
+// region, which it does not otherwise use): every slot has one reader, which
+// clears it once read.
+template <bool kSlots>
+__device__ __forceinline__ void publish_count(const DecodeArgs& a, int g, int p, int total, int lane) {
+  if constexpr (kSlots) {
+    unsigned* slots = reinterpret_cast<unsigned*>(a.state) + (size_t)g * a.S * a.S + p;
+    for (int r = p + 1 + lane; r < a.S; r += 64) st_dev(slots + (size_t)r * a.S, kReady | (unsigned)total);
+  } else if (lane == 0) {
+    st_dev(&a.status[(size_t)g * a.S + p], kReady | (unsigned)total);
+  }
+}
+
 struct NoEarly {
   __device__ void prepare() {}
   __device__ void barrier() { __syncthreads(); }
@@ -843,11 +859,61 @@ struct EarlyTail {
   __device__ void wait_words() const { __builtin_amdgcn_s_waitcnt(8 | (0x7 << 4) | (0xf << 8)); }
 };
 
-// kRouteOnly: stages 1-2 alone (what Native8B.route() runs): the selection,
-// the union tiles and the ids, with no attention; the empty split states are
-// still published and merged (without writing out), since that hand-off is
-// what tells workgroup 0 that every workgroup is done with the published
-// words it then clears.
+// The route-only launch after phase 5 (what Native8B.route() runs: the
+// selection, the union tiles and the ids, no attention): wave 0 polls the
+// lower tiles' counts from this tile's slots (clearing each once read), the
+// tile writes its ids, and the group's last workgroup writes count, features /
+// valid / raw and clears the statistics and candidates -- every workgroup
+// published its count after its phase 4, so none reads them any more.
+template <int KW>
+__device__ __forceinline__ void route_finish(const DecodeArgs& a, int g, int p, DecodeLds& lds, const int* rows) {
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, S = a.S;
+  const int n_sel = lds.nsel;
+  if (w == 0) {
+    constexpr int kC = (KW + 1) / 2;  // 64-lane chunks of S <= 32 KW lower tiles
+    unsigned* slots = reinterpret_cast<unsigned*>(a.state) + ((size_t)g * S + p) * S;  // tile p's slots
+    unsigned v[kC], gen[kPollGens][kC];
+#pragma unroll
+    for (int c = 0; c < kC; ++c) v[c] = 0u;
+    auto issue = [&](int gg) {
+#pragma unroll
+      for (int c = 0; c < kC; ++c) gen[gg][c] = ld_dev(slots + min(64 * c + lane, S - 1));
+    };
+    auto take = [&](int gg) {
+      bool ok = true;
+#pragma unroll
+      for (int c = 0; c < kC; ++c)
+        if (64 * c + lane < p) {
+          v[c] = v[c] ? v[c] : gen[gg][c];
+          ok = ok && v[c] != 0u;
+        }
+      return __ballot(!ok) == 0;
+    };
+    poll_generations<kC>(issue, take, [&] { if (lane == 0) report_error(a.err, a.err_host); }, a.spin);
+    unsigned prefix = 0;
+#pragma unroll
+    for (int c = 0; c < kC; ++c) {
+      const int q = 64 * c + lane;
+      prefix += (unsigned)wave_sum_i(q < p ? (int)(v[c] & ~kReady) : 0);
+      if (q < p) st_dev(slots + q, 0u);  // read: clear for the next launch
+    }
+    if (lane == 0) {
+      lds.base = (int)prefix;
+      if (p == S - 1) a.count[g] = (int32_t)(prefix + (unsigned)n_sel);
+    }
+  }
+  __syncthreads();
+  int32_t* dst = a.ids + (size_t)g * a.ids_stride + lds.base;
+  for (int i = tid; i < n_sel; i += kDT) dst[i] = rows[i];
+  if (p == S - 1) {
+    if (w == 0)
+      write_selection(lds.win, lds.need, a.counts + (size_t)g * kFP, a.features + (size_t)g * kTop,
+                      a.valid + (size_t)g * kTop, a.raw + g);
+    for (int i = tid; i < kChunks * kHq; i += kDT) st_dev(&a.stats[(size_t)g * kChunks * kHq + i], 0ull);
+    for (int i = tid; i < S * kTop; i += kDT) st_dev(&a.cand[(size_t)g * S * kTop + i], 0ull);
+  }
+}
+
 // kWide: union tiles of 65-128 words (the host's choice when tw > 64), whose
 // two chunks' words phase 4 requests.
 template <int KW, bool kGiven = false, bool kCap = false, bool kEarlyTail = false, bool kRouteOnly = false,
@@ -969,10 +1035,8 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
         m &= m - 1u;
       }
       const int total = __builtin_amdgcn_readlane(incl, 63);
-      if (lane == 0) {
-        lds.nsel = total;
-        st_dev(&a.status[(size_t)g * a.S + p], kReady | (unsigned)total);
-      }
+      if (lane == 0) lds.nsel = total;
+      publish_count<kRouteOnly>(a, g, p, total, lane);
     }
   } else {
     const int chunks = (a.tw + kTileWords - 1) / kTileWords;  // <= 8
@@ -1026,13 +1090,18 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
         rows[at++] = wd * 32 + (int)__builtin_ctz(m);
         m &= m - 1u;
       }
-      if (w == chunks - 1 && lane == 63) {
-        lds.nsel = off + incl;
-        st_dev(&a.status[(size_t)g * a.S + p], kReady | (unsigned)(off + incl));
+      if (w == chunks - 1) {
+        const int total = __builtin_amdgcn_readlane(off + incl, 63);
+        if (lane == 0) lds.nsel = total;
+        publish_count<kRouteOnly>(a, g, p, total, lane);
       }
     }
   }
   __syncthreads();
+  if constexpr (kRouteOnly) {
+    route_finish<KW>(a, g, p, lds, rows);
+    return;
+  }
   // the lower tiles' counts, requested once this workgroup's first K/V loads
   // are in flight and used after the attention (no barrier in between)
   unsigned lower[kMaxSplits / 64];  // 0 = not loaded yet (a workgroup without rows never prefetches)
@@ -1195,7 +1264,7 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
         mfma_blocks16<1>(st, ek, ev, early_nv);
       }
 #endif
-      const int n_rows = kRouteOnly ? 0 : n_sel + (t_hi - t_lo) - early_rows;
+      const int n_rows = n_sel + (t_hi - t_lo) - early_rows;
       attend_rows([&](int r) { return r < n_sel ? rows[r] : a.H + t_lo + early_rows + (r - n_sel); }, n_rows,
                   !id_list);
     }
@@ -1262,10 +1331,7 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     // workgroup 0 that this workgroup no longer reads any published word);
     // publish_sliced's first barrier waits for every wave's stash and also
     // publishes lds.base to every wave
-    if constexpr (kRouteOnly)
-      __syncthreads();  // lds.base to every wave
-    else
-      publish_sliced(lds.mf, a.state + (size_t)(g * a.S + p) * kHq * kSlices * kSliceW);
+    publish_sliced(lds.mf, a.state + (size_t)(g * a.S + p) * kHq * kSlices * kSliceW);
   }
   if constexpr (kCap) {
     // ascending, from the union word: rows[] holds them in window order
@@ -1283,22 +1349,6 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     if (p == a.S - 1 && w == 0)
       write_selection(lds.win, lds.need, a.counts + (size_t)g * kFP, a.features + (size_t)g * kTop,
                       a.valid + (size_t)g * kTop, a.raw + g);
-  if constexpr (kRouteOnly) {
-    // no attention: the group's last workgroup past its look-back (a ticket
-    // per workgroup) clears the statistics, candidates and tile counts, which
-    // no workgroup reads any more, and resets the ticket counter
-    __syncthreads();  // wave 0's look-back reads are done
-    if (tid == 0) lds.nsel = (int)inc_dev(&a.done[g]);
-    __syncthreads();
-    if (lds.nsel == a.S - 1) {
-      for (int i = tid; i < kChunks * kHq; i += kDT) st_dev(&a.stats[(size_t)g * kChunks * kHq + i], 0ull);
-      for (int i = tid; i < a.S * kTop; i += kDT) st_dev(&a.cand[(size_t)g * a.S * kTop + i], 0ull);
-      for (int i = tid; i < a.S; i += kDT) st_dev(&a.status[(size_t)g * a.S + i], 0u);
-      if (tid == 0) st_dev(&a.done[g], 0u);
-    }
-    return;
-  }
-
   // ---- 9. workgroups 0..15 each merge one (head, 32-dim slice) of the S
   // split states into out[g] and clear the words they read; workgroup 0
   // also clears the group's statistics, candidates and tile counts (every
@@ -1355,7 +1405,7 @@ int spin_limit() { return __atomic_load_n(&g_spin_limit, __ATOMIC_RELAXED); }
 // The walk's records and the route-and-union launch's ticket counters come
 // last: the other launches touch the first `walk` bytes only.
 struct DecodeWorkLayout {
-  size_t err, stats, cand, status, state, walk, done, total;
+  size_t err, stats, cand, status, state, walk, total;
   DecodeWorkLayout(int groups, int S) {
     size_t o = 0;
     auto take = [&](size_t n) { const size_t at = o; o += (n + 255) & ~(size_t)255; return at; };
@@ -1365,7 +1415,6 @@ struct DecodeWorkLayout {
     status = take((size_t)groups * S * sizeof(unsigned));
     state = take((size_t)groups * S * kHq * kSlices * kSliceW * sizeof(float));
     walk = take((size_t)groups * kWindows * S * kPacked * sizeof(unsigned));
-    done = take((size_t)groups * sizeof(unsigned));
     total = o;
   }
 };
@@ -1494,7 +1543,6 @@ static int decode_launch(uint64_t q, uint64_t moments, uint64_t counts, uint64_t
   a.spin = spin_limit();
   a.state = reinterpret_cast<float*>(w + L.state);
   a.walk = reinterpret_cast<unsigned*>(w + L.walk);
-  a.done = reinterpret_cast<unsigned*>(w + L.done);
   a.limit = (int)std::min<int64_t>(limit, H);
   a.features = reinterpret_cast<int64_t*>(features);
   a.valid = reinterpret_cast<float*>(valid);
