@@ -1401,9 +1401,10 @@ int spin_limit() { return __atomic_load_n(&g_spin_limit, __ATOMIC_RELAXED); }
 }  // namespace prismkv
 
 // Work layout (bytes) for the split count of `groups` groups:
-// err (the error word, then the host-word slot at byte 8) | stats | candidates | status | state | walk | done.
-// The walk's records and the route-and-union launch's ticket counters come
-// last: the other launches touch the first `walk` bytes only.
+// err (the error word, then the host-word slot at byte 8) | stats | candidates | status | state | walk.
+// The capped walk's records come last: the other launches touch the first
+// `walk` bytes only (the route-and-union launch keeps its count slots in the
+// state region).
 struct DecodeWorkLayout {
   size_t err, stats, cand, status, state, walk, total;
   DecodeWorkLayout(int groups, int S) {
