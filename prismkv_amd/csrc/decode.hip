@@ -982,23 +982,29 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   if constexpr (kCap) {
     // the capped launch lists its rows during the walk (phase 6)
   } else if (id_list) {
-    // ---- 5'. the workgroup's share of the group's list (count ids, then the
-    // T tail rows H .. H + T - 1): rows [p per, (p + 1) per) as positions
-    const int given_cnt = a.count_in[g];
-    const int cnt = min(max(given_cnt, 0), a.H), total = cnt + a.T;
-    const int per = (total + a.S - 1) / a.S;
-    const int lo = min(total, p * per), n = min(total, lo + per) - lo;
+    // ---- 5'. the workgroup's 16-position chunks of the group's list (count
+    // ids, then the T tail rows H .. H + T - 1): chunks p, p + S, p + 2S, ...
+    // A workgroup's positions do not depend on count, so its first kDT ids
+    // are requested together with count instead of after it lands; only the
+    // list's last chunk is partial.
     const int32_t* idg = a.ids_in + (size_t)g * a.ids_stride;
+    auto pos_of = [&](int k) { return (p + a.S * (k >> 4)) * 16 + (k & 15); };  // list entry k -> position
+    const int given_cnt = a.count_in[g];
+    const int id0 = idg[min(pos_of(tid), (int)a.ids_stride - 1)];  // in the id row whatever count is
+    const int cnt = min(max(given_cnt, 0), a.H), total = cnt + a.T;
+    const int chunks = (total + 15) / 16;
+    const int mine = chunks > p ? (chunks - p + a.S - 1) / a.S : 0;  // this workgroup's chunks
+    const int n = mine ? 16 * (mine - 1) + min(16, total - 16 * (p + a.S * (mine - 1))) : 0;
     bool bad = p == 0 && tid == 0 && given_cnt != cnt;
-    for (int i = tid; i < n; i += kDT) {
-      const int j = lo + i;
+    for (int k = tid; k < n; k += kDT) {
+      const int j = pos_of(k);
       int r = a.H + (j - cnt);
       if (j < cnt) {
-        const int id = idg[j];
+        const int id = k == tid ? id0 : idg[j];
         bad |= id < 0 || id >= a.H;
         r = min(max(id, 0), a.H - 1);
       }
-      rows[i] = r;
+      rows[k] = r;
     }
     if (bad) report_error(a.err, a.err_host, kErrIds);  // the rows stay in range (clamped)
     if (tid == 0) lds.nsel = n;
@@ -1116,7 +1122,11 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   // the list's last block is partial: a wave's block whose lanes mostly
   // repeat one row still costs about a third of a full block's load time,
   // so whole blocks are dealt rather than equal row counts.
-  const int T = a.tail_dev ? min(max(tail_word, 0), a.T) : a.T;
+  int tail_now = tail_word;
+  // (the given-selection kernels: without this the compiler converts the word
+  // to a scalar right after its load, which waits a whole round trip at launch)
+  if constexpr (kGiven) asm volatile("" : "+v"(tail_now));
+  const int T = a.tail_dev ? min(max(tail_now, 0), a.T) : a.T;
   const int tail_per = id_list ? 0 : (T + a.S - 1) / a.S;  // an id list holds its tail rows
   const int t_lo = min(T, p * tail_per), t_hi = min(T, t_lo + tail_per);
   // the list: the tile's tokens, then the tail rows the early blocks did not take
@@ -1596,8 +1606,8 @@ static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t b
 
 // ---- stage 3 over a given id list ---------------------------------------
 // The decode's phases 6-9 with each workgroup's rows read from the group's id
-// list (an even share of count[g] + T rows per workgroup, the tail rows last)
-// instead of a union tile: round-robin 16-row MFMA blocks, the sliced split
+// list (every S-th 16-row chunk of count[g] ids + T tail rows, the tail rows
+// last) instead of a union tile: round-robin 16-row MFMA blocks, the sliced split
 // states and the 16 merging workgroups, with the decode's bounded waits and
 // error word (word 0 of the region, its host-word slot at byte 8).
 namespace prismkv {
@@ -1637,7 +1647,8 @@ int attend_list(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t count
   a.count_in = reinterpret_cast<const int32_t*>(count);
   const dim3 grid(S, groups), block(kDT);
   hipStream_t s = (hipStream_t)stream;
-  const size_t rows_bytes = (size_t)((H + T + S - 1) / S) * sizeof(int);
+  // a workgroup's list: at most ceil(ceil((H + T) / 16) / S) 16-row chunks
+  const size_t rows_bytes = (size_t)16 * (((H + T + 15) / 16 + S - 1) / S) * sizeof(int);
   if (S <= 32) hipLaunchKernelGGL((decode_kernel<1, true>), grid, block, rows_bytes, s, a);
   else if (S <= 64) hipLaunchKernelGGL((decode_kernel<2, true>), grid, block, rows_bytes, s, a);
   else if (S <= 128) hipLaunchKernelGGL((decode_kernel<4, true>), grid, block, rows_bytes, s, a);
