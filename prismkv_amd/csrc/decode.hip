@@ -945,9 +945,11 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     if (w == 0 && !id_list) {
       bool ok = false;
       int f = 0;
-      if (lane < kTop && a.valid[(size_t)g * kTop + lane] > 0.f) {
+      if (lane < kTop) {
+        // both requested at once (not the id only where valid holds)
+        const float vl = a.valid[(size_t)g * kTop + lane];
         const int64_t fe = a.features[(size_t)g * kTop + lane];
-        ok = fe >= 0 && fe < kF;
+        ok = vl > 0.f && fe >= 0 && fe < kF;
         f = (int)fe;
       }
       const unsigned long long m = __ballot(ok);
