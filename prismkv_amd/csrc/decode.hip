@@ -107,6 +107,7 @@ struct DecodeArgs {
   float* state;  // [G][S][4 heads][4 slices][34] published split states
   unsigned* walk;  // [G][4 windows][S][8] published pattern counts (capped launch)
   int limit;       // the strict unique cap's limit (capped launch)
+  int rows16;      // capped launch: rows and tiles 16-byte aligned (the walk reads its words 4 a lane)
   int64_t* features;
   float* valid;
   int* raw;
@@ -666,7 +667,37 @@ __device__ __forceinline__ uint32_t capped_walk(const DecodeArgs& a, int g, int 
   const uint32_t wmask = !col ? 0u : (wd == nw - 1 && (a.H & 31)) ? (1u << (a.H & 31)) - 1u : ~0u;
   // every ranked row's word, all requested at once, kept in LDS
   uint32_t* words = reinterpret_cast<uint32_t*>(rows + 32 * a.tw);
-  {
+  if (a.rows16) {
+    // aligned rows and tiles: wave w takes ranks w and w + 8, lane l words
+    // 4 l .. 4 l + 3 of each 256-word part of the tile (16-byte loads: a
+    // CU's load instructions, not their bytes, bound this)
+    constexpr int kRanks = kTop / (kDT / 64), kParts = kDT / 256;  // 2, 2
+    uint4 q[kRanks][kParts];
+#pragma unroll
+    for (int i = 0; i < kRanks; ++i) {
+      const int r = w + (kDT / 64) * i;
+      const uint32_t* row = a.bits + ((size_t)g * kF + (r < nr ? lds.sel_rows[r] : 0)) * a.row_words;
+      const __amdgpu_buffer_rsrc_t res = raw_buffer(row, r < nr ? (int)a.row_words * 4 : 0);  // past the row: 0
+#pragma unroll
+      for (int j = 0; j < kParts; ++j)
+        q[i][j] = 256 * j < a.tw ? load_nt16_buf(res, (unsigned)(p * a.tw + 256 * j + 4 * lane) * 4u)
+                                 : make_uint4(0u, 0u, 0u, 0u);
+    }
+#pragma unroll
+    for (int i = 0; i < kRanks; ++i)
+#pragma unroll
+      for (int j = 0; j < kParts; ++j) {
+        const int t = 256 * j + 4 * lane, wt = p * a.tw + t;
+        uint32_t m[4] = {q[i][j].x, q[i][j].y, q[i][j].z, q[i][j].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          m[e] = t + e < a.tw && wt + e < nw ? m[e] : 0u;
+          if (wt + e == nw - 1 && (a.H & 31)) m[e] &= (1u << (a.H & 31)) - 1u;
+        }
+        *reinterpret_cast<uint4*>(&words[(w + (kDT / 64) * i) * kDT + t]) = make_uint4(m[0], m[1], m[2], m[3]);
+      }
+    __syncthreads();  // every rank's words, for every thread
+  } else {
     uint32_t v[kTop];
     const uint32_t* gb = a.bits + (size_t)g * kF * a.row_words + (col ? wd : 0);
 #pragma unroll
@@ -921,7 +952,7 @@ template <int KW, bool kGiven = false, bool kCap = false, bool kEarlyTail = fals
 __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   const int p = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   __shared__ DecodeLds lds;
-  extern __shared__ int rows[];  // the tile's selected tokens, ascending (32 tw of them)
+  extern __shared__ __align__(16) int rows[];  // the tile's selected tokens, ascending (32 tw of them)
   // the tail length: the host's T, or the device word clamped to it (the
   // host checked the K/V extents for T).  The word is requested now, with
   // no branch (without a device word the load reads q and is ignored), so
@@ -1546,6 +1577,10 @@ static int decode_launch(uint64_t q, uint64_t moments, uint64_t counts, uint64_t
   a.T = T;
   a.S = S;
   a.tw = ((H + 31) / 32 + S - 1) / S;
+  // the capped walk reads its words 4 a lane: a tile of a multiple of 4
+  // words, and rows16 when the rows are of a multiple of 4 words too
+  if (limit >= 0) a.tw = (a.tw + 3) & ~3;
+  a.rows16 = limit >= 0 && row_words % 4 == 0;
   a.tail_dev = tail_dev;
   a.stats = reinterpret_cast<unsigned long long*>(w + L.stats);
   a.cand = reinterpret_cast<unsigned long long*>(w + L.cand);
