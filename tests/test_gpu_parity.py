@@ -428,6 +428,39 @@ def test_capped_decode_groups(groups):
     log(f"  groups={groups}: kept buckets per cap {kept}")
 
 
+def test_capped_decode_unaligned_rows():
+    # prismkv_decode_capped reads the walk's words 4 a lane when every bucket
+    # row is 16-byte aligned (row_words a multiple of 4, as Native8B lays the
+    # bitmaps out) and one word a thread otherwise: the same bitmaps with one
+    # padding word a row (odd row_words) give bit-identical outputs
+    case = cases.native_case(32768, 40, "random", seed=19)
+    op, q, k, v = operator(case)
+    s = torch.cuda.current_stream().cuda_stream
+    groups = 8
+    work = torch.zeros(op.lib.query("prismkv_decode_work_bytes", groups, op.capacity), dtype=torch.uint8,
+                       device="cuda")
+    padded = torch.zeros(op.bits.shape[0], op.bits.shape[1], op.row_words + 1, dtype=op.bits.dtype, device="cuda")
+    padded[:, :, :op.row_words] = op.bits
+    assert op.row_words % 4 == 0 and (op.row_words + 1) % 4 != 0
+    for cap in (0.01, 0.05, 1.0):
+        op.unique_cap = cap
+        outs = []
+        for bits, rw in ((op.bits, op.row_words), (padded, op.row_words + 1)):
+            for x in (op.features, op.valid, op.raw, op.ids, op.count, op.out):
+                x.zero_()
+            op.lib.call("prismkv_decode_capped", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(),
+                        bits.data_ptr(), k.data_ptr(), v.data_ptr(), work.data_ptr(), op.features.data_ptr(),
+                        op.valid.data_ptr(), op.raw.data_ptr(), op.ids.data_ptr(), op.count.data_ptr(),
+                        op.out.data_ptr(), groups, op.history, k.shape[1] - op.history, op.capacity,
+                        op._cap_limit(), rw, k.stride(0), v.stride(0), op.capacity, nbytes(work), stream=s)
+            torch.cuda.synchronize()
+            assert int(work[:4].view(torch.int32)[0]) == 0  # no bounded wait gave up
+            outs.append([x.clone() for x in (op.features, op.valid, op.raw, op.ids, op.count, op.out)])
+        for a, b in zip(*outs):
+            assert torch.equal(a, b), cap
+        log(f"  cap={cap}: aligned and odd row_words identical, unique ids {outs[0][4].tolist()}")
+
+
 @pytest.mark.parametrize("groups", [1, 2, 3, 4, 5, 7])
 def test_fused_decode_fewer_groups(groups):
     # prismkv_decode on the first `groups` groups runs 256 / groups workgroups
