@@ -122,8 +122,8 @@ int prismkv_build_bits(uint64_t ids, uint64_t offsets, uint64_t bits, int groups
 /* Stage 3 (replaces attention_tuned, src/prismkv/native8b.py:91-102;
  * semantics src/prismkv/core.py:170-183): when H + T <= 16384 x S (S =
  * min(256, max(32, 256 / groups)) workgroups per group, all resident), the
- * fused decode's attention phases over every S-th 16-row chunk of each
- * group's count + T rows per workgroup; otherwise split-K with the merge fused into
+ * fused decode's attention phases over each group's count + T rows (every
+ * S-th 16-row chunk per workgroup; contiguous shares past 512 S rows); otherwise split-K with the merge fused into
  * the last workgroup of each group.  splits in [1,1024] (the partition does
  * not change the result).  `work` (prismkv_attend_work_bytes) is zero-filled
  * once before first use and left zeroed; its first 32-bit word is the error

@@ -1015,25 +1015,30 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   if constexpr (kCap) {
     // the capped launch lists its rows during the walk (phase 6)
   } else if (id_list) {
-    // ---- 5'. the workgroup's 16-position chunks of the group's list (count
-    // ids, then the T tail rows H .. H + T - 1): chunks p, p + S, p + 2S, ...
-    // A workgroup's positions do not depend on count, so its first kDT ids
-    // are requested together with count instead of after it lands; only the
-    // list's last chunk is partial.
+    // ---- 5'. the workgroup's entries of the group's list (count ids, then
+    // the T tail rows H .. H + T - 1).  A list of at most kDT S entries (a
+    // sparse union) goes in 16-position chunks p, p + S, p + 2S, ... (kDT
+    // entries a workgroup at most), positions that do not depend on count,
+    // so their ids are requested together with count instead of after it
+    // lands.  A longer list goes in contiguous even shares, which keep each
+    // workgroup's K/V reads local; its ids are read once count has landed.
     const int32_t* idg = a.ids_in + (size_t)g * a.ids_stride;
-    auto pos_of = [&](int k) { return (p + a.S * (k >> 4)) * 16 + (k & 15); };  // list entry k -> position
     const int given_cnt = a.count_in[g];
-    const int id0 = idg[min(pos_of(tid), (int)a.ids_stride - 1)];  // in the id row whatever count is
+    const int id0 = idg[min((p + a.S * (tid >> 4)) * 16 + (tid & 15), (int)a.ids_stride - 1)];  // in the id row
     const int cnt = min(max(given_cnt, 0), a.H), total = cnt + a.T;
-    const int chunks = (total + 15) / 16;
-    const int mine = chunks > p ? (chunks - p + a.S - 1) / a.S : 0;  // this workgroup's chunks
-    const int n = mine ? 16 * (mine - 1) + min(16, total - 16 * (p + a.S * (mine - 1))) : 0;
+    const bool inter = total <= kDT * a.S;  // uniform
+    const int chunks = (total + 15) / 16, per = (total + a.S - 1) / a.S;
+    const int mine = chunks > p ? (chunks - p + a.S - 1) / a.S : 0;  // interleaved: this workgroup's chunks
+    const int lo = min(total, p * per);                             // contiguous: the first position
+    const int n = inter ? (mine ? 16 * (mine - 1) + min(16, total - 16 * (p + a.S * (mine - 1))) : 0)
+                        : min(total, lo + per) - lo;
+    auto pos_of = [&](int k) { return inter ? (p + a.S * (k >> 4)) * 16 + (k & 15) : lo + k; };
     bool bad = p == 0 && tid == 0 && given_cnt != cnt;
     for (int k = tid; k < n; k += kDT) {
       const int j = pos_of(k);
       int r = a.H + (j - cnt);
       if (j < cnt) {
-        const int id = k == tid ? id0 : idg[j];
+        const int id = inter && k == tid ? id0 : idg[j];
         bad |= id < 0 || id >= a.H;
         r = min(max(id, 0), a.H - 1);
       }
@@ -1643,8 +1648,9 @@ static int decode_impl(uint64_t q, uint64_t moments, uint64_t counts, uint64_t b
 
 // ---- stage 3 over a given id list ---------------------------------------
 // The decode's phases 6-9 with each workgroup's rows read from the group's id
-// list (every S-th 16-row chunk of count[g] ids + T tail rows, the tail rows
-// last) instead of a union tile: round-robin 16-row MFMA blocks, the sliced split
+// list (count[g] ids, then the T tail rows: every S-th 16-row chunk of a list
+// of at most 512 S entries, even contiguous shares of a longer one) instead
+// of a union tile: round-robin 16-row MFMA blocks, the sliced split
 // states and the 16 merging workgroups, with the decode's bounded waits and
 // error word (word 0 of the region, its host-word slot at byte 8).
 namespace prismkv {
@@ -1684,8 +1690,9 @@ int attend_list(uint64_t q, uint64_t k, uint64_t v, uint64_t ids, uint64_t count
   a.count_in = reinterpret_cast<const int32_t*>(count);
   const dim3 grid(S, groups), block(kDT);
   hipStream_t s = (hipStream_t)stream;
-  // a workgroup's list: at most ceil(ceil((H + T) / 16) / S) 16-row chunks
-  const size_t rows_bytes = (size_t)16 * (((H + T + 15) / 16 + S - 1) / S) * sizeof(int);
+  // a workgroup's list: at most kDT interleaved entries, or a contiguous
+  // share of ceil((H + T) / S)
+  const size_t rows_bytes = (size_t)std::max(kDT, (H + T + S - 1) / S) * sizeof(int);
   if (S <= 32) hipLaunchKernelGGL((decode_kernel<1, true>), grid, block, rows_bytes, s, a);
   else if (S <= 64) hipLaunchKernelGGL((decode_kernel<2, true>), grid, block, rows_bytes, s, a);
   else if (S <= 128) hipLaunchKernelGGL((decode_kernel<4, true>), grid, block, rows_bytes, s, a);
