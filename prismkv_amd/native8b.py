@@ -450,7 +450,8 @@ class Native8B:
         accepted for compatibility; the softmax is exact, so the partition does
         not change the result.  The launch is the fused decode's attention
         phases over the selection's ids (every S-th 16-row chunk of a group's
-        rows per workgroup, contiguous shares of a list longer than 512 S); a wait that gives up is reported at the next call."""
+        rows per workgroup, contiguous shares of a list longer than 512 S);
+        a wait that gives up is reported at the next call."""
         self._check_kv(q, k, v, splits, schedule)
         self.check_errors()
         self.lib.call("prismkv_attend", q.data_ptr(), k.data_ptr(), v.data_ptr(), self.ids.data_ptr(),
