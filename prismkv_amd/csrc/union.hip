@@ -116,9 +116,11 @@ __global__ __launch_bounds__(kUT) void union_kernel(const uint32_t* __restrict__
     // wave 0 compacts the valid, in-range selections (an out-of-range id selects nothing)
     bool ok = false;
     int f = 0;
-    if (tid < kSel && valid[(size_t)g * kSel + tid] > 0.f) {
+    if (tid < kSel) {
+      // both requested at once (not the id only where valid holds)
+      const float vl = valid[(size_t)g * kSel + tid];
       const int64_t fe = features[(size_t)g * kSel + tid];
-      ok = fe >= 0 && fe < kF;
+      ok = vl > 0.f && fe >= 0 && fe < kF;
       f = (int)fe;
     }
     const unsigned long long m = __ballot(ok);
