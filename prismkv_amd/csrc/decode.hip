@@ -9,10 +9,13 @@
 // padding rules of kernels/ppu_8b/route_parallel.cu:12,23,29 and the ascending
 // emission of kernels/ppu_8b/union.cu:26.
 //
-// Two more launches share these phases: route_kernel runs phases 1-4 alone
-// (prismkv_route_single), and decode_kernel<KW, true> runs phases 5-9 on a
+// Other launches share these phases: route_kernel runs phases 1-4 alone
+// (prismkv_route_single); decode_kernel<KW, true> runs phases 5-9 on a
 // selection read from features / valid (prismkv_union_attend, after a strict
-// unique cap has walked it).
+// unique cap has walked it) or phases 6-9 on a given id list (prismkv_attend);
+// the capped variant runs the budgeted walk between phases 4 and 6
+// (prismkv_decode_capped); the route-only variant stops after the ids
+// (prismkv_route_union).
 //
 // Grid (S, G) x 512, S = clamp(256 / G, 32, 256) (32 for 8 groups: the whole
 // launch is resident at once, one workgroup per CU, at any history).  Workgroup p
@@ -31,16 +34,19 @@
 //      publish its 16 best;
 //   4. read the group's S x 16 candidates as they land and rank them: the
 //      group's Top-16 is among them, and every workgroup computes the same
-//      winners; workgroup 0 writes features / valid / raw;
-//   5. union tile: one wave per 64 of its tw words ORs the selected rows and
-//      compacts the set bits into an LDS token list, publishing the tile's
-//      count (and requesting the lower tiles' counts);
-//   6. attention over the tile's tokens plus its tail share: wave w takes a
-//      contiguous eighth of the rows in 16-row MFMA blocks, with the K/V
-//      loads of four blocks in flight at once;
+//      winners; meanwhile each wave requests the tile's bitmap words of its
+//      best candidates' rows (and, for long tails, its first tail block);
+//   5. union tile: OR the winners' rows over the tile's words (prefetched in
+//      phase 4 for tiles of up to 128 words) and compact the set bits into
+//      an LDS token list, publishing the tile's count;
+//   6. attention over the tile's tokens plus its tail share in 16-row MFMA
+//      blocks dealt round-robin to the waves, the K/V loads of up to four
+//      blocks per wave in flight at once (the lower tiles' counts requested
+//      meanwhile);
 //   7. the tile's ids offset: prefix = sum of the counts of the lower tiles;
 //   8. its split state (per head max, denominator, acc[128]) is published,
-//      then the tile's ids go to ids[g][prefix ...];
+//      then the tile's ids go to ids[g][prefix ...], and the group's last
+//      workgroup writes features / valid / raw;
 //   9. workgroups 0..15 each read one (head, 32-dim slice) of the S split
 //      states as they land, merge it into out[g] and clear the words they
 //      read; workgroup 0 also clears the group's statistics, candidates and
@@ -48,7 +54,7 @@
 // Published words hold the bitwise complement of their value, so a zero
 // word (as cleared, or as the zero-filled workspace starts) reads as "not
 // yet written": readers poll the data itself, one memory round trip after
-// the writer's store, with no flags and no drains.  Waits only involve the
+// the writer's store, with no flags and no fences.  Waits only involve the
 // workgroups of one group, which the in-order dispatcher starts back to back
 // (S <= 256 fit on the GPU at once); every wait is bounded and reports
 // through the error word instead of hanging.  Data crosses workgroups only
