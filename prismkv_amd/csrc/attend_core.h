@@ -158,7 +158,7 @@ __device__ __forceinline__ void attend_step(const float (&qf)[kHq][8], const R (
 
 // Merges the 32 slot states of the workgroup in LDS and stores the result as
 // split state `stp` ((max, den, acc[128]) per head; head h at stp + h * hstride).
-__device__ void store_wg_state(const SlotState& s, AttendLds& lds, float* stp, size_t hstride) {
+__device__ inline void store_wg_state(const SlotState& s, AttendLds& lds, float* stp, size_t hstride) {
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, q16 = lane & 15, slot = lane >> 4;
   __syncthreads();  // LDS shared with the caller's earlier phases is free again
   // gather the slot's per-head max / denominator into every lane

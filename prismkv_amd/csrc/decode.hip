@@ -235,7 +235,6 @@ __device__ __forceinline__ void poll_generations(Issue&& issue, Ready&& ready, R
 __device__ __forceinline__ int row_of(unsigned long long key) { return min(key_bucket(key), kF - 1); }
 
 // Published words: the complement of the value's bits, so 0 = not yet.
-__device__ __forceinline__ void pub(float* p, float v) { st_dev(reinterpret_cast<unsigned*>(p), ~__float_as_uint(v)); }
 __device__ __forceinline__ void pub2(unsigned long long* p, float a, float b) {
   st_dev(p, ~(((unsigned long long)__float_as_uint(b) << 32) | (unsigned long long)__float_as_uint(a)));
 }
