@@ -428,6 +428,38 @@ def test_capped_decode_groups(groups):
     log(f"  groups={groups}: kept buckets per cap {kept}")
 
 
+@pytest.mark.parametrize("groups", [1, 2, 3, 5, 7])
+def test_route_union_fewer_groups(groups):
+    # prismkv_route_union on the first `groups` groups runs 256 / groups
+    # workgroups per group (64 .. 256: count slots of 64 .. 256 readers, each
+    # reader polling up to 4 chunks of 64 lower tiles); it selects and lists
+    # exactly what the 8-group launch does for those groups, twice in a row
+    # on one workspace, which it leaves zero
+    op, q, k, v = device_layer(16384, 16, seed=21)
+    s = torch.cuda.current_stream().cuda_stream
+    op.route(q)
+    torch.cuda.synchronize()
+    want = route_outputs(op)
+    work = torch.zeros(op.lib.query("prismkv_decode_work_bytes", groups, op.capacity), dtype=torch.uint8,
+                       device="cuda")
+    for call in range(2):
+        feats, valid, raw = torch.zeros_like(op.features), torch.zeros_like(op.valid), torch.zeros_like(op.raw)
+        ids, count = torch.zeros_like(op.ids), torch.zeros_like(op.count)
+        op.lib.call("prismkv_route_union", q.data_ptr(), op.moments.data_ptr(), op.n.data_ptr(), op.bits.data_ptr(),
+                    work.data_ptr(), feats.data_ptr(), valid.data_ptr(), raw.data_ptr(), ids.data_ptr(),
+                    count.data_ptr(), groups, op.history, op.capacity, op.row_words, op.capacity, nbytes(work),
+                    stream=s)
+        torch.cuda.synchronize()
+        assert int(work[:4].view(torch.int32)[0]) == 0  # no bounded wait gave up
+        got = (feats.cpu().numpy(), valid.cpu().numpy(), raw.cpu().numpy(), ids.cpu().numpy(), count.cpu().numpy())
+        for g in range(groups):
+            assert np.array_equal(got[0][g], want[0][g]) and np.array_equal(got[1][g], want[1][g]), (call, g)
+            assert got[2][g] == want[2][g] and got[4][g] == want[4][g], (call, g)
+            assert np.array_equal(got[3][g][:got[4][g]], want[3][g][:want[4][g]]), (call, g)
+        assert not bool(work[16:].any()), "the workspace is left zero"
+    log(f"  groups={groups}: route_union equals the 8-group launch, unique ids {got[4][:groups].tolist()}")
+
+
 def test_capped_decode_unaligned_rows():
     # prismkv_decode_capped reads the walk's words 4 a lane when every bucket
     # row is 16-byte aligned (row_words a multiple of 4, as Native8B lays the
