@@ -415,6 +415,11 @@ __device__ __forceinline__ void publish_count(const DecodeArgs& a, int g, int p,
   }
 }
 
+template <bool B>
+struct BoolTag {
+  static constexpr bool value = B;
+};
+
 struct NoEarly {
   __device__ void prepare() {}
   __device__ void barrier() { __syncthreads(); }
@@ -966,7 +971,9 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
   // Early tail (the uncapped decode): each wave's 16-row block of the
   // workgroup's tail rows is requested in phase 4, behind the bitmap words,
   // so it streams in while the selection finishes and the union is built
-  // (HBM is otherwise idle then); phase 6 attends it first.
+  // (HBM is otherwise idle then); in phase 6 it takes one slot of the
+  // wave's first round, whose other blocks' loads are issued before it is
+  // waited for (it can land after the union is built).
   constexpr bool kEarly = kEarlyTail && !kGiven && !kCap && !kRouteOnly && !PRISMKV_VALU_ATTENTION;
   constexpr int kPfChunks = kWide && !kGiven && !kCap ? 2 : 1;  // union chunks prefetched in phase 4
   int early_n = 0;
@@ -1220,18 +1227,33 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
     // attends n rows, row r at K/V row pos_of(r) (clamped into the group's
     // rows; rows past n repeat the block's first row and are masked); with
     // `look`, wave 0 requests the lower tiles' counts once its first K/V
-    // loads are in flight
-    auto attend_rows = [&](auto&& pos_of, int n, bool look) {
+    // loads are in flight.  pre_n > 0: the wave's early tail block (ek / ev,
+    // pre_n rows, requested in phase 4 and possibly still in flight) takes
+    // slot 0 of the first round, whose other slots take the list's first
+    // blocks, so the round's loads are issued before the early rows are
+    // waited for.
+    auto attend_rows = [&](auto&& pos_of, int n, bool look, auto pre_tag, int pre_n) {
       const int n_blocks = (n + 15) >> 4;
       auto row_pos = [&](int r, int base) {
         const int pos = pos_of(r < n ? r : base);
         return pos < 0 ? 0 : (pos > last_row ? last_row : pos);
       };
-      for (int k0 = kWaves - 1 - wu; k0 < n_blocks; k0 += kPerRound * kWaves) {  // blocks k0 + 8 i
+      // one round: the list's blocks k0 + 8 i in slots i (slots i + 1 with
+      // the early block in slot 0)
+      auto round = [&](int k0, auto pre_tag) {
+        constexpr int kShift = decltype(pre_tag)::value ? 1 : 0;
         uint4 kr[kPerRound][4], vr[kPerRound][4];
 #pragma unroll
         for (int i = 0; i < kPerRound; ++i) {
-          const int base = 16 * (k0 + kWaves * i);
+          if (i < kShift) {
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              kr[i][c] = ek[0][c];
+              vr[i][c] = ev[0][c];
+            }
+            continue;
+          }
+          const int base = 16 * (k0 + kWaves * (i - kShift));
           if (base < n) {  // uniform per wave
 #if PRISMKV_VALU_ATTENTION
 #pragma unroll
@@ -1267,9 +1289,69 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
 #else
         int nv[kPerRound];
 #pragma unroll
-        for (int i = 0; i < kPerRound; ++i) nv[i] = max(0, min(16, n - 16 * (k0 + kWaves * i)));
+        for (int i = 0; i < kPerRound; ++i)
+          nv[i] = i < kShift ? pre_n : max(0, min(16, n - 16 * (k0 + kWaves * (i - kShift))));
         mfma_blocks16<kPerRound>(st, kr, vr, nv);
 #endif
+      };
+      int k0 = kWaves - 1 - wu;
+#if !PRISMKV_VALU_ATTENTION
+      if constexpr (decltype(pre_tag)::value) {
+        if (pre_n > 0) {  // uniform
+          round(k0, BoolTag<true>{});
+          k0 += (kPerRound - 1) * kWaves;
+        }
+      }
+#endif
+      if constexpr (kCap) {
+        // (the rounds written out: as calls of `round` the capped launch's
+        // code is scheduled differently and measured 0.14 us slower)
+        for (; k0 < n_blocks; k0 += kPerRound * kWaves) {  // blocks k0 + 8 i
+          uint4 kr[kPerRound][4], vr[kPerRound][4];
+#pragma unroll
+          for (int i = 0; i < kPerRound; ++i) {
+            const int base = 16 * (k0 + kWaves * i);
+            if (base < n) {  // uniform per wave
+#if PRISMKV_VALU_ATTENTION
+#pragma unroll
+              for (int b = 0; b < 4; ++b) {
+                const size_t at = (size_t)row_pos(base + 4 * slot + b, base) * kD + 8 * q16;
+                kr[i][b] = load_nt16(kg + at);
+                vr[i][b] = load_nt16(vg + at);
+              }
+#else
+              const unsigned ko = (unsigned)row_pos(base + j, base) * (2 * kD) + 16 * qd;
+#pragma unroll
+              for (int c = 0; c < 4; ++c) kr[i][c] = load_nt16_buf(kbuf, ko + 64 * c);
+#pragma unroll
+              for (int t = 0; t < 4; ++t)
+                vr[i][t] = load_nt16_buf(vbuf, (unsigned)row_pos(base + 4 * qd + t, base) * (2 * kD) + 16 * j);
+#endif
+            }
+          }
+          asm volatile("" ::: "memory");  // every load of the round is in flight before any is used
+          if (look && k0 == kWaves - 1 - wu && wu == 0) {
+#pragma unroll
+            for (int c = 0; c < kMaxSplits / 64; ++c) {
+              const int qq = 64 * c + lane;
+              if (qq < p) lower[c] = ld_dev(&a.status[(size_t)g * a.S + qq]);
+            }
+          }
+#if PRISMKV_VALU_ATTENTION
+#pragma unroll
+          for (int i = 0; i < kPerRound; ++i) {
+            const int base = 16 * (k0 + kWaves * i);
+            if (base < n) attend_step(qf, kr[i], vr[i], max(0, min(4, n - base - 4 * slot)), st);
+          }
+#else
+          int nv[kPerRound];
+#pragma unroll
+          for (int i = 0; i < kPerRound; ++i) nv[i] = max(0, min(16, n - 16 * (k0 + kWaves * i)));
+          mfma_blocks16<kPerRound>(st, kr, vr, nv);
+#endif
+        }
+      } else {
+        for (; k0 < n_blocks; k0 += kPerRound * kWaves) round(k0, BoolTag<false>{});
       }
     };
     if constexpr (kCap) {
@@ -1279,9 +1361,9 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
       int listed = 0, attended = 0;
       walked = capped_walk(a, g, p, lds, rows, &keep, &listed, &attended, [&](int lo, int n) {
         if (lo < 0)
-          attend_rows([&](int r) { return a.H + t_lo + r; }, t_hi - t_lo, false);
+          attend_rows([&](int r) { return a.H + t_lo + r; }, t_hi - t_lo, false, BoolTag<false>{}, 0);
         else
-          attend_rows([&](int r) { return rows[lo + r]; }, n, false);
+          attend_rows([&](int r) { return rows[lo + r]; }, n, false, BoolTag<false>{}, 0);
       });
       // the tile's count for the look-back, and its ascending ids' offsets
       const int c = __popc(walked), incl = wave_scan_i(c);
@@ -1292,7 +1374,7 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
       walked_at += incl - c;
       n_sel = listed;
       if (tid == 0) st_dev(&a.status[(size_t)g * a.S + p], kReady | (unsigned)listed);
-      attend_rows([&](int r) { return rows[attended + r]; }, listed - attended, true);
+      attend_rows([&](int r) { return rows[attended + r]; }, listed - attended, true, BoolTag<false>{}, 0);
       // the kept buckets (in rank order, compacted) into features / valid /
       // raw, by a workgroup that merges nothing
       if (p == a.S - 1 && w == 0) {
@@ -1309,17 +1391,11 @@ __global__ __launch_bounds__(kDT) void decode_kernel(DecodeArgs a) {
         if (lane == 0) a.raw[g] = nb;
       }
     } else {
-#if !PRISMKV_VALU_ATTENTION
-      // the early tail block, requested in phase 4, has landed: attend it first
-      // (its registers are free again before the rounds' loads need theirs)
-      if (early_n > 0) {  // uniform
-        const int early_nv[1] = {early_n};
-        mfma_blocks16<1>(st, ek, ev, early_nv);
-      }
-#endif
+      // the tile's tokens and the tail rows the early blocks did not take;
+      // the early block goes with the first round
       const int n_rows = n_sel + (t_hi - t_lo) - early_rows;
       attend_rows([&](int r) { return r < n_sel ? rows[r] : a.H + t_lo + early_rows + (r - n_sel); }, n_rows,
-                  !id_list);
+                  !id_list, BoolTag<true>{}, early_n);
     }
 
     // each wave stashes its state as soon as its attention ends: the LDS
