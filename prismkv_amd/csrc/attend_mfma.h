@@ -1,12 +1,12 @@
 // Sparse attention of one wave on the matrix cores in 16-row blocks: QK^T
-// and PV both as v_mfma_f32_16x16x32_bf16, online softmax in fp32.
+// as v_mfma_f32_16x16x32_bf16, PV as v_mfma_f32_16x16x16_bf16, online
+// softmax in fp32.
 //
 // Semantics: src/prismkv/core.py:170-183 (exact softmax over the selected
 // rows and the tail, scale 1/sqrt(d)): scores are fp32 sums of exact bf16
 // products; probabilities stay fp32 up to the PV product, where each is
-// split into a bf16 head and a bf16 remainder (both in one product's
-// reduction), so P.V carries ~16 significant bits of P instead of bf16's 8;
-// accumulation is fp32.
+// split into a bf16 head and a bf16 remainder (two products), so P.V carries
+// ~16 significant bits of P instead of bf16's 8; accumulation is fp32.
 //
 // Operand layouts (lane l, j = l % 16, q = l / 16; r = 0..3 fp32 results,
 // D[i][jj] with i = 4q + r, jj = j for both shapes):
@@ -15,11 +15,9 @@
 //        row j of the block, dims 32c + 8q .. +8 -- one 16-byte load per
 //        chunk of its own row -- and Q[head j] (zero for j >= 4).  The scores
 //        of rows 4q + r for head j land in lane l.
-//   PV (16x16x32: A[i][k] with i = j, k = 8q + t; B[k][jj] with jj = j):
-//        D[head][dim] = P . V with the reduction index k = 8q + t taking
-//        row 4q + (t & 3), the head of its P for t < 4 and the remainder for
-//        t >= 4 -- exactly the rows the lane scored, so P needs no lane
-//        exchange, and V's rows 4q .. 4q + 3 go in twice; the 8 column
+//   PV (16x16x16: A[i][k] with i = j, k = 4q + t; B[k][jj] with jj = j):
+//        D[head][dim] = P . V with the reduction index k = 4q + t exactly
+//        the rows the lane scored, so P needs no lane exchange; the 8 column
 //        blocks n map dim 8j + n to column j, so lane l reads rows 4q + t at
 //        dims 8j .. 8j + 8 (16-byte loads; each load instruction covers 4
 //        whole rows) and pairs them per dim with v_perm.  Lanes 0-15 end
@@ -75,6 +73,8 @@ __device__ __forceinline__ unsigned dim_pair(const uint4& a, const uint4& b) {
   return __builtin_amdgcn_perm(wb, wa, (N & 1) ? 0x07060302u : 0x05040100u);
 }
 
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
 // Up to NB blocks of 16 rows as ONE step of the online softmax: the QK
 // products of every block first (independent MFMA chains), then one
 // running-max update for all of them (lazy: the max moves only when a score
@@ -122,6 +122,7 @@ __device__ __forceinline__ void mfma_blocks16(MfmaAttn& st, const uint4 (&kr)[NB
 #pragma unroll
       for (int r = 0; r < kHq; ++r) st.acc[n][r] *= ah[r];
   }
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
     if (nvalid[i] <= 0) continue;  // uniform
@@ -137,17 +138,15 @@ __device__ __forceinline__ void mfma_blocks16(MfmaAttn& st, const uint4 (&kr)[NB
       hi[t] = b >> 16;
       lo[t] = f32_to_bf16(p[t] - __uint_as_float(b & 0xffff0000u));
     }
-    // one 16x16x32 product per column block: k = 8q + t holds the head of
-    // P's row 4q + t for t < 4 and its remainder for t >= 4, and V's rows
-    // 4q .. 4q + 3 twice, so the reduction over k sums head and remainder
-    // products of the lane's four rows
-    const u32x4 pu = {hi[0] | hi[1] << 16, hi[2] | hi[3] << 16, lo[0] | lo[1] << 16, lo[2] | lo[3] << 16};
-    const bf16x8 pb = __builtin_bit_cast(bf16x8, pu);
+    const u32x2 uh = {hi[0] | hi[1] << 16, hi[2] | hi[3] << 16};
+    const u32x2 ul = {lo[0] | lo[1] << 16, lo[2] | lo[3] << 16};
+    const s16x4 ph = __builtin_bit_cast(s16x4, uh), pl = __builtin_bit_cast(s16x4, ul);
 #define PRISMKV_PVB(N)                                                                   \
     {                                                                                    \
-      const unsigned v01 = dim_pair<N>(vr[i][0], vr[i][1]), v23 = dim_pair<N>(vr[i][2], vr[i][3]); \
-      const u32x4 vu = {v01, v23, v01, v23};                                             \
-      st.acc[N] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pb, __builtin_bit_cast(bf16x8, vu), st.acc[N], 0, 0, 0); \
+      const u32x2 vu = {dim_pair<N>(vr[i][0], vr[i][1]), dim_pair<N>(vr[i][2], vr[i][3])}; \
+      const s16x4 vb = __builtin_bit_cast(s16x4, vu);                                    \
+      st.acc[N] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ph, vb, st.acc[N], 0, 0, 0); \
+      st.acc[N] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pl, vb, st.acc[N], 0, 0, 0); \
     }
     PRISMKV_PVB(0) PRISMKV_PVB(1) PRISMKV_PVB(2) PRISMKV_PVB(3)
     PRISMKV_PVB(4) PRISMKV_PVB(5) PRISMKV_PVB(6) PRISMKV_PVB(7)

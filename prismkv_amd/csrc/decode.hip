@@ -67,7 +67,7 @@
 #include "score.h"
 
 // The attention phase runs on the matrix cores (v_mfma_f32_16x16x32_bf16 for
-// QK and for PV).  Building with -DPRISMKV_VALU_ATTENTION=1 swaps in the
+// QK, 16x16x16 for PV).  Building with -DPRISMKV_VALU_ATTENTION=1 swaps in the
 // fp32 VALU attention of attend_core.h (same loads, online softmax, state
 // layout and merge) for the A/B that chose the matrix cores: 26.9 against
 // 30.3 us per layer at H = 65536 on MI355X.
