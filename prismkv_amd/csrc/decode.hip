@@ -41,8 +41,9 @@
 //      an LDS token list, publishing the tile's count;
 //   6. attention over the tile's tokens plus its tail share in 16-row MFMA
 //      blocks dealt round-robin to the waves, the K/V loads of up to four
-//      blocks per wave in flight at once (the lower tiles' counts requested
-//      meanwhile);
+//      blocks per wave in flight at once (a wave's early tail block,
+//      requested in phase 4, takes one slot of its first round; the lower
+//      tiles' counts requested meanwhile);
 //   7. the tile's ids offset: prefix = sum of the counts of the lower tiles;
 //   8. its split state (per head max, denominator, acc[128]) is published,
 //      then the tile's ids go to ids[g][prefix ...], and the group's last
