@@ -204,7 +204,7 @@ constexpr int kPollGens = PRISMKV_POLL_GENS;  // generations of a poll's loads i
 
 // Polls published words with kPollGens generations of kLoads unconditional
 // loads each in flight (issue(g) requests generation g, ready(g) takes it
-// and returns the caller's uniform verdict).  Nothing else is in flight
+// and returns whether every word has landed, uniform).  Nothing else is in flight
 // after the drain, so each generation is waited for exactly with
 // vmcnt((kPollGens - 1) kLoads), leaving the later ones outstanding; the
 // generations are issued poll_stagger() apart and so keep landing apart.
