@@ -73,6 +73,15 @@ def test_8b_geometry_64k_topk8():
     check_case(cases.topk8_case(H=65536, T=256, seed=2), splits_list=(16, 64, 128), schedules=(0,))
 
 
+def test_8b_geometry_64k_long_tail():
+    # the update policy leaves tails of up to 4096 rows between index updates
+    # (configs/submitted_8b.json:14).  2100 rows are 66 per workgroup at 32
+    # workgroups per group: the fused decode requests each wave's first tail
+    # block early (16 rows for waves 0-3, 2 for wave 4, none for waves 5-7)
+    # and attends it in a slot of the wave's first round
+    check_case(cases.topk8_case(H=65536, T=2100, seed=3), splits_list=(64,), schedules=(0,))
+
+
 def adversarial_case(name, H=4096, T=40, seed=11):
     rng = np.random.default_rng(seed)
     k = cases.bf16_normal((seed, 0), (8, H + T, 128))
