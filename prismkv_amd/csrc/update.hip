@@ -66,7 +66,8 @@ constexpr int kMaxTieBlocks = 4096;  // contiguous ranges of a per group for the
 constexpr int kTieMinLen = 65536;    // values per range at least (multiple of 4 * kUT)
 constexpr int kTieGrid = 256;        // workgroups per group of the tie kernels
 constexpr int kCenterParts = 64;     // row ranges of the center sum
-constexpr int kListCap = 1 << 17;    // candidates per group of the compact list (see refine)
+constexpr int kListChunk = 256;      // list entries a wave reserves at once once its workgroup's buffer is full
+constexpr unsigned kListSlack = (unsigned)kRefineBlocks * (kUT / 64) * kListChunk;  // unfilled chunk tails, at most
 constexpr int kMaxBuild = 1 << 20;   // keys per group of a build (N * F < 2^32 flat indices)
 constexpr int kBuildCenter = 1;      // prismkv_build flag: compute the center (else it is an input)
 
@@ -128,7 +129,8 @@ struct UpdateArgs {
   unsigned* hist;  // [G][kLevels][kRep][kBins]
   unsigned* ctl;   // [G][kCtl]
   unsigned* tcount;  // [G][tie_blocks] ties per contiguous range of a
-  uint2* list;       // [G][kListCap] (flat index, value bits) of the values at or above tau's first digit
+  uint2* list;       // [G][list_cap] (flat index, value bits) of the values at or above tau's first digit
+  unsigned list_cap;  // entries per group (0 bits: an unfilled chunk entry)
   int H, N;          // first key row / bitmap column, keys indexed
   long long budget;  // N * key_mean
   int tie_blocks;
@@ -366,7 +368,7 @@ __global__ __launch_bounds__(kUT) void digit_kernel(UpdateArgs a, int level) {
       // every value the selection can take lies in the first digit's bin or
       // above it: (count - found_rem) above, found_ties in it.  If they fit,
       // the first refine pass collects them and the later passes read only them.
-      ctl[kListed] = (unsigned long long)(count - found_rem) + found_ties <= (unsigned long long)kListCap;
+      ctl[kListed] = (unsigned long long)(count - found_rem) + found_ties + kListSlack <= (unsigned long long)a.list_cap;
       ctl[kListLen] = 0;
     }
     ctl[kMode] = kModeTopK;
@@ -391,9 +393,12 @@ __global__ __launch_bounds__(kUT) void digit_kernel(UpdateArgs a, int level) {
 // when the digit kernel found that they fit (ctl kListed), also collects every
 // positive value whose first digit is at or above tau's into the group's
 // compact list: a workgroup gathers its own in LDS (slots by LDS atomics) and
-// reserves its range of the list with one global atomic at its end (a wave
-// that finds the LDS buffer full reserves its own slots instead); level 2
-// and the emit then read only the list.
+// reserves its range of the list with one global atomic at its end; once the
+// LDS buffer is full, each wave writes into chunks of kListChunk entries of
+// the list that it reserves one at a time and zero-fills the unused tail of
+// its last one (an index build's candidates, about 8 per key, overflow every
+// buffer).  Level 2 and the emit then read only the list, skipping zero
+// entries.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kUT) void refine_kernel(UpdateArgs a, int level) {
   const int g = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
@@ -414,17 +419,20 @@ __global__ __launch_bounds__(kUT) void refine_kernel(UpdateArgs a, int level) {
   const int shift_hi = level == 1 ? 20 : 9;  // bits above this level's digit
   const int shift = level == 1 ? 9 : 0;
   const unsigned dmask = level == 1 ? 0x7ffu : 0x1ffu;
-  uint2* list = a.list + (size_t)g * kListCap;
+  uint2* list = a.list + (size_t)g * a.list_cap;
   if (level == 2 && listed) {
-    const unsigned len = min(ctl[kListLen], (unsigned)kListCap);
+    const unsigned len = min(ctl[kListLen], a.list_cap);
     for (unsigned i = blockIdx.x * kUT + tid; i < len; i += gridDim.x * kUT) {
       const unsigned u = list[i].y;
-      if ((u >> shift_hi) == prefix) atomicAdd(&hist[(u >> shift) & dmask], 1u);
+      if (u != 0u && (u >> shift_hi) == prefix) atomicAdd(&hist[(u >> shift) & dmask], 1u);
     }
   } else {
     const size_t n = (size_t)a.N * kF;
     const float4* ag = reinterpret_cast<const float4*>(a.act + (size_t)g * n);
     const bool collect = level == 1 && listed;
+    // this wave's chunk of the list, once the workgroup's buffer is full:
+    // entries [c_at, c_at + c_n) are filled (c_n = kListChunk: none to fill)
+    unsigned c_at = 0u, c_n = (unsigned)kListChunk;
     for (size_t i = (size_t)blockIdx.x * kUT + tid; i < (n / 4 + kUT - 1) / kUT * kUT;
          i += (size_t)gridDim.x * kUT) {  // every lane of a wave iterates alike (the list's ballot)
       const bool in = i < n / 4;
@@ -445,21 +453,36 @@ __global__ __launch_bounds__(kUT) void refine_kernel(UpdateArgs a, int level) {
             if (at + cnt <= (unsigned)kBuf) {  // uniform
               if (take) buf[at + rank] = make_uint2((unsigned)(4 * i + j), u);
             } else {
-              // the buffer is full: straight to the list.  Reservations come in
-              // increasing order, so every one that fitted lies below the first
-              // that did not, and the buffer's valid entries are those below it.
-              unsigned g_at = 0u;
-              if (lane == 0) {
-                atomicMin(&first_miss, at);
-                g_at = atomicAdd(&ctl[kListLen], cnt);
+              // the buffer is full: into the wave's chunk of the list, a new
+              // chunk reserved (one global atomic per kListChunk entries) for
+              // what does not fit.  Reservations come in increasing order, so
+              // every one that fitted the buffer lies below the first that did
+              // not, and the buffer's valid entries are those below it.
+              if (lane == 0) atomicMin(&first_miss, at);
+              const unsigned room = (unsigned)kListChunk - c_n;  // uniform
+              unsigned nat = 0u;
+              if (cnt > room) {  // uniform
+                if (lane == 0) nat = atomicAdd(&ctl[kListLen], (unsigned)kListChunk);
+                nat = __shfl(nat, 0);
               }
-              g_at = __shfl(g_at, 0);
-              if (take && g_at + rank < (unsigned)kListCap) list[g_at + rank] = make_uint2((unsigned)(4 * i + j), u);
+              if (take) {
+                const unsigned dst = rank < room ? c_at + c_n + rank : nat + (rank - room);
+                if (dst < a.list_cap) list[dst] = make_uint2((unsigned)(4 * i + j), u);
+              }
+              if (cnt > room) {
+                c_at = nat;
+                c_n = cnt - room;
+              } else {
+                c_n += cnt;
+              }
             }
           }
         }
       }
     }
+    // the unfilled tail of the wave's chunk reads as no entry (value bits 0)
+    for (unsigned e = c_n + lane; e < (unsigned)kListChunk; e += 64)
+      if (c_at + e < a.list_cap) list[c_at + e] = make_uint2(0u, 0u);
   }
   __syncthreads();
   unsigned* hg = hist_of(a, g, level) + (blockIdx.x % kRep) * kBins;
@@ -471,7 +494,7 @@ __global__ __launch_bounds__(kUT) void refine_kernel(UpdateArgs a, int level) {
   if (tid == 0) base_s = atomicAdd(&ctl[kListLen], nb);
   __syncthreads();
   for (unsigned i = tid; i < nb; i += kUT)
-    if (base_s + i < (unsigned)kListCap) list[base_s + i] = buf[i];
+    if (base_s + i < a.list_cap) list[base_s + i] = buf[i];
 }
 
 __device__ __forceinline__ void set_member(const UpdateArgs& a, int g, unsigned flat) {
@@ -490,12 +513,12 @@ __global__ __launch_bounds__(kUT) void emit_kernel(UpdateArgs a) {
   const float tau = __uint_as_float(ctl[kTau]);
   const bool take_ties = mode == kModeTopK && !ctl[kOrdered] && tau > 0.f;
   if (mode == kModeTopK && ctl[kListed]) {  // every candidate is in the compact list
-    const uint2* list = a.list + (size_t)g * kListCap;
-    const unsigned len = min(ctl[kListLen], (unsigned)kListCap);
+    const uint2* list = a.list + (size_t)g * a.list_cap;
+    const unsigned len = min(ctl[kListLen], a.list_cap);
     for (unsigned i = blockIdx.x * kUT + tid; i < len; i += gridDim.x * kUT) {
       const uint2 e = list[i];
       const float v = __uint_as_float(e.y);
-      if (v > tau || (take_ties && v == tau)) set_member(a, g, e.x);
+      if (e.y != 0u && (v > tau || (take_ties && v == tau))) set_member(a, g, e.x);
     }
     return;
   }
@@ -1077,11 +1100,13 @@ using namespace prismkv;
 // Work layout (bytes) for `groups` groups and blocks of N keys: the regions
 // that must start at zero (histograms, control words) and the other scratch
 // first, at offsets that depend on the group count only, then the block's
-// activations [groups][N][3000] f32 last.  A workspace sized for the largest
-// block therefore serves every smaller block: no call finds another call's
-// activations where it expects zeroed histograms.
+// activations [groups][N][3000] f32 and the compact candidate list
+// [groups][list_cap] (sized by N).  A workspace sized for the largest block
+// therefore serves every smaller block: no call finds another call's
+// activations or list where it expects zeroed histograms.
 struct UpdateLayout {
-  size_t hist, ctl, tcount, part, list, act, total;
+  size_t hist, ctl, tcount, part, act, list, total;
+  unsigned list_cap;
   UpdateLayout(int groups, int N) {
     size_t o = 0;
     auto take = [&](size_t n) { const size_t at = o; o += (n + 255) & ~(size_t)255; return at; };
@@ -1089,8 +1114,11 @@ struct UpdateLayout {
     ctl = take((size_t)groups * kCtl * sizeof(unsigned));
     tcount = take((size_t)groups * kMaxTieBlocks * 2 * sizeof(unsigned));
     part = take((size_t)groups * kCenterParts * kD * sizeof(double));
-    list = take((size_t)groups * kListCap * sizeof(uint2));
     act = take((size_t)groups * N * kF * sizeof(float));
+    // the compact list: room for 16 candidates per key (twice the 8 H
+    // budget of an index build) plus the chunk tails, at least 2^19
+    list_cap = N > 0 ? std::max(1u << 19, 16u * (unsigned)N + kListSlack) : 0u;
+    list = take((size_t)groups * list_cap * sizeof(uint2));
     total = o;
   }
 };
@@ -1115,6 +1143,7 @@ static UpdateArgs make_args(uint64_t k, uint64_t W, uint64_t b, uint64_t center,
   a.ctl = reinterpret_cast<unsigned*>(w + L.ctl);
   a.tcount = reinterpret_cast<unsigned*>(w + L.tcount);
   a.list = reinterpret_cast<uint2*>(w + L.list);
+  a.list_cap = L.list_cap;
   a.H = H;
   a.N = N;
   a.budget = (long long)N * key_mean;

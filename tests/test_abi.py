@@ -61,13 +61,16 @@ def test_work_size_queries(lib):
     assert lib.query("prismkv_build_work_bytes", 1, 1 << 20) >= (1 << 20) * 3000 * 4
     assert lib.query("prismkv_build_work_bytes", 1, (1 << 20) + 1) == 0
     assert lib.query("prismkv_build_work_bytes", 0, 16) == 0
-    # the activations sit last, after regions whose offsets depend on the group count only
+    # the activations follow regions whose offsets depend on the group count
+    # only; after them the compact candidate list: at least 2^19 entries of
+    # 8 bytes per group, 16 per key for a build's long blocks
     at = lib.query("prismkv_update_act_offset", 8)
     assert at > 0 and at % 256 == 0 and lib.query("prismkv_update_act_offset", 0) == 0
     for n in (1, 37, 4096):
-        assert lib.query("prismkv_update_work_bytes", 8, n) - at == (8 * n * 3000 * 4 + 255) // 256 * 256
-    assert lib.query("prismkv_build_work_bytes", 3, 1000) - lib.query("prismkv_update_act_offset", 3) == \
-        (3 * 1000 * 3000 * 4 + 255) // 256 * 256
+        act = (8 * n * 3000 * 4 + 255) // 256 * 256
+        assert lib.query("prismkv_update_work_bytes", 8, n) - at >= act + 8 * (1 << 19) * 8
+    assert lib.query("prismkv_build_work_bytes", 3, 65536) - lib.query("prismkv_update_act_offset", 3) >= \
+        3 * 65536 * 3000 * 4 + 3 * 16 * 65536 * 8
 
 
 def call_raw(lib, name, *args):

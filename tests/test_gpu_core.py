@@ -56,10 +56,11 @@ def test_positive_global_topk(kind):
         flat[262144:263168] = big[1024:]
         count = 1500
     elif kind == "wide_bin":
-        # 200000 positive values in tau's first-digit bin: more candidates than
-        # the compact list holds, so the later passes scan every value
+        # 600000 positive values in tau's first-digit bin: more candidates than
+        # the compact list holds (2^19 entries less the chunk tails' 2^18 at
+        # this block size), so the later passes scan every value
         a = 1.0 + torch.rand(N, F, generator=gen, device="cuda") * 0.0625
-        a.view(-1)[200000:] = -1.0
+        a.view(-1)[600000:] = -1.0
         count = 5000
     if kind == "random":
         a = a.relu()
