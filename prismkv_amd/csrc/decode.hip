@@ -327,45 +327,80 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int g, int h, i
   };
   poll_generations<1 + kPer>(issue, [&](int gen) { return __syncthreads_and(take(gen)) != 0; },
                               [&] { if (tid == 0) report_error(a.err, a.err_host); }, a.spin);
-  // M = max over splits, den = sum of weighted denominators (fixed order)
-  float2 mz = make_float2(-INFINITY, 0.f);
-  if (tid < S) {
-    const unsigned long long r = ~rmz;
-    mz = make_float2(__uint_as_float((unsigned)r), __uint_as_float((unsigned)(r >> 32)));
-    lds.fin.mz[tid] = mz;
-  }
-  float m = wave_max(mz.x);
-  if (lane == 0) lds.fin.red[w] = m;
-  __syncthreads();
-  float M = -INFINITY;
-#pragma unroll
-  for (int i = 0; i < kDT / 64; ++i) M = fmaxf(M, lds.fin.red[i]);
-  const float wk = (tid < S && mz.x != -INFINITY) ? exp2f(mz.x - M) : 0.f;
-  const float dsum = wave_sum(wk * mz.y);
-  __syncthreads();  // everyone has read red[] as maxima
-  if (lane == 0) lds.fin.red[w] = dsum;
-  // weighted accumulators of this thread's splits
-  float v = 0.f;
-#pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int k = sg + kGroups * i;
-    if (k < S) {
-      const float mk = lds.fin.mz[k].x;
-      const float wgt = mk == -INFINITY ? 0.f : exp2f(mk - M);
-      v = fmaf(wgt, __uint_as_float(~racc[i]), v);
+  if constexpr (KW <= 2) {
+    // S <= 64: wave 0 holds every split's (max, den), so it derives M, the
+    // splits' weights and the denominator alone and the other waves read the
+    // weights behind one barrier (the same values and order as below)
+    if (w == 0) {
+      float2 mz = make_float2(-INFINITY, 0.f);
+      if (tid < S) {
+        const unsigned long long r = ~rmz;
+        mz = make_float2(__uint_as_float((unsigned)r), __uint_as_float((unsigned)(r >> 32)));
+      }
+      const float M = wave_max(mz.x);
+      const float wk = (tid < S && mz.x != -INFINITY) ? exp2f(mz.x - M) : 0.f;
+      const float dsum = wave_sum(wk * mz.y);
+      if (tid < S) lds.fin.mz[tid].x = wk;
+      if (lane == 0) lds.fin.red[0] = dsum;
     }
-  }
-  lds.fin.part[sg][d] = v;
-  __syncthreads();
-  if (tid < 32) {
-    float den = 0.f;
+    __syncthreads();
+    float v = 0.f;
 #pragma unroll
-    for (int i = 0; i < kDT / 64; ++i) den += lds.fin.red[i];
-    float acc = 0.f;
+    for (int i = 0; i < kPer; ++i) {
+      const int k = sg + kGroups * i;
+      if (k < S) v = fmaf(lds.fin.mz[k].x, __uint_as_float(~racc[i]), v);
+    }
+    lds.fin.part[sg][d] = v;
+    __syncthreads();
+    if (tid < 32) {
+      const float den = lds.fin.red[0];
+      float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i < kGroups; ++i) acc += lds.fin.part[i][tid];
-    if (a.out)  // the route-and-union launch merges only to clear (no output)
-      a.out[((size_t)g * kHq + h) * kD + c * (kD / kSlices) + tid] = f32_to_bf16(den > 0.f ? acc / den : 0.f);
+      for (int i = 0; i < kGroups; ++i) acc += lds.fin.part[i][tid];
+      if (a.out)  // the route-and-union launch merges only to clear (no output)
+        a.out[((size_t)g * kHq + h) * kD + c * (kD / kSlices) + tid] = f32_to_bf16(den > 0.f ? acc / den : 0.f);
+    }
+  } else {
+    // M = max over splits, den = sum of weighted denominators (fixed order)
+    float2 mz = make_float2(-INFINITY, 0.f);
+    if (tid < S) {
+      const unsigned long long r = ~rmz;
+      mz = make_float2(__uint_as_float((unsigned)r), __uint_as_float((unsigned)(r >> 32)));
+      lds.fin.mz[tid] = mz;
+    }
+    float m = wave_max(mz.x);
+    if (lane == 0) lds.fin.red[w] = m;
+    __syncthreads();
+    float M = -INFINITY;
+  #pragma unroll
+    for (int i = 0; i < kDT / 64; ++i) M = fmaxf(M, lds.fin.red[i]);
+    const float wk = (tid < S && mz.x != -INFINITY) ? exp2f(mz.x - M) : 0.f;
+    const float dsum = wave_sum(wk * mz.y);
+    __syncthreads();  // everyone has read red[] as maxima
+    if (lane == 0) lds.fin.red[w] = dsum;
+    // weighted accumulators of this thread's splits
+    float v = 0.f;
+  #pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int k = sg + kGroups * i;
+      if (k < S) {
+        const float mk = lds.fin.mz[k].x;
+        const float wgt = mk == -INFINITY ? 0.f : exp2f(mk - M);
+        v = fmaf(wgt, __uint_as_float(~racc[i]), v);
+      }
+    }
+    lds.fin.part[sg][d] = v;
+    __syncthreads();
+    if (tid < 32) {
+      float den = 0.f;
+  #pragma unroll
+      for (int i = 0; i < kDT / 64; ++i) den += lds.fin.red[i];
+      float acc = 0.f;
+  #pragma unroll
+      for (int i = 0; i < kGroups; ++i) acc += lds.fin.part[i][tid];
+      if (a.out)  // the route-and-union launch merges only to clear (no output)
+        a.out[((size_t)g * kHq + h) * kD + c * (kD / kSlices) + tid] = f32_to_bf16(den > 0.f ? acc / den : 0.f);
+    }
   }
   // every word read above has been consumed (the barrier follows the last use)
   for (int i = tid; i < S * kSliceW; i += kDT) {
