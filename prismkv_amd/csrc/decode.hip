@@ -325,14 +325,9 @@ __device__ __forceinline__ void merge_slice(const DecodeArgs& a, int g, int h, i
       }
     return ok;
   };
-  // up to 64 splits each wave waits for its own words only (the barrier
-  // after wave 0's weights then waits for every wave); beyond, the
-  // workgroup waits as one
-  poll_generations<1 + kPer>(issue,
-                              [&](int gen) {
-                                if constexpr (KW <= 2) return __ballot(!take(gen)) == 0;
-                                else return __syncthreads_and(take(gen)) != 0;
-                              },
+  // each wave waits for its own words only: the first barrier below then
+  // waits for every wave
+  poll_generations<1 + kPer>(issue, [&](int gen) { return __ballot(!take(gen)) == 0; },
                               [&] { if (lane == 0) report_error(a.err, a.err_host); }, a.spin);
   if constexpr (KW <= 2) {
     // S <= 64: wave 0 holds every split's (max, den), so it derives M, the
